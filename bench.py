@@ -1,0 +1,249 @@
+#!/usr/bin/env python3
+"""Benchmark of the SF37 MoE FFN layer on one MI355X.
+
+Workload: one MoE layer decode step of 8 tokens,
+E=288 experts, K=4096, F=1280, top-8, Q3GU gate/up + Q2D down experts and a
+Q8_0 shared expert, router logits injected i.i.d. N(0,1) (uniform routing).
+A step is the whole layer on device-resident inputs: router GEMV over the 8
+tokens, top-8 selection, shared expert, routed experts, shared + routed.
+
+Steps rotate over --layers independently seeded layers (each with its own
+input tokens), so consecutive steps never reuse weights and the 256 MB
+last-level cache cannot serve them.  value = algorithmic HBM bytes per step
+(distinct selected experts x 6,225,920 + shared 16,711,680 + router
+4,718,592 + x/out activations) / measured step time.
+
+roofline: the dominant kernel (routed gate/up), its algorithmic bytes per
+launch over its average launch time from HIP events on the launch stream in
+a second, identical pass with stage events enabled.  cpu_baseline: the
+reference CPU MoE path (sf37_ops.c/sf37_quant.c built with the reference
+`make cpu` flags) on one step's tokens, single core.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import os
+import platform
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+import numpy as np  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+EXPERT_BYTES = 6_225_920
+GATE_UP_EXPERT_BYTES = 2 * 2_252_800
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--layers", type=int, default=8, help="distinct layers rotated per step")
+    ap.add_argument("--seed", type=int, default=1234)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    return ap.parse_args()
+
+
+class Hip:
+    """hipEvent timing on the null stream (the library's launch stream)."""
+
+    def __init__(self):
+        self.L = C.CDLL("libamdhip64.so")
+        self.L.hipEventCreate.argtypes = [C.POINTER(C.c_void_p)]
+        self.L.hipEventRecord.argtypes = [C.c_void_p, C.c_void_p]
+        self.L.hipEventSynchronize.argtypes = [C.c_void_p]
+        self.L.hipEventElapsedTime.argtypes = [C.POINTER(C.c_float), C.c_void_p, C.c_void_p]
+        self.L.hipDeviceSynchronize.argtypes = []
+
+    def event(self):
+        e = C.c_void_p()
+        assert self.L.hipEventCreate(C.byref(e)) == 0
+        return e
+
+    def record(self, e, stream=None):
+        assert self.L.hipEventRecord(e, stream) == 0
+
+    def elapsed_ms(self, a, b):
+        assert self.L.hipEventSynchronize(b) == 0
+        t = C.c_float()
+        assert self.L.hipEventElapsedTime(C.byref(t), a, b) == 0
+        return t.value
+
+    def sync(self):
+        assert self.L.hipDeviceSynchronize() == 0
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only; --gpus {args.gpus} is not supported "
+              "(expert parallelism across GPUs is described in DESIGN.md, not built)", file=sys.stderr)
+        sys.exit(2)
+
+    from sf37_amd import configs, hip, moe
+
+    hip.init()
+    H = Hip()
+    n_tok, E, K, F, TOPK = 8, moe.EXPERTS, moe.EMBD, moe.EXPERT_FF, moe.EXPERT_USED
+
+    layers, xs, lgs, sels = [], [], [], []
+    for l in range(args.layers):
+        seed = moe.layer_seed(args.seed, l)
+        layers.append(moe.SynthLayer(seed=seed))
+        xs.append(configs.x_device(1, seed, n_tok))
+        lg = configs.logits_for(1, seed, n_tok)
+        lgs.append(hip.Tensor.from_array(lg))
+    logit_scratch = hip.Tensor.alloc(n_tok * E * 4)
+    out = hip.Tensor.alloc(n_tok * K * 4)
+    sel = hip.Tensor.alloc(n_tok * TOPK * 4)
+    wts = hip.Tensor.alloc(n_tok * TOPK * 4)
+    L = hip.lib()
+
+    router_keys, key_store = [], []
+    for lay in layers:
+        k = np.zeros(64, np.uint8)               # model-map key for the router (kept alive)
+        key_store.append(k)
+        router_keys.append(k.ctypes.data)
+        hip.check(L.sf37_hip_register_device_range(k.ctypes.data, lay.router.nbytes, 0, lay.router.nbytes,
+                                                   lay.router), "register router")
+    structs = [lay.weights_struct() for lay in layers]
+
+    def step(i):
+        l = i % args.layers
+        lay = layers[l]
+        # router GEMV over the step's tokens (its bytes belong to the layer); the
+        # selection then uses the injected logits of config 1
+        hip.check(L.sf37_hip_matmul_f32_mapped(logit_scratch, router_keys[l], lay.router.nbytes, 0, K, E,
+                                               xs[l], n_tok), "router gemv")
+        hip.check(L.sf37_hip_moe_layer(out, sel, wts, structs[l], lgs[l], xs[l], n_tok), "moe layer")
+
+    # distinct experts per layer's routing (for the byte count)
+    step_bytes, gu_bytes = [], []
+    for l in range(args.layers):
+        step(l)
+        s = sel.read(np.int32).reshape(n_tok, TOPK)
+        sels.append(s)
+        distinct = len(np.unique(s))
+        act = n_tok * K * 4 * 2
+        step_bytes.append(distinct * EXPERT_BYTES + layers[l].shared_bytes() + layers[l].router_bytes() + act)
+        gu_bytes.append(distinct * GATE_UP_EXPERT_BYTES + n_tok * 16 * 268 + n_tok * TOPK * F * 4)
+    hip.synchronize()
+
+    for i in range(args.warmup):
+        step(i)
+    H.sync()
+    a, b = H.event(), H.event()
+    H.record(a)
+    for i in range(args.steps):
+        step(i)
+    H.record(b)
+    ms = H.elapsed_ms(a, b)
+    H.sync()
+    ms_per_step = ms / args.steps
+    mean_bytes = float(np.mean([step_bytes[i % args.layers] for i in range(args.steps)]))
+    value = mean_bytes / (ms_per_step * 1e-3) / 1e9
+
+    # second identical pass with stage events: per-kernel launch times
+    L.sf37_hip_profile_enable(1)
+    hip.profile_read()
+    for i in range(args.steps):
+        step(i)
+    prof = hip.profile_read()
+    L.sf37_hip_profile_enable(0)
+    gu_ms, gu_n = prof["gate_up"]
+    gu_avg_ms = gu_ms / max(gu_n, 1)
+    gu_mean_bytes = float(np.mean([gu_bytes[i % args.layers] for i in range(args.steps)]))
+    achieved = gu_mean_bytes / (gu_avg_ms * 1e-3) / 1e9
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "gate_up_decode8_traffic.json")
+    if os.path.exists(tpath):
+        traffic = json.load(open(tpath)).get("hbm_bytes_per_launch")
+
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(layers[0], xs[0], sels[0], step_bytes[0], n_tok, args.cpu_seconds)
+
+    stages = {k: {"ms_per_launch": round(v[0] / max(v[1], 1), 5), "launches": v[1]} for k, v in prof.items() if v[1]}
+    line = {
+        "metric": "MoE layer decode HBM GB/s (% of peak); prefill tokens/s/layer, MFMA util",
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic (seeded N(0,0.02) weights quantized by the reference quantizer; x ~ N(0,1); "
+                "injected N(0,1) router logits)",
+        "config": {"workload": "BASELINE configs[1]: one MoE layer decode step, 8 tokens, uniform routing",
+                   "experts": E, "hidden": K, "expert_ff": F, "top_k": TOPK,
+                   "formats": "Q3GU gate/up, Q2D down, Q8_0 shared, fp32 router",
+                   "layers_rotated": args.layers, "hbm_bytes_per_step": int(mean_bytes),
+                   "pct_of_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 2)},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "kernel": "gate_up (routed Q3 gate/up + SwiGLU*w)",
+                     "bytes_per_launch": int(gu_mean_bytes), "ms_per_launch": round(gu_avg_ms, 5)},
+        "cpu_baseline": cpu,
+        "stages": stages,
+    }
+    print(json.dumps(line), flush=True)
+
+
+def cpu_baseline(layer, x_dev, sel, step_bytes, n_tok, budget_s):
+    """Reference CPU MoE path on this step's tokens (1 core)."""
+    import oracle
+    kind = "reference"
+    lib = oracle.cpu_baseline_lib("reference")
+    if lib is None:
+        kind = "port"
+        lib = oracle.cpu_baseline_lib("port")
+    if lib is None:
+        return None
+    K, F, E = layer.in_dim, layer.mid_dim, layer.n_expert
+    dense = layer.host_dense()
+    experts = layer.host_experts(np.unique(sel))
+    x = x_dev.read(np.float32).reshape(n_tok, K)
+    out = np.zeros(K, np.float32)
+    got_sel = np.zeros(8, np.int32)
+    fp = lambda a: a.ctypes.data_as(C.POINTER(C.c_float))
+    bp = lambda a: a.ctypes.data_as(C.POINTER(C.c_uint8))
+    reps, t0 = 0, time.perf_counter()
+    # router logits on the CPU come from x (the CPU path has no injected
+    # logits), so it may pick other experts; the timing covers the same work
+    # (router + shared + 8 routed experts per token)
+    while True:
+        for t in range(n_tok):
+            lib.sf37cpu_moe_ffn_token(fp(out), got_sel.ctypes.data_as(C.POINTER(C.c_int32)), fp(dense["router"]),
+                                      fp(dense["router_bias"]), bp(experts["gate"]), bp(experts["up"]),
+                                      bp(experts["down"]), bp(dense["sh_gate"]), bp(dense["sh_up"]),
+                                      bp(dense["sh_down"]), E, 8, K, F, 0.0, 0.0, fp(np.ascontiguousarray(x[t])))
+        reps += 1
+        if time.perf_counter() - t0 >= budget_s or reps >= 20:
+            break
+    dt = (time.perf_counter() - t0) / reps
+    cpu_model = platform.processor() or ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu_model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"value": round(step_bytes / dt / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": kind,
+            "sample": f"{reps} x one 8-token decode step of layer 0 through the reference CPU MoE path "
+                      f"(layer_moe_ffn composition, sf37.c:2127-2194), {dt * 1e3:.1f} ms/step on {cpu_model}"}
+
+
+if __name__ == "__main__":
+    main()

@@ -105,6 +105,8 @@ def lib():
             "orc_moe_layer_q8k": (None, [_f, _i32, _f, _f, _f, _f, _u8, _u8, _u8, _u8, _u8, _u8,
                                          _u32v, _u32v, _u32v, _u32v, C.c_float, C.c_float,
                                          C.c_float, _f, _u32v]),
+            "orc_expf_array": (None, [_f, _f, _u64]),
+            "orc_sigmoid_array": (None, [_f, _f, _u64]),
             "orc_rng_u64": (C.c_uint64, [_u64, _u64, _u64]),
             "orc_rng_normal": (C.c_float, [_u64, _u64, _u64]),
             "orc_fill_normal": (None, [_f, _u64, _u64, _u64, _u64, C.c_float]),

@@ -856,3 +856,13 @@ void orc_gen_quant_rows(int type, uint8_t *dst, uint64_t row0, uint64_t nrows,
     }
     free(row);
 }
+
+/* Host libm expf / the engine sigmoid over an array (checker for the
+ * device exp; sf37_ops.c:9-16). */
+void orc_expf_array(float *out, const float *x, uint64_t n) {
+    for (uint64_t i = 0; i < n; i++) out[i] = expf(x[i]);
+}
+
+void orc_sigmoid_array(float *out, const float *x, uint64_t n) {
+    for (uint64_t i = 0; i < n; i++) out[i] = orc_sigmoid(x[i]);
+}

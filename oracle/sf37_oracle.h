@@ -166,6 +166,9 @@ void orc_moe_layer_q8k(float *out, int32_t *selected_out, float *weights_out,
                        float clamp_routed, float clamp_shared, float scale,
                        const float *x, uint32_t n_tok);
 
+void orc_expf_array(float *out, const float *x, uint64_t n);
+void orc_sigmoid_array(float *out, const float *x, uint64_t n);
+
 /* ---- synthetic inputs (harness; no reference counterpart) --------------- */
 uint64_t orc_rng_u64(uint64_t seed, uint64_t stream, uint64_t index);
 float orc_rng_normal(uint64_t seed, uint64_t stream, uint64_t index);

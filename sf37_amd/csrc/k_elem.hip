@@ -1,0 +1,69 @@
+// k_elem.hip - elementwise ops for gfx950: SwiGLU with clamp (sf37_ops.c:30-42),
+// in-place add (sf37_cuda.cu:2137-2151) and RMSNorm with (w + 1) weights
+// (sf37_ops.c:22-28: binary64 sum of squares, scale = 1 / sqrtf(mean + eps)).
+#include "sf37_dev.h"
+#include "sf37_launch.h"
+
+namespace {
+
+__global__ void __launch_bounds__(256) swiglu_kernel(float *__restrict__ out,
+                                                     const float *__restrict__ gate,
+                                                     const float *__restrict__ up, uint64_t n,
+                                                     float clamp) {
+    const uint64_t i = (uint64_t)blockIdx.x * 256u + threadIdx.x;
+    if (i >= n) return;
+    out[i] = sf37_swiglu_mid(gate[i], up[i], 1.0f, clamp);
+}
+
+__global__ void __launch_bounds__(256) add_kernel(float *__restrict__ dst,
+                                                  const float *__restrict__ src, uint64_t n) {
+    const uint64_t i = (uint64_t)blockIdx.x * 256u + threadIdx.x;
+    if (i < n) dst[i] = dst[i] + src[i];
+}
+
+__global__ void __launch_bounds__(256) rms_norm_kernel(float *__restrict__ out,
+                                                       const float *__restrict__ x,
+                                                       const void *__restrict__ w, int bf16,
+                                                       uint32_t n, float eps) {
+    __shared__ double part[4];
+    const float *xr = x + (uint64_t)blockIdx.x * n;
+    float *orow = out + (uint64_t)blockIdx.x * n;
+    double ss = 0.0;
+    for (uint32_t i = threadIdx.x; i < n; i += 256u) ss += (double)xr[i] * (double)xr[i];
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
+    if ((threadIdx.x & 63u) == 0) part[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    const double tot = (part[0] + part[1]) + (part[2] + part[3]);
+    const float scale = 1.0f / __builtin_sqrtf((float)(tot / (double)n) + eps);
+    for (uint32_t i = threadIdx.x; i < n; i += 256u) {
+        const float wf = bf16 ? __uint_as_float((uint32_t)((const uint16_t *)w)[i] << 16)
+                              : ((const float *)w)[i];
+        orow[i] = xr[i] * scale * (wf + 1.0f);
+    }
+}
+
+}  // namespace
+
+extern "C" int sf37k_swiglu(float *out, const float *gate, const float *up, uint64_t n, float clamp,
+                            sf37_stream_t s) {
+    if (n == 0) return 0;
+    hipLaunchKernelGGL(swiglu_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)s,
+                       out, gate, up, n, clamp);
+    return (int)hipGetLastError();
+}
+
+extern "C" int sf37k_add_inplace(float *dst, const float *src, uint64_t n, sf37_stream_t s) {
+    if (n == 0) return 0;
+    hipLaunchKernelGGL(add_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)s,
+                       dst, src, n);
+    return (int)hipGetLastError();
+}
+
+extern "C" int sf37k_rms_norm(float *out, const float *x, const void *w, int w_is_bf16, uint32_t n,
+                              uint32_t n_tok, float eps, sf37_stream_t s) {
+    if (n_tok == 0) return 0;
+    hipLaunchKernelGGL(rms_norm_kernel, dim3(n_tok), dim3(256), 0, (hipStream_t)s, out, x, w,
+                       w_is_bf16, n, eps);
+    return (int)hipGetLastError();
+}

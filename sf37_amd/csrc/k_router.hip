@@ -1,0 +1,198 @@
+// k_router.hip - router logits and top-k gating for gfx950.
+//
+// Logits: out[t][e] = sum_k W[e][k] * x[t][k], accumulated in binary64 as
+// the engine's CPU path does (sf37.c:1970-1976).  Tiled: a workgroup owns
+// 32 experts x 32 tokens, stages 64-wide K slices of both operands in LDS
+// and each thread accumulates a 2x2 patch in double.  The same kernel serves
+// decode (one token column) and prefill.
+//
+// Selection (sf37.c:2144-2157, sf37_cuda.cu:4866-4997): one wave per token.
+// p = sigmoid(logit), score = p + bias, k rounds of a wave-wide arg-max under
+// (score desc, index asc), weights = p / max(sum p, 1e-20) * scale with the
+// sum taken in slot order.
+#include "sf37_dev.h"
+#include "sf37_launch.h"
+
+namespace {
+
+constexpr int RT_E = 32, RT_T = 32, RT_K = 64;
+
+__global__ void __launch_bounds__(256) f32_matmul_kernel(float *__restrict__ out,
+                                                         const float *__restrict__ w,
+                                                         const float *__restrict__ x,
+                                                         uint64_t in_dim, uint64_t out_dim,
+                                                         uint64_t n_tok) {
+    __shared__ float ws[RT_E][RT_K + 1];
+    __shared__ float xs[RT_T][RT_K + 1];
+    const uint64_t e0 = (uint64_t)blockIdx.x * RT_E;
+    const uint64_t t0 = (uint64_t)blockIdx.y * RT_T;
+    const uint32_t tid = threadIdx.x;
+    const uint32_t te = (tid & 15u) * 2u, tt = (tid >> 4) * 2u;
+    double acc[2][2] = {{0.0, 0.0}, {0.0, 0.0}};
+    for (uint64_t k0 = 0; k0 < in_dim; k0 += RT_K) {
+        for (uint32_t i = tid; i < RT_E * RT_K; i += 256u) {
+            const uint32_t r = i / RT_K, c = i % RT_K;
+            const uint64_t e = e0 + r, k = k0 + c;
+            ws[r][c] = (e < out_dim && k < in_dim) ? w[e * in_dim + k] : 0.0f;
+            const uint64_t t = t0 + r;
+            xs[r][c] = (t < n_tok && k < in_dim) ? x[t * in_dim + k] : 0.0f;
+        }
+        __syncthreads();
+#pragma unroll 8
+        for (int c = 0; c < RT_K; c++) {
+            const double w0 = ws[te][c], w1 = ws[te + 1][c];
+            const double x0 = xs[tt][c], x1 = xs[tt + 1][c];
+            acc[0][0] = __builtin_fma(w0, x0, acc[0][0]);
+            acc[0][1] = __builtin_fma(w0, x1, acc[0][1]);
+            acc[1][0] = __builtin_fma(w1, x0, acc[1][0]);
+            acc[1][1] = __builtin_fma(w1, x1, acc[1][1]);
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const uint64_t e = e0 + te + i, t = t0 + tt + j;
+            if (e < out_dim && t < n_tok) out[t * out_dim + e] = (float)acc[i][j];
+        }
+}
+
+// Decode GEMV (n_tok small): one workgroup per expert row, 4 waves split K,
+// binary64 partial sums combined in LDS.
+__global__ void __launch_bounds__(256) f32_matvec_kernel(float *__restrict__ out,
+                                                         const float *__restrict__ w,
+                                                         const float *__restrict__ x,
+                                                         uint64_t in_dim, uint64_t out_dim,
+                                                         uint32_t n_tok) {
+    constexpr int MAXT = 8;
+    __shared__ double part[MAXT][4];
+    const uint64_t e = blockIdx.x;
+    const uint32_t t0 = blockIdx.y * MAXT;
+    const uint32_t nt = n_tok - t0 < (uint32_t)MAXT ? n_tok - t0 : (uint32_t)MAXT;
+    const float *wr = w + e * in_dim;
+    double acc[MAXT];
+#pragma unroll
+    for (int t = 0; t < MAXT; t++) acc[t] = 0.0;
+    for (uint64_t k = threadIdx.x; k < in_dim; k += 256u) {
+        const double wv = wr[k];
+#pragma unroll
+        for (int t = 0; t < MAXT; t++)
+            if ((uint32_t)t < nt) acc[t] = __builtin_fma(wv, (double)x[(uint64_t)(t0 + t) * in_dim + k], acc[t]);
+    }
+#pragma unroll
+    for (int t = 0; t < MAXT; t++) {
+        double v = acc[t];
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+        if ((threadIdx.x & 63u) == 0) part[t][threadIdx.x >> 6] = v;
+    }
+    __syncthreads();
+    if (threadIdx.x < nt) {
+        const uint32_t t = threadIdx.x;
+        const double v = (part[t][0] + part[t][1]) + (part[t][2] + part[t][3]);
+        out[(uint64_t)(t0 + t) * out_dim + e] = (float)v;
+    }
+}
+
+__device__ __forceinline__ bool better(float av, uint32_t ai, float bv, uint32_t bi) {
+    return av > bv || (av == bv && ai < bi);
+}
+
+constexpr int RS_PER_LANE = 16;  // up to 1024 experts
+
+__global__ void __launch_bounds__(256) router_select_kernel(int32_t *__restrict__ selected,
+                                                            float *__restrict__ weights,
+                                                            float *__restrict__ probs,
+                                                            const float *__restrict__ logits,
+                                                            const float *__restrict__ bias,
+                                                            uint32_t n_experts, uint32_t topk,
+                                                            float scale, uint32_t n_tok) {
+    const uint32_t t = blockIdx.x * 4u + (threadIdx.x >> 6);
+    const uint32_t lane = threadIdx.x & 63u;
+    if (t >= n_tok) return;
+    const float *lg = logits + (uint64_t)t * n_experts;
+    float prob[RS_PER_LANE], score[RS_PER_LANE];
+    uint32_t taken = 0;   // bit j: local entry j already selected
+#pragma unroll
+    for (int j = 0; j < RS_PER_LANE; j++) {
+        const uint32_t e = lane + 64u * j;
+        prob[j] = 0.0f;
+        score[j] = -__builtin_inff();
+        if (e < n_experts) {
+            const float p = sf37_sigmoid(lg[e]);
+            prob[j] = p;
+            score[j] = p + bias[e];
+            if (probs) probs[(uint64_t)t * n_experts + e] = p;
+        } else {
+            taken |= 1u << j;
+        }
+    }
+    float sel_p[16];
+    uint32_t sel_i[16];
+    for (uint32_t k = 0; k < topk; k++) {
+        float bs = -__builtin_inff(), bp = 0.0f;
+        uint32_t bi = 0xffffffffu;
+        int bj = -1;
+#pragma unroll
+        for (int j = 0; j < RS_PER_LANE; j++) {
+            const uint32_t e = lane + 64u * j;
+            if (!((taken >> j) & 1u) && better(score[j], e, bs, bi)) {
+                bs = score[j];
+                bp = prob[j];
+                bi = e;
+                bj = j;
+            }
+        }
+        float ws = bs, wp = bp;
+        uint32_t wi = bi;
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) {
+            const float os = __shfl_xor(ws, off, 64);
+            const float op = __shfl_xor(wp, off, 64);
+            const uint32_t oi = __shfl_xor(wi, off, 64);
+            if (better(os, oi, ws, wi)) {
+                ws = os;
+                wp = op;
+                wi = oi;
+            }
+        }
+        if (wi != 0xffffffffu && bi == wi && bj >= 0) taken |= 1u << bj;
+        sel_p[k] = wi == 0xffffffffu ? 0.0f : wp;
+        sel_i[k] = wi;
+    }
+    if (lane == 0) {
+        float sum = 0.0f;
+        for (uint32_t k = 0; k < topk; k++) sum += sel_p[k];
+        if (sum < 1.0e-20f) sum = 1.0e-20f;
+        for (uint32_t k = 0; k < topk; k++) {
+            selected[(uint64_t)t * topk + k] = sel_i[k] == 0xffffffffu ? -1 : (int32_t)sel_i[k];
+            weights[(uint64_t)t * topk + k] = sel_p[k] / sum * scale;
+        }
+    }
+}
+
+}  // namespace
+
+extern "C" int sf37k_f32_matmul(float *out, const float *w, const float *x, uint64_t in_dim,
+                                uint64_t out_dim, uint64_t n_tok, sf37_stream_t s) {
+    if (out_dim == 0 || n_tok == 0) return 0;
+    if (n_tok <= 16) {
+        hipLaunchKernelGGL(f32_matvec_kernel, dim3((unsigned)out_dim, (unsigned)((n_tok + 7) / 8)),
+                           dim3(256), 0, (hipStream_t)s, out, w, x, in_dim, out_dim, (uint32_t)n_tok);
+    } else {
+        hipLaunchKernelGGL(f32_matmul_kernel,
+                           dim3((unsigned)((out_dim + RT_E - 1) / RT_E), (unsigned)((n_tok + RT_T - 1) / RT_T)),
+                           dim3(256), 0, (hipStream_t)s, out, w, x, in_dim, out_dim, n_tok);
+    }
+    return (int)hipGetLastError();
+}
+
+extern "C" int sf37k_router_select(int32_t *selected, float *weights, float *probs,
+                                   const float *logits, const float *bias, uint32_t n_experts,
+                                   uint32_t topk, float scale, uint32_t n_tok, sf37_stream_t s) {
+    if (n_tok == 0) return 0;
+    hipLaunchKernelGGL(router_select_kernel, dim3((n_tok + 3) / 4), dim3(256), 0, (hipStream_t)s,
+                       selected, weights, probs, logits, bias, n_experts, topk, scale, n_tok);
+    return (int)hipGetLastError();
+}

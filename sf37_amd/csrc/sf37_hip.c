@@ -1,0 +1,1107 @@
+/*
+ * sf37_hip.c - host side of the MI355X MoE backend: the C ABI declared in
+ * include/sf37_hip.h.  Argument checks follow the reference backend
+ * (sf37_cuda.cu, cited per function) and run before any launch; kernels
+ * live in the .hip files and are reached through sf37_launch.h.
+ *
+ * Device buffers: every allocation made here carries SF37_PAD bytes of
+ * slack past its end, because the weight-block kernels read whole dwords
+ * around blocks that end on a 2-byte boundary.
+ */
+#define __HIP_PLATFORM_AMD__ 1
+#include <hip/hip_runtime_api.h>
+
+#include <stdint.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "../../include/sf37_hip.h"
+#include "sf37_launch.h"
+
+#define SF37_PAD 256u
+#define QK SF37_HIP_QK_K
+#define Q3B SF37_HIP_Q3_BLOCK_SIZE
+#define Q2B SF37_HIP_Q2_BLOCK_SIZE
+#define Q8B SF37_HIP_Q8_0_BLOCK_SIZE
+#define Q8KB SF37_HIP_Q8K_BLOCK_SIZE
+
+struct sf37_hip_tensor {
+    void *ptr;
+    uint64_t bytes;
+    int owned;
+};
+
+/* ------------------------------------------------------------------------ */
+/* state                                                                     */
+/* ------------------------------------------------------------------------ */
+
+static int g_init;
+static hipStream_t g_stream;
+static void *g_scratch;
+static uint64_t g_scratch_bytes;
+static int g_model_fd = -1;
+
+static sf37_hip_tensor *g_layer_bufs[6];
+static uint64_t g_layer_buf_bytes[6];
+
+static int64_t g_opt_q8k = 1;
+static int64_t g_opt_q8k_min_rows = 512;
+static int64_t g_opt_write_gate_up = 0;
+
+typedef struct {
+    const uint8_t *map;
+    uint64_t off, bytes;
+    void *dev;
+    int owned;   /* allocated here (freed on evict/cleanup) */
+    int cache;   /* on-demand cache entry (dropped by evict) */
+} map_range;
+
+static map_range *g_ranges;
+static size_t g_nranges, g_cap_ranges;
+
+static int hip_ok(hipError_t err, const char *what) {
+    if (err == hipSuccess) return 1;
+    fprintf(stderr, "sf37: HIP %s failed: %s\n", what, hipGetErrorString(err));
+    (void)hipGetLastError();
+    return 0;
+}
+
+/* ---- stage profiling (events around launches) ---------------------------- */
+typedef struct {
+    hipEvent_t a, b;
+    uint32_t stage;
+} prof_pair;
+
+static int g_prof_on;
+static prof_pair *g_prof;
+static size_t g_nprof, g_cap_prof;
+static hipEvent_t g_prof_open;
+
+static const char *const k_stage_names[SF37_HIP_N_STAGES] = {
+    "router", "select", "q8_0_act", "q8_0_gemm", "swiglu", "q8k_x", "dispatch",
+    "gate_up", "q8k_mid", "down", "combine", "add", "other"};
+
+static void prof_begin(void) {
+    if (!g_prof_on) return;
+    if (hipEventCreate(&g_prof_open) != hipSuccess || hipEventRecord(g_prof_open, g_stream) != hipSuccess) {
+        g_prof_open = NULL;
+        (void)hipGetLastError();
+    }
+}
+
+static void prof_end(uint32_t stage) {
+    if (!g_prof_on || !g_prof_open) return;
+    hipEvent_t e;
+    if (hipEventCreate(&e) != hipSuccess || hipEventRecord(e, g_stream) != hipSuccess) {
+        (void)hipGetLastError();
+        return;
+    }
+    if (g_nprof == g_cap_prof) {
+        const size_t cap = g_cap_prof ? 2 * g_cap_prof : 256;
+        prof_pair *n = (prof_pair *)realloc(g_prof, cap * sizeof(prof_pair));
+        if (!n) return;
+        g_prof = n;
+        g_cap_prof = cap;
+    }
+    prof_pair pp = {g_prof_open, e, stage};
+    g_prof[g_nprof++] = pp;
+    g_prof_open = NULL;
+}
+
+static int launch_ok(int err, const char *what) { return hip_ok((hipError_t)err, what); }
+
+/* Launch wrapper: events around the launch when profiling. */
+#define LAUNCH(stage, call, what) (prof_begin(), launch_ok((call), (what)) ? (prof_end(stage), 1) : 0)
+
+int sf37_hip_profile_enable(int on) {
+    g_prof_on = on ? 1 : 0;
+    return 1;
+}
+
+const char *sf37_hip_profile_stage_name(uint32_t stage) {
+    return stage < SF37_HIP_N_STAGES ? k_stage_names[stage] : NULL;
+}
+
+int sf37_hip_profile_read(double *ms, uint64_t *count, uint32_t n_stages) {
+    if (!g_init) return 0;
+    for (uint32_t i = 0; i < n_stages; i++) {
+        if (ms) ms[i] = 0.0;
+        if (count) count[i] = 0;
+    }
+    if (!hip_ok(hipStreamSynchronize(g_stream), "profile sync")) return 0;
+    for (size_t i = 0; i < g_nprof; i++) {
+        float t = 0.0f;
+        if (hipEventElapsedTime(&t, g_prof[i].a, g_prof[i].b) == hipSuccess && g_prof[i].stage < n_stages) {
+            if (ms) ms[g_prof[i].stage] += t;
+            if (count) count[g_prof[i].stage]++;
+        }
+        (void)hipEventDestroy(g_prof[i].a);
+        (void)hipEventDestroy(g_prof[i].b);
+    }
+    (void)hipGetLastError();
+    g_nprof = 0;
+    return 1;
+}
+
+static int ensure_init(void) {
+    if (g_init) return 1;
+    return sf37_hip_init();
+}
+
+static uint64_t align256(uint64_t v) { return (v + 255u) & ~(uint64_t)255u; }
+
+/* One reusable scratch area (the reference's cuda_tmp_alloc,
+ * sf37_cuda.cu:1579-1592).  Growing it waits for queued work first. */
+static char *scratch_get(uint64_t bytes, const char *what) {
+    if (bytes <= g_scratch_bytes && g_scratch) return (char *)g_scratch;
+    if (g_scratch) {
+        if (!hip_ok(hipStreamSynchronize(g_stream), "scratch sync")) return NULL;
+        (void)hipFree(g_scratch);
+        g_scratch = NULL;
+        g_scratch_bytes = 0;
+    }
+    void *p = NULL;
+    if (!hip_ok(hipMalloc(&p, bytes + SF37_PAD), what)) return NULL;
+    g_scratch = p;
+    g_scratch_bytes = bytes;
+    return (char *)p;
+}
+
+/* Weight rows and activations are read with dword loads. */
+static int aligned4(const void *p) {
+    if (((uintptr_t)p & 3u) == 0) return 1;
+    fprintf(stderr, "sf37: HIP buffer %p is not 4-byte aligned\n", p);
+    return 0;
+}
+
+static int q8k_use_for(uint64_t rows) {
+    return g_opt_q8k && rows >= (uint64_t)g_opt_q8k_min_rows;
+}
+
+static int mapped_range_ok(uint64_t model_size, uint64_t offset, uint64_t bytes) {
+    return offset <= model_size && bytes <= model_size - offset;   /* sf37_cuda.cu:5843-5845 */
+}
+
+/* ------------------------------------------------------------------------ */
+/* runtime (sf37_cuda.cu:1594-1680)                                          */
+/* ------------------------------------------------------------------------ */
+
+int sf37_hip_device_count(void) {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) {
+        (void)hipGetLastError();
+        return -1;
+    }
+    return n;
+}
+
+void sf37_hip_print_devices(void) {
+    const int n = sf37_hip_device_count();
+    if (n < 0) {
+        fprintf(stderr, "sf37: HIP device query failed\n");
+        return;
+    }
+    for (int i = 0; i < n; i++) {
+        hipDeviceProp_t p;
+        if (hipGetDeviceProperties(&p, i) != hipSuccess) continue;
+        fprintf(stderr, "sf37: HIP device %d: %s (%s), %d CUs, %.1f GiB\n", i, p.name,
+                p.gcnArchName, p.multiProcessorCount, (double)p.totalGlobalMem / (1u << 30));
+    }
+}
+
+int sf37_hip_init(void) {
+    if (g_init) return 1;
+    if (!hip_ok(hipSetDevice(0), "set device")) return 0;
+    g_stream = NULL;
+    g_init = 1;
+    return 1;
+}
+
+static void free_ranges(int cache_only) {
+    size_t w = 0;
+    for (size_t i = 0; i < g_nranges; i++) {
+        if (!cache_only || g_ranges[i].cache) {
+            if (g_ranges[i].owned && g_ranges[i].dev) (void)hipFree(g_ranges[i].dev);
+        } else {
+            g_ranges[w++] = g_ranges[i];
+        }
+    }
+    g_nranges = w;
+}
+
+void sf37_hip_cleanup(void) {
+    if (!g_init) return;
+    (void)hipDeviceSynchronize();
+    free_ranges(0);
+    free(g_ranges);
+    g_ranges = NULL;
+    g_cap_ranges = 0;
+    if (g_scratch) (void)hipFree(g_scratch);
+    g_scratch = NULL;
+    g_scratch_bytes = 0;
+    for (int i = 0; i < 6; i++) {
+        if (g_layer_bufs[i]) {
+            (void)hipFree(g_layer_bufs[i]->ptr);
+            free(g_layer_bufs[i]);
+        }
+        g_layer_bufs[i] = NULL;
+        g_layer_buf_bytes[i] = 0;
+    }
+    g_init = 0;
+}
+
+int sf37_hip_synchronize(void) {
+    if (!ensure_init()) return 0;
+    return hip_ok(hipStreamSynchronize(g_stream), "synchronize");
+}
+
+int sf37_hip_memory_info(uint64_t *free_bytes, uint64_t *total_bytes) {
+    if (!ensure_init()) return 0;
+    size_t f = 0, t = 0;
+    if (!hip_ok(hipMemGetInfo(&f, &t), "memory info")) return 0;
+    if (free_bytes) *free_bytes = f;
+    if (total_bytes) *total_bytes = t;
+    return 1;
+}
+
+/* Layer markers only bracket per-layer work in the reference (weight
+ * streaming); with every weight resident there is nothing to do. */
+int sf37_hip_begin_layer(uint32_t layer) {
+    (void)layer;
+    return ensure_init();
+}
+
+void sf37_hip_end_layer(void) {}
+
+int sf37_hip_set_stream(void *stream) {
+    if (!ensure_init()) return 0;
+    g_stream = (hipStream_t)stream;
+    return 1;
+}
+
+void *sf37_hip_get_stream(void) { return (void *)g_stream; }
+
+int sf37_hip_set_option(const char *name, int64_t value) {
+    if (!name) return 0;
+    if (!strcmp(name, "q8k")) g_opt_q8k = value ? 1 : 0;
+    else if (!strcmp(name, "q8k_min_rows")) g_opt_q8k_min_rows = value < 0 ? 0 : value;
+    else if (!strcmp(name, "moe_write_gate_up")) g_opt_write_gate_up = value ? 1 : 0;
+    else return 0;
+    return 1;
+}
+
+int64_t sf37_hip_get_option(const char *name) {
+    if (!name) return -1;
+    if (!strcmp(name, "q8k")) return g_opt_q8k;
+    if (!strcmp(name, "q8k_min_rows")) return g_opt_q8k_min_rows;
+    if (!strcmp(name, "moe_write_gate_up")) return g_opt_write_gate_up;
+    return -1;
+}
+
+/* ------------------------------------------------------------------------ */
+/* tensors (sf37_cuda.cu:1680-1850)                                          */
+/* ------------------------------------------------------------------------ */
+
+static sf37_hip_tensor *tensor_new(void *ptr, uint64_t bytes, int owned) {
+    sf37_hip_tensor *t = (sf37_hip_tensor *)calloc(1, sizeof(*t));
+    if (!t) return NULL;
+    t->ptr = ptr;
+    t->bytes = bytes;
+    t->owned = owned;
+    return t;
+}
+
+sf37_hip_tensor *sf37_hip_tensor_alloc(uint64_t bytes) {
+    if (!ensure_init()) return NULL;
+    void *p = NULL;
+    if (!hip_ok(hipMalloc(&p, bytes + SF37_PAD), "tensor alloc")) return NULL;
+    sf37_hip_tensor *t = tensor_new(p, bytes, 1);
+    if (!t) (void)hipFree(p);
+    return t;
+}
+
+sf37_hip_tensor *sf37_hip_tensor_alloc_managed(uint64_t bytes) {
+    if (!ensure_init()) return NULL;
+    void *p = NULL;
+    if (!hip_ok(hipMallocManaged(&p, bytes + SF37_PAD, hipMemAttachGlobal), "managed tensor alloc"))
+        return NULL;
+    sf37_hip_tensor *t = tensor_new(p, bytes, 1);
+    if (!t) (void)hipFree(p);
+    return t;
+}
+
+void sf37_hip_tensor_free(sf37_hip_tensor *tensor) {
+    if (!tensor) return;
+    if (tensor->owned && tensor->ptr) {
+        (void)hipStreamSynchronize(g_stream);
+        (void)hipFree(tensor->ptr);
+    }
+    free(tensor);
+}
+
+uint64_t sf37_hip_tensor_bytes(const sf37_hip_tensor *tensor) { return tensor ? tensor->bytes : 0; }
+
+void *sf37_hip_tensor_device_ptr(const sf37_hip_tensor *tensor) { return tensor ? tensor->ptr : NULL; }
+
+sf37_hip_tensor *sf37_hip_tensor_view(const sf37_hip_tensor *base, uint64_t offset, uint64_t bytes) {
+    if (!base || offset > base->bytes || bytes > base->bytes - offset) return NULL;
+    return tensor_new((char *)base->ptr + offset, bytes, 0);
+}
+
+int sf37_hip_tensor_write(sf37_hip_tensor *tensor, uint64_t offset, const void *data, uint64_t bytes) {
+    if (!tensor || (!data && bytes) || offset > tensor->bytes || bytes > tensor->bytes - offset) return 0;
+    if (!bytes) return 1;
+    if (!hip_ok(hipMemcpyAsync((char *)tensor->ptr + offset, data, bytes, hipMemcpyHostToDevice, g_stream),
+                "tensor write"))
+        return 0;
+    return hip_ok(hipStreamSynchronize(g_stream), "tensor write sync");
+}
+
+int sf37_hip_tensor_read(const sf37_hip_tensor *tensor, uint64_t offset, void *data, uint64_t bytes) {
+    if (!tensor || (!data && bytes) || offset > tensor->bytes || bytes > tensor->bytes - offset) return 0;
+    if (!bytes) return 1;
+    if (!hip_ok(hipMemcpyAsync(data, (const char *)tensor->ptr + offset, bytes, hipMemcpyDeviceToHost,
+                               g_stream),
+                "tensor read"))
+        return 0;
+    return hip_ok(hipStreamSynchronize(g_stream), "tensor read sync");
+}
+
+int sf37_hip_tensor_copy(sf37_hip_tensor *dst, uint64_t dst_offset, const sf37_hip_tensor *src,
+                         uint64_t src_offset, uint64_t bytes) {
+    if (!dst || !src || dst_offset > dst->bytes || bytes > dst->bytes - dst_offset ||
+        src_offset > src->bytes || bytes > src->bytes - src_offset)
+        return 0;
+    if (!bytes) return 1;
+    return hip_ok(hipMemcpyAsync((char *)dst->ptr + dst_offset, (const char *)src->ptr + src_offset, bytes,
+                                 hipMemcpyDeviceToDevice, g_stream),
+                  "tensor copy");
+}
+
+int sf37_hip_tensor_fill_f32(sf37_hip_tensor *tensor, float value, uint64_t count) {
+    if (!tensor || count > tensor->bytes / sizeof(float)) return 0;
+    if (!count) return 1;
+    uint32_t bits;
+    memcpy(&bits, &value, 4);
+    return hip_ok(hipMemsetD32Async((hipDeviceptr_t)tensor->ptr, (int)bits, count, g_stream), "tensor fill");
+}
+
+/* ------------------------------------------------------------------------ */
+/* model map (sf37_cuda.cu:1131-1188, 1418-1478)                             */
+/* ------------------------------------------------------------------------ */
+
+static int range_push(const uint8_t *map, uint64_t off, uint64_t bytes, void *dev, int owned, int cache) {
+    if (g_nranges == g_cap_ranges) {
+        const size_t cap = g_cap_ranges ? g_cap_ranges * 2 : 16;
+        map_range *n = (map_range *)realloc(g_ranges, cap * sizeof(map_range));
+        if (!n) return 0;
+        g_ranges = n;
+        g_cap_ranges = cap;
+    }
+    map_range r = {map, off, bytes, dev, owned, cache};
+    g_ranges[g_nranges++] = r;
+    return 1;
+}
+
+static int upload_range(const uint8_t *map, uint64_t off, uint64_t bytes, int cache, const char *label) {
+    void *dev = NULL;
+    char what[160];
+    snprintf(what, sizeof(what), "model range upload (%s)", label ? label : "range");
+    if (!hip_ok(hipMalloc(&dev, bytes + SF37_PAD), what)) return 0;
+    if (!hip_ok(hipMemcpy(dev, map + off, bytes, hipMemcpyHostToDevice), what) ||
+        !range_push(map, off, bytes, dev, 1, cache)) {
+        (void)hipFree(dev);
+        return 0;
+    }
+    return 1;
+}
+
+/* Device address of map[offset, offset+bytes): a registered range, else an
+ * on-demand cached copy (kept until sf37_hip_evict_model_cache). */
+static const void *model_ptr(const void *model_map, uint64_t offset, uint64_t bytes, const char *label) {
+    const uint8_t *map = (const uint8_t *)model_map;
+    for (size_t i = g_nranges; i-- > 0;) {   /* newest registration wins */
+        const map_range *r = &g_ranges[i];
+        if (r->map == map && offset >= r->off && bytes <= r->bytes && offset - r->off <= r->bytes - bytes)
+            return (const char *)r->dev + (offset - r->off);
+    }
+    if (!ensure_init() || !upload_range(map, offset, bytes, 1, label)) return NULL;
+    return g_ranges[g_nranges - 1].dev;
+}
+
+int sf37_hip_set_model_fd(int fd) {
+    g_model_fd = fd;   /* weights are uploaded from the map; the fd is not needed */
+    return 1;
+}
+
+int sf37_hip_set_model_map_range(const void *model_map, uint64_t model_size, uint64_t map_offset,
+                                 uint64_t map_size, uint64_t max_tensor_bytes) {
+    (void)max_tensor_bytes;
+    if (!model_map || !mapped_range_ok(model_size, map_offset, map_size) || !ensure_init()) return 0;
+    if (!map_size) return 1;
+    return upload_range((const uint8_t *)model_map, map_offset, map_size, 0, "model map");
+}
+
+int sf37_hip_set_model_map_spans(const void *model_map, uint64_t model_size, const uint64_t *offsets,
+                                 const uint64_t *sizes, uint32_t count, uint64_t max_tensor_bytes) {
+    if (!model_map || (count && (!offsets || !sizes))) return 0;
+    for (uint32_t i = 0; i < count; i++)
+        if (!sf37_hip_set_model_map_range(model_map, model_size, offsets[i], sizes[i], max_tensor_bytes))
+            return 0;
+    return 1;
+}
+
+int sf37_hip_cache_model_range(const void *model_map, uint64_t model_size, uint64_t offset, uint64_t bytes,
+                               const char *label) {
+    if (!model_map || !mapped_range_ok(model_size, offset, bytes)) return 0;
+    return model_ptr(model_map, offset, bytes, label) != NULL;
+}
+
+void sf37_hip_evict_model_cache(const char *reason) {
+    (void)reason;
+    if (!g_init) return;
+    (void)hipStreamSynchronize(g_stream);
+    free_ranges(1);
+}
+
+int sf37_hip_register_device_range(const void *model_map, uint64_t model_size, uint64_t map_offset,
+                                   uint64_t bytes, const sf37_hip_tensor *device) {
+    if (!model_map || !device || bytes > device->bytes || !mapped_range_ok(model_size, map_offset, bytes) ||
+        !ensure_init())
+        return 0;
+    return range_push((const uint8_t *)model_map, map_offset, bytes, device->ptr, 0, 0);
+}
+
+/* ------------------------------------------------------------------------ */
+/* elementwise / norm (sf37_cuda.cu:2037-2180, 6117-6164)                    */
+/* ------------------------------------------------------------------------ */
+
+int sf37_hip_rms_norm_weight1_f32(sf37_hip_tensor *out, const sf37_hip_tensor *x,
+                                  const sf37_hip_tensor *weight, uint32_t n, float eps) {
+    if (!out || !x || !weight || !ensure_init()) return 0;
+    if (out->bytes < (uint64_t)n * 4u || x->bytes < (uint64_t)n * 4u || weight->bytes < (uint64_t)n * 4u) return 0;
+    return LAUNCH(SF37_HIP_STAGE_OTHER, sf37k_rms_norm((float *)out->ptr, (const float *)x->ptr, weight->ptr, 0, n, 1, eps,
+                                    (sf37_stream_t)g_stream),
+                     "rms_norm_weight1 launch");
+}
+
+int sf37_hip_rms_norm_weight1_bf16(sf37_hip_tensor *out, const sf37_hip_tensor *x,
+                                   const sf37_hip_tensor *weight, uint32_t n, float eps) {
+    if (!out || !x || !weight || !ensure_init()) return 0;
+    if (out->bytes < (uint64_t)n * 4u || x->bytes < (uint64_t)n * 4u || weight->bytes < (uint64_t)n * 2u) return 0;
+    return LAUNCH(SF37_HIP_STAGE_OTHER, sf37k_rms_norm((float *)out->ptr, (const float *)x->ptr, weight->ptr, 1, n, 1, eps,
+                                    (sf37_stream_t)g_stream),
+                     "rms_norm_weight1_bf16 launch");
+}
+
+int sf37_hip_rms_norm_weight1_bf16_mapped(sf37_hip_tensor *out, const sf37_hip_tensor *x,
+                                          const void *model_map, uint64_t model_size,
+                                          uint64_t weight_offset, uint32_t n, float eps) {
+    return sf37_hip_rms_norm_weight1_bf16_batch_mapped(out, x, model_map, model_size, weight_offset, n, 1, eps);
+}
+
+int sf37_hip_rms_norm_weight1_bf16_batch_mapped(sf37_hip_tensor *out, const sf37_hip_tensor *x,
+                                                const void *model_map, uint64_t model_size,
+                                                uint64_t weight_offset, uint32_t n, uint32_t n_tok,
+                                                float eps) {
+    if (!out || !x || !model_map || n_tok == 0 || !ensure_init()) return 0;
+    const uint64_t bytes = (uint64_t)n * n_tok * 4u;
+    if (!mapped_range_ok(model_size, weight_offset, (uint64_t)n * 2u) || out->bytes < bytes || x->bytes < bytes)
+        return 0;
+    const void *w = model_ptr(model_map, weight_offset, (uint64_t)n * 2u, "rms norm weight");
+    if (!w) return 0;
+    return LAUNCH(SF37_HIP_STAGE_OTHER, sf37k_rms_norm((float *)out->ptr, (const float *)x->ptr, w, 1, n, n_tok, eps,
+                                    (sf37_stream_t)g_stream),
+                     "rms_norm_weight1_bf16 batch launch");
+}
+
+int sf37_hip_add_inplace_f32(sf37_hip_tensor *dst, const sf37_hip_tensor *src, uint64_t n) {
+    if (!dst || !src || !ensure_init()) return 0;
+    if (dst->bytes < n * 4u || src->bytes < n * 4u) return 0;
+    return LAUNCH(SF37_HIP_STAGE_ADD, sf37k_add_inplace((float *)dst->ptr, (const float *)src->ptr, n, (sf37_stream_t)g_stream),
+                     "add inplace f32 launch");
+}
+
+int sf37_hip_swiglu_f32(sf37_hip_tensor *out, const sf37_hip_tensor *gate, const sf37_hip_tensor *up,
+                        uint64_t n, float clamp) {
+    if (!out || !gate || !up || !ensure_init()) return 0;
+    if (out->bytes < n * 4u || gate->bytes < n * 4u || up->bytes < n * 4u) return 0;
+    return LAUNCH(SF37_HIP_STAGE_SWIGLU, sf37k_swiglu((float *)out->ptr, (const float *)gate->ptr, (const float *)up->ptr, n, clamp,
+                                  (sf37_stream_t)g_stream),
+                     "swiglu launch");
+}
+
+/* ------------------------------------------------------------------------ */
+/* Q8_0 (sf37_cuda.cu:3319-3781, 6405-6440, 6649-6916)                       */
+/* ------------------------------------------------------------------------ */
+
+static int q8_0_run(float *out0, float *out1, const uint8_t *w0, const uint8_t *w1, uint64_t in_dim,
+                    uint64_t out_dim, const float *x, uint64_t n_tok) {
+    const uint64_t nb = (in_dim + 31u) / 32u;
+    if (!aligned4(x) || !aligned4(out0) || (out1 && !aligned4(out1))) return 0;
+    const uint64_t xq_bytes = align256(n_tok * nb * 32u);
+    char *s = scratch_get(xq_bytes + n_tok * nb * 4u, "q8_0 activations");
+    if (!s) return 0;
+    int8_t *xq = (int8_t *)s;
+    float *xs = (float *)(s + xq_bytes);
+    if (!LAUNCH(SF37_HIP_STAGE_Q8_0_ACT, sf37k_q8_0_quantize(xq, xs, x, in_dim, n_tok, (sf37_stream_t)g_stream), "q8_0 quantize launch"))
+        return 0;
+    return LAUNCH(SF37_HIP_STAGE_Q8_0_GEMM, sf37k_q8_0_matmul(out0, out1, w0, w1, xq, xs, in_dim, out_dim, n_tok, (sf37_stream_t)g_stream),
+                     "q8_0 matmul launch");
+}
+
+static uint64_t q8_0_bytes(uint64_t in_dim, uint64_t out_dim) { return out_dim * ((in_dim + 31u) / 32u) * Q8B; }
+
+int sf37_hip_matvec_q8_0(sf37_hip_tensor *out, const sf37_hip_tensor *weights, uint64_t in_dim,
+                         uint64_t out_dim, const sf37_hip_tensor *x) {
+    if (!out || !weights || !x || !ensure_init()) return 0;
+    if (out->bytes < out_dim * 4u || x->bytes < in_dim * 4u || weights->bytes < q8_0_bytes(in_dim, out_dim)) return 0;
+    return q8_0_run((float *)out->ptr, NULL, (const uint8_t *)weights->ptr, NULL, in_dim, out_dim,
+                    (const float *)x->ptr, 1);
+}
+
+int sf37_hip_matvec_q8_0_pair(sf37_hip_tensor *out0, sf37_hip_tensor *out1, const sf37_hip_tensor *weights0,
+                              const sf37_hip_tensor *weights1, uint64_t in_dim, uint64_t out_dim,
+                              const sf37_hip_tensor *x) {
+    if (!out0 || !out1 || !weights0 || !weights1 || !x || !ensure_init()) return 0;
+    const uint64_t wb = q8_0_bytes(in_dim, out_dim);
+    if (out0->bytes < out_dim * 4u || out1->bytes < out_dim * 4u || x->bytes < in_dim * 4u ||
+        weights0->bytes < wb || weights1->bytes < wb)
+        return 0;
+    return q8_0_run((float *)out0->ptr, (float *)out1->ptr, (const uint8_t *)weights0->ptr,
+                    (const uint8_t *)weights1->ptr, in_dim, out_dim, (const float *)x->ptr, 1);
+}
+
+int sf37_hip_matvec_q8_0_mapped(sf37_hip_tensor *out, const void *model_map, uint64_t model_size,
+                                uint64_t weight_offset, uint64_t in_dim, uint64_t out_dim,
+                                const sf37_hip_tensor *x) {
+    return sf37_hip_matmul_q8_0_mapped(out, model_map, model_size, weight_offset, in_dim, out_dim, x, 1);
+}
+
+int sf37_hip_matmul_q8_0_mapped(sf37_hip_tensor *out, const void *model_map, uint64_t model_size,
+                                uint64_t weight_offset, uint64_t in_dim, uint64_t out_dim,
+                                const sf37_hip_tensor *x, uint64_t n_tok) {
+    if (!out || !model_map || !x || n_tok == 0 || !ensure_init()) return 0;
+    const uint64_t wb = q8_0_bytes(in_dim, out_dim);
+    if (!mapped_range_ok(model_size, weight_offset, wb) || out->bytes < n_tok * out_dim * 4u ||
+        x->bytes < n_tok * in_dim * 4u)
+        return 0;
+    const uint8_t *w = (const uint8_t *)model_ptr(model_map, weight_offset, wb, "q8_0 weights");
+    if (!w) return 0;
+    return q8_0_run((float *)out->ptr, NULL, w, NULL, in_dim, out_dim, (const float *)x->ptr, n_tok);
+}
+
+int sf37_hip_matmul_q8_0_pair_mapped(sf37_hip_tensor *out0, sf37_hip_tensor *out1, const void *model_map,
+                                     uint64_t model_size, uint64_t weight0_offset, uint64_t weight1_offset,
+                                     uint64_t in_dim, uint64_t out_dim, const sf37_hip_tensor *x,
+                                     uint64_t n_tok) {
+    if (!out0 || !out1 || !model_map || !x || n_tok == 0 || !ensure_init()) return 0;
+    const uint64_t wb = q8_0_bytes(in_dim, out_dim);
+    if (!mapped_range_ok(model_size, weight0_offset, wb) || !mapped_range_ok(model_size, weight1_offset, wb) ||
+        out0->bytes < n_tok * out_dim * 4u || out1->bytes < n_tok * out_dim * 4u || x->bytes < n_tok * in_dim * 4u)
+        return 0;
+    const uint8_t *w0 = (const uint8_t *)model_ptr(model_map, weight0_offset, wb, "q8_0 pair weights 0");
+    const uint8_t *w1 = (const uint8_t *)model_ptr(model_map, weight1_offset, wb, "q8_0 pair weights 1");
+    if (!w0 || !w1) return 0;
+    return q8_0_run((float *)out0->ptr, (float *)out1->ptr, w0, w1, in_dim, out_dim, (const float *)x->ptr, n_tok);
+}
+
+int sf37_hip_matvec_q8_0_pair_mapped(sf37_hip_tensor *out0, sf37_hip_tensor *out1, const void *model_map,
+                                     uint64_t model_size, uint64_t weight0_offset, uint64_t weight1_offset,
+                                     uint64_t in_dim, uint64_t out_dim, const sf37_hip_tensor *x) {
+    return sf37_hip_matmul_q8_0_pair_mapped(out0, out1, model_map, model_size, weight0_offset, weight1_offset,
+                                            in_dim, out_dim, x, 1);
+}
+
+/* ------------------------------------------------------------------------ */
+/* f32 router GEMV/GEMM (sf37_cuda.cu:4100-4147, 7034-7113)                  */
+/* ------------------------------------------------------------------------ */
+
+int sf37_hip_matvec_f32(sf37_hip_tensor *out, const sf37_hip_tensor *weights, uint64_t in_dim,
+                        uint64_t out_dim, const sf37_hip_tensor *x) {
+    if (!out || !weights || !x || !ensure_init()) return 0;
+    if (out->bytes < out_dim * 4u || x->bytes < in_dim * 4u || weights->bytes < out_dim * in_dim * 4u) return 0;
+    return LAUNCH(SF37_HIP_STAGE_ROUTER, sf37k_f32_matmul((float *)out->ptr, (const float *)weights->ptr, (const float *)x->ptr, in_dim,
+                                      out_dim, 1, (sf37_stream_t)g_stream),
+                     "f32 matvec launch");
+}
+
+int sf37_hip_matvec_f32_mapped(sf37_hip_tensor *out, const void *model_map, uint64_t model_size,
+                               uint64_t weight_offset, uint64_t in_dim, uint64_t out_dim,
+                               const sf37_hip_tensor *x) {
+    return sf37_hip_matmul_f32_mapped(out, model_map, model_size, weight_offset, in_dim, out_dim, x, 1);
+}
+
+int sf37_hip_matmul_f32_mapped(sf37_hip_tensor *out, const void *model_map, uint64_t model_size,
+                               uint64_t weight_offset, uint64_t in_dim, uint64_t out_dim,
+                               const sf37_hip_tensor *x, uint64_t n_tok) {
+    if (!out || !model_map || !x || n_tok == 0 || !ensure_init()) return 0;
+    const uint64_t wb = out_dim * in_dim * 4u;
+    if (!mapped_range_ok(model_size, weight_offset, wb) || out->bytes < n_tok * out_dim * 4u ||
+        x->bytes < n_tok * in_dim * 4u)
+        return 0;
+    const float *w = (const float *)model_ptr(model_map, weight_offset, wb, "f32 weights");
+    if (!w) return 0;
+    return LAUNCH(SF37_HIP_STAGE_ROUTER, sf37k_f32_matmul((float *)out->ptr, w, (const float *)x->ptr, in_dim, out_dim, n_tok,
+                                      (sf37_stream_t)g_stream),
+                     "f32 matmul launch");
+}
+
+/* ------------------------------------------------------------------------ */
+/* Q3 / Q2 GEMV (sf37_cuda.cu:5783-5841, 7677-7755)                          */
+/* ------------------------------------------------------------------------ */
+
+static int qlow_matvec(int q3, float *out, const uint8_t *w, uint64_t in_dim, uint64_t out_dim, const float *x) {
+    const uint64_t nb = in_dim / QK;
+    if (!aligned4(w) || !aligned4(x) || !aligned4(out)) return 0;
+    if (q8k_use_for(out_dim) && nb <= 128u) {
+        void *xq = scratch_get(nb * Q8KB, "q3/q2 q8k activation");
+        if (!xq) return 0;
+        if (!LAUNCH(SF37_HIP_STAGE_Q8K_X, sf37k_q8k_quantize(xq, x, (uint32_t)in_dim, 1, (sf37_stream_t)g_stream), "q8k quantize launch"))
+            return 0;
+        return launch_ok(q3 ? sf37k_q3_q8k_matvec(out, w, xq, (uint32_t)nb, out_dim, (sf37_stream_t)g_stream)
+                            : sf37k_q2_q8k_matvec(out, w, xq, (uint32_t)nb, out_dim, (sf37_stream_t)g_stream),
+                         q3 ? "q3 asym q8k matvec launch" : "q2 asym q8k matvec launch");
+    }
+    return launch_ok(q3 ? sf37k_q3_f32_matvec(out, w, x, in_dim, out_dim, (sf37_stream_t)g_stream)
+                        : sf37k_q2_f32_matvec(out, w, x, in_dim, out_dim, (sf37_stream_t)g_stream),
+                     q3 ? "q3 asym matvec launch" : "q2 asym matvec launch");
+}
+
+static int qlow_checked(int q3, sf37_hip_tensor *out, const sf37_hip_tensor *weights, uint64_t in_dim,
+                        uint64_t out_dim, const sf37_hip_tensor *x) {
+    if (!out || !weights || !x || in_dim % QK != 0 || !ensure_init()) return 0;
+    const uint64_t wb = out_dim * (in_dim / QK) * (q3 ? Q3B : Q2B);
+    if (out->bytes < out_dim * 4u || x->bytes < in_dim * 4u || weights->bytes < wb) return 0;
+    return qlow_matvec(q3, (float *)out->ptr, (const uint8_t *)weights->ptr, in_dim, out_dim, (const float *)x->ptr);
+}
+
+int sf37_hip_matvec_q3_asym(sf37_hip_tensor *out, const sf37_hip_tensor *weights, uint64_t in_dim,
+                            uint64_t out_dim, const sf37_hip_tensor *x) {
+    return qlow_checked(1, out, weights, in_dim, out_dim, x);
+}
+
+int sf37_hip_matvec_q2_asym(sf37_hip_tensor *out, const sf37_hip_tensor *weights, uint64_t in_dim,
+                            uint64_t out_dim, const sf37_hip_tensor *x) {
+    return qlow_checked(0, out, weights, in_dim, out_dim, x);
+}
+
+static int qlow_mapped(int q3, sf37_hip_tensor *out, const void *model_map, uint64_t model_size,
+                       uint64_t weight_offset, uint64_t in_dim, uint64_t out_dim, const sf37_hip_tensor *x) {
+    if (!out || !model_map || !x || in_dim % QK != 0 || !ensure_init()) return 0;
+    const uint64_t wb = out_dim * (in_dim / QK) * (q3 ? Q3B : Q2B);
+    if (!mapped_range_ok(model_size, weight_offset, wb) || out->bytes < out_dim * 4u || x->bytes < in_dim * 4u)
+        return 0;
+    const uint8_t *w = (const uint8_t *)model_ptr(model_map, weight_offset, wb, q3 ? "q3 weights" : "q2 weights");
+    if (!w) return 0;
+    return qlow_matvec(q3, (float *)out->ptr, w, in_dim, out_dim, (const float *)x->ptr);
+}
+
+int sf37_hip_matvec_q3_asym_mapped(sf37_hip_tensor *out, const void *model_map, uint64_t model_size,
+                                   uint64_t weight_offset, uint64_t in_dim, uint64_t out_dim,
+                                   const sf37_hip_tensor *x) {
+    return qlow_mapped(1, out, model_map, model_size, weight_offset, in_dim, out_dim, x);
+}
+
+int sf37_hip_matvec_q2_asym_mapped(sf37_hip_tensor *out, const void *model_map, uint64_t model_size,
+                                   uint64_t weight_offset, uint64_t in_dim, uint64_t out_dim,
+                                   const sf37_hip_tensor *x) {
+    return qlow_mapped(0, out, model_map, model_size, weight_offset, in_dim, out_dim, x);
+}
+
+/* ------------------------------------------------------------------------ */
+/* router (sf37_cuda.cu:4999-5033, 7757-7966)                                */
+/* ------------------------------------------------------------------------ */
+
+#define ROUTER_MAX_EXPERTS 1024u
+
+static int router_run(sf37_hip_tensor *selected, sf37_hip_tensor *weights, sf37_hip_tensor *probs,
+                      const sf37_hip_tensor *logits, const float *bias, uint32_t n_experts, uint32_t topk,
+                      float scale, uint32_t n_tok) {
+    if (n_experts > ROUTER_MAX_EXPERTS) {
+        fprintf(stderr, "sf37: HIP router_select supports at most %u experts\n", ROUTER_MAX_EXPERTS);
+        return 0;
+    }
+    return LAUNCH(SF37_HIP_STAGE_SELECT, sf37k_router_select((int32_t *)selected->ptr, (float *)weights->ptr,
+                                         probs ? (float *)probs->ptr : NULL, (const float *)logits->ptr, bias,
+                                         n_experts, topk, scale, n_tok, (sf37_stream_t)g_stream),
+                     "router_select launch");
+}
+
+int sf37_hip_router_select(sf37_hip_tensor *selected, sf37_hip_tensor *weights, sf37_hip_tensor *probs,
+                           const sf37_hip_tensor *logits, const sf37_hip_tensor *bias, uint32_t n_experts,
+                           uint32_t topk, float scale) {
+    if (!selected || !weights || !logits || !bias || n_experts == 0 || topk == 0 || topk > 16u ||
+        !ensure_init())
+        return 0;
+    if (selected->bytes < (uint64_t)topk * 4u || weights->bytes < (uint64_t)topk * 4u ||
+        logits->bytes < (uint64_t)n_experts * 4u || bias->bytes < (uint64_t)n_experts * 4u ||
+        (probs && probs->bytes < (uint64_t)n_experts * 4u))
+        return 0;
+    return router_run(selected, weights, probs, logits, (const float *)bias->ptr, n_experts, topk, scale, 1);
+}
+
+int sf37_hip_router_select_mapped(sf37_hip_tensor *selected, sf37_hip_tensor *weights, sf37_hip_tensor *probs,
+                                  const sf37_hip_tensor *logits, const void *model_map, uint64_t model_size,
+                                  uint64_t bias_offset, uint32_t n_experts, uint32_t topk, float scale) {
+    return sf37_hip_router_select_batch_mapped(selected, weights, probs, logits, model_map, model_size,
+                                               bias_offset, n_experts, topk, scale, 1);
+}
+
+int sf37_hip_router_select_batch_mapped(sf37_hip_tensor *selected, sf37_hip_tensor *weights,
+                                        sf37_hip_tensor *probs, const sf37_hip_tensor *logits,
+                                        const void *model_map, uint64_t model_size, uint64_t bias_offset,
+                                        uint32_t n_experts, uint32_t topk, float scale, uint32_t n_tok) {
+    if (!selected || !weights || !logits || !model_map || n_experts == 0 || topk == 0 || topk > 16u ||
+        n_tok == 0 || !ensure_init())
+        return 0;
+    const uint64_t bias_bytes = (uint64_t)n_experts * 4u;
+    if (!mapped_range_ok(model_size, bias_offset, bias_bytes) ||
+        logits->bytes < (uint64_t)n_tok * n_experts * 4u || selected->bytes < (uint64_t)n_tok * topk * 4u ||
+        weights->bytes < (uint64_t)n_tok * topk * 4u || (probs && probs->bytes < (uint64_t)n_tok * n_experts * 4u))
+        return 0;
+    const float *bias = (const float *)model_ptr(model_map, bias_offset, bias_bytes, "router_bias");
+    if (!bias) return 0;
+    return router_run(selected, weights, probs, logits, bias, n_experts, topk, scale, n_tok);
+}
+
+/* ------------------------------------------------------------------------ */
+/* routed experts (sf37_cuda.cu:5269-5781, 7968-8314)                        */
+/* ------------------------------------------------------------------------ */
+
+#define DISPATCH_MAX_EXPERTS 512u
+
+typedef struct {
+    const uint8_t *gate_w, *up_w, *down_w;
+    const int32_t *selected;
+    const float *weights;
+    uint32_t n_expert, topk, in_dim, mid_dim, out_dim;
+    float clamp;
+    const float *x;
+    uint32_t n_tok;
+} routed_args;
+
+/* Scratch of the Q8_K routed pipeline; mid/down_pair/gate/up may point
+ * into caller tensors.  Returns the byte size when base == NULL. */
+typedef struct {
+    void *xq, *midq;
+    uint32_t *ginfo, *sorted, *counts, *offsets;
+    float *mid, *down_pair;
+} routed_scratch;
+
+static uint64_t routed_layout(const routed_args *a, int slots, int need_mid, int need_down, char *base,
+                              routed_scratch *s) {
+    const uint64_t pairs = (uint64_t)a->n_tok * a->topk;
+    const uint64_t groups = slots ? a->topk : a->n_expert;
+    uint64_t off = 0;
+#define RESERVE(field, type, bytes)                                    \
+    do {                                                               \
+        if (base) s->field = (type)(base + off);                       \
+        off = align256(off + (bytes));                                 \
+    } while (0)
+    RESERVE(xq, void *, (uint64_t)a->n_tok * (a->in_dim / QK) * Q8KB);
+    RESERVE(midq, void *, pairs * (a->mid_dim / QK) * Q8KB);
+    RESERVE(ginfo, uint32_t *, (3u + 2u * groups) * 4u);
+    RESERVE(sorted, uint32_t *, pairs * 4u);
+    RESERVE(counts, uint32_t *, (uint64_t)a->n_expert * 4u);
+    RESERVE(offsets, uint32_t *, ((uint64_t)a->n_expert + 1u) * 4u);
+    if (need_mid) RESERVE(mid, float *, pairs * a->mid_dim * 4u);
+    if (need_down) RESERVE(down_pair, float *, pairs * a->out_dim * 4u);
+#undef RESERVE
+    return off;
+}
+
+/* Q8_K pipeline: quantize x, group pairs by expert (slots = one group per
+ * slot of a single token), gate/up + SwiGLU*w, quantize mid, down, combine. */
+static int routed_q8k(const routed_args *a, float *out, float *mid, float *down_pair, float *gate_out,
+                      float *up_out, int slots) {
+    if (!aligned4(a->gate_w) || !aligned4(a->up_w) || !aligned4(a->down_w) || !aligned4(a->x) ||
+        !aligned4(out) || (mid && !aligned4(mid)) || (down_pair && !aligned4(down_pair)))
+        return 0;
+    routed_scratch s;
+    memset(&s, 0, sizeof(s));
+    const uint64_t bytes = routed_layout(a, slots, mid == NULL, down_pair == NULL, NULL, &s);
+    char *base = scratch_get(bytes, "routed moe scratch");
+    if (!base) return 0;
+    routed_layout(a, slots, mid == NULL, down_pair == NULL, base, &s);
+    if (!mid) mid = s.mid;
+    if (!down_pair) down_pair = s.down_pair;
+    const sf37_stream_t st = (sf37_stream_t)g_stream;
+    const uint32_t pairs = a->n_tok * a->topk;
+    const uint32_t groups = slots ? a->topk : a->n_expert;
+    if (!LAUNCH(SF37_HIP_STAGE_Q8K_X, sf37k_q8k_quantize(s.xq, a->x, a->in_dim, a->n_tok, st), "routed_moe q8k input quantize launch"))
+        return 0;
+    if (slots) {
+        if (!LAUNCH(SF37_HIP_STAGE_DISPATCH, sf37k_moe_slots(s.ginfo, s.sorted, a->selected, a->topk, a->n_expert, st),
+                       "routed_moe slot groups launch"))
+            return 0;
+    } else if (!LAUNCH(SF37_HIP_STAGE_DISPATCH, sf37k_moe_dispatch(s.ginfo, s.sorted, s.counts, s.offsets, a->selected, pairs,
+                                             a->n_expert, st),
+                          "routed_moe dispatch launch")) {
+        return 0;
+    }
+    if (!LAUNCH(SF37_HIP_STAGE_GATE_UP, sf37k_moe_gate_up(mid, gate_out, up_out, a->gate_w, a->up_w, s.xq, s.ginfo, s.sorted,
+                                     a->weights, groups, pairs, a->topk, a->in_dim, a->mid_dim, a->clamp, st),
+                   "routed_moe q8k gate/up launch"))
+        return 0;
+    if (!LAUNCH(SF37_HIP_STAGE_Q8K_MID, sf37k_q8k_quantize(s.midq, mid, a->mid_dim, pairs, st), "routed_moe q8k mid quantize launch"))
+        return 0;
+    if (!LAUNCH(SF37_HIP_STAGE_DOWN, sf37k_moe_down(down_pair, a->down_w, s.midq, s.ginfo, s.sorted, groups, pairs, a->mid_dim,
+                                  a->out_dim, st),
+                   "routed_moe q8k down launch"))
+        return 0;
+    return LAUNCH(SF37_HIP_STAGE_COMBINE, sf37k_moe_combine(out, down_pair, a->topk, a->out_dim, a->n_tok, st),
+                     "routed_moe combine launch");
+}
+
+/* fp32-activation path for one token (sf37_cuda.cu:5382-5446). */
+static int routed_f32(const routed_args *a, float *out, float *mid, float *down_slot, float *gate_out,
+                      float *up_out) {
+    const sf37_stream_t st = (sf37_stream_t)g_stream;
+    if (!LAUNCH(SF37_HIP_STAGE_GATE_UP, sf37k_moe_gate_up_f32(mid, gate_out, up_out, a->gate_w, a->up_w, a->x, a->selected,
+                                         a->weights, a->topk, a->in_dim, a->mid_dim, a->n_expert, a->clamp, st),
+                   "routed_moe gate/up launch"))
+        return 0;
+    if (!LAUNCH(SF37_HIP_STAGE_DOWN, sf37k_moe_down_f32(down_slot, a->down_w, mid, a->selected, a->topk, a->mid_dim, a->out_dim,
+                                      a->n_expert, st),
+                   "routed_moe down launch"))
+        return 0;
+    return LAUNCH(SF37_HIP_STAGE_COMBINE, sf37k_moe_combine(out, down_slot, a->topk, a->out_dim, 1, st), "routed_moe sum launch");
+}
+
+static int routed_one_impl(sf37_hip_tensor *out, sf37_hip_tensor *gate, sf37_hip_tensor *up,
+                           sf37_hip_tensor *mid, sf37_hip_tensor *down, const routed_args *a) {
+    float *go = g_opt_write_gate_up ? (float *)gate->ptr : NULL;
+    float *uo = g_opt_write_gate_up ? (float *)up->ptr : NULL;
+    if (q8k_use_for(a->mid_dim) && q8k_use_for(a->out_dim))
+        return routed_q8k(a, (float *)out->ptr, (float *)mid->ptr, (float *)down->ptr, go, uo, 1);
+    return routed_f32(a, (float *)out->ptr, (float *)mid->ptr, (float *)down->ptr, go, uo);
+}
+
+static int routed_common_checks(sf37_hip_tensor *out, sf37_hip_tensor *gate, sf37_hip_tensor *up,
+                                sf37_hip_tensor *mid, sf37_hip_tensor *down, const sf37_hip_tensor *selected,
+                                const sf37_hip_tensor *weights, uint32_t n_total_expert, uint32_t topk,
+                                uint32_t in_dim, uint32_t mid_dim, uint32_t out_dim, const sf37_hip_tensor *x,
+                                uint32_t n_tok) {
+    if (!out || !gate || !up || !mid || !down || !selected || !weights || !x || n_total_expert == 0 ||
+        topk == 0 || in_dim == 0 || mid_dim == 0 || out_dim == 0 || n_tok == 0 || in_dim % QK != 0 ||
+        mid_dim % QK != 0)
+        return 0;
+    const uint64_t pm = (uint64_t)topk * mid_dim * 4u;
+    return out->bytes >= (uint64_t)n_tok * out_dim * 4u && gate->bytes >= pm && up->bytes >= pm &&
+           mid->bytes >= pm && down->bytes >= (uint64_t)topk * out_dim * 4u &&
+           selected->bytes >= (uint64_t)n_tok * topk * 4u && weights->bytes >= (uint64_t)n_tok * topk * 4u &&
+           x->bytes >= (uint64_t)n_tok * in_dim * 4u;
+}
+
+int sf37_hip_routed_moe_one(sf37_hip_tensor *out, sf37_hip_tensor *gate, sf37_hip_tensor *up,
+                            sf37_hip_tensor *mid, sf37_hip_tensor *down, const sf37_hip_tensor *moe_gate,
+                            const sf37_hip_tensor *moe_up, const sf37_hip_tensor *moe_down,
+                            const sf37_hip_tensor *selected, const sf37_hip_tensor *weights,
+                            uint32_t n_total_expert, uint32_t topk, uint32_t in_dim, uint32_t expert_mid_dim,
+                            uint32_t out_dim, float clamp, const sf37_hip_tensor *x) {
+    if (!ensure_init() || !moe_gate || !moe_up || !moe_down ||
+        !routed_common_checks(out, gate, up, mid, down, selected, weights, n_total_expert, topk, in_dim,
+                              expert_mid_dim, out_dim, x, 1))
+        return 0;
+    const uint64_t gb = (uint64_t)n_total_expert * expert_mid_dim * (in_dim / QK) * Q3B;
+    const uint64_t db = (uint64_t)n_total_expert * out_dim * (expert_mid_dim / QK) * Q2B;
+    if (moe_gate->bytes < gb || moe_up->bytes < gb || moe_down->bytes < db) return 0;
+    routed_args a = {(const uint8_t *)moe_gate->ptr, (const uint8_t *)moe_up->ptr, (const uint8_t *)moe_down->ptr,
+                     (const int32_t *)selected->ptr, (const float *)weights->ptr, n_total_expert, topk, in_dim,
+                     expert_mid_dim, out_dim, clamp, (const float *)x->ptr, 1};
+    return routed_one_impl(out, gate, up, mid, down, &a);
+}
+
+static int resolve_experts(const void *model_map, uint64_t model_size, uint64_t gate_offset, uint64_t up_offset,
+                           uint64_t down_offset, uint32_t n_total_expert, uint32_t in_dim, uint32_t mid_dim,
+                           uint32_t out_dim, const uint8_t **g, const uint8_t **u, const uint8_t **d) {
+    const uint64_t gb = (uint64_t)n_total_expert * mid_dim * (in_dim / QK) * Q3B;
+    const uint64_t db = (uint64_t)n_total_expert * out_dim * (mid_dim / QK) * Q2B;
+    if (!mapped_range_ok(model_size, gate_offset, gb) || !mapped_range_ok(model_size, up_offset, gb) ||
+        !mapped_range_ok(model_size, down_offset, db))
+        return 0;
+    *g = (const uint8_t *)model_ptr(model_map, gate_offset, gb, "moe_gate");
+    *u = (const uint8_t *)model_ptr(model_map, up_offset, gb, "moe_up");
+    *d = (const uint8_t *)model_ptr(model_map, down_offset, db, "moe_down");
+    return *g && *u && *d;
+}
+
+int sf37_hip_routed_moe_one_mapped(sf37_hip_tensor *out, sf37_hip_tensor *gate, sf37_hip_tensor *up,
+                                   sf37_hip_tensor *mid, sf37_hip_tensor *down, const void *model_map,
+                                   uint64_t model_size, uint64_t gate_offset, uint64_t up_offset,
+                                   uint64_t down_offset, const sf37_hip_tensor *selected,
+                                   const sf37_hip_tensor *weights, uint32_t n_total_expert, uint32_t topk,
+                                   uint32_t in_dim, uint32_t expert_mid_dim, uint32_t out_dim, float clamp,
+                                   const sf37_hip_tensor *x) {
+    if (!model_map || !ensure_init() ||
+        !routed_common_checks(out, gate, up, mid, down, selected, weights, n_total_expert, topk, in_dim,
+                              expert_mid_dim, out_dim, x, 1))
+        return 0;
+    routed_args a = {NULL, NULL, NULL, (const int32_t *)selected->ptr, (const float *)weights->ptr, n_total_expert,
+                     topk, in_dim, expert_mid_dim, out_dim, clamp, (const float *)x->ptr, 1};
+    if (!resolve_experts(model_map, model_size, gate_offset, up_offset, down_offset, n_total_expert, in_dim,
+                         expert_mid_dim, out_dim, &a.gate_w, &a.up_w, &a.down_w))
+        return 0;
+    return routed_one_impl(out, gate, up, mid, down, &a);
+}
+
+int sf37_hip_routed_moe_batch_mapped(sf37_hip_tensor *out, sf37_hip_tensor *gate, sf37_hip_tensor *up,
+                                     sf37_hip_tensor *mid, sf37_hip_tensor *down, const void *model_map,
+                                     uint64_t model_size, uint64_t gate_offset, uint64_t up_offset,
+                                     uint64_t down_offset, const sf37_hip_tensor *selected,
+                                     const sf37_hip_tensor *weights, uint32_t n_total_expert, uint32_t topk,
+                                     uint32_t in_dim, uint32_t expert_mid_dim, uint32_t out_dim, float clamp,
+                                     const sf37_hip_tensor *x, uint32_t n_tok) {
+    if (!model_map || !ensure_init() ||
+        !routed_common_checks(out, gate, up, mid, down, selected, weights, n_total_expert, topk, in_dim,
+                              expert_mid_dim, out_dim, x, n_tok))
+        return 0;
+    routed_args a = {NULL, NULL, NULL, (const int32_t *)selected->ptr, (const float *)weights->ptr, n_total_expert,
+                     topk, in_dim, expert_mid_dim, out_dim, clamp, (const float *)x->ptr, n_tok};
+    if (!resolve_experts(model_map, model_size, gate_offset, up_offset, down_offset, n_total_expert, in_dim,
+                         expert_mid_dim, out_dim, &a.gate_w, &a.up_w, &a.down_w))
+        return 0;
+    const uint64_t pairs = (uint64_t)n_tok * topk;
+    if (n_tok > 1u && pairs <= 0xffffffffu && n_total_expert <= DISPATCH_MAX_EXPERTS &&
+        q8k_use_for(expert_mid_dim) && q8k_use_for(out_dim)) {
+        /* the caller's mid receives the per-pair SwiGLU output when it is big
+         * enough (sf37_cuda.cu:5665-5674) */
+        float *mid_pair = mid->bytes >= pairs * expert_mid_dim * 4u ? (float *)mid->ptr : NULL;
+        return routed_q8k(&a, (float *)out->ptr, mid_pair, NULL, NULL, NULL, 0);
+    }
+    /* per-token loop, as the reference's fallback (sf37_cuda.cu:5734-5780) */
+    for (uint32_t t = 0; t < n_tok; t++) {
+        sf37_hip_tensor ov = {(char *)out->ptr + (uint64_t)t * out_dim * 4u, (uint64_t)out_dim * 4u, 0};
+        const uint64_t mp = (uint64_t)topk * expert_mid_dim * 4u;
+        sf37_hip_tensor mv = {mid->bytes >= (uint64_t)n_tok * mp ? (char *)mid->ptr + (uint64_t)t * mp : mid->ptr, mp,
+                              0};
+        routed_args at = a;
+        at.selected = a.selected + (uint64_t)t * topk;
+        at.weights = a.weights + (uint64_t)t * topk;
+        at.x = a.x + (uint64_t)t * in_dim;
+        at.n_tok = 1;
+        if (!routed_one_impl(&ov, gate, up, &mv, down, &at)) return 0;
+    }
+    return 1;
+}
+
+/* ------------------------------------------------------------------------ */
+/* extensions                                                                */
+/* ------------------------------------------------------------------------ */
+
+int sf37_hip_q8k_quantize(sf37_hip_tensor *out, const sf37_hip_tensor *x, uint32_t in_dim, uint32_t n_rows) {
+    if (!out || !x || in_dim % QK != 0 || !ensure_init()) return 0;
+    if (out->bytes < (uint64_t)n_rows * (in_dim / QK) * Q8KB || x->bytes < (uint64_t)n_rows * in_dim * 4u) return 0;
+    return LAUNCH(SF37_HIP_STAGE_Q8K_X, sf37k_q8k_quantize(out->ptr, (const float *)x->ptr, in_dim, n_rows, (sf37_stream_t)g_stream),
+                     "q8k quantize launch");
+}
+
+int sf37_hip_moe_dispatch(sf37_hip_tensor *counts, sf37_hip_tensor *offsets, sf37_hip_tensor *sorted_pairs,
+                          const sf37_hip_tensor *selected, uint32_t n_pairs, uint32_t n_expert) {
+    if (!counts || !offsets || !sorted_pairs || !selected || n_expert == 0 || n_expert > DISPATCH_MAX_EXPERTS ||
+        !ensure_init())
+        return 0;
+    if (counts->bytes < (uint64_t)n_expert * 4u || offsets->bytes < ((uint64_t)n_expert + 1u) * 4u ||
+        sorted_pairs->bytes < (uint64_t)n_pairs * 4u || selected->bytes < (uint64_t)n_pairs * 4u)
+        return 0;
+    uint32_t *ginfo = (uint32_t *)scratch_get((3u + 2u * (uint64_t)n_expert) * 4u, "dispatch groups");
+    if (!ginfo) return 0;
+    return LAUNCH(SF37_HIP_STAGE_DISPATCH, sf37k_moe_dispatch(ginfo, (uint32_t *)sorted_pairs->ptr, (uint32_t *)counts->ptr,
+                                        (uint32_t *)offsets->ptr, (const int32_t *)selected->ptr, n_pairs,
+                                        n_expert, (sf37_stream_t)g_stream),
+                     "dispatch launch");
+}
+
+/* Whole layer: scratch holds logits, selection, the shared expert's
+ * activations and the routed output; the routed pipeline then takes the
+ * scratch area, so everything it needs from here lives in ls[]. */
+int sf37_hip_moe_layer(sf37_hip_tensor *out, sf37_hip_tensor *selected, sf37_hip_tensor *weights,
+                       const sf37_hip_moe_layer_weights *w, const sf37_hip_tensor *logits_in,
+                       const sf37_hip_tensor *x, uint32_t n_tok) {
+    if (!out || !w || !x || n_tok == 0 || !ensure_init()) return 0;
+    const uint32_t E = w->n_expert, K = w->topk, D = w->in_dim, F = w->mid_dim;
+    if (!w->router_bias || !w->gate || !w->up || !w->down || !w->sh_gate || !w->sh_up || !w->sh_down || E == 0 ||
+        K == 0 || K > 16u || D % QK != 0 || F % QK != 0 || (!logits_in && !w->router))
+        return 0;
+    if (out->bytes < (uint64_t)n_tok * D * 4u || x->bytes < (uint64_t)n_tok * D * 4u ||
+        (logits_in && logits_in->bytes < (uint64_t)n_tok * E * 4u) ||
+        (selected && selected->bytes < (uint64_t)n_tok * K * 4u) ||
+        (weights && weights->bytes < (uint64_t)n_tok * K * 4u))
+        return 0;
+    /* layer-owned buffers (separate from the routed scratch) */
+    sf37_hip_tensor **ls = g_layer_bufs;
+    uint64_t *ls_bytes = g_layer_buf_bytes;
+    const uint64_t need[6] = {(uint64_t)n_tok * E * 4u, (uint64_t)n_tok * K * 4u, (uint64_t)n_tok * K * 4u,
+                              (uint64_t)n_tok * F * 4u * 3u, (uint64_t)n_tok * D * 4u,
+                              (uint64_t)n_tok * K * ((uint64_t)F + D) * 4u};
+    for (int i = 0; i < 6; i++) {
+        if (!ls[i] || ls_bytes[i] < need[i]) {
+            if (ls[i]) sf37_hip_tensor_free(ls[i]);
+            ls[i] = sf37_hip_tensor_alloc(need[i]);
+            ls_bytes[i] = need[i];
+            if (!ls[i]) return 0;
+        }
+    }
+    const sf37_stream_t st = (sf37_stream_t)g_stream;
+    float *logits = logits_in ? (float *)logits_in->ptr : (float *)ls[0]->ptr;
+    int32_t *sel = selected ? (int32_t *)selected->ptr : (int32_t *)ls[1]->ptr;
+    float *wts = weights ? (float *)weights->ptr : (float *)ls[2]->ptr;
+    float *sh = (float *)ls[3]->ptr;   /* gate | up | mid for the shared expert */
+    float *routed = (float *)ls[4]->ptr;
+    if (!logits_in && !LAUNCH(SF37_HIP_STAGE_ROUTER, sf37k_f32_matmul(logits, (const float *)w->router->ptr, (const float *)x->ptr, D, E,
+                                                  n_tok, st),
+                                 "moe_layer router launch"))
+        return 0;
+    if (E > ROUTER_MAX_EXPERTS ||
+        !LAUNCH(SF37_HIP_STAGE_SELECT, sf37k_router_select(sel, wts, NULL, logits, (const float *)w->router_bias->ptr, E, K, w->scale,
+                                       n_tok, st),
+                   "moe_layer router_select launch"))
+        return 0;
+    /* shared expert: Q8_0 gate/up pair -> SwiGLU -> Q8_0 down into out */
+    if (!q8_0_run(sh, sh + (uint64_t)n_tok * F, (const uint8_t *)w->sh_gate->ptr, (const uint8_t *)w->sh_up->ptr, D,
+                  F, (const float *)x->ptr, n_tok) ||
+        !LAUNCH(SF37_HIP_STAGE_SWIGLU, sf37k_swiglu(sh + 2u * (uint64_t)n_tok * F, sh, sh + (uint64_t)n_tok * F, (uint64_t)n_tok * F,
+                                w->clamp_shared, st),
+                   "moe_layer shared swiglu launch") ||
+        !q8_0_run((float *)out->ptr, NULL, (const uint8_t *)w->sh_down->ptr, NULL, F, D,
+                  sh + 2u * (uint64_t)n_tok * F, n_tok))
+        return 0;
+    routed_args a = {(const uint8_t *)w->gate->ptr, (const uint8_t *)w->up->ptr, (const uint8_t *)w->down->ptr, sel,
+                     wts, E, K, D, F, D, w->clamp_routed, (const float *)x->ptr, n_tok};
+    const int slots = n_tok == 1u;
+    if (!slots && E > DISPATCH_MAX_EXPERTS) return 0;
+    if (!q8k_use_for(F) || !q8k_use_for(D)) {
+        if (n_tok != 1u) return 0;
+        if (!routed_f32(&a, routed, (float *)ls[5]->ptr, (float *)ls[5]->ptr + (uint64_t)K * F, NULL, NULL))
+            return 0;
+    } else if (!routed_q8k(&a, routed, NULL, NULL, NULL, NULL, slots)) {
+        return 0;
+    }
+    return LAUNCH(SF37_HIP_STAGE_ADD, sf37k_add_inplace((float *)out->ptr, routed, (uint64_t)n_tok * D, st), "moe_layer add launch");
+}
+
+int sf37_hip_synth_normal(sf37_hip_tensor *dst, uint64_t n, uint64_t seed, uint64_t stream, uint64_t index0,
+                          float sigma) {
+    if (!dst || dst->bytes < n * 4u || !ensure_init()) return 0;
+    return LAUNCH(SF37_HIP_STAGE_OTHER, sf37k_synth_normal((float *)dst->ptr, n, seed, stream, index0, sigma, (sf37_stream_t)g_stream),
+                     "synth normal launch");
+}
+
+int sf37_hip_synth_quant_rows(int type, sf37_hip_tensor *dst, uint64_t row0, uint64_t nrows, uint64_t ncols,
+                              uint64_t seed, uint64_t stream, float sigma) {
+    if (!dst || !ensure_init() || (type != 0 && type != 2 && type != 3)) return 0;
+    const uint64_t qk = type == 0 ? 32u : QK;
+    const uint64_t bs = type == 0 ? Q8B : (type == 3 ? Q3B : Q2B);
+    if (ncols % qk != 0 || dst->bytes < nrows * (ncols / qk) * bs) return 0;
+    return LAUNCH(SF37_HIP_STAGE_OTHER, sf37k_synth_quant_rows(type, (uint8_t *)dst->ptr, row0, nrows, ncols, seed, stream, sigma,
+                                            (sf37_stream_t)g_stream),
+                     "synth quant launch");
+}
+
+int sf37_hip_sigmoid_array(sf37_hip_tensor *out, const sf37_hip_tensor *x, uint64_t n, int mode) {
+    if (!out || !x || out->bytes < n * 4u || x->bytes < n * 4u || !ensure_init()) return 0;
+    return LAUNCH(SF37_HIP_STAGE_OTHER, sf37k_sigmoid_array((float *)out->ptr, (const float *)x->ptr, n, mode, (sf37_stream_t)g_stream),
+                     "sigmoid array launch");
+}

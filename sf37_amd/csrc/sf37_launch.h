@@ -1,0 +1,101 @@
+/*
+ * sf37_launch.h - C-linkage kernel launchers shared by sf37_hip.c (host C)
+ * and the .hip kernel files.  Plain pointers and sizes only; every launcher
+ * enqueues on the given stream and returns a hipError_t as int (0 = ok).
+ * Shapes are validated by the callers in sf37_hip.c before any launch.
+ */
+#ifndef SF37_LAUNCH_H
+#define SF37_LAUNCH_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t *sf37_stream_t;
+
+/* Q8_K activations (268-byte blocks, natural element order). */
+int sf37k_q8k_quantize(void *out, const float *x, uint32_t in_dim, uint32_t n_rows,
+                       sf37_stream_t s);
+/* Q3/Q2 x Q8_K GEMV (canonical order) from a pre-quantized activation. */
+int sf37k_q3_q8k_matvec(float *out, const uint8_t *w, const void *xq, uint32_t nblk,
+                        uint64_t out_dim, sf37_stream_t s);
+int sf37k_q2_q8k_matvec(float *out, const uint8_t *w, const void *xq, uint32_t nblk,
+                        uint64_t out_dim, sf37_stream_t s);
+/* fp32-activation Q3/Q2 GEMV (the reference's small-shape path). */
+int sf37k_q3_f32_matvec(float *out, const uint8_t *w, const float *x, uint64_t in_dim,
+                        uint64_t out_dim, sf37_stream_t s);
+int sf37k_q2_f32_matvec(float *out, const uint8_t *w, const float *x, uint64_t in_dim,
+                        uint64_t out_dim, sf37_stream_t s);
+
+/* fp32 dense GEMV/GEMM with binary64 accumulation (router logits). */
+int sf37k_f32_matmul(float *out, const float *w, const float *x, uint64_t in_dim,
+                     uint64_t out_dim, uint64_t n_tok, sf37_stream_t s);
+/* Router: sigmoid, +bias, top-k (score desc, index asc), renormalise. */
+int sf37k_router_select(int32_t *selected, float *weights, float *probs,
+                        const float *logits, const float *bias, uint32_t n_experts,
+                        uint32_t topk, float scale, uint32_t n_tok, sf37_stream_t s);
+
+/* Q8_0 activations (32-wide) and Q8_0 GEMV / pair / batch. */
+int sf37k_q8_0_quantize(int8_t *xq, float *xscale, const float *x, uint64_t in_dim,
+                        uint64_t n_tok, sf37_stream_t s);
+int sf37k_q8_0_matmul(float *out0, float *out1, const uint8_t *w0, const uint8_t *w1,
+                      const int8_t *xq, const float *xscale, uint64_t in_dim,
+                      uint64_t out_dim, uint64_t n_tok, sf37_stream_t s);
+
+/* Elementwise. */
+int sf37k_swiglu(float *out, const float *gate, const float *up, uint64_t n, float clamp,
+                 sf37_stream_t s);
+int sf37k_add_inplace(float *dst, const float *src, uint64_t n, sf37_stream_t s);
+int sf37k_rms_norm(float *out, const float *x, const void *w, int w_is_bf16, uint32_t n,
+                   uint32_t n_tok, float eps, sf37_stream_t s);
+
+/* Routed experts, Q8_K path.  Work is organised in groups: group g covers
+ * pairs sorted[pair_off[g] .. pair_off[g+1]) that all use expert
+ * group_expert[g]; a pair p is token p / topk, slot p % topk. */
+int sf37k_moe_gate_up(float *mid, float *gate_out, float *up_out, const uint8_t *gate_w,
+                      const uint8_t *up_w, const void *xq, const uint32_t *group_info,
+                      const uint32_t *sorted_pairs, const float *weights, uint32_t max_groups,
+                      uint32_t max_group_pairs, uint32_t topk, uint32_t in_dim,
+                      uint32_t mid_dim, float clamp, sf37_stream_t s);
+int sf37k_moe_down(float *down_pair, const uint8_t *down_w, const void *midq,
+                   const uint32_t *group_info, const uint32_t *sorted_pairs,
+                   uint32_t max_groups, uint32_t max_group_pairs, uint32_t mid_dim,
+                   uint32_t out_dim, sf37_stream_t s);
+int sf37k_moe_combine(float *out, const float *down_pair, uint32_t topk, uint32_t out_dim,
+                      uint32_t n_tok, sf37_stream_t s);
+/* Build the groups from selected experts: stable counting sort of pairs by
+ * expert.  group_info layout: [0] = n_groups, [1 .. 1+E] = group pair
+ * offsets, [2+E .. 2+2E) = group experts; counts/offsets per expert also. */
+int sf37k_moe_dispatch(uint32_t *group_info, uint32_t *sorted_pairs, uint32_t *counts,
+                       uint32_t *offsets, const int32_t *selected, uint32_t n_pairs,
+                       uint32_t n_expert, sf37_stream_t s);
+/* One group per slot for a single token (no sort), as routed_moe_one. */
+int sf37k_moe_slots(uint32_t *group_info, uint32_t *sorted_pairs, const int32_t *selected,
+                    uint32_t topk, uint32_t n_expert, sf37_stream_t s);
+
+/* fp32-activation routed experts (the reference's small-shape path). */
+int sf37k_moe_gate_up_f32(float *mid, float *gate_out, float *up_out, const uint8_t *gate_w,
+                          const uint8_t *up_w, const float *x, const int32_t *selected,
+                          const float *weights, uint32_t topk, uint32_t in_dim,
+                          uint32_t mid_dim, uint32_t n_expert, float clamp, sf37_stream_t s);
+int sf37k_moe_down_f32(float *down_slot, const uint8_t *down_w, const float *mid,
+                       const int32_t *selected, uint32_t topk, uint32_t mid_dim,
+                       uint32_t out_dim, uint32_t n_expert, sf37_stream_t s);
+
+/* Synthetic inputs (harness): N(0, sigma) fp32 fill and generate+quantize
+ * rows in the Q8_0 (type 0), Q2 (type 2) or Q3 (type 3) layouts. */
+int sf37k_synth_normal(float *dst, uint64_t n, uint64_t seed, uint64_t stream,
+                       uint64_t index0, float sigma, sf37_stream_t s);
+int sf37k_synth_quant_rows(int type, uint8_t *dst, uint64_t row0, uint64_t nrows,
+                           uint64_t ncols, uint64_t seed, uint64_t stream, float sigma,
+                           sf37_stream_t s);
+/* Elementwise exp/sigmoid of a float array (for exhaustive parity tests). */
+int sf37k_sigmoid_array(float *out, const float *x, uint64_t n, int mode, sf37_stream_t s);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

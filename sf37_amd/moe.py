@@ -1,0 +1,103 @@
+"""Synthetic SF37 MoE layers resident in HBM, and thin wrappers over the
+C ABI entry points that run them.
+
+A layer is generated on the device from one seed: router
+W_r ~ N(0, 0.02) fp32, router bias 0, 288 experts whose fp32 gate/up
+[1280 x 4096] and down [4096 x 1280] rows ~ N(0, 0.02) are quantized to
+Q3GU / Q2D by the reference quantizer, and a Q8_0 shared expert, all from
+counter-based streams so any part can be regenerated bit-identically.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+from . import hip
+from .hip import Tensor, check, lib
+
+EMBD = 4096          # sf37.c:36
+EXPERTS = 288        # sf37.c:44
+EXPERT_USED = 8      # sf37.c:45
+EXPERT_FF = 1280     # sf37.c:46
+
+STREAM = {"router": 1, "gate": 2, "up": 3, "down": 4, "sh_gate": 5, "sh_up": 6, "sh_down": 7, "norm": 8}
+
+
+def layer_seed(master: int, layer: int) -> int:
+    return master * 1000003 + layer
+
+
+def swiglu_limit(il: int, shared: bool) -> float:
+    """Per-layer SwiGLU clamp, sf37.c:2103-2106."""
+    if il in (43, 44):
+        return 16.0 if shared else 7.0
+    return 0.0
+
+
+class SynthLayer:
+    """One MoE layer's weights on the device."""
+
+    def __init__(self, seed: int, n_expert: int = EXPERTS, in_dim: int = EMBD, mid_dim: int = EXPERT_FF,
+                 topk: int = EXPERT_USED, il: int = 3, sigma: float = 0.02):
+        self.seed, self.n_expert, self.in_dim, self.mid_dim, self.topk, self.il = \
+            seed, n_expert, in_dim, mid_dim, topk, il
+        E, D, F = n_expert, in_dim, mid_dim
+        self.g_row = D // 256 * hip.Q3_BLOCK
+        self.d_row = F // 256 * hip.Q2_BLOCK
+        self.router = hip.synth_normal(E * D, seed, STREAM["router"], sigma=sigma)
+        self.router_bias = Tensor.from_array(np.zeros(E, np.float32))
+        self.gate = hip.synth_quant("q3", E * F, D, seed, STREAM["gate"], sigma=sigma)
+        self.up = hip.synth_quant("q3", E * F, D, seed, STREAM["up"], sigma=sigma)
+        self.down = hip.synth_quant("q2", E * D, F, seed, STREAM["down"], sigma=sigma)
+        self.sh_gate = hip.synth_quant("q8_0", F, D, seed, STREAM["sh_gate"], sigma=sigma)
+        self.sh_up = hip.synth_quant("q8_0", F, D, seed, STREAM["sh_up"], sigma=sigma)
+        self.sh_down = hip.synth_quant("q8_0", D, F, seed, STREAM["sh_down"], sigma=sigma)
+        self.clamp_routed = swiglu_limit(il, False)
+        self.clamp_shared = swiglu_limit(il, True)
+
+    # bytes moved by one pass over the routed experts in `experts`
+    def expert_bytes(self) -> int:
+        return self.mid_dim * self.g_row * 2 + self.in_dim * self.d_row
+
+    def shared_bytes(self) -> int:
+        return self.sh_gate.nbytes + self.sh_up.nbytes + self.sh_down.nbytes
+
+    def router_bytes(self) -> int:
+        return self.router.nbytes
+
+    def weights_struct(self, scale: float = 3.0) -> hip.LayerWeights:
+        return hip.LayerWeights(self.router.h, self.router_bias.h, self.gate.h, self.up.h, self.down.h,
+                                self.sh_gate.h, self.sh_up.h, self.sh_down.h, self.n_expert, self.topk,
+                                self.in_dim, self.mid_dim, scale, self.clamp_routed, self.clamp_shared)
+
+    def host_experts(self, experts) -> dict:
+        """Host copies of the given experts' packed rows (for the CPU oracle),
+        in an array with the full expert stride but only those experts filled."""
+        E, F, D = self.n_expert, self.mid_dim, self.in_dim
+        gate = np.zeros(E * F * self.g_row, np.uint8)
+        up = np.zeros_like(gate)
+        down = np.zeros(E * D * self.d_row, np.uint8)
+        gb, db = F * self.g_row, D * self.d_row
+        ids = {int(v) for v in np.ravel(experts)}
+        for e in sorted({v if 0 <= v < E else 0 for v in ids}):      # invalid ids act as expert 0
+            gate[e * gb:(e + 1) * gb] = self.gate.read(np.uint8, offset=e * gb, count=gb)
+            up[e * gb:(e + 1) * gb] = self.up.read(np.uint8, offset=e * gb, count=gb)
+            down[e * db:(e + 1) * db] = self.down.read(np.uint8, offset=e * db, count=db)
+        return {"gate": gate, "up": up, "down": down}
+
+    def host_dense(self) -> dict:
+        return {"router": self.router.read(np.float32), "router_bias": self.router_bias.read(np.float32),
+                "sh_gate": self.sh_gate.read(np.uint8), "sh_up": self.sh_up.read(np.uint8),
+                "sh_down": self.sh_down.read(np.uint8)}
+
+    def free(self) -> None:
+        for t in (self.router, self.router_bias, self.gate, self.up, self.down, self.sh_gate, self.sh_up,
+                  self.sh_down):
+            t.free()
+
+
+def moe_layer(layer: SynthLayer, x: Tensor, n_tok: int, out: Tensor, selected: Tensor | None = None,
+              weights: Tensor | None = None, logits: Tensor | None = None, scale: float = 3.0) -> None:
+    """out = shared(x) + routed(x) for n_tok tokens (sf37_hip_moe_layer)."""
+    w = layer.weights_struct(scale)
+    check(lib().sf37_hip_moe_layer(out.h, selected.h if selected else None, weights.h if weights else None,
+                                   w, logits.h if logits else None, x.h, n_tok), "moe_layer")
