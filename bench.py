@@ -5,7 +5,9 @@ Workload: one MoE layer decode step of 8 tokens,
 E=288 experts, K=4096, F=1280, top-8, Q3GU gate/up + Q2D down experts and a
 Q8_0 shared expert, router logits injected i.i.d. N(0,1) (uniform routing).
 A step is the whole layer on device-resident inputs: router GEMV over the 8
-tokens, top-8 selection, shared expert, routed experts, shared + routed.
+tokens (computed although the injected logits drive the selection), top-8
+selection, shared expert, routed experts, shared + routed.  With the fused
+decode path that is three kernel launches.
 
 Steps rotate over --layers independently seeded layers (each with its own
 input tokens), so consecutive steps never reuse weights and the 256 MB
@@ -13,11 +15,11 @@ last-level cache cannot serve them.  value = algorithmic HBM bytes per step
 (distinct selected experts x 6,225,920 + shared 16,711,680 + router
 4,718,592 + x/out activations) / measured step time.
 
-roofline: the dominant kernel (routed gate/up), its algorithmic bytes per
-launch over its average launch time from HIP events on the launch stream in
-a second, identical pass with stage events enabled.  cpu_baseline: the
-reference CPU MoE path (sf37_ops.c/sf37_quant.c built with the reference
-`make cpu` flags) on one step's tokens, single core.
+roofline: the kernel with the largest share of the step time, its
+algorithmic bytes per launch over its average launch time from HIP events
+on the launch stream in a second, identical pass with stage events enabled.
+cpu_baseline: the reference CPU MoE path (sf37_ops.c/sf37_quant.c built with
+the reference `make cpu` flags) on one step's tokens, single core.
 """
 from __future__ import annotations
 
@@ -37,6 +39,8 @@ import numpy as np  # noqa: E402
 HBM_PEAK_GBS = 8000.0
 EXPERT_BYTES = 6_225_920
 GATE_UP_EXPERT_BYTES = 2 * 2_252_800
+DOWN_EXPERT_BYTES = 1_720_320
+Q8K_BLOCK = 268
 
 
 def parse():
@@ -100,40 +104,42 @@ def main():
         xs.append(configs.x_device(1, seed, n_tok))
         lg = configs.logits_for(1, seed, n_tok)
         lgs.append(hip.Tensor.from_array(lg))
-    logit_scratch = hip.Tensor.alloc(n_tok * E * 4)
     out = hip.Tensor.alloc(n_tok * K * 4)
     sel = hip.Tensor.alloc(n_tok * TOPK * 4)
     wts = hip.Tensor.alloc(n_tok * TOPK * 4)
     L = hip.lib()
-
-    router_keys, key_store = [], []
-    for lay in layers:
-        k = np.zeros(64, np.uint8)               # model-map key for the router (kept alive)
-        key_store.append(k)
-        router_keys.append(k.ctypes.data)
-        hip.check(L.sf37_hip_register_device_range(k.ctypes.data, lay.router.nbytes, 0, lay.router.nbytes,
-                                                   lay.router), "register router")
+    # the router GEMV runs inside the layer although injected logits select
+    hip.set_option("router_with_logits", 1)
     structs = [lay.weights_struct() for lay in layers]
 
     def step(i):
         l = i % args.layers
-        lay = layers[l]
-        # router GEMV over the step's tokens (its bytes belong to the layer); the
-        # selection then uses the injected logits of config 1
-        hip.check(L.sf37_hip_matmul_f32_mapped(logit_scratch, router_keys[l], lay.router.nbytes, 0, K, E,
-                                               xs[l], n_tok), "router gemv")
         hip.check(L.sf37_hip_moe_layer(out, sel, wts, structs[l], lgs[l], xs[l], n_tok), "moe layer")
 
-    # distinct experts per layer's routing (for the byte count)
-    step_bytes, gu_bytes = [], []
+    # distinct experts per layer's routing -> algorithmic bytes per step and
+    # per kernel of the fused path
+    P = n_tok * TOPK
+    step_bytes, kern_bytes = [], []
     for l in range(args.layers):
         step(l)
         s = sel.read(np.int32).reshape(n_tok, TOPK)
         sels.append(s)
         distinct = len(np.unique(s))
+        lay = layers[l]
         act = n_tok * K * 4 * 2
-        step_bytes.append(distinct * EXPERT_BYTES + layers[l].shared_bytes() + layers[l].router_bytes() + act)
-        gu_bytes.append(distinct * GATE_UP_EXPERT_BYTES + n_tok * 16 * 268 + n_tok * TOPK * F * 4)
+        step_bytes.append(distinct * EXPERT_BYTES + lay.shared_bytes() + lay.router_bytes() + act)
+        sh_gu = lay.sh_gate.nbytes + lay.sh_up.nbytes
+        kern_bytes.append({
+            # router weights + x in, logits + Q8_K/Q8_0 of x out
+            "dec_route": lay.router_bytes() + n_tok * K * 4 + n_tok * E * 4 + n_tok * (K // 256) * Q8K_BLOCK
+                         + n_tok * K + n_tok * (K // 32) * 4,
+            # routed + shared gate/up weights, activations in, mid (f32 + Q8_K) out
+            "dec_up": distinct * GATE_UP_EXPERT_BYTES + sh_gu + n_tok * (K // 256) * Q8K_BLOCK + n_tok * K
+                      + P * F * 4 + P * (F // 256) * Q8K_BLOCK + n_tok * F * 9,
+            # routed + shared down weights, mid in, per-pair partials + out
+            "dec_down": distinct * DOWN_EXPERT_BYTES + lay.sh_down.nbytes + P * (F // 256) * Q8K_BLOCK
+                        + n_tok * F + P * K * 4 * 2 + n_tok * K * 4 * 2,
+        })
     hip.synchronize()
 
     for i in range(args.warmup):
@@ -157,12 +163,15 @@ def main():
         step(i)
     prof = hip.profile_read()
     L.sf37_hip_profile_enable(0)
-    gu_ms, gu_n = prof["gate_up"]
-    gu_avg_ms = gu_ms / max(gu_n, 1)
-    gu_mean_bytes = float(np.mean([gu_bytes[i % args.layers] for i in range(args.steps)]))
-    achieved = gu_mean_bytes / (gu_avg_ms * 1e-3) / 1e9
+    kern = max(("dec_route", "dec_up", "dec_down"), key=lambda k: prof[k][0])
+    k_ms, k_n = prof[kern]
+    if k_n == 0:
+        raise SystemExit("bench.py: the fused decode kernels did not run")
+    k_avg_ms = k_ms / k_n
+    k_mean_bytes = float(np.mean([kern_bytes[i % args.layers][kern] for i in range(args.steps)]))
+    achieved = k_mean_bytes / (k_avg_ms * 1e-3) / 1e9
     traffic = None
-    tpath = os.path.join(ROOT, "profiles", "gate_up_decode8_traffic.json")
+    tpath = os.path.join(ROOT, "profiles", f"{kern}_decode8_traffic.json")
     if os.path.exists(tpath):
         traffic = json.load(open(tpath)).get("hbm_bytes_per_launch")
 
@@ -192,8 +201,7 @@ def main():
                    "pct_of_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 2)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "kernel": "gate_up (routed Q3 gate/up + SwiGLU*w)",
-                     "bytes_per_launch": int(gu_mean_bytes), "ms_per_launch": round(gu_avg_ms, 5)},
+                     "kernel": kern, "bytes_per_launch": int(k_mean_bytes), "ms_per_launch": round(k_avg_ms, 5)},
         "cpu_baseline": cpu,
         "stages": stages,
     }

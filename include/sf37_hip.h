@@ -227,6 +227,12 @@ void *sf37_hip_get_stream(void);
  *   "q8k"               0 disables the Q8_K path (SF37_CUDA_NO_QLOW_Q8K)
  *   "moe_write_gate_up" 1 also writes gate/up outputs in routed_moe_one
  *                       (SF37_CUDA_MOE_WRITE_GATE_UP)
+ *   "decode_fused"      1 (default): batches of up to 16 tokens on the Q8_K
+ *                       path run as three fused launches; 0 uses one launch
+ *                       per stage.  Results are identical either way.
+ *   "router_with_logits" 1: sf37_hip_moe_layer computes the router GEMV even
+ *                       when logits_in is given (its result is unused; for
+ *                       benchmarks that inject routing but keep the cost)
  * Returns 1 for a known name. */
 int sf37_hip_set_option(const char *name, int64_t value);
 int64_t sf37_hip_get_option(const char *name);
@@ -277,7 +283,12 @@ enum {
     SF37_HIP_STAGE_ROUTER = 0, SF37_HIP_STAGE_SELECT, SF37_HIP_STAGE_Q8_0_ACT, SF37_HIP_STAGE_Q8_0_GEMM,
     SF37_HIP_STAGE_SWIGLU, SF37_HIP_STAGE_Q8K_X, SF37_HIP_STAGE_DISPATCH, SF37_HIP_STAGE_GATE_UP,
     SF37_HIP_STAGE_Q8K_MID, SF37_HIP_STAGE_DOWN, SF37_HIP_STAGE_COMBINE, SF37_HIP_STAGE_ADD,
-    SF37_HIP_STAGE_OTHER, SF37_HIP_N_STAGES
+    SF37_HIP_STAGE_OTHER,
+    /* the fused decode layer (up to 16 tokens): route = router GEMV + x
+     * quantisation + top-k + grouping, up = routed and shared gate/up with
+     * SwiGLU and mid quantisation, down = routed and shared down + combine */
+    SF37_HIP_STAGE_DEC_ROUTE, SF37_HIP_STAGE_DEC_UP, SF37_HIP_STAGE_DEC_DOWN,
+    SF37_HIP_N_STAGES
 };
 int sf37_hip_profile_enable(int on);
 int sf37_hip_profile_read(double *ms, uint64_t *count, uint32_t n_stages);

@@ -119,3 +119,29 @@ __device__ __forceinline__ uint32_t q3_load(uint32_t *w, const uint8_t *p) {
     return (uint32_t)(addr & 3u);
 }
 
+
+// Copy the bytes [src, src + n) of global memory into LDS with direct
+// global->LDS dwordx4 loads: each wave instruction moves 64 x 16 contiguous
+// bytes, so weight tiles are read fully coalesced whatever their block size.
+// The copy starts at the 16-byte boundary at or below src, so dst (16-byte
+// aligned) must hold n + 31 bytes; returns the offset of src inside dst.
+// Reads up to 15 bytes past src + n, inside the slack every library
+// allocation carries.  All threads of the workgroup call it; lds_copy_wait()
+// must follow before dst is read.
+__device__ __forceinline__ uint32_t lds_copy(uint8_t *dst, const uint8_t *src, uint32_t n) {
+    const uintptr_t a = (uintptr_t)src, a0 = a & ~(uintptr_t)15;
+    const uint32_t off = (uint32_t)(a - a0);
+    const uint32_t chunks = (off + n + 15u) >> 4;
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u, nw = blockDim.x >> 6;
+    for (uint32_t c0 = wave * 64u; c0 < chunks; c0 += nw * 64u) {
+        const uint32_t c = c0 + lane;
+        if (c < chunks)
+            __builtin_amdgcn_global_load_lds((const void *)(a0 + 16u * (uintptr_t)c), dst + 16u * c0, 16, 0, 0);
+    }
+    return off;
+}
+
+__device__ __forceinline__ void lds_copy_wait() {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+}

@@ -41,7 +41,8 @@ __host__ __device__ inline uint64_t sf37_exp2_tab(uint32_t i) {
     return tab[i & 31u];
 }
 
-__host__ __device__ inline float sf37_expf(float x) {
+// tab: the 32 table words (sf37_exp2_tab), e.g. staged in LDS by the caller.
+__host__ __device__ inline float sf37_expf_t(float x, const uint64_t *tab) {
     const uint32_t ux = __builtin_bit_cast(uint32_t, x);
     const uint32_t abstop = (ux >> 20) & 0x7ffu;
     if (abstop >= 0x42bu) {                       // |x| >= 88 or nan
@@ -60,7 +61,7 @@ __host__ __device__ inline float sf37_expf(float x) {
     const uint64_t ki = __builtin_bit_cast(uint64_t, kd);
     kd = kd - shift;
     const double r = __builtin_fma(inv_ln2_n, xd, -kd);
-    uint64_t t = sf37_exp2_tab((uint32_t)(ki & 31u));
+    uint64_t t = tab ? tab[ki & 31u] : sf37_exp2_tab((uint32_t)(ki & 31u));
     t += ki << 47;
     const double s = __builtin_bit_cast(double, t);
     const double z = __builtin_fma(c0, r, c1);
@@ -71,24 +72,38 @@ __host__ __device__ inline float sf37_expf(float x) {
     return (float)y;
 }
 
+__host__ __device__ inline float sf37_expf(float x) { return sf37_expf_t(x, nullptr); }
+
 // sf37_ops.c:9-16
-__host__ __device__ inline float sf37_sigmoid(float x) {
+__host__ __device__ inline float sf37_sigmoid_t(float x, const uint64_t *tab) {
     if (x >= 0.0f) {
-        const float z = sf37_expf(-x);
+        const float z = sf37_expf_t(-x, tab);
         return 1.0f / (1.0f + z);
     }
-    const float z = sf37_expf(x);
+    const float z = sf37_expf_t(x, tab);
     return z / (1.0f + z);
 }
 
+__host__ __device__ inline float sf37_sigmoid(float x) { return sf37_sigmoid_t(x, nullptr); }
+
+// Stage the exp table into LDS (all threads may call; caller syncs).
+__device__ inline void sf37_stage_exp_tab(uint64_t *lds_tab) {
+    for (uint32_t i = threadIdx.x; i < 32u; i += blockDim.x) lds_tab[i] = sf37_exp2_tab(i);
+}
+
 // ((g * sigmoid(g)) * u) * w with the routed/shared clamp (sf37_cuda.cu:4444-4456).
-__device__ __forceinline__ float sf37_swiglu_mid(float g, float u, float w, float clamp) {
+__device__ __forceinline__ float sf37_swiglu_mid_t(float g, float u, float w, float clamp,
+                                                  const uint64_t *tab) {
     if (clamp > 1.0e-6f) {
         if (g > clamp) g = clamp;
         if (u > clamp) u = clamp;
         if (u < -clamp) u = -clamp;
     }
-    return g * sf37_sigmoid(g) * u * w;
+    return g * sf37_sigmoid_t(g, tab) * u * w;
+}
+
+__device__ __forceinline__ float sf37_swiglu_mid(float g, float u, float w, float clamp) {
+    return sf37_swiglu_mid_t(g, u, w, clamp, nullptr);
 }
 
 __device__ __forceinline__ float sf37_f16(uint32_t h16) {

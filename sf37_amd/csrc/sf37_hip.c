@@ -48,6 +48,13 @@ static uint64_t g_layer_buf_bytes[6];
 static int64_t g_opt_q8k = 1;
 static int64_t g_opt_q8k_min_rows = 512;
 static int64_t g_opt_write_gate_up = 0;
+static int64_t g_opt_decode = 1;
+static int64_t g_opt_router_always = 0;
+
+/* arrival counters of the fused decode kernels: zeroed once, left zero by
+ * every completed launch */
+static uint32_t *g_dec_cnt;
+static uint64_t g_dec_cnt_words;
 
 typedef struct {
     const uint8_t *map;
@@ -80,7 +87,7 @@ static hipEvent_t g_prof_open;
 
 static const char *const k_stage_names[SF37_HIP_N_STAGES] = {
     "router", "select", "q8_0_act", "q8_0_gemm", "swiglu", "q8k_x", "dispatch",
-    "gate_up", "q8k_mid", "down", "combine", "add", "other"};
+    "gate_up", "q8k_mid", "down", "combine", "add", "other", "dec_route", "dec_up", "dec_down"};
 
 static void prof_begin(void) {
     if (!g_prof_on) return;
@@ -240,6 +247,9 @@ void sf37_hip_cleanup(void) {
     if (g_scratch) (void)hipFree(g_scratch);
     g_scratch = NULL;
     g_scratch_bytes = 0;
+    if (g_dec_cnt) (void)hipFree(g_dec_cnt);
+    g_dec_cnt = NULL;
+    g_dec_cnt_words = 0;
     for (int i = 0; i < 6; i++) {
         if (g_layer_bufs[i]) {
             (void)hipFree(g_layer_bufs[i]->ptr);
@@ -287,6 +297,8 @@ int sf37_hip_set_option(const char *name, int64_t value) {
     if (!strcmp(name, "q8k")) g_opt_q8k = value ? 1 : 0;
     else if (!strcmp(name, "q8k_min_rows")) g_opt_q8k_min_rows = value < 0 ? 0 : value;
     else if (!strcmp(name, "moe_write_gate_up")) g_opt_write_gate_up = value ? 1 : 0;
+    else if (!strcmp(name, "decode_fused")) g_opt_decode = value ? 1 : 0;
+    else if (!strcmp(name, "router_with_logits")) g_opt_router_always = value ? 1 : 0;
     else return 0;
     return 1;
 }
@@ -296,6 +308,8 @@ int64_t sf37_hip_get_option(const char *name) {
     if (!strcmp(name, "q8k")) return g_opt_q8k;
     if (!strcmp(name, "q8k_min_rows")) return g_opt_q8k_min_rows;
     if (!strcmp(name, "moe_write_gate_up")) return g_opt_write_gate_up;
+    if (!strcmp(name, "decode_fused")) return g_opt_decode;
+    if (!strcmp(name, "router_with_logits")) return g_opt_router_always;
     return -1;
 }
 
@@ -855,6 +869,151 @@ static int routed_q8k(const routed_args *a, float *out, float *mid, float *down_
                      "routed_moe combine launch");
 }
 
+/* ---- fused decode path (k_decode.hip) ------------------------------------ */
+
+/* Extra inputs of the fused path beyond the routed arguments. */
+typedef struct {
+    uint32_t flags;
+    const float *router_w, *router_bias, *logits_sel;
+    const uint8_t *sh_gate, *sh_up, *sh_down;
+    float scale, clamp_shared;
+    int32_t *sel;   /* selection output when SELECT (NULL = scratch) */
+    float *wts;
+} dec_extra;
+
+static uint32_t *dec_counters(uint64_t words) {
+    if (g_dec_cnt && words <= g_dec_cnt_words) return g_dec_cnt;
+    if (g_dec_cnt) {
+        if (!hip_ok(hipStreamSynchronize(g_stream), "decode counter sync")) return NULL;
+        (void)hipFree(g_dec_cnt);
+        g_dec_cnt = NULL;
+        g_dec_cnt_words = 0;
+    }
+    void *p = NULL;
+    if (!hip_ok(hipMalloc(&p, words * 4u + SF37_PAD), "decode counter alloc")) return NULL;
+    if (!hip_ok(hipMemset(p, 0, words * 4u + SF37_PAD), "decode counter clear") ||
+        !hip_ok(hipDeviceSynchronize(), "decode counter clear sync")) {
+        (void)hipFree(p);
+        return NULL;
+    }
+    g_dec_cnt = (uint32_t *)p;
+    g_dec_cnt_words = words;
+    return g_dec_cnt;
+}
+
+/* Shapes the fused kernels take: at most 16 tokens and top-16, square
+ * down projection, 256-multiple dims, the Q8_K numerics the staged path
+ * would pick, and LDS within 64 KiB. */
+static int decode_eligible(const routed_args *a, uint32_t flags) {
+    if (!g_opt_decode || a->n_tok == 0 || a->n_tok > SF37_DEC_MAX_TOK || a->topk == 0 || a->topk > 16u ||
+        a->topk > a->n_expert || a->out_dim != a->in_dim || a->in_dim % QK != 0 || a->mid_dim % QK != 0 ||
+        !q8k_use_for(a->mid_dim) || !q8k_use_for(a->out_dim))
+        return 0;
+    if ((flags & SF37_DEC_SELECT) && a->n_expert > ROUTER_MAX_EXPERTS) return 0;
+    if ((flags & SF37_DEC_SLOTS) && a->n_tok != 1u) return 0;
+    return 1;
+}
+
+/* out = [shared +] sum over slots of the routed experts; mid / down_pair /
+ * gate_out / up_out receive per-pair results when given (pairs x F, pairs x
+ * D), else scratch is used. */
+static int decode_run(const routed_args *a, const dec_extra *ex, float *out, float *mid, float *down_pair,
+                      float *gate_out, float *up_out) {
+    if (!aligned4(a->gate_w) || !aligned4(a->up_w) || !aligned4(a->down_w) || !aligned4(a->x) ||
+        !aligned4(out) || (mid && !aligned4(mid)) || (down_pair && !aligned4(down_pair)))
+        return 0;
+    const uint32_t T = a->n_tok, E = a->n_expert, K = a->in_dim, F = a->mid_dim, TK = a->topk;
+    const uint64_t P = (uint64_t)T * TK;
+    const uint32_t G = (uint32_t)(P < E ? P : E);
+    const int sh = (ex->flags & SF37_DEC_SHARED) != 0;
+    sf37_dec_params p;
+    memset(&p, 0, sizeof(p));
+    p.T = T;
+    p.E = E;
+    p.K = K;
+    p.F = F;
+    p.topk = TK;
+    p.G = G;
+    p.scale = ex->scale;
+    p.clamp_routed = a->clamp;
+    p.clamp_shared = ex->clamp_shared;
+    p.flags = ex->flags;
+    p.x = a->x;
+    p.router_w = ex->router_w;
+    p.router_bias = ex->router_bias;
+    p.logits_sel = ex->logits_sel;
+    p.gate_w = a->gate_w;
+    p.up_w = a->up_w;
+    p.down_w = a->down_w;
+    p.sh_gate = ex->sh_gate;
+    p.sh_up = ex->sh_up;
+    p.sh_down = ex->sh_down;
+    p.gate_out = gate_out;
+    p.up_out = up_out;
+    p.out = out;
+    if (sf37k_decode_lds(&p) > 65536u) return 0;
+    /* scratch layout */
+    uint64_t off = 0, o_xq, o_xq8, o_xs8, o_gi, o_so, o_mid = 0, o_mq, o_gu = 0, o_smq = 0, o_sms = 0, o_dp = 0,
+                      o_sho = 0, o_lg = 0, o_sel = 0, o_wts = 0;
+#define TAKE(var, bytes)            \
+    do {                            \
+        var = off;                  \
+        off = align256(off + (bytes)); \
+    } while (0)
+    TAKE(o_xq, (uint64_t)T * (K / QK) * Q8KB);
+    TAKE(o_xq8, (uint64_t)T * K);
+    TAKE(o_xs8, (uint64_t)T * (K / 32u) * 4u);
+    TAKE(o_gi, (3u + 2u * (uint64_t)G) * 4u);
+    TAKE(o_so, P * 4u);
+    if (!mid) TAKE(o_mid, P * F * 4u);
+    TAKE(o_mq, P * (F / QK) * Q8KB);
+    if (sh) {
+        TAKE(o_gu, 2u * (uint64_t)T * F * 4u);
+        TAKE(o_smq, (uint64_t)T * F);
+        TAKE(o_sms, (uint64_t)T * (F / 32u) * 4u);
+        TAKE(o_sho, (uint64_t)T * K * 4u);
+    }
+    if (!down_pair) TAKE(o_dp, P * K * 4u);
+    if (ex->flags & SF37_DEC_ROUTER) TAKE(o_lg, (uint64_t)T * E * 4u);
+    if ((ex->flags & SF37_DEC_SELECT) && !ex->sel) TAKE(o_sel, P * 4u);
+    if ((ex->flags & SF37_DEC_SELECT) && !ex->wts) TAKE(o_wts, P * 4u);
+#undef TAKE
+    char *base = scratch_get(off, "decode scratch");
+    uint32_t *cnt = dec_counters((uint64_t)sf37k_decode_counters(T, TK, E, K, F));
+    if (!base || !cnt) return 0;
+    p.xq = base + o_xq;
+    p.xq8 = (int8_t *)(base + o_xq8);
+    p.xs8 = (float *)(base + o_xs8);
+    p.ginfo = (uint32_t *)(base + o_gi);
+    p.sorted = (uint32_t *)(base + o_so);
+    p.mid = mid ? mid : (float *)(base + o_mid);
+    p.midq = base + o_mq;
+    if (sh) {
+        p.sh_gu = (float *)(base + o_gu);
+        p.sh_mq = (int8_t *)(base + o_smq);
+        p.sh_ms = (float *)(base + o_sms);
+        p.sh_out = (float *)(base + o_sho);
+    }
+    p.down_pair = down_pair ? down_pair : (float *)(base + o_dp);
+    p.logits = (ex->flags & SF37_DEC_ROUTER) ? (float *)(base + o_lg) : NULL;
+    if (ex->flags & SF37_DEC_SELECT) {
+        p.sel = ex->sel ? ex->sel : (int32_t *)(base + o_sel);
+        p.wts = ex->wts ? ex->wts : (float *)(base + o_wts);
+        if (!p.logits_sel) p.logits_sel = p.logits;
+        if (!p.logits_sel || !p.router_bias) return 0;
+    } else {
+        p.sel = (int32_t *)a->selected;
+        p.wts = (float *)a->weights;
+    }
+    if ((ex->flags & SF37_DEC_ROUTER) && !p.router_w) return 0;
+    if (sh && (!p.sh_gate || !p.sh_up || !p.sh_down)) return 0;
+    p.cnt = cnt;
+    const sf37_stream_t st = (sf37_stream_t)g_stream;
+    return LAUNCH(SF37_HIP_STAGE_DEC_ROUTE, sf37k_decode_route(&p, st), "decode route launch") &&
+           LAUNCH(SF37_HIP_STAGE_DEC_UP, sf37k_decode_up(&p, st), "decode up launch") &&
+           LAUNCH(SF37_HIP_STAGE_DEC_DOWN, sf37k_decode_down(&p, st), "decode down launch");
+}
+
 /* fp32-activation path for one token (sf37_cuda.cu:5382-5446). */
 static int routed_f32(const routed_args *a, float *out, float *mid, float *down_slot, float *gate_out,
                       float *up_out) {
@@ -874,6 +1033,12 @@ static int routed_one_impl(sf37_hip_tensor *out, sf37_hip_tensor *gate, sf37_hip
                            sf37_hip_tensor *mid, sf37_hip_tensor *down, const routed_args *a) {
     float *go = g_opt_write_gate_up ? (float *)gate->ptr : NULL;
     float *uo = g_opt_write_gate_up ? (float *)up->ptr : NULL;
+    if (decode_eligible(a, SF37_DEC_SLOTS)) {
+        dec_extra ex;
+        memset(&ex, 0, sizeof(ex));
+        ex.flags = SF37_DEC_SLOTS;
+        return decode_run(a, &ex, (float *)out->ptr, (float *)mid->ptr, (float *)down->ptr, go, uo);
+    }
     if (q8k_use_for(a->mid_dim) && q8k_use_for(a->out_dim))
         return routed_q8k(a, (float *)out->ptr, (float *)mid->ptr, (float *)down->ptr, go, uo, 1);
     return routed_f32(a, (float *)out->ptr, (float *)mid->ptr, (float *)down->ptr, go, uo);
@@ -969,6 +1134,11 @@ int sf37_hip_routed_moe_batch_mapped(sf37_hip_tensor *out, sf37_hip_tensor *gate
         /* the caller's mid receives the per-pair SwiGLU output when it is big
          * enough (sf37_cuda.cu:5665-5674) */
         float *mid_pair = mid->bytes >= pairs * expert_mid_dim * 4u ? (float *)mid->ptr : NULL;
+        if (decode_eligible(&a, 0)) {
+            dec_extra ex;
+            memset(&ex, 0, sizeof(ex));
+            return decode_run(&a, &ex, (float *)out->ptr, mid_pair, NULL, NULL, NULL);
+        }
         return routed_q8k(&a, (float *)out->ptr, mid_pair, NULL, NULL, NULL, 0);
     }
     /* per-token loop, as the reference's fallback (sf37_cuda.cu:5734-5780) */
@@ -1045,14 +1215,33 @@ int sf37_hip_moe_layer(sf37_hip_tensor *out, sf37_hip_tensor *selected, sf37_hip
         }
     }
     const sf37_stream_t st = (sf37_stream_t)g_stream;
+    const int run_router = !logits_in || (g_opt_router_always && w->router);
+    routed_args a = {(const uint8_t *)w->gate->ptr, (const uint8_t *)w->up->ptr, (const uint8_t *)w->down->ptr, NULL,
+                     NULL, E, K, D, F, D, w->clamp_routed, (const float *)x->ptr, n_tok};
+    if (decode_eligible(&a, SF37_DEC_SELECT | SF37_DEC_SHARED)) {
+        dec_extra ex;
+        memset(&ex, 0, sizeof(ex));
+        ex.flags = SF37_DEC_SELECT | SF37_DEC_SHARED | (run_router ? SF37_DEC_ROUTER : 0u);
+        ex.router_w = w->router ? (const float *)w->router->ptr : NULL;
+        ex.router_bias = (const float *)w->router_bias->ptr;
+        ex.logits_sel = logits_in ? (const float *)logits_in->ptr : NULL;
+        ex.sh_gate = (const uint8_t *)w->sh_gate->ptr;
+        ex.sh_up = (const uint8_t *)w->sh_up->ptr;
+        ex.sh_down = (const uint8_t *)w->sh_down->ptr;
+        ex.scale = w->scale;
+        ex.clamp_shared = w->clamp_shared;
+        ex.sel = selected ? (int32_t *)selected->ptr : NULL;
+        ex.wts = weights ? (float *)weights->ptr : NULL;
+        return decode_run(&a, &ex, (float *)out->ptr, NULL, NULL, NULL, NULL);
+    }
     float *logits = logits_in ? (float *)logits_in->ptr : (float *)ls[0]->ptr;
     int32_t *sel = selected ? (int32_t *)selected->ptr : (int32_t *)ls[1]->ptr;
     float *wts = weights ? (float *)weights->ptr : (float *)ls[2]->ptr;
     float *sh = (float *)ls[3]->ptr;   /* gate | up | mid for the shared expert */
     float *routed = (float *)ls[4]->ptr;
-    if (!logits_in && !LAUNCH(SF37_HIP_STAGE_ROUTER, sf37k_f32_matmul(logits, (const float *)w->router->ptr, (const float *)x->ptr, D, E,
-                                                  n_tok, st),
-                                 "moe_layer router launch"))
+    if (run_router && !LAUNCH(SF37_HIP_STAGE_ROUTER, sf37k_f32_matmul((float *)ls[0]->ptr, (const float *)w->router->ptr,
+                                                      (const float *)x->ptr, D, E, n_tok, st),
+                              "moe_layer router launch"))
         return 0;
     if (E > ROUTER_MAX_EXPERTS ||
         !LAUNCH(SF37_HIP_STAGE_SELECT, sf37k_router_select(sel, wts, NULL, logits, (const float *)w->router_bias->ptr, E, K, w->scale,
@@ -1068,8 +1257,8 @@ int sf37_hip_moe_layer(sf37_hip_tensor *out, sf37_hip_tensor *selected, sf37_hip
         !q8_0_run((float *)out->ptr, NULL, (const uint8_t *)w->sh_down->ptr, NULL, F, D,
                   sh + 2u * (uint64_t)n_tok * F, n_tok))
         return 0;
-    routed_args a = {(const uint8_t *)w->gate->ptr, (const uint8_t *)w->up->ptr, (const uint8_t *)w->down->ptr, sel,
-                     wts, E, K, D, F, D, w->clamp_routed, (const float *)x->ptr, n_tok};
+    a.selected = sel;
+    a.weights = wts;
     const int slots = n_tok == 1u;
     if (!slots && E > DISPATCH_MAX_EXPERTS) return 0;
     if (!q8k_use_for(F) || !q8k_use_for(D)) {

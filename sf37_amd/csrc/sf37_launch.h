@@ -94,6 +94,48 @@ int sf37k_synth_quant_rows(int type, uint8_t *dst, uint64_t row0, uint64_t nrows
 /* Elementwise exp/sigmoid of a float array (for exhaustive parity tests). */
 int sf37k_sigmoid_array(float *out, const float *x, uint64_t n, int mode, sf37_stream_t s);
 
+/* Fused decode layer (up to 16 tokens): route, up, down in three launches
+ * (k_decode.hip).  Pointers are device addresses; flags select the parts
+ * that run.  cnt holds sf37k_decode_counters(...) zero-initialised words
+ * that the kernels leave zero again when they finish. */
+#define SF37_DEC_MAX_TOK 16u
+#define SF37_DEC_ROUTER 1u   /* router GEMV of x into logits */
+#define SF37_DEC_SELECT 2u   /* top-k from logits_sel (else sel/wts are inputs) */
+#define SF37_DEC_SHARED 4u   /* shared expert, out = shared + routed */
+#define SF37_DEC_SLOTS 8u    /* one group per slot of a single token */
+typedef struct sf37_dec_params {
+    uint32_t T, E, K, F, topk, G;
+    float scale, clamp_routed, clamp_shared;
+    uint32_t flags;
+    const float *x, *router_w, *router_bias, *logits_sel;
+    const uint8_t *gate_w, *up_w, *down_w, *sh_gate, *sh_up, *sh_down;
+    float *logits;
+    int32_t *sel;
+    float *wts;
+    void *xq;            /* T x K/256 Q8_K blocks */
+    int8_t *xq8;         /* T x K Q8_0 codes */
+    float *xs8;          /* T x K/32 Q8_0 scales */
+    uint32_t *ginfo;     /* [0] groups, [1..G+1] pair offsets, [G+2..2G+2) experts */
+    uint32_t *sorted;    /* pairs ordered by (expert, pair) */
+    float *mid;          /* pairs x F SwiGLU * weight */
+    void *midq;          /* pairs x F/256 Q8_K blocks */
+    float *gate_out, *up_out;   /* optional pairs x F */
+    float *sh_gu;        /* 2 x T x F shared gate | up */
+    int8_t *sh_mq;       /* T x F Q8_0 codes of the shared mid */
+    float *sh_ms;        /* T x F/32 scales */
+    float *down_pair;    /* pairs x K */
+    float *sh_out;       /* T x K */
+    float *out;          /* T x K */
+    uint32_t *cnt;
+} sf37_dec_params;
+int sf37k_decode_counters(uint32_t T, uint32_t topk, uint32_t E, uint32_t K, uint32_t F);
+/* LDS bytes the up/down launches need (the caller keeps them <= 64 KiB). */
+uint64_t sf37k_decode_lds(const sf37_dec_params *p);
+/* The three launches, in this order on one stream. */
+int sf37k_decode_route(const sf37_dec_params *p, sf37_stream_t s);
+int sf37k_decode_up(const sf37_dec_params *p, sf37_stream_t s);
+int sf37k_decode_down(const sf37_dec_params *p, sf37_stream_t s);
+
 #ifdef __cplusplus
 }
 #endif

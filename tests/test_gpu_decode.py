@@ -1,0 +1,209 @@
+"""GPU parity of the fused decode path (three launches for up to 16 tokens).
+
+The fused kernels and the staged kernels (one launch per stage, option
+decode_fused=0) follow the same canonical operation order, so every output
+must agree bit for bit; each shape is also checked against the CPU oracle on
+a case the oracle finishes in seconds.  Cases cover token counts 1..16, odd
+counts, experts shared by every token (groups larger than one pass of four
+pairs), invalid expert ids, duplicate experts within a token, the layer-43
+SwiGLU clamps and the router computed on the device.
+"""
+import ctypes as C
+import sys
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+E, K, F, TOPK = 288, 4096, 1280, 8
+
+
+def say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def H():
+    from sf37_amd import hip
+    hip.init()
+    yield hip
+    hip.set_option("decode_fused", 1)
+    hip.synchronize()
+
+
+@pytest.fixture(scope="module")
+def O():
+    import oracle
+    oracle.lib()
+    return oracle
+
+
+@pytest.fixture(scope="module")
+def layer(H):
+    from sf37_amd.moe import SynthLayer
+    say("generating BASELINE-shape layer (seed 77)")
+    L = SynthLayer(seed=77)
+    H.synchronize()
+    yield L
+    L.free()
+
+
+_KEYS = []
+
+
+def map_key():
+    """A host address used as a model-map key, kept alive for the session so
+    no later key can reuse it."""
+    k = np.zeros(64, np.uint8)
+    _KEYS.append(k)
+    return k.ctypes.data
+
+
+def bits(a):
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+
+def assert_bitexact(got, want, what):
+    g, w = np.ravel(bits(got)), np.ravel(bits(want))
+    bad = np.flatnonzero(g != w)
+    assert bad.size == 0, (f"{what}: {bad.size} of {g.size} differ; first at {bad[0]}: "
+                           f"{np.ravel(got)[bad[0]]!r} vs {np.ravel(want)[bad[0]]!r}")
+
+
+def skewed_logits(rng, n_tok, hot=(5, 6, 7, 8, 9)):
+    """N(0,1) logits with a few experts every token picks (groups of n_tok pairs)."""
+    lg = rng.standard_normal((n_tok, E)).astype(np.float32)
+    lg[:, list(hot)] += 8.0
+    return lg
+
+
+def run_layer(H, layer, x, logits, fused, clamps=None, scale=3.0):
+    n_tok = x.shape[0]
+    H.set_option("decode_fused", 1 if fused else 0)
+    try:
+        w = layer.weights_struct(scale)
+        if clamps is not None:
+            w.clamp_routed, w.clamp_shared = clamps
+        out, sel, wt = H.Tensor.alloc(n_tok * K * 4), H.Tensor.alloc(n_tok * TOPK * 4), \
+            H.Tensor.alloc(n_tok * TOPK * 4)
+        xt = H.Tensor.from_array(x)
+        lt = H.Tensor.from_array(logits) if logits is not None else None
+        H.check(H.lib().sf37_hip_moe_layer(out, sel, wt, w, lt, xt, n_tok), "moe_layer")
+        return (out.read(np.float32).reshape(n_tok, K), sel.read(np.int32).reshape(n_tok, TOPK),
+                wt.read(np.float32).reshape(n_tok, TOPK))
+    finally:
+        H.set_option("decode_fused", 1)
+
+
+@pytest.mark.parametrize("n_tok,routing", [(1, "uniform"), (3, "skewed"), (8, "uniform"), (8, "skewed"),
+                                           (13, "uniform"), (16, "skewed")])
+def test_fused_layer_equals_staged(H, layer, n_tok, routing):
+    rng = np.random.default_rng(1000 + n_tok)
+    x = rng.standard_normal((n_tok, K)).astype(np.float32)
+    logits = skewed_logits(rng, n_tok) if routing == "skewed" else rng.standard_normal((n_tok, E)).astype(np.float32)
+    say(f"fused vs staged: {n_tok} tokens, {routing} routing")
+    a = run_layer(H, layer, x, logits, True)
+    b = run_layer(H, layer, x, logits, False)
+    assert np.array_equal(a[1], b[1])
+    assert_bitexact(a[2], b[2], "weights")
+    assert_bitexact(a[0], b[0], f"out ({n_tok} tokens, {routing})")
+
+
+def test_fused_layer_router_on_device_and_clamps(H, layer):
+    """Router logits computed in the fused route kernel (no injected logits),
+    with the layer-43 clamps (routed 7, shared 16)."""
+    rng = np.random.default_rng(5)
+    x = (rng.standard_normal((5, K)) * 3).astype(np.float32)
+    for clamps in (None, (7.0, 16.0)):
+        say(f"router on device, clamps {clamps}")
+        a = run_layer(H, layer, x, None, True, clamps)
+        b = run_layer(H, layer, x, None, False, clamps)
+        assert np.array_equal(a[1], b[1])
+        assert_bitexact(a[2], b[2], "weights")
+        assert_bitexact(a[0], b[0], f"out clamps {clamps}")
+
+
+def test_fused_layer_16_tokens_against_oracle(H, O, layer):
+    """16 tokens, skewed routing, clamps on: bit-exact against the oracle."""
+    rng = np.random.default_rng(16)
+    x = rng.standard_normal((16, K)).astype(np.float32)
+    logits = skewed_logits(rng, 16)
+    say("fused 16 tokens vs oracle")
+    out, sel, w = run_layer(H, layer, x, logits, True, (7.0, 16.0))
+    dense = layer.host_dense()
+    weights = dict(layer.host_experts(np.append(np.ravel(sel), 0)), **dense, n_expert=E, mid_dim=F)
+    want, wsel, ww = O.moe_layer_q8k(weights, x, logits=logits, clamp_routed=7.0, clamp_shared=16.0)
+    assert np.array_equal(sel, wsel)
+    assert_bitexact(w, ww, "weights")
+    assert_bitexact(out, want, "16-token layer")
+
+
+def test_fused_routed_batch_mapped(H, O, layer):
+    """routed_moe_batch_mapped for 5 tokens at the full shape, with an invalid
+    id and an expert repeated inside one token: out and per-pair mid equal
+    the staged path and the oracle."""
+    n_tok = 5
+    rng = np.random.default_rng(55)
+    sel = np.stack([rng.choice(E, TOPK, replace=False) for _ in range(n_tok)]).astype(np.int32)
+    sel[1, 2] = -1
+    sel[2, 5] = sel[2, 1]
+    sel[3, :4] = sel[0, :4]
+    w = (rng.random((n_tok, TOPK)) * 0.5).astype(np.float32)
+    x = rng.standard_normal((n_tok, K)).astype(np.float32)
+    gb, db = layer.gate.nbytes, layer.down.nbytes
+    total = 2 * gb + db
+    key = map_key()
+    L = H.lib()
+    for off, t in ((0, layer.gate), (gb, layer.up), (2 * gb, layer.down)):
+        H.check(L.sf37_hip_register_device_range(key, total, off, t.nbytes, t), "register")
+    st, wt, xt = H.Tensor.from_array(sel), H.Tensor.from_array(w), H.Tensor.from_array(x)
+    res = []
+    for fused in (True, False):
+        H.set_option("decode_fused", 1 if fused else 0)
+        try:
+            out, g, u, d = H.Tensor.alloc(n_tok * K * 4), H.Tensor.alloc(TOPK * F * 4), \
+                H.Tensor.alloc(TOPK * F * 4), H.Tensor.alloc(TOPK * K * 4)
+            m = H.Tensor.alloc(n_tok * TOPK * F * 4)
+            H.check(L.sf37_hip_routed_moe_batch_mapped(out, g, u, m, d, key, total, 0, gb, 2 * gb, st,
+                                                       wt, E, TOPK, K, F, K, 0.0, xt, n_tok), "batch")
+            res.append((out.read(np.float32).reshape(n_tok, K), m.read(np.float32).reshape(n_tok * TOPK, F)))
+        finally:
+            H.set_option("decode_fused", 1)
+    assert_bitexact(res[0][0], res[1][0], "fused vs staged out")
+    assert_bitexact(res[0][1], res[1][1], "fused vs staged mid")
+    host = layer.host_experts(np.append(np.ravel(sel), 0))
+    want, want_mid = O.routed_moe_batch_q8k(host["gate"], host["up"], host["down"], sel, w, E, K, F, K, 0.0, x)
+    assert_bitexact(res[0][0], want, "batch out vs oracle")
+    assert_bitexact(res[0][1], want_mid, "batch mid vs oracle")
+
+
+def test_fused_routed_one_duplicates(H, O, layer):
+    """routed_moe_one (one group per slot) with a repeated expert and the
+    gate/up export option: all outputs equal the staged path."""
+    rng = np.random.default_rng(9)
+    sel = rng.choice(E, TOPK, replace=False).astype(np.int32)
+    sel[6] = sel[2]
+    w = (rng.random(TOPK) * 0.6).astype(np.float32)
+    x = rng.standard_normal(K).astype(np.float32)
+    st, wt, xt = H.Tensor.from_array(sel), H.Tensor.from_array(w), H.Tensor.from_array(x)
+    res = []
+    H.set_option("moe_write_gate_up", 1)
+    try:
+        for fused in (True, False):
+            H.set_option("decode_fused", 1 if fused else 0)
+            out, g, u, m, d = (H.Tensor.alloc(K * 4), H.Tensor.alloc(TOPK * F * 4), H.Tensor.alloc(TOPK * F * 4),
+                               H.Tensor.alloc(TOPK * F * 4), H.Tensor.alloc(TOPK * K * 4))
+            H.check(H.lib().sf37_hip_routed_moe_one(out, g, u, m, d, layer.gate, layer.up, layer.down, st, wt, E,
+                                                    TOPK, K, F, K, 0.0, xt), "routed_moe_one")
+            res.append([t.read(np.float32) for t in (out, g, u, m, d)])
+    finally:
+        H.set_option("moe_write_gate_up", 0)
+        H.set_option("decode_fused", 1)
+    for name, a, b in zip(("out", "gate", "up", "mid", "down"), res[0], res[1]):
+        assert_bitexact(a, b, f"routed_moe_one {name}")
+    host = layer.host_experts(sel)
+    want, want_mid, _ = O.routed_moe_one_q8k(host["gate"], host["up"], host["down"], sel, w, E, K, F, K, 0.0, x)
+    assert_bitexact(res[0][0], want, "routed_moe_one vs oracle")
+    assert_bitexact(res[0][3].reshape(TOPK, F), want_mid, "routed_moe_one mid vs oracle")
