@@ -129,16 +129,20 @@ def main():
         act = n_tok * K * 4 * 2
         step_bytes.append(distinct * EXPERT_BYTES + lay.shared_bytes() + lay.router_bytes() + act)
         sh_gu = lay.sh_gate.nbytes + lay.sh_up.nbytes
+        nb, nbf = K // 256, F // 256
         kern_bytes.append({
-            # router weights + x in, logits + Q8_K/Q8_0 of x out
-            "dec_route": lay.router_bytes() + n_tok * K * 4 + n_tok * E * 4 + n_tok * (K // 256) * Q8K_BLOCK
+            # router weights + x in; logits, x activation blocks (288 B) and Q8_0 of x out
+            "dec_route": lay.router_bytes() + n_tok * K * 4 + n_tok * E * 4 + n_tok * nb * 288
                          + n_tok * K + n_tok * (K // 32) * 4,
-            # routed + shared gate/up weights, activations in, mid (f32 + Q8_K) out
-            "dec_up": distinct * GATE_UP_EXPERT_BYTES + sh_gu + n_tok * (K // 256) * Q8K_BLOCK + n_tok * K
-                      + P * F * 4 + P * (F // 256) * Q8K_BLOCK + n_tok * F * 9,
-            # routed + shared down weights, mid in, per-pair partials + out
-            "dec_down": distinct * DOWN_EXPERT_BYTES + lay.sh_down.nbytes + P * (F // 256) * Q8K_BLOCK
-                        + n_tok * F + P * K * 4 * 2 + n_tok * K * 4 * 2,
+            # shared gate/up weights + Q8_0 x in, gate/up rows out
+            "dec_shared_up": sh_gu + n_tok * K + n_tok * (K // 32) * 4 + 2 * n_tok * F * 4,
+            # routed gate/up weights of the distinct experts + x blocks in, mid out
+            "dec_up": distinct * GATE_UP_EXPERT_BYTES + n_tok * nb * 288 + P * F * 4,
+            # mid in, activation blocks out; shared gate/up in, Q8_0 mid out
+            "dec_mid": P * F * 4 + P * nbf * 288 + 2 * n_tok * F * 4 + n_tok * F + n_tok * (F // 32) * 4,
+            # routed + shared down weights, mid blocks in, per-pair rows out and back, out
+            "dec_down": distinct * DOWN_EXPERT_BYTES + lay.sh_down.nbytes + P * nbf * 288 + n_tok * F
+                        + P * K * 4 * 2 + n_tok * K * 4 * 3,
         })
     hip.synchronize()
 
@@ -163,7 +167,7 @@ def main():
         step(i)
     prof = hip.profile_read()
     L.sf37_hip_profile_enable(0)
-    kern = max(("dec_route", "dec_up", "dec_down"), key=lambda k: prof[k][0])
+    kern = max(("dec_route", "dec_shared_up", "dec_up", "dec_mid", "dec_down"), key=lambda k: prof[k][0])
     k_ms, k_n = prof[kern]
     if k_n == 0:
         raise SystemExit("bench.py: the fused decode kernels did not run")

@@ -1,37 +1,45 @@
-// k_decode.hip - the MoE layer for decode batches (up to 16 tokens) in three
-// launches on gfx950.
+// k_decode.hip - the MoE layer for decode batches (up to 16 tokens) on
+// gfx950, in five launches on one stream:
 //
-//   route : router GEMV (binary64 accumulation) and the Q8_K / Q8_0
-//           quantisation of x; the last workgroup to finish runs top-k for
-//           every token, groups the (token, slot) pairs by expert and clears
-//           the counters of the next two launches.
-//   up    : routed gate/up (Q3 x Q8_K) with SwiGLU * routing weight, and the
-//           shared expert's gate/up (Q8_0).  The last workgroup of each
-//           256-row block quantises that block of mid to Q8_K; the last of
-//           each 32-row shared block applies SwiGLU and quantises to Q8_0.
-//   down  : routed down (Q2 x Q8_K) per pair and the shared down (Q8_0); the
-//           last workgroup of each 64-row tile forms out = shared + sum over
-//           slots in slot order.
+//   route     : router GEMV (binary64 accumulation) and the Q8_K / Q8_0
+//               quantisation of x; the last workgroup to finish runs top-k
+//               for every token, groups the (token, slot) pairs by expert
+//               and clears the down kernel's tile counters.
+//   shared_up : the shared expert's Q8_0 gate/up rows (LDS tiles).
+//   up        : routed Q3 gate/up with SwiGLU * routing weight; a lane owns
+//               one 110-byte block, a wave two rows of gate and up, and the
+//               canonical block-order chain runs as a DPP scan.
+//   mid       : Q8_K of the routed mid, SwiGLU + Q8_0 of the shared mid.
+//   down      : routed Q2 down (lane = row, activations through the scalar
+//               cache) and the shared Q8_0 down; the last wave of each
+//               64-row tile forms out = shared + sum over slots in slot order.
 //
-// Hand-offs between workgroups use agent-coherent stores and loads and an atomic
-// arrival counter; the workgroup that brings a counter to its target does
-// the dependent work and resets the counter.  Nothing waits on another
+// Hand-offs inside a launch (logits to the top-k workgroup, per-pair down
+// rows to the combining wave) use agent-coherent stores and loads and an
+// atomic arrival counter; the workgroup or wave that completes a counter
+// does the dependent work and resets it.  Nothing waits on another
 // workgroup, so every wave always runs to completion.
 //
 // Arithmetic is the canonical order of the oracle (sf37_blocks.h), the
 // reference CPU order for the Q8_0 shared expert (sf37_ops.c:92-108), and
-// slot-order combines, so results equal the separate-kernel path bit for bit.
+// slot-order combines, so results equal the staged kernels bit for bit.
 #include "sf37_blocks.h"
+#include "sf37_router.h"
 #include "sf37_launch.h"
 
 namespace {
 
 constexpr uint32_t DEC_MAX_TOK = 16;
 constexpr uint32_t DEC_TPC = 4;      // pairs per pass in the routed kernels
-constexpr uint32_t UP_RT = 8;        // routed gate/up rows per workgroup
 constexpr uint32_t SH_RS = 2;        // shared gate/up rows per workgroup
-constexpr uint32_t DN_TILE = 64;     // down rows per workgroup (= combine tile)
-constexpr uint32_t SH_SUB = 16;      // shared down rows per pass
+constexpr uint32_t DN_TILE = 64;     // down rows per item (= combine tile)
+constexpr uint32_t DN_MAX_NB = 5;    // down blocks per row held in registers (F <= 1280)
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4a4 __attribute__((ext_vector_type(4), aligned(4)));
+// Activation blocks read through the scalar cache (every lane of a wave
+// reads the same block): constant address space, so loads become s_load.
+typedef const __attribute__((address_space(4))) act_t c_act;
 
 __device__ __forceinline__ uint32_t clamp_expert(int32_t e, uint32_t n) {
     return (e < 0 || (uint32_t)e >= n) ? 0u : (uint32_t)e;
@@ -63,102 +71,26 @@ __device__ __forceinline__ bool arrive_last(uint32_t *counter, uint32_t target, 
     return *flag != 0;
 }
 
-// One token's top-k by a full wave (sf37.c:2144-2157): lane l owns experts
-// l + 64j.  Ties go to the lower index; weights = p / max(sum p, 1e-20) * scale.
-__device__ void wave_topk(const float *lg, const float *bias, uint32_t E, uint32_t topk, float scale,
-                          const uint64_t *tab, int32_t *sel_out, float *w_out) {
-    const uint32_t lane = threadIdx.x & 63u;
-    float prob[16], score[16];
-    uint32_t taken = 0;
-#pragma unroll
-    for (int j = 0; j < 16; j++) {
-        const uint32_t e = lane + 64u * j;
-        prob[j] = 0.0f;
-        score[j] = -__builtin_inff();
-        if (e < E) {
-            const float p = sf37_sigmoid_t(ld_shared(lg + e), tab);
-            prob[j] = p;
-            score[j] = p + bias[e];
-        } else {
-            taken |= 1u << j;
-        }
-    }
-    float sum = 0.0f;
-    for (uint32_t k = 0; k < topk; k++) {
-        float bs = -__builtin_inff(), bp = 0.0f;
-        uint32_t bi = 0xffffffffu;
-        int bj = -1;
-#pragma unroll
-        for (int j = 0; j < 16; j++) {
-            const uint32_t e = lane + 64u * j;
-            const bool better = score[j] > bs || (score[j] == bs && e < bi);
-            if (!((taken >> j) & 1u) && better) {
-                bs = score[j];
-                bp = prob[j];
-                bi = e;
-                bj = j;
-            }
-        }
-        float ws = bs, wp = bp;
-        uint32_t wi = bi;
-#pragma unroll
-        for (int off = 32; off > 0; off >>= 1) {
-            const float os = __shfl_xor(ws, off, 64);
-            const float op = __shfl_xor(wp, off, 64);
-            const uint32_t oi = __shfl_xor(wi, off, 64);
-            if (os > ws || (os == ws && oi < wi)) {
-                ws = os;
-                wp = op;
-                wi = oi;
-            }
-        }
-        if (wi != 0xffffffffu && bi == wi && bj >= 0) taken |= 1u << bj;
-        const float pk = wi == 0xffffffffu ? 0.0f : wp;
-        sum += pk;                                   // slot order, every lane identical
-        if (lane == 0) {
-            sel_out[k] = wi == 0xffffffffu ? -1 : (int32_t)wi;
-            w_out[k] = pk;
-        }
-    }
-    if (sum < 1.0e-20f) sum = 1.0e-20f;
-    if (lane == 0)
-        for (uint32_t k = 0; k < topk; k++) w_out[k] = w_out[k] / sum * scale;
-}
-
 }  // namespace
 
 using dec_params = sf37_dec_params;
 
 namespace {
 
-// counter layout: [0] route, then routed mid blocks G*(F/256), shared mid
-// blocks F/32, down tiles K/64
-__device__ __forceinline__ uint32_t *cnt_up(const dec_params &p) { return p.cnt + 1; }
-__device__ __forceinline__ uint32_t *cnt_sh(const dec_params &p) { return p.cnt + 1 + p.G * (p.F / SF37_QK); }
-__device__ __forceinline__ uint32_t *cnt_dn(const dec_params &p) {
-    return p.cnt + 1 + p.G * (p.F / SF37_QK) + p.F / 32u;
-}
+// counter layout: [0] route, [1..3) reserved, then K/64 down tiles
+constexpr uint32_t CNT_FIXED = 3;
+__device__ __forceinline__ uint32_t *cnt_dn(const dec_params &p) { return p.cnt + CNT_FIXED; }
 
 // LDS layout sizes, shared by the kernels and the host-side launch plan.
 // A weight tile buffer holds the tile plus the copy's leading offset.
 __host__ __device__ constexpr uint32_t tile_buf(uint32_t bytes) { return (bytes + 31u + 15u) & ~15u; }
-__host__ __device__ constexpr uint32_t up_routed_tile(uint32_t K) { return UP_RT * (K / SF37_QK) * SF37_Q3_BYTES; }
 __host__ __device__ constexpr uint32_t up_shared_tile(uint32_t K) { return SH_RS * (K / 32u) * SF37_Q8_0_BYTES; }
-__host__ __device__ constexpr uint32_t dn_routed_tile(uint32_t F) { return DN_TILE * (F / SF37_QK) * SF37_Q2_BYTES; }
-__host__ __device__ constexpr uint32_t dn_shared_tile(uint32_t F) { return SH_SUB * (F / 32u) * SF37_Q8_0_BYTES; }
-__host__ __device__ constexpr size_t lds_up_routed(uint32_t K) {
-    return 2u * (size_t)tile_buf(up_routed_tile(K)) + (size_t)DEC_TPC * (K / SF37_QK) * sizeof(act_block) +
-           (size_t)DEC_TPC * 2u * UP_RT * (K / SF37_QK) * 4u + (size_t)DEC_TPC * 2u * UP_RT * 4u;
+// up workgroup: x of every token, then group info, sorted pairs, weights
+__host__ __device__ constexpr size_t lds_up_routed(uint32_t K, uint32_t T, uint32_t G, uint32_t P) {
+    return (size_t)T * (K / SF37_QK) * sizeof(act_t) + (size_t)(3u + 2u * G + 2u * P) * 4u;
 }
 __host__ __device__ constexpr size_t lds_up_shared(uint32_t K, uint32_t T) {
     return 2u * (size_t)tile_buf(up_shared_tile(K)) + (size_t)T * 2u * SH_RS * (K / 32u) * 4u;
-}
-__host__ __device__ constexpr size_t lds_dn_routed(uint32_t F) {
-    return (size_t)tile_buf(dn_routed_tile(F)) + (size_t)DEC_TPC * (F / SF37_QK) * sizeof(act_block) +
-           (size_t)DEC_TPC * DN_TILE * (F / SF37_QK) * 4u;
-}
-__host__ __device__ constexpr size_t lds_dn_shared(uint32_t F, uint32_t T) {
-    return (size_t)tile_buf(dn_shared_tile(F)) + (size_t)T * SH_SUB * (F / 32u) * 4u;
 }
 
 // Q8_0 block (34 bytes) at LDS byte offset L of base: scale, eight i8x4 words.
@@ -179,43 +111,6 @@ __device__ __forceinline__ float q8_0_lds(const uint8_t *base, uint32_t L, uint3
 // route
 // ---------------------------------------------------------------------------
 
-// Router logits of expert e for NT tokens: thread i accumulates k = i,
-// i + 256, ... in binary64 (the order of the separate router GEMV kernel),
-// then a butterfly per wave and (w0 + w1) + (w2 + w3).  All loads of a
-// 1024-wide slice are issued before the first fma.
-template <int NT>
-__device__ void router_row(const dec_params &p, uint32_t e, uint32_t t0, double (*part)[4]) {
-    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
-    const float *wr = p.router_w + (uint64_t)e * p.K;
-    double acc[NT];
-#pragma unroll
-    for (int t = 0; t < NT; t++) acc[t] = 0.0;
-    for (uint32_t k0 = 0; k0 < p.K; k0 += 256u * 4u) {
-        float wv[4], xv[NT][4];
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const uint32_t k = k0 + 256u * j + threadIdx.x;
-            wv[j] = k < p.K ? wr[k] : 0.0f;
-#pragma unroll
-            for (int t = 0; t < NT; t++) xv[t][j] = k < p.K ? p.x[(uint64_t)(t0 + t) * p.K + k] : 0.0f;
-        }
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            if (k0 + 256u * j + threadIdx.x < p.K) {
-#pragma unroll
-                for (int t = 0; t < NT; t++) acc[t] = __builtin_fma((double)wv[j], (double)xv[t][j], acc[t]);
-            }
-        }
-    }
-#pragma unroll
-    for (int t = 0; t < NT; t++) {
-        double v = acc[t];
-#pragma unroll
-        for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-        if (lane == 0) part[t0 + t][wave] = v;
-    }
-}
-
 __global__ void __launch_bounds__(256) dec_route_kernel(dec_params p, uint32_t n_router) {
     __shared__ double part[DEC_MAX_TOK][4];
     __shared__ uint64_t tab[32];
@@ -228,22 +123,11 @@ __global__ void __launch_bounds__(256) dec_route_kernel(dec_params p, uint32_t n
     const uint32_t nb = p.K / SF37_QK;
     if (blockIdx.x < n_router) {
         const uint32_t e = blockIdx.x;
-        // tokens in passes of at most 8 (register budget); the weight row
-        // is re-read from cache by the second pass
-        for (uint32_t t0 = 0; t0 < p.T; t0 += 8u) {
-            switch (p.T - t0 < 8u ? p.T - t0 : 8u) {
-#define SF37_ROUTER_CASE(n) \
-    case n: router_row<n>(p, e, t0, part); break;
-                SF37_ROUTER_CASE(1) SF37_ROUTER_CASE(2) SF37_ROUTER_CASE(3) SF37_ROUTER_CASE(4)
-                SF37_ROUTER_CASE(5) SF37_ROUTER_CASE(6) SF37_ROUTER_CASE(7) SF37_ROUTER_CASE(8)
-#undef SF37_ROUTER_CASE
-                default: break;
-            }
-        }
+        sf37_router_rows(p.router_w + (uint64_t)e * p.K, p.x, p.K, p.T, part);
         __syncthreads();
         if (threadIdx.x < p.T) {
             const uint32_t t = threadIdx.x;
-            st_shared(p.logits + (uint64_t)t * p.E + e, (float)((part[t][0] + part[t][1]) + (part[t][2] + part[t][3])));
+            st_shared(p.logits + (uint64_t)t * p.E + e, sf37_router_combine(part[t]));
         }
     } else {
         // Q8_K (and Q8_0) of one 256-block of one token per wave
@@ -257,11 +141,12 @@ __global__ void __launch_bounds__(256) dec_route_kernel(dec_params p, uint32_t n
             int8_t qk[4];
             int gsum;
             const float d = q8k_codes4(v, qk, gsum);
-            q8k_block *y = (q8k_block *)p.xq + wq;
-            ((uint32_t *)y->qs)[lane] = (uint32_t)(uint8_t)qk[0] | ((uint32_t)(uint8_t)qk[1] << 8) |
-                                        ((uint32_t)(uint8_t)qk[2] << 16) | ((uint32_t)(uint8_t)qk[3] << 24);
+            act_t *y = (act_t *)p.xq + wq;
+            uint8_t *qb = (uint8_t *)y->qs;
+#pragma unroll
+            for (int k = 0; k < 4; k++) qb[q3x_pos(4u * lane + k)] = (uint8_t)qk[k];
             if (lane == 0) y->d = d;
-            if ((lane & 15u) == 0) y->gsums[lane >> 4] = (int16_t)gsum;
+            if ((lane & 15u) == 0) y->gs[lane >> 4] = gsum;
             if (p.flags & SF37_DEC_SHARED) {
                 // Q8_0 (sf37_ops.c:57-90): a 32-wide block is 8 lanes
                 float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
@@ -287,14 +172,21 @@ __global__ void __launch_bounds__(256) dec_route_kernel(dec_params p, uint32_t n
     if (!arrive_last(p.cnt, gridDim.x, &flag)) return;
 
     // ---- last workgroup: clear the next counters, top-k, groups ----------
-    const uint32_t n_clear = p.G * (p.F / SF37_QK) + p.F / 32u + p.K / DN_TILE;
+    const uint32_t n_clear = CNT_FIXED - 1u + p.K / DN_TILE;
     for (uint32_t i = threadIdx.x; i < n_clear; i += blockDim.x) p.cnt[1 + i] = 0u;
     sf37_stage_exp_tab(tab);
     __syncthreads();
     if (p.flags & SF37_DEC_SELECT) {
-        for (uint32_t t = wave; t < p.T; t += 4u)
-            wave_topk(p.logits_sel + (uint64_t)t * p.E, p.router_bias, p.E, p.topk, p.scale, tab,
-                      p.sel + (uint64_t)t * p.topk, p.wts + (uint64_t)t * p.topk);
+        // wave w: tokens w, w + 4, ... two at a time
+        for (uint32_t t = wave; t < p.T; t += 8u) {
+            const uint32_t t2 = t + 4u < p.T ? t + 4u : t;
+            const float *lg0 = p.logits_sel + (uint64_t)t * p.E, *lg1 = p.logits_sel + (uint64_t)t2 * p.E;
+            int32_t *so[2] = {p.sel + (uint64_t)t * p.topk, p.sel + (uint64_t)t2 * p.topk};
+            float *wo[2] = {p.wts + (uint64_t)t * p.topk, p.wts + (uint64_t)t2 * p.topk};
+            float *po[2] = {nullptr, nullptr};
+            sf37_wave_topk<2>([lg0, lg1](uint32_t k, uint32_t e) { return ld_shared((k ? lg1 : lg0) + e); },
+                              p.router_bias, p.E, p.topk, p.scale, tab, so, wo, po);
+        }
     }
     __syncthreads();
     const uint32_t P = p.T * p.topk;
@@ -318,6 +210,7 @@ __global__ void __launch_bounds__(256) dec_route_kernel(dec_params p, uint32_t n
         if (threadIdx.x < P) {
             const uint32_t i = threadIdx.x, e = s_e[i];
             uint32_t less = 0, eq_before = 0;
+#pragma unroll 8
             for (uint32_t q = 0; q < P; q++) {
                 const uint32_t f = s_e[q];
                 less += f < e ? 1u : 0u;
@@ -331,6 +224,7 @@ __global__ void __launch_bounds__(256) dec_route_kernel(dec_params p, uint32_t n
         if (threadIdx.x < P && s_first[threadIdx.x]) {
             const uint32_t i = threadIdx.x, e = s_e[i];
             uint32_t gi = 0;
+#pragma unroll 8
             for (uint32_t q = 0; q < P; q++) gi += (s_first[q] && s_e[q] < e) ? 1u : 0u;
             p.ginfo[1u + gi] = s_less[i];
             p.ginfo[2u + p.G + gi] = e;
@@ -346,118 +240,13 @@ __global__ void __launch_bounds__(256) dec_route_kernel(dec_params p, uint32_t n
 }
 
 // ---------------------------------------------------------------------------
-// up
+// shared gate/up: one workgroup per SH_RS rows, terms in LDS, then the
+// reference's sequential block sum per (matrix, token, row)
 // ---------------------------------------------------------------------------
-__device__ void up_routed(const dec_params &p, uint32_t wg, unsigned char *smem, const uint64_t *tab,
-                          int *flag) {
-    const uint32_t nblk = p.K / SF37_QK;
-    const uint32_t tiles = p.F / UP_RT;
-    const uint32_t g = wg / tiles, tile = wg - g * tiles;
-    const uint32_t ng = p.ginfo[0];
-    if (g >= ng) return;
-    const uint32_t p0 = p.ginfo[1 + g], p1 = p.ginfo[2 + g];
-    const uint32_t e = p.ginfo[2 + p.G + g];
-    const uint32_t row0 = tile * UP_RT;
-    const uint32_t tbytes = up_routed_tile(p.K), wbuf = tile_buf(tbytes);
-    uint8_t *wl = smem;                                             // gate tile | up tile
-    act_block *xs = (act_block *)(smem + 2u * wbuf);                // [TPC][nblk]
-    float *red = (float *)(xs + DEC_TPC * nblk);                    // [TPC][2R][nblk]
-    float *res = red + DEC_TPC * 2u * UP_RT * nblk;                 // [TPC][2R]
-    const uint64_t row_bytes = (uint64_t)nblk * SF37_Q3_BYTES;
-    const uint64_t src = (uint64_t)e * p.F * row_bytes + (uint64_t)row0 * row_bytes;
-    const uint32_t og = lds_copy(wl, p.gate_w + src, tbytes);
-    const uint32_t ou = wbuf + lds_copy(wl + wbuf, p.up_w + src, tbytes);
-    const uint32_t units = 2u * UP_RT * nblk;
-    for (uint32_t c0 = p0; c0 < p1; c0 += DEC_TPC) {
-        const uint32_t nt = p1 - c0 < DEC_TPC ? p1 - c0 : DEC_TPC;
-        for (uint32_t t = 0; t < nt; t++)
-            stage_act<true>(xs + t * nblk, (const q8k_block *)p.xq + (uint64_t)(p.sorted[c0 + t] / p.topk) * nblk, nblk);
-        lds_copy_wait();
-        for (uint32_t u = threadIdx.x; u < units; u += blockDim.x) {
-            const uint32_t m = u / (UP_RT * nblk);
-            const uint32_t rb = u - m * UP_RT * nblk;
-            const uint32_t r = rb / nblk, b = rb - r * nblk;
-            float bs[DEC_TPC] = {0.0f, 0.0f, 0.0f, 0.0f};
-            const uint32_t L = (m ? ou : og) + (r * nblk + b) * SF37_Q3_BYTES;
-            const uint32_t *wp = (const uint32_t *)(wl + (L & ~3u));
-            uint32_t raw[28], a[27];
-#pragma unroll
-            for (int k = 0; k < 28; k++) raw[k] = wp[k];
-            q3_realign(a, raw, L & 3u);
-#pragma unroll
-            for (int gg = 0; gg < 4; gg++) {
-                const uint32_t d0 = a[3 + 6 * gg], d1 = a[4 + 6 * gg], d2 = a[5 + 6 * gg];
-                const uint32_t d3 = a[6 + 6 * gg], d4 = a[7 + 6 * gg], d5 = a[8 + 6 * gg];
-                const uint32_t c[8] = {d0, align_bits(d1, d0, 24), align_bits(d2, d1, 16), d2 >> 8,
-                                       d3, align_bits(d4, d3, 24), align_bits(d5, d4, 16), d5 >> 8};
-                uint32_t lo[8], hi[8];
-#pragma unroll
-                for (int k = 0; k < 8; k++) q3_unpack8(c[k], lo[k], hi[k]);
-                const int32_t zp = (int32_t)((a[2] >> (8 * gg)) & 7u);
-                const float sc = sf37_f16(a[gg >> 1] >> (16 * (gg & 1)));
-#pragma unroll
-                for (uint32_t t = 0; t < DEC_TPC; t++) {
-                    if (t < nt) {
-                        const act_block &x = xs[t * nblk + b];
-                        int32_t acc = 0;
-#pragma unroll
-                        for (int k = 0; k < 8; k++) {
-                            acc = sdot4(lo[k], x.qs[16 * gg + 2 * k], acc);
-                            acc = sdot4(hi[k], x.qs[16 * gg + 2 * k + 1], acc);
-                        }
-                        bs[t] = __builtin_fmaf(sc, (float)(acc - zp * x.gs[gg]), bs[t]);
-                    }
-                }
-            }
-            for (uint32_t t = 0; t < nt; t++) red[(t * 2u * UP_RT + m * UP_RT + r) * nblk + b] = bs[t];
-        }
-        __syncthreads();
-        for (uint32_t i = threadIdx.x; i < nt * 2u * UP_RT; i += blockDim.x) {
-            const uint32_t t = i / (2u * UP_RT), mr = i - t * 2u * UP_RT;
-            const float *rv = red + (t * 2u * UP_RT + mr) * nblk;
-            float acc = 0.0f;
-            for (uint32_t b = 0; b < nblk; b++) acc = __builtin_fmaf(xs[t * nblk + b].d, rv[b], acc);
-            res[t * 2u * UP_RT + mr] = acc;
-        }
-        __syncthreads();
-        for (uint32_t i = threadIdx.x; i < nt * UP_RT; i += blockDim.x) {
-            const uint32_t t = i / UP_RT, r = i - t * UP_RT;
-            const uint32_t pr = p.sorted[c0 + t];
-            const float gv = res[t * 2u * UP_RT + r], uv = res[t * 2u * UP_RT + UP_RT + r];
-            const uint64_t o = (uint64_t)pr * p.F + row0 + r;
-            if (p.gate_out) {
-                p.gate_out[o] = gv;
-                p.up_out[o] = uv;
-            }
-            st_shared(p.mid + o, sf37_swiglu_mid_t(gv, uv, p.wts[pr], p.clamp_routed, tab));
-        }
-        __syncthreads();
-    }
-    // last of the 256/UP_RT tiles of this 256-row block quantises it for every pair
-    const uint32_t nbm = p.F / SF37_QK, blk = row0 / SF37_QK;
-    if (!arrive_last(cnt_up(p) + g * nbm + blk, SF37_QK / UP_RT, flag)) return;
-    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
-    for (uint32_t i = p0 + wave; i < p1; i += blockDim.x >> 6) {
-        const uint32_t pr = p.sorted[i];
-        const float *mv = p.mid + (uint64_t)pr * p.F + (uint64_t)blk * SF37_QK + 4u * lane;
-        float v[4];
-#pragma unroll
-        for (int k = 0; k < 4; k++) v[k] = ld_shared(mv + k);
-        int8_t qk[4];
-        int gsum;
-        const float d = q8k_codes4(v, qk, gsum);
-        q8k_block *y = (q8k_block *)p.midq + (uint64_t)pr * nbm + blk;
-        ((uint32_t *)y->qs)[lane] = (uint32_t)(uint8_t)qk[0] | ((uint32_t)(uint8_t)qk[1] << 8) |
-                                    ((uint32_t)(uint8_t)qk[2] << 16) | ((uint32_t)(uint8_t)qk[3] << 24);
-        if (lane == 0) y->d = d;
-        if ((lane & 15u) == 0) y->gsums[lane >> 4] = (int16_t)gsum;
-    }
-    if (threadIdx.x == 0) cnt_up(p)[g * nbm + blk] = 0u;
-}
-
-__device__ void up_shared(const dec_params &p, uint32_t ws, unsigned char *smem, const uint64_t *tab, int *flag) {
+__global__ void __launch_bounds__(256) dec_shup_kernel(dec_params p) {
+    extern __shared__ __align__(16) unsigned char smem[];
     const uint32_t nb8 = p.K / 32u;
-    const uint32_t row0 = ws * SH_RS;
+    const uint32_t row0 = blockIdx.x * SH_RS;
     const uint32_t tbytes = up_shared_tile(p.K), wbuf = tile_buf(tbytes);
     const uint64_t row_bytes = (uint64_t)nb8 * SF37_Q8_0_BYTES;
     uint8_t *wl = smem;                                             // gate tile | up tile
@@ -487,50 +276,235 @@ __device__ void up_shared(const dec_params &p, uint32_t ws, unsigned char *smem,
         const float *rv = red + (uint64_t)i * nb8;
         float acc = 0.0f;
         for (uint32_t b = 0; b < nb8; b++) acc = acc + rv[b];
-        st_shared(p.sh_gu + ((uint64_t)m * p.T + t) * p.F + row0 + r, acc);
+        p.sh_gu[((uint64_t)m * p.T + t) * p.F + row0 + r] = acc;
     }
-    // last of the 32/RS workgroups of a 32-row block: SwiGLU and Q8_0 of mid
-    const uint32_t blk = row0 / 32u;
-    if (!arrive_last(cnt_sh(p) + blk, 32u / SH_RS, flag)) return;
-    const uint32_t hw = threadIdx.x >> 5, l = threadIdx.x & 31u;
-    for (uint32_t t = hw; t < p.T; t += blockDim.x >> 5) {
-        const uint64_t o = (uint64_t)t * p.F + (uint64_t)blk * 32u + l;
-        const float v = sf37_swiglu_mid_t(ld_shared(p.sh_gu + o), ld_shared(p.sh_gu + (uint64_t)p.T * p.F + o), 1.0f,
-                                          p.clamp_shared, tab);
-        float amax = fabsf(v);
-#pragma unroll
-        for (int off = 16; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 32));
-        int8_t qv = 0;
-        float d = 0.0f;
-        if (amax != 0.0f) {
-            d = amax / 127.0f;
-            const float is = 1.0f / d;
-            qv = (int8_t)(int)fminf(fmaxf(__builtin_rintf(is * v), -128.0f), 127.0f);
-        }
-        p.sh_mq[o] = qv;
-        if (l == 0) p.sh_ms[(uint64_t)t * (p.F / 32u) + blk] = d;
-    }
-    if (threadIdx.x == 0) cnt_sh(p)[blk] = 0u;
 }
 
-__global__ void __launch_bounds__(256) dec_up_kernel(dec_params p, uint32_t n_routed) {
+// ---------------------------------------------------------------------------
+// routed gate/up
+// ---------------------------------------------------------------------------
+
+// 28 dwords of a Q3 block from the dword boundary at or below p, as seven
+// 16-byte loads (dword alignment suffices on gfx950).
+__device__ __forceinline__ void load_q3(uint32_t w[28], const uint8_t *p) {
+    const u32x4a4 *q = (const u32x4a4 *)(p - ((uintptr_t)p & 3u));
+#pragma unroll
+    for (int i = 0; i < 7; i++) {
+        const u32x4a4 v = q[i];
+        w[4 * i] = v.x;
+        w[4 * i + 1] = v.y;
+        w[4 * i + 2] = v.z;
+        w[4 * i + 3] = v.w;
+    }
+}
+
+// Block value blk = sum_g fma(s_g, I_g) of one realigned Q3 block (a[0..26])
+// against NT activations (act_t in LDS, Q3 layout), in group order.
+template <int NT>
+__device__ __forceinline__ void q3_block_dots(const uint32_t *a, const act_t *const *x, float bs[4]) {
+#pragma unroll
+    for (int t = 0; t < NT; t++) bs[t] = 0.0f;
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+        uint32_t c0[8], c1[8];
+        q3_unpack32(a, 12 + 24 * g, c0);
+        q3_unpack32(a, 24 + 24 * g, c1);
+        const int32_t zp = (int32_t)((a[2] >> (8 * g)) & 7u);
+        const float sc = sf37_f16(a[g >> 1] >> (16 * (g & 1)));
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+            const u32x4 *xq = (const u32x4 *)&x[t]->qs[16 * g];
+            int32_t acc = 0;
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const u32x4 v0 = xq[2 * h], v1 = xq[2 * h + 1];
+                const uint32_t *c = h ? c1 : c0;
+                acc = sdot4(c[0], v0.x, acc);
+                acc = sdot4(c[1], v0.y, acc);
+                acc = sdot4(c[2], v0.z, acc);
+                acc = sdot4(c[3], v0.w, acc);
+                acc = sdot4(c[4], v1.x, acc);
+                acc = sdot4(c[5], v1.y, acc);
+                acc = sdot4(c[6], v1.z, acc);
+                acc = sdot4(c[7], v1.w, acc);
+            }
+            bs[t] = __builtin_fmaf(sc, (float)(acc - __mul24(zp, x[t]->gs[g])), bs[t]);
+        }
+    }
+}
+
+// acc = fma(d_b, bs_b, acc) over the blocks b = 0..nb-1 held by lanes 0..nb-1
+// of each 16-lane row: a scan with row_shr:1, exact canonical order.  The
+// row's total ends in lane nb-1.
+__device__ __forceinline__ float block_chain(float d, float bs, uint32_t nb) {
+    float acc = __builtin_fmaf(d, bs, 0.0f);
+    for (uint32_t st = 1; st < nb; st++) {
+        const float prev =
+            __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, acc), 0x111, 0xf, 0xf, true));
+        acc = __builtin_fmaf(d, bs, prev);
+    }
+    return acc;
+}
+
+// Keeps the compiler from hoisting work on w out of a loop (an empty asm
+// that may change the registers), so unpacked codes are not all kept live.
+template <int N>
+__device__ __forceinline__ void opaque(uint32_t *w) {
+#pragma unroll
+    for (int i = 0; i < N; i++) asm volatile("" : "+v"(w[i]));
+}
+
+// An item is 2 rows of one group's expert for both matrices: lane = matrix
+// (gate/up) | row | block, so each wave reads two contiguous 2-row spans.
+// Waves stride over the items (adjacent waves, adjacent rows) and load the
+// next item's blocks while computing the current one.  The x of every token
+// sits in LDS; the gate lane of each row applies SwiGLU * routing weight.
+__global__ void __launch_bounds__(256) dec_up_kernel(dec_params p) {
     extern __shared__ __align__(16) unsigned char smem[];
     __shared__ uint64_t tab[32];
-    __shared__ int flag;
+    const uint32_t nbK = p.K / SF37_QK, P = p.T * p.topk;
+    act_t *xs = (act_t *)smem;
+    uint32_t *gi = (uint32_t *)(xs + p.T * nbK);
+    uint32_t *so = gi + 3u + 2u * p.G;
+    float *wt = (float *)(so + P);
+    sf37_stage_exp_tab(tab);
+    const uint32_t n_x = p.T * nbK * (uint32_t)(sizeof(act_t) / 16u);
+    for (uint32_t i = threadIdx.x; i < n_x; i += blockDim.x) ((u32x4 *)xs)[i] = ((const u32x4 *)p.xq)[i];
+    for (uint32_t i = threadIdx.x; i < 3u + 2u * p.G; i += blockDim.x) gi[i] = p.ginfo[i];
+    for (uint32_t i = threadIdx.x; i < P; i += blockDim.x) {
+        so[i] = p.sorted[i];
+        wt[i] = p.wts[i];
+    }
+    __syncthreads();
+
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t m = lane >> 5, rr = (lane >> 4) & 1u, b = lane & 15u;
+    const uint32_t bl = b < nbK ? b : nbK - 1u;                    // lanes past the row repeat its last block
+    const bool out_lane = m == 0u && b == nbK - 1u;
+    const uint32_t ipg = p.F / 2u, n_items = gi[0] * ipg;
+    const uint32_t nw = gridDim.x * (blockDim.x >> 6);
+    const uint64_t row_bytes = (uint64_t)nbK * SF37_Q3_BYTES, exp_bytes = (uint64_t)p.F * row_bytes;
+    const uint8_t *W = m ? p.up_w : p.gate_w;
+    auto block_ptr = [&](uint32_t item) -> const uint8_t * {
+        const uint32_t g = item / ipg, rp = item - g * ipg;
+        return W + (uint64_t)gi[2u + p.G + g] * exp_bytes + (uint64_t)(2u * rp + rr) * row_bytes +
+               (uint64_t)bl * SF37_Q3_BYTES;
+    };
+    uint32_t item = blockIdx.x * (blockDim.x >> 6) + wave;
+    if (item >= n_items) return;
+    uint32_t nxt[28];
+    load_q3(nxt, block_ptr(item));
+    for (; item < n_items; item += nw) {
+        uint32_t raw[28], a[27];
+#pragma unroll
+        for (int k = 0; k < 28; k++) raw[k] = nxt[k];
+        const uint8_t *cur = block_ptr(item);
+        if (item + nw < n_items) load_q3(nxt, block_ptr(item + nw));
+        q3_realign(a, raw, (uint32_t)((uintptr_t)cur & 3u));
+        const uint32_t g = item / ipg, row = 2u * (item - g * ipg) + rr;
+        const uint32_t p0 = gi[1u + g], p1 = gi[2u + g];
+        for (uint32_t c0 = p0; c0 < p1; c0 += DEC_TPC) {
+            const uint32_t nt = p1 - c0 < DEC_TPC ? p1 - c0 : DEC_TPC;
+            opaque<27>(a);
+            const act_t *x[DEC_TPC];
+#pragma unroll
+            for (uint32_t t = 0; t < DEC_TPC; t++) x[t] = xs + (so[c0 + (t < nt ? t : 0u)] / p.topk) * nbK + bl;
+            float bs[DEC_TPC];
+            switch (nt) {
+                case 1: q3_block_dots<1>(a, x, bs); break;
+                case 2: q3_block_dots<2>(a, x, bs); break;
+                case 3: q3_block_dots<3>(a, x, bs); break;
+                default: q3_block_dots<4>(a, x, bs); break;
+            }
+#pragma unroll
+            for (uint32_t t = 0; t < DEC_TPC; t++) {
+                if (t < nt) {
+                    const float acc = block_chain(x[t]->d, bs[t], nbK);
+                    const float up = __shfl_xor(acc, 32, 64);
+                    if (out_lane) {
+                        const uint32_t pr = so[c0 + t];
+                        const uint64_t o = (uint64_t)pr * p.F + row;
+                        if (p.gate_out) {
+                            p.gate_out[o] = acc;
+                            p.up_out[o] = up;
+                        }
+                        p.mid[o] = sf37_swiglu_mid_t(acc, up, wt[pr], p.clamp_routed, tab);
+                    }
+                }
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// mid: Q8_K of the routed mid (one wave per pair and 256-row block, Q2 act
+// layout) and, for the shared expert, SwiGLU + Q8_0 (one half-wave per token
+// and 32-row block)
+// ---------------------------------------------------------------------------
+__global__ void __launch_bounds__(256) dec_mid_kernel(dec_params p) {
+    __shared__ uint64_t tab[32];
     sf37_stage_exp_tab(tab);
     __syncthreads();
-    if (blockIdx.x < n_routed) up_routed(p, blockIdx.x, smem, tab, &flag);
-    else up_shared(p, blockIdx.x - n_routed, smem, tab, &flag);
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t w = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    const uint32_t nbm = p.F / SF37_QK, n_routed = p.T * p.topk * nbm;
+    if (w < n_routed) {
+        const uint32_t pr = w / nbm, blk = w - pr * nbm;
+        const float *mv = p.mid + (uint64_t)pr * p.F + (uint64_t)blk * SF37_QK + 4u * lane;
+        float v[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) v[k] = mv[k];
+        int8_t qk[4];
+        int gsum;
+        const float d = q8k_codes4(v, qk, gsum);
+        act_t *y = (act_t *)p.midq + w;
+        uint8_t *qb = (uint8_t *)y->qs;
+#pragma unroll
+        for (int k = 0; k < 4; k++) qb[q2_perm_pos(4u * lane + k)] = (uint8_t)qk[k];
+        if (lane == 0) y->d = d;
+        if ((lane & 15u) == 0) y->gs[lane >> 4] = gsum;
+        return;
+    }
+    if (!(p.flags & SF37_DEC_SHARED)) return;
+    const uint32_t nb8 = p.F / 32u;
+    const uint32_t hw = 2u * (w - n_routed) + (lane >> 5), l = lane & 31u;
+    if (hw >= p.T * nb8) return;
+    const uint32_t t = hw / nb8, blk = hw - t * nb8;
+    const uint64_t o = (uint64_t)t * p.F + (uint64_t)blk * 32u + l;
+    const float v = sf37_swiglu_mid_t(p.sh_gu[o], p.sh_gu[(uint64_t)p.T * p.F + o], 1.0f, p.clamp_shared, tab);
+    float amax = fabsf(v);
+#pragma unroll
+    for (int off = 16; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 32));
+    int8_t qv = 0;
+    float d = 0.0f;
+    if (amax != 0.0f) {
+        d = amax / 127.0f;
+        const float is = 1.0f / d;
+        qv = (int8_t)(int)fminf(fmaxf(__builtin_rintf(is * v), -128.0f), 127.0f);
+    }
+    p.sh_mq[o] = qv;
+    if (l == 0) p.sh_ms[(uint64_t)t * nb8 + blk] = d;
 }
 
 // ---------------------------------------------------------------------------
 // down + combine
 // ---------------------------------------------------------------------------
-__device__ void down_combine(const dec_params &p, uint32_t tile) {
-    const uint32_t row0 = tile * DN_TILE;
-    const uint32_t n = p.T * DN_TILE;
-    for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) {
-        const uint32_t t = i / DN_TILE, r = row0 + (i - t * DN_TILE);
+
+// Wave-level arrival: the wave's stores are acknowledged, then lane 0 adds n
+// to the counter.  True in every lane of the wave that completed target.
+__device__ __forceinline__ bool wave_arrive(uint32_t *counter, uint32_t n, uint32_t target) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    uint32_t old = 0;
+    if ((threadIdx.x & 63u) == 0) old = atomicAdd(counter, n);
+    old = __shfl(old, 0, 64);
+    return old + n == target;
+}
+
+// out = [shared +] sum over slots, for the 64 rows of one tile; lane = row.
+__device__ void tile_combine(const dec_params &p, uint32_t tile) {
+    const uint32_t r = tile * DN_TILE + (threadIdx.x & 63u);
+    for (uint32_t t = 0; t < p.T; t++) {
         float acc = 0.0f;
         for (uint32_t s = 0; s < p.topk; s++) acc = acc + ld_shared(p.down_pair + ((uint64_t)t * p.topk + s) * p.K + r);
         const uint64_t o = (uint64_t)t * p.K + r;
@@ -538,115 +512,169 @@ __device__ void down_combine(const dec_params &p, uint32_t tile) {
     }
 }
 
-__device__ void down_routed(const dec_params &p, uint32_t wg, unsigned char *smem) {
-    const uint32_t nblk = p.F / SF37_QK;
-    const uint32_t tiles = p.K / DN_TILE;
-    const uint32_t g = wg / tiles, tile = wg - g * tiles;
-    const uint32_t p0 = p.ginfo[1 + g], p1 = p.ginfo[2 + g];
-    const uint32_t e = p.ginfo[2 + p.G + g];
-    const uint32_t tbytes = dn_routed_tile(p.F), wbuf = tile_buf(tbytes);
-    uint8_t *wl = smem;
-    act_block *xs = (act_block *)(smem + wbuf);                     // [TPC][nblk]
-    float *red = (float *)(xs + DEC_TPC * nblk);                    // [TPC][TILE][nblk]
-    const uint32_t row0 = tile * DN_TILE;
-    const uint64_t row_bytes = (uint64_t)nblk * SF37_Q2_BYTES;
-    const uint32_t od = lds_copy(wl, p.down_w + (uint64_t)e * p.K * row_bytes + (uint64_t)row0 * row_bytes, tbytes);
-    const uint32_t units = DN_TILE * nblk;
+// Block values of one Q2 block (21 dwords in a) against NT activation blocks
+// read through the scalar cache: bs[t] = sum_g fma(s_g, I_g).
+template <int NT>
+__device__ __forceinline__ void q2_block_dots(const uint32_t *a, c_act *const *x, float bs[4]) {
+#pragma unroll
+    for (int t = 0; t < NT; t++) bs[t] = 0.0f;
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+        uint32_t c[16];
+#pragma unroll
+        for (int j = 0; j < 4; j++) q2_unpack16(a[3 + 4 * g + j], c[4 * j], c[4 * j + 1], c[4 * j + 2], c[4 * j + 3]);
+        const int32_t zp = (int32_t)((a[2] >> (8 * g)) & 3u);
+        const float sc = sf37_f16(a[g >> 1] >> (16 * (g & 1)));
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+            int32_t acc = 0;
+#pragma unroll
+            for (int k = 0; k < 16; k++) acc = sdot4(c[k], x[t]->qs[16 * g + k], acc);
+            bs[t] = __builtin_fmaf(sc, (float)(acc - __mul24(zp, x[t]->gs[g])), bs[t]);
+        }
+    }
+}
+
+// NT pairs sorted[c0 ..] against a row's NB blocks in w: canonical block
+// order acc = fma(d_b, blk_b, acc), result to down_pair.
+template <int NB, int NT>
+__device__ __forceinline__ void down_pass(const dec_params &p, const uint32_t *w, uint32_t c0, uint32_t row) {
+    uint32_t pr[NT];
+#pragma unroll
+    for (int t = 0; t < NT; t++) pr[t] = __builtin_amdgcn_readfirstlane(p.sorted[c0 + t]);
+    float acc[DEC_TPC] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int b = 0; b < NB; b++) {
+        c_act *x[DEC_TPC];
+#pragma unroll
+        for (int t = 0; t < NT; t++) x[t] = (c_act *)((const act_t *)p.midq + (uint64_t)pr[t] * NB + b);
+        float bs[DEC_TPC];
+        q2_block_dots<NT>(w + 21 * b, x, bs);
+#pragma unroll
+        for (int t = 0; t < NT; t++) acc[t] = __builtin_fmaf(x[t]->d, bs[t], acc[t]);
+    }
+#pragma unroll
+    for (int t = 0; t < NT; t++) st_shared(p.down_pair + (uint64_t)pr[t] * p.K + row, acc[t]);
+}
+
+// Routed down of one (group, 64-row tile): lane = row, the row's NB blocks
+// loaded at once (a wave reads one contiguous 64-row span), pairs of the
+// group in passes of up to four.
+template <int NB>
+__device__ void down_item(const dec_params &p, uint32_t g, uint32_t tile) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t p0 = p.ginfo[1u + g], p1 = p.ginfo[2u + g], e = p.ginfo[2u + p.G + g];
+    const uint32_t row = tile * DN_TILE + lane;
+    const uint64_t row_bytes = (uint64_t)NB * SF37_Q2_BYTES;
+    const uint32_t *src = (const uint32_t *)(p.down_w + ((uint64_t)e * p.K + row) * row_bytes);
+    constexpr int N = NB * 21, N4 = N / 4;
+    uint32_t w[N];
+    const u32x4a4 *s4 = (const u32x4a4 *)src;
+#pragma unroll
+    for (int i = 0; i < N4; i++) {
+        const u32x4a4 v = s4[i];
+        w[4 * i] = v.x;
+        w[4 * i + 1] = v.y;
+        w[4 * i + 2] = v.z;
+        w[4 * i + 3] = v.w;
+    }
+#pragma unroll
+    for (int i = 4 * N4; i < N; i++) w[i] = src[i];
     for (uint32_t c0 = p0; c0 < p1; c0 += DEC_TPC) {
         const uint32_t nt = p1 - c0 < DEC_TPC ? p1 - c0 : DEC_TPC;
-        for (uint32_t t = 0; t < nt; t++)
-            stage_act<false>(xs + t * nblk, (const q8k_block *)p.midq + (uint64_t)p.sorted[c0 + t] * nblk, nblk);
-        lds_copy_wait();
-        for (uint32_t u = threadIdx.x; u < units; u += blockDim.x) {
-            const uint32_t r = u / nblk, b = u - r * nblk;
-            float bs[DEC_TPC] = {0.0f, 0.0f, 0.0f, 0.0f};
-            uint32_t a[21];
-            const uint32_t *wp = (const uint32_t *)(wl + ((od + (r * nblk + b) * SF37_Q2_BYTES) & ~3u));
+        opaque<N>(w);
+        switch (nt) {
+            case 1: down_pass<NB, 1>(p, w, c0, row); break;
+            case 2: down_pass<NB, 2>(p, w, c0, row); break;
+            case 3: down_pass<NB, 3>(p, w, c0, row); break;
+            default: down_pass<NB, 4>(p, w, c0, row); break;
+        }
+    }
+}
+
+// Shared down rows for every token: lane = (row, token), the reference's
+// block order acc = acc + (isum * ws) * xs, with the loads of 8 blocks
+// issued before their terms are added.
+__device__ void down_shared_item(const dec_params &p, uint32_t r0, uint32_t nrows) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t t = lane % p.T, rl = lane / p.T;
+    const uint32_t row = r0 + (rl < nrows ? rl : 0u), nb8 = p.F / 32u;
+    const uint8_t *wr = p.sh_down + (uint64_t)row * nb8 * SF37_Q8_0_BYTES;
+    const int8_t *xq = p.sh_mq + (uint64_t)t * p.F;
+    const float *xs = p.sh_ms + (uint64_t)t * nb8;
+    float acc = 0.0f;
+    for (uint32_t b0 = 0; b0 < nb8; b0 += 8u) {
+        uint32_t raw[8][10], xv[8][8];
+        float xsc[8];
 #pragma unroll
-            for (int k = 0; k < 21; k++) a[k] = wp[k];
+        for (int j = 0; j < 8; j++) {
+            const uint32_t b = b0 + j < nb8 ? b0 + j : nb8 - 1u;
+            const uint8_t *blk = wr + (uint64_t)b * SF37_Q8_0_BYTES;
+            const uint32_t *wp = (const uint32_t *)(blk - ((uintptr_t)blk & 3u));
 #pragma unroll
-            for (int gg = 0; gg < 4; gg++) {
-                uint32_t cw[16];
+            for (int k = 0; k < 10; k++) raw[j][k] = wp[k];
+            const u32x4 *xp = (const u32x4 *)(xq + (uint64_t)b * 32u);
+            const u32x4 x0 = xp[0], x1 = xp[1];
+            xv[j][0] = x0.x; xv[j][1] = x0.y; xv[j][2] = x0.z; xv[j][3] = x0.w;
+            xv[j][4] = x1.x; xv[j][5] = x1.y; xv[j][6] = x1.z; xv[j][7] = x1.w;
+            xsc[j] = xs[b];
+        }
 #pragma unroll
-                for (int j = 0; j < 4; j++)
-                    q2_unpack16(a[3 + 4 * gg + j], cw[4 * j], cw[4 * j + 1], cw[4 * j + 2], cw[4 * j + 3]);
-                const int32_t zp = (int32_t)((a[2] >> (8 * gg)) & 3u);
-                const float sc = sf37_f16(a[gg >> 1] >> (16 * (gg & 1)));
+        for (int j = 0; j < 8; j++) {
+            if (b0 + j < nb8) {
+                const uint32_t o = (uint32_t)((uintptr_t)(wr + (uint64_t)(b0 + j) * SF37_Q8_0_BYTES) & 3u);
+                uint32_t a[9];
 #pragma unroll
-                for (uint32_t t = 0; t < DEC_TPC; t++) {
-                    if (t < nt) {
-                        const act_block &x = xs[t * nblk + b];
-                        int32_t acc = 0;
+                for (int k = 0; k < 9; k++) a[k] = align_bytes(raw[j][k + 1], raw[j][k], o);
+                int32_t isum = 0;
 #pragma unroll
-                        for (int k = 0; k < 16; k++) acc = sdot4(cw[k], x.qs[16 * gg + k], acc);
-                        bs[t] = __builtin_fmaf(sc, (float)(acc - zp * x.gs[gg]), bs[t]);
-                    }
-                }
+                for (int k = 0; k < 8; k++) isum = sdot4(align_bytes(a[k + 1], a[k], 2), xv[j][k], isum);
+                acc = acc + (float)isum * sf37_f16(a[0]) * xsc[j];
             }
-            for (uint32_t t = 0; t < nt; t++) red[(t * DN_TILE + r) * nblk + b] = bs[t];
         }
-        __syncthreads();
-        for (uint32_t i = threadIdx.x; i < nt * DN_TILE; i += blockDim.x) {
-            const uint32_t t = i / DN_TILE, r = i - t * DN_TILE;
-            const float *rv = red + (t * DN_TILE + r) * nblk;
-            float acc = 0.0f;
-            for (uint32_t b = 0; b < nblk; b++) acc = __builtin_fmaf(xs[t * nblk + b].d, rv[b], acc);
-            st_shared(p.down_pair + (uint64_t)p.sorted[c0 + t] * p.K + row0 + r, acc);
-        }
-        __syncthreads();
     }
+    if (rl < nrows) st_shared(p.sh_out + (uint64_t)t * p.K + row, acc);
 }
 
-// Shared down rows [row0, row0 + SH_SUB) for every token.
-__device__ void down_shared(const dec_params &p, uint32_t row0, unsigned char *smem) {
-    const uint32_t nb8 = p.F / 32u;
-    const uint32_t tbytes = dn_shared_tile(p.F), wbuf = tile_buf(tbytes);
-    const uint64_t row_bytes = (uint64_t)nb8 * SF37_Q8_0_BYTES;
-    uint8_t *wl = smem;
-    float *red = (float *)(smem + wbuf);                            // [T][SUB][nb8]
-    const uint32_t ow = lds_copy(wl, p.sh_down + (uint64_t)row0 * row_bytes, tbytes);
-    lds_copy_wait();
-    for (uint32_t u = threadIdx.x; u < SH_SUB * nb8; u += blockDim.x) {
-        const uint32_t r = u / nb8, b = u - r * nb8;
-        uint32_t q[8];
-        const float wsc = q8_0_lds(wl, ow + (r * nb8 + b) * SF37_Q8_0_BYTES, q);
-        for (uint32_t t = 0; t < p.T; t++) {
-            const uint32_t *xv = (const uint32_t *)(p.sh_mq + (uint64_t)t * p.F + (uint64_t)b * 32u);
-            int32_t isum = 0;
-#pragma unroll
-            for (int k = 0; k < 8; k++) isum = sdot4(q[k], xv[k], isum);
-            red[((uint64_t)t * SH_SUB + r) * nb8 + b] = (float)isum * wsc * p.sh_ms[(uint64_t)t * nb8 + b];
+// Waves take items in order: [0, n_sh) shared-down spans of rpw rows, then
+// ng * K/64 routed (group, tile) items.  Arrivals count rows; a tile is
+// complete at 64 rows per group (+ 64 for the shared expert), and its last
+// wave writes out.
+__global__ void __launch_bounds__(256) dec_down_kernel(dec_params p) {
+    const uint32_t tiles = p.K / DN_TILE, ng = p.ginfo[0];
+    const bool sh = (p.flags & SF37_DEC_SHARED) != 0;
+    const uint32_t rpw = 64u / p.T;                                 // shared rows per wave
+    const uint32_t spt = (DN_TILE + rpw - 1u) / rpw;                // shared items per tile
+    const uint32_t n_sh = sh ? tiles * spt : 0u;
+    const uint32_t n_items = n_sh + ng * tiles;
+    const uint32_t target = DN_TILE * (ng + (sh ? 1u : 0u));
+    const uint32_t nbF = p.F / SF37_QK;
+    const uint32_t nw = gridDim.x * (blockDim.x >> 6);
+    for (uint32_t item = blockIdx.x * (blockDim.x >> 6) + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+         item < n_items; item += nw) {
+        uint32_t tile, rows;
+        if (item < n_sh) {
+            tile = item / spt;
+            const uint32_t k = item - tile * spt, r0 = k * rpw;
+            rows = DN_TILE - r0 < rpw ? DN_TILE - r0 : rpw;
+            down_shared_item(p, tile * DN_TILE + r0, rows);
+        } else {
+            const uint32_t it = item - n_sh, g = it / tiles;
+            tile = it - g * tiles;
+            rows = DN_TILE;
+            switch (nbF) {
+                case 1: down_item<1>(p, g, tile); break;
+                case 2: down_item<2>(p, g, tile); break;
+                case 3: down_item<3>(p, g, tile); break;
+                case 4: down_item<4>(p, g, tile); break;
+                default: down_item<5>(p, g, tile); break;
+            }
+        }
+        if (wave_arrive(cnt_dn(p) + tile, rows, target)) {
+            tile_combine(p, tile);
+            if ((threadIdx.x & 63u) == 0) cnt_dn(p)[tile] = 0u;
         }
     }
-    __syncthreads();
-    for (uint32_t i = threadIdx.x; i < p.T * SH_SUB; i += blockDim.x) {
-        const uint32_t t = i / SH_SUB, r = i - t * SH_SUB;
-        const float *rv = red + (uint64_t)i * nb8;
-        float acc = 0.0f;
-        for (uint32_t b = 0; b < nb8; b++) acc = acc + rv[b];
-        st_shared(p.sh_out + (uint64_t)t * p.K + row0 + r, acc);
-    }
-}
-
-__global__ void __launch_bounds__(320) dec_down_kernel(dec_params p, uint32_t n_routed) {
-    extern __shared__ __align__(16) unsigned char smem[];
-    __shared__ int flag;
-    const uint32_t tiles = p.K / DN_TILE;
-    uint32_t tile;
-    if (blockIdx.x < n_routed) {
-        const uint32_t g = blockIdx.x / tiles;
-        tile = blockIdx.x - g * tiles;
-        if (g >= p.ginfo[0]) return;
-        down_routed(p, blockIdx.x, smem);
-    } else {
-        const uint32_t s = blockIdx.x - n_routed;
-        tile = s / (DN_TILE / SH_SUB);
-        down_shared(p, s * SH_SUB, smem);
-    }
-    const uint32_t target = p.ginfo[0] + ((p.flags & SF37_DEC_SHARED) ? DN_TILE / SH_SUB : 0u);
-    if (!arrive_last(cnt_dn(p) + tile, target, &flag)) return;
-    down_combine(p, tile);
-    if (threadIdx.x == 0) cnt_dn(p)[tile] = 0u;
 }
 
 }  // namespace
@@ -654,38 +682,80 @@ __global__ void __launch_bounds__(320) dec_down_kernel(dec_params p, uint32_t n_
 namespace {
 
 struct dec_shape {
-    uint32_t n_router, n_xq, n_up_routed, n_up_shared, n_dn_routed, n_dn_shared;
-    size_t lds_up, lds_dn;
+    uint32_t n_router, n_xq, n_shup, n_up, n_mid, n_dn;
+    size_t lds_up, lds_shup;
 };
+
+uint32_t device_cus() {
+    static int cus = 0;
+    if (!cus) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+            cus = 256;
+    }
+    return (uint32_t)cus;
+}
+
+uint32_t device_max_lds() {
+    static int lds = 0;
+    if (!lds) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess || lds <= 0)
+            lds = 65536;
+    }
+    return (uint32_t)lds;
+}
+
+constexpr uint32_t LDS_PER_CU = 160u * 1024u;
 
 dec_shape dec_plan(const dec_params &p) {
     dec_shape d;
     const uint32_t nb = p.K / SF37_QK;
     const bool sh = (p.flags & SF37_DEC_SHARED) != 0;
+    const uint32_t cus = device_cus();
     d.n_router = (p.flags & SF37_DEC_ROUTER) ? p.E : 0u;
     d.n_xq = (p.T * nb + 3u) / 4u;
-    const size_t up_r = lds_up_routed(p.K), up_s = sh ? lds_up_shared(p.K, p.T) : 0u;
-    d.lds_up = up_r > up_s ? up_r : up_s;
-    const size_t dn_r = lds_dn_routed(p.F), dn_s = sh ? lds_dn_shared(p.F, p.T) : 0u;
-    d.lds_dn = dn_r > dn_s ? dn_r : dn_s;
-    d.n_up_routed = p.G * (p.F / UP_RT);
-    d.n_up_shared = sh ? p.F / SH_RS : 0u;
-    d.n_dn_routed = p.G * (p.K / DN_TILE);
-    d.n_dn_shared = sh ? p.K / SH_SUB : 0u;
+    d.lds_up = lds_up_routed(p.K, p.T, p.G, p.T * p.topk);
+    d.lds_shup = lds_up_shared(p.K, p.T);
+    d.n_shup = sh ? p.F / SH_RS : 0u;
+    // every up workgroup resident at once: at most 3 per CU, fewer if LDS-bound
+    uint32_t per_cu = (uint32_t)(LDS_PER_CU / (d.lds_up + 512u));
+    per_cu = per_cu > 3u ? 3u : per_cu < 1u ? 1u : per_cu;
+    d.n_up = per_cu * cus;
+    const uint32_t n_mid_waves = p.T * p.topk * (p.F / SF37_QK) + (sh ? (p.T * (p.F / 32u) + 1u) / 2u : 0u);
+    d.n_mid = (n_mid_waves + 3u) / 4u;
+    d.n_dn = 2u * cus;
     return d;
 }
 
 }  // namespace
 
 extern "C" int sf37k_decode_counters(uint32_t T, uint32_t topk, uint32_t E, uint32_t K, uint32_t F) {
-    const uint32_t P = T * topk, G = P < E ? P : E;
-    return (int)(1u + G * (F / SF37_QK) + F / 32u + K / DN_TILE);
+    (void)T; (void)topk; (void)E; (void)F;
+    return (int)(CNT_FIXED + K / DN_TILE);
 }
 
-extern "C" uint64_t sf37k_decode_lds(const sf37_dec_params *pp) {
-    const dec_shape d = dec_plan(*pp);
-    return d.lds_up > d.lds_dn ? d.lds_up : d.lds_dn;
+extern "C" int sf37k_decode_supported(uint32_t T, uint32_t topk, uint32_t E, uint32_t K, uint32_t F, int shared) {
+    if (T == 0 || T > DEC_MAX_TOK || topk == 0 || K % SF37_QK || F % SF37_QK || K / SF37_QK > 16u ||
+        F / SF37_QK > DN_MAX_NB || K % DN_TILE)
+        return 0;
+    const uint32_t P = T * topk, G = P < E ? P : E;
+    if (lds_up_routed(K, T, G, P) > device_max_lds()) return 0;
+    if (shared && lds_up_shared(K, T) > device_max_lds()) return 0;
+    return 1;
 }
+
+namespace {
+int set_lds(const void *fn, size_t bytes, size_t *opted) {
+    if (bytes <= *opted) return 0;
+    const hipError_t err = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+    if (err != hipSuccess) return (int)err;
+    *opted = bytes;
+    return 0;
+}
+}  // namespace
 
 extern "C" int sf37k_decode_route(const sf37_dec_params *pp, sf37_stream_t s) {
     const dec_shape d = dec_plan(*pp);
@@ -693,16 +763,33 @@ extern "C" int sf37k_decode_route(const sf37_dec_params *pp, sf37_stream_t s) {
     return (int)hipGetLastError();
 }
 
+extern "C" int sf37k_decode_shared_up(const sf37_dec_params *pp, sf37_stream_t s) {
+    const dec_shape d = dec_plan(*pp);
+    if (!d.n_shup) return 0;
+    static size_t opted = 65536;
+    const int err = set_lds((const void *)dec_shup_kernel, d.lds_shup, &opted);
+    if (err) return err;
+    hipLaunchKernelGGL(dec_shup_kernel, dim3(d.n_shup), dim3(256), d.lds_shup, (hipStream_t)s, *pp);
+    return (int)hipGetLastError();
+}
+
 extern "C" int sf37k_decode_up(const sf37_dec_params *pp, sf37_stream_t s) {
     const dec_shape d = dec_plan(*pp);
-    hipLaunchKernelGGL(dec_up_kernel, dim3(d.n_up_routed + d.n_up_shared), dim3(256), d.lds_up, (hipStream_t)s, *pp,
-                       d.n_up_routed);
+    static size_t opted = 65536;
+    const int err = set_lds((const void *)dec_up_kernel, d.lds_up, &opted);
+    if (err) return err;
+    hipLaunchKernelGGL(dec_up_kernel, dim3(d.n_up), dim3(256), d.lds_up, (hipStream_t)s, *pp);
+    return (int)hipGetLastError();
+}
+
+extern "C" int sf37k_decode_mid(const sf37_dec_params *pp, sf37_stream_t s) {
+    const dec_shape d = dec_plan(*pp);
+    hipLaunchKernelGGL(dec_mid_kernel, dim3(d.n_mid), dim3(256), 0, (hipStream_t)s, *pp);
     return (int)hipGetLastError();
 }
 
 extern "C" int sf37k_decode_down(const sf37_dec_params *pp, sf37_stream_t s) {
     const dec_shape d = dec_plan(*pp);
-    hipLaunchKernelGGL(dec_down_kernel, dim3(d.n_dn_routed + d.n_dn_shared), dim3(320), d.lds_dn, (hipStream_t)s,
-                       *pp, d.n_dn_routed);
+    hipLaunchKernelGGL(dec_down_kernel, dim3(d.n_dn), dim3(256), 0, (hipStream_t)s, *pp);
     return (int)hipGetLastError();
 }

@@ -10,7 +10,7 @@
 // p = sigmoid(logit), score = p + bias, k rounds of a wave-wide arg-max under
 // (score desc, index asc), weights = p / max(sum p, 1e-20) * scale with the
 // sum taken in slot order.
-#include "sf37_dev.h"
+#include "sf37_router.h"
 #include "sf37_launch.h"
 
 namespace {
@@ -58,8 +58,11 @@ __global__ void __launch_bounds__(256) f32_matmul_kernel(float *__restrict__ out
         }
 }
 
-// Decode GEMV (n_tok small): one workgroup per expert row, 4 waves split K,
-// binary64 partial sums combined in LDS.
+// Decode GEMV (n_tok small): one workgroup per expert row and 8 tokens.
+// For in_dim a multiple of 256 the row is split into contiguous per-thread
+// slices (sf37_router.h, the order the fused decode path uses); otherwise
+// thread i takes k = i, i + 256, ...  Binary64 partial sums per wave are
+// combined as (w0 + w1) + (w2 + w3).
 __global__ void __launch_bounds__(256) f32_matvec_kernel(float *__restrict__ out,
                                                          const float *__restrict__ w,
                                                          const float *__restrict__ x,
@@ -71,35 +74,32 @@ __global__ void __launch_bounds__(256) f32_matvec_kernel(float *__restrict__ out
     const uint32_t t0 = blockIdx.y * MAXT;
     const uint32_t nt = n_tok - t0 < (uint32_t)MAXT ? n_tok - t0 : (uint32_t)MAXT;
     const float *wr = w + e * in_dim;
-    double acc[MAXT];
+    if (in_dim % 256u == 0 && in_dim <= 0xffffffffu) {
+        sf37_router_rows(wr, x + (uint64_t)t0 * in_dim, (uint32_t)in_dim, nt, part);
+    } else {
+        double acc[MAXT];
 #pragma unroll
-    for (int t = 0; t < MAXT; t++) acc[t] = 0.0;
-    for (uint64_t k = threadIdx.x; k < in_dim; k += 256u) {
-        const double wv = wr[k];
+        for (int t = 0; t < MAXT; t++) acc[t] = 0.0;
+        for (uint64_t k = threadIdx.x; k < in_dim; k += 256u) {
+            const double wv = wr[k];
 #pragma unroll
-        for (int t = 0; t < MAXT; t++)
-            if ((uint32_t)t < nt) acc[t] = __builtin_fma(wv, (double)x[(uint64_t)(t0 + t) * in_dim + k], acc[t]);
-    }
+            for (int t = 0; t < MAXT; t++)
+                if ((uint32_t)t < nt) acc[t] = __builtin_fma(wv, (double)x[(uint64_t)(t0 + t) * in_dim + k], acc[t]);
+        }
 #pragma unroll
-    for (int t = 0; t < MAXT; t++) {
-        double v = acc[t];
+        for (int t = 0; t < MAXT; t++) {
+            double v = acc[t];
 #pragma unroll
-        for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-        if ((threadIdx.x & 63u) == 0) part[t][threadIdx.x >> 6] = v;
+            for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+            if ((threadIdx.x & 63u) == 0) part[t][threadIdx.x >> 6] = v;
+        }
     }
     __syncthreads();
     if (threadIdx.x < nt) {
         const uint32_t t = threadIdx.x;
-        const double v = (part[t][0] + part[t][1]) + (part[t][2] + part[t][3]);
-        out[(uint64_t)(t0 + t) * out_dim + e] = (float)v;
+        out[(uint64_t)(t0 + t) * out_dim + e] = sf37_router_combine(part[t]);
     }
 }
-
-__device__ __forceinline__ bool better(float av, uint32_t ai, float bv, uint32_t bi) {
-    return av > bv || (av == bv && ai < bi);
-}
-
-constexpr int RS_PER_LANE = 16;  // up to 1024 experts
 
 __global__ void __launch_bounds__(256) router_select_kernel(int32_t *__restrict__ selected,
                                                             float *__restrict__ weights,
@@ -108,68 +108,16 @@ __global__ void __launch_bounds__(256) router_select_kernel(int32_t *__restrict_
                                                             const float *__restrict__ bias,
                                                             uint32_t n_experts, uint32_t topk,
                                                             float scale, uint32_t n_tok) {
+    __shared__ uint64_t tab[32];
+    sf37_stage_exp_tab(tab);
+    __syncthreads();
     const uint32_t t = blockIdx.x * 4u + (threadIdx.x >> 6);
-    const uint32_t lane = threadIdx.x & 63u;
     if (t >= n_tok) return;
     const float *lg = logits + (uint64_t)t * n_experts;
-    float prob[RS_PER_LANE], score[RS_PER_LANE];
-    uint32_t taken = 0;   // bit j: local entry j already selected
-#pragma unroll
-    for (int j = 0; j < RS_PER_LANE; j++) {
-        const uint32_t e = lane + 64u * j;
-        prob[j] = 0.0f;
-        score[j] = -__builtin_inff();
-        if (e < n_experts) {
-            const float p = sf37_sigmoid(lg[e]);
-            prob[j] = p;
-            score[j] = p + bias[e];
-            if (probs) probs[(uint64_t)t * n_experts + e] = p;
-        } else {
-            taken |= 1u << j;
-        }
-    }
-    float sel_p[16];
-    uint32_t sel_i[16];
-    for (uint32_t k = 0; k < topk; k++) {
-        float bs = -__builtin_inff(), bp = 0.0f;
-        uint32_t bi = 0xffffffffu;
-        int bj = -1;
-#pragma unroll
-        for (int j = 0; j < RS_PER_LANE; j++) {
-            const uint32_t e = lane + 64u * j;
-            if (!((taken >> j) & 1u) && better(score[j], e, bs, bi)) {
-                bs = score[j];
-                bp = prob[j];
-                bi = e;
-                bj = j;
-            }
-        }
-        float ws = bs, wp = bp;
-        uint32_t wi = bi;
-#pragma unroll
-        for (int off = 32; off > 0; off >>= 1) {
-            const float os = __shfl_xor(ws, off, 64);
-            const float op = __shfl_xor(wp, off, 64);
-            const uint32_t oi = __shfl_xor(wi, off, 64);
-            if (better(os, oi, ws, wi)) {
-                ws = os;
-                wp = op;
-                wi = oi;
-            }
-        }
-        if (wi != 0xffffffffu && bi == wi && bj >= 0) taken |= 1u << bj;
-        sel_p[k] = wi == 0xffffffffu ? 0.0f : wp;
-        sel_i[k] = wi;
-    }
-    if (lane == 0) {
-        float sum = 0.0f;
-        for (uint32_t k = 0; k < topk; k++) sum += sel_p[k];
-        if (sum < 1.0e-20f) sum = 1.0e-20f;
-        for (uint32_t k = 0; k < topk; k++) {
-            selected[(uint64_t)t * topk + k] = sel_i[k] == 0xffffffffu ? -1 : (int32_t)sel_i[k];
-            weights[(uint64_t)t * topk + k] = sel_p[k] / sum * scale;
-        }
-    }
+    int32_t *so[1] = {selected + (uint64_t)t * topk};
+    float *wo[1] = {weights + (uint64_t)t * topk};
+    float *po[1] = {probs ? probs + (uint64_t)t * n_experts : nullptr};
+    sf37_wave_topk<1>([lg](uint32_t, uint32_t e) { return lg[e]; }, bias, n_experts, topk, scale, tab, so, wo, po);
 }
 
 }  // namespace

@@ -145,3 +145,75 @@ __device__ __forceinline__ void lds_copy_wait() {
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
 }
+
+// ---------------------------------------------------------------------------
+// Activation blocks for the fused decode kernels: 256 Q8_K codes in the
+// order the weight unpack produces (Q3: q3x_pos, Q2: q2_perm_pos), the
+// scale d and the four 64-wide code sums, padded to 288 bytes so a block
+// is a whole number of 16-byte chunks.
+// ---------------------------------------------------------------------------
+struct __attribute__((aligned(16))) act_t {
+    uint32_t qs[64];
+    float d;
+    int32_t gs[4];
+    uint32_t pad[3];
+};
+static_assert(sizeof(act_t) == 288, "act_t is 288 bytes");
+
+// Byte position of element i (0..255) of a block in the Q3 act layout: chunk
+// c = i / 32 (12 payload bytes), code j = i % 32 sits in dword 8c + j % 8,
+// byte j / 8 -- the order q3_unpack32 produces.
+__host__ __device__ inline uint32_t q3x_pos(uint32_t i) {
+    const uint32_t c = i >> 5, j = i & 31u;
+    return ((c << 3) + (j & 7u)) * 4u + (j >> 3);
+}
+
+__device__ __forceinline__ uint32_t vperm(uint32_t hi, uint32_t lo, uint32_t sel) {
+    return __builtin_amdgcn_perm(hi, lo, sel);
+}
+
+// Bytes S, S+3, S+6, S+9 of the dword array w -> bytes 0..3 (S is a
+// compile-time constant after inlining, so the selectors fold).
+__device__ __forceinline__ uint32_t gather_every3(const uint32_t *w, int S) {
+    const int d0 = S >> 2;
+    uint32_t sel = 0;
+    for (int k = 0; k < 4; k++) {
+        const int pos = S + 3 * k, d = (pos >> 2) - d0, b = pos & 3;
+        sel |= (uint32_t)(d <= 1 ? d * 4 + b : 0x0c) << (8 * k);
+    }
+    uint32_t t = vperm(w[d0 + 1], w[d0], sel);
+    const int d3 = ((S + 9) >> 2) - d0;
+    if (d3 >= 2) {
+        uint32_t sel2 = 0;
+        for (int k = 0; k < 4; k++) {
+            const int pos = S + 3 * k, d = (pos >> 2) - d0, b = pos & 3;
+            sel2 |= (uint32_t)(d <= 1 ? k : d == 2 ? 4 + b : 0x0c) << (8 * k);
+        }
+        t = vperm(w[d0 + 2], t, sel2);
+    }
+    if (d3 >= 3) {
+        uint32_t sel3 = 0;
+        for (int k = 0; k < 4; k++) {
+            const int pos = S + 3 * k, d = (pos >> 2) - d0, b = pos & 3;
+            sel3 |= (uint32_t)(d <= 2 ? k : 4 + b) << (8 * k);
+        }
+        t = vperm(w[d0 + 3], t, sel3);
+    }
+    return t;
+}
+
+// 32 three-bit codes (LSB-first) in the 12 bytes at byte S of w -> eight
+// i8x4 words, word r byte a = code 8a + r.  Gathering bytes 3a, 3a+1, 3a+2
+// puts code 8a + r at bit 3r of a 24-bit lane, so each word is one or two
+// shifts and masks.
+__device__ __forceinline__ void q3_unpack32(const uint32_t *w, int S, uint32_t c[8]) {
+    const uint32_t D0 = gather_every3(w, S), D1 = gather_every3(w, S + 1), D2 = gather_every3(w, S + 2);
+    c[0] = D0 & 0x07070707u;
+    c[1] = (D0 >> 3) & 0x07070707u;
+    c[2] = ((D0 >> 6) & 0x03030303u) | ((D1 << 2) & 0x04040404u);
+    c[3] = (D1 >> 1) & 0x07070707u;
+    c[4] = (D1 >> 4) & 0x07070707u;
+    c[5] = ((D1 >> 7) & 0x01010101u) | ((D2 << 1) & 0x06060606u);
+    c[6] = (D2 >> 2) & 0x07070707u;
+    c[7] = (D2 >> 5) & 0x07070707u;
+}

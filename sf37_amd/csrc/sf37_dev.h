@@ -42,15 +42,12 @@ __host__ __device__ inline uint64_t sf37_exp2_tab(uint32_t i) {
 }
 
 // tab: the 32 table words (sf37_exp2_tab), e.g. staged in LDS by the caller.
+// Branch-free: the reduction runs for every input and the special cases
+// (|x| >= 88 that overflow or underflow, infinities, NaN) are selected at the
+// end, so unrolled calls stay straight-line code on the GPU.
 __host__ __device__ inline float sf37_expf_t(float x, const uint64_t *tab) {
     const uint32_t ux = __builtin_bit_cast(uint32_t, x);
     const uint32_t abstop = (ux >> 20) & 0x7ffu;
-    if (abstop >= 0x42bu) {                       // |x| >= 88 or nan
-        if (ux == 0xff800000u) return 0.0f;
-        if (abstop >= 0x7f8u) return x + x;
-        if (x > 0x1.62e42ep6f) return __builtin_inff();
-        if (x < -0x1.9fe368p6f) return 0.0f;
-    }
     const double inv_ln2_n = 0x1.71547652b82fep+0 * 32.0;   // 32 / ln 2
     const double shift = 0x1.8p+52;
     const double c0 = 0x1.c6af84b912394p-5 / (32.0 * 32.0 * 32.0);
@@ -69,19 +66,23 @@ __host__ __device__ inline float sf37_expf_t(float x, const uint64_t *tab) {
     double y = __builtin_fma(c2, r, 1.0);
     y = __builtin_fma(z, r2, y);
     y = y * s;
-    return (float)y;
+    float res = (float)y;
+    if (abstop >= 0x42bu) {                       // |x| >= 88 or nan (selects)
+        res = x < -0x1.9fe368p6f ? 0.0f : res;
+        res = x > 0x1.62e42ep6f ? __builtin_inff() : res;
+        res = abstop >= 0x7f8u ? x + x : res;
+        res = ux == 0xff800000u ? 0.0f : res;
+    }
+    return res;
 }
 
 __host__ __device__ inline float sf37_expf(float x) { return sf37_expf_t(x, nullptr); }
 
-// sf37_ops.c:9-16
+// sf37_ops.c:9-16: x >= 0 ? 1 / (1 + e^-x) : e^x / (1 + e^x), branch-free.
 __host__ __device__ inline float sf37_sigmoid_t(float x, const uint64_t *tab) {
-    if (x >= 0.0f) {
-        const float z = sf37_expf_t(-x, tab);
-        return 1.0f / (1.0f + z);
-    }
-    const float z = sf37_expf_t(x, tab);
-    return z / (1.0f + z);
+    const bool pos = x >= 0.0f;
+    const float z = sf37_expf_t(pos ? -x : x, tab);
+    return (pos ? 1.0f : z) / (1.0f + z);
 }
 
 __host__ __device__ inline float sf37_sigmoid(float x) { return sf37_sigmoid_t(x, nullptr); }

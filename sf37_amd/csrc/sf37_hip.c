@@ -87,7 +87,7 @@ static hipEvent_t g_prof_open;
 
 static const char *const k_stage_names[SF37_HIP_N_STAGES] = {
     "router", "select", "q8_0_act", "q8_0_gemm", "swiglu", "q8k_x", "dispatch",
-    "gate_up", "q8k_mid", "down", "combine", "add", "other", "dec_route", "dec_up", "dec_down"};
+    "gate_up", "q8k_mid", "down", "combine", "add", "other", "dec_route", "dec_up", "dec_down", "dec_shared_up", "dec_mid"};
 
 static void prof_begin(void) {
     if (!g_prof_on) return;
@@ -911,7 +911,8 @@ static int decode_eligible(const routed_args *a, uint32_t flags) {
         return 0;
     if ((flags & SF37_DEC_SELECT) && a->n_expert > ROUTER_MAX_EXPERTS) return 0;
     if ((flags & SF37_DEC_SLOTS) && a->n_tok != 1u) return 0;
-    return 1;
+    return sf37k_decode_supported(a->n_tok, a->topk, a->n_expert, a->in_dim, a->mid_dim,
+                                  (flags & SF37_DEC_SHARED) != 0);
 }
 
 /* out = [shared +] sum over slots of the routed experts; mid / down_pair /
@@ -951,7 +952,6 @@ static int decode_run(const routed_args *a, const dec_extra *ex, float *out, flo
     p.gate_out = gate_out;
     p.up_out = up_out;
     p.out = out;
-    if (sf37k_decode_lds(&p) > 65536u) return 0;
     /* scratch layout */
     uint64_t off = 0, o_xq, o_xq8, o_xs8, o_gi, o_so, o_mid = 0, o_mq, o_gu = 0, o_smq = 0, o_sms = 0, o_dp = 0,
                       o_sho = 0, o_lg = 0, o_sel = 0, o_wts = 0;
@@ -960,13 +960,13 @@ static int decode_run(const routed_args *a, const dec_extra *ex, float *out, flo
         var = off;                  \
         off = align256(off + (bytes)); \
     } while (0)
-    TAKE(o_xq, (uint64_t)T * (K / QK) * Q8KB);
+    TAKE(o_xq, (uint64_t)T * (K / QK) * SF37_DEC_ACT_BYTES);
     TAKE(o_xq8, (uint64_t)T * K);
     TAKE(o_xs8, (uint64_t)T * (K / 32u) * 4u);
     TAKE(o_gi, (3u + 2u * (uint64_t)G) * 4u);
     TAKE(o_so, P * 4u);
     if (!mid) TAKE(o_mid, P * F * 4u);
-    TAKE(o_mq, P * (F / QK) * Q8KB);
+    TAKE(o_mq, P * (F / QK) * SF37_DEC_ACT_BYTES);
     if (sh) {
         TAKE(o_gu, 2u * (uint64_t)T * F * 4u);
         TAKE(o_smq, (uint64_t)T * F);
@@ -1010,7 +1010,9 @@ static int decode_run(const routed_args *a, const dec_extra *ex, float *out, flo
     p.cnt = cnt;
     const sf37_stream_t st = (sf37_stream_t)g_stream;
     return LAUNCH(SF37_HIP_STAGE_DEC_ROUTE, sf37k_decode_route(&p, st), "decode route launch") &&
+           (!sh || LAUNCH(SF37_HIP_STAGE_DEC_SHARED_UP, sf37k_decode_shared_up(&p, st), "decode shared up launch")) &&
            LAUNCH(SF37_HIP_STAGE_DEC_UP, sf37k_decode_up(&p, st), "decode up launch") &&
+           LAUNCH(SF37_HIP_STAGE_DEC_MID, sf37k_decode_mid(&p, st), "decode mid launch") &&
            LAUNCH(SF37_HIP_STAGE_DEC_DOWN, sf37k_decode_down(&p, st), "decode down launch");
 }
 

@@ -94,7 +94,7 @@ int sf37k_synth_quant_rows(int type, uint8_t *dst, uint64_t row0, uint64_t nrows
 /* Elementwise exp/sigmoid of a float array (for exhaustive parity tests). */
 int sf37k_sigmoid_array(float *out, const float *x, uint64_t n, int mode, sf37_stream_t s);
 
-/* Fused decode layer (up to 16 tokens): route, up, down in three launches
+/* Fused decode layer (up to 16 tokens): route, shared_up, up, mid, down
  * (k_decode.hip).  Pointers are device addresses; flags select the parts
  * that run.  cnt holds sf37k_decode_counters(...) zero-initialised words
  * that the kernels leave zero again when they finish. */
@@ -103,6 +103,7 @@ int sf37k_sigmoid_array(float *out, const float *x, uint64_t n, int mode, sf37_s
 #define SF37_DEC_SELECT 2u   /* top-k from logits_sel (else sel/wts are inputs) */
 #define SF37_DEC_SHARED 4u   /* shared expert, out = shared + routed */
 #define SF37_DEC_SLOTS 8u    /* one group per slot of a single token */
+#define SF37_DEC_ACT_BYTES 288u  /* activation block: 256 codes, d, 4 sums, pad */
 typedef struct sf37_dec_params {
     uint32_t T, E, K, F, topk, G;
     float scale, clamp_routed, clamp_shared;
@@ -112,13 +113,13 @@ typedef struct sf37_dec_params {
     float *logits;
     int32_t *sel;
     float *wts;
-    void *xq;            /* T x K/256 Q8_K blocks */
+    void *xq;            /* T x K/256 activation blocks (Q3 order) */
     int8_t *xq8;         /* T x K Q8_0 codes */
     float *xs8;          /* T x K/32 Q8_0 scales */
     uint32_t *ginfo;     /* [0] groups, [1..G+1] pair offsets, [G+2..2G+2) experts */
     uint32_t *sorted;    /* pairs ordered by (expert, pair) */
     float *mid;          /* pairs x F SwiGLU * weight */
-    void *midq;          /* pairs x F/256 Q8_K blocks */
+    void *midq;          /* pairs x F/256 activation blocks (Q2 order) */
     float *gate_out, *up_out;   /* optional pairs x F */
     float *sh_gu;        /* 2 x T x F shared gate | up */
     int8_t *sh_mq;       /* T x F Q8_0 codes of the shared mid */
@@ -129,11 +130,14 @@ typedef struct sf37_dec_params {
     uint32_t *cnt;
 } sf37_dec_params;
 int sf37k_decode_counters(uint32_t T, uint32_t topk, uint32_t E, uint32_t K, uint32_t F);
-/* LDS bytes the up/down launches need (the caller keeps them <= 64 KiB). */
-uint64_t sf37k_decode_lds(const sf37_dec_params *p);
-/* The three launches, in this order on one stream. */
+/* 1 if the fused kernels take this shape (token count, dims, LDS). */
+int sf37k_decode_supported(uint32_t T, uint32_t topk, uint32_t E, uint32_t K, uint32_t F, int shared);
+/* The launches, in this order on one stream (shared_up only with
+ * SF37_DEC_SHARED). */
 int sf37k_decode_route(const sf37_dec_params *p, sf37_stream_t s);
+int sf37k_decode_shared_up(const sf37_dec_params *p, sf37_stream_t s);
 int sf37k_decode_up(const sf37_dec_params *p, sf37_stream_t s);
+int sf37k_decode_mid(const sf37_dec_params *p, sf37_stream_t s);
 int sf37k_decode_down(const sf37_dec_params *p, sf37_stream_t s);
 
 #ifdef __cplusplus

@@ -104,7 +104,14 @@ def test_fused_layer_equals_staged(H, layer, n_tok, routing):
     x = rng.standard_normal((n_tok, K)).astype(np.float32)
     logits = skewed_logits(rng, n_tok) if routing == "skewed" else rng.standard_normal((n_tok, E)).astype(np.float32)
     say(f"fused vs staged: {n_tok} tokens, {routing} routing")
-    a = run_layer(H, layer, x, logits, True)
+    H.lib().sf37_hip_profile_enable(1)
+    H.profile_read()
+    try:
+        a = run_layer(H, layer, x, logits, True)
+        prof = H.profile_read()
+    finally:
+        H.lib().sf37_hip_profile_enable(0)
+    assert prof["dec_up"][1] == 1 and prof["dec_down"][1] == 1, "fused kernels did not run"
     b = run_layer(H, layer, x, logits, False)
     assert np.array_equal(a[1], b[1])
     assert_bitexact(a[2], b[2], "weights")
