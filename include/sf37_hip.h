@@ -286,10 +286,10 @@ enum {
     SF37_HIP_STAGE_OTHER,
     /* the fused decode layer (up to 16 tokens): route = router GEMV + x
      * quantisation + top-k + grouping, up = routed gate/up with SwiGLU,
-     * down = routed and shared down + combine, shared_up = shared gate/up,
-     * mid = quantisation of the routed and shared mid */
+     * down = routed down, shared_up = shared gate/up, mid = quantisation of
+     * the routed and shared mid, combine = shared down + slot-order sum */
     SF37_HIP_STAGE_DEC_ROUTE, SF37_HIP_STAGE_DEC_UP, SF37_HIP_STAGE_DEC_DOWN,
-    SF37_HIP_STAGE_DEC_SHARED_UP, SF37_HIP_STAGE_DEC_MID,
+    SF37_HIP_STAGE_DEC_SHARED_UP, SF37_HIP_STAGE_DEC_MID, SF37_HIP_STAGE_DEC_COMBINE,
     SF37_HIP_N_STAGES
 };
 int sf37_hip_profile_enable(int on);

@@ -34,6 +34,8 @@ constexpr uint32_t DEC_TPC = 4;      // pairs per pass in the routed kernels
 constexpr uint32_t SH_RS = 2;        // shared gate/up rows per workgroup
 constexpr uint32_t DN_TILE = 64;     // down rows per item (= combine tile)
 constexpr uint32_t DN_MAX_NB = 5;    // down blocks per row held in registers (F <= 1280)
+constexpr uint32_t DN_WG_WAVES = 2;  // waves per combine workgroup (one LDS tile each)
+constexpr uint32_t DN_TPC = 2;       // pairs per pass in the routed down kernel
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4a4 __attribute__((ext_vector_type(4), aligned(4)));
@@ -77,14 +79,23 @@ using dec_params = sf37_dec_params;
 
 namespace {
 
-// counter layout: [0] route, [1..3) reserved, then K/64 down tiles
+// counter layout: [0] route arrivals, [1..3) reserved
 constexpr uint32_t CNT_FIXED = 3;
-__device__ __forceinline__ uint32_t *cnt_dn(const dec_params &p) { return p.cnt + CNT_FIXED; }
 
 // LDS layout sizes, shared by the kernels and the host-side launch plan.
 // A weight tile buffer holds the tile plus the copy's leading offset.
 __host__ __device__ constexpr uint32_t tile_buf(uint32_t bytes) { return (bytes + 31u + 15u) & ~15u; }
 __host__ __device__ constexpr uint32_t up_shared_tile(uint32_t K) { return SH_RS * (K / 32u) * SF37_Q8_0_BYTES; }
+// down: per-wave tile buffer holding a routed 64-row tile; shared-down
+// items take as many rows as fit (and as the 64 lanes allow for T tokens)
+__host__ __device__ constexpr uint32_t dn_buf_bytes(uint32_t F) {
+    return tile_buf(DN_TILE * (F / SF37_QK) * SF37_Q2_BYTES);
+}
+__host__ __device__ constexpr uint32_t sh_dn_rows(uint32_t F, uint32_t T) {
+    return (64u / T) < (DN_TILE * (F / SF37_QK) * SF37_Q2_BYTES) / ((F / 32u) * SF37_Q8_0_BYTES)
+               ? 64u / T
+               : (DN_TILE * (F / SF37_QK) * SF37_Q2_BYTES) / ((F / 32u) * SF37_Q8_0_BYTES);
+}
 // up workgroup: x of every token, then group info, sorted pairs, weights
 __host__ __device__ constexpr size_t lds_up_routed(uint32_t K, uint32_t T, uint32_t G, uint32_t P) {
     return (size_t)T * (K / SF37_QK) * sizeof(act_t) + (size_t)(3u + 2u * G + 2u * P) * 4u;
@@ -172,7 +183,7 @@ __global__ void __launch_bounds__(256) dec_route_kernel(dec_params p, uint32_t n
     if (!arrive_last(p.cnt, gridDim.x, &flag)) return;
 
     // ---- last workgroup: clear the next counters, top-k, groups ----------
-    const uint32_t n_clear = CNT_FIXED - 1u + p.K / DN_TILE;
+    const uint32_t n_clear = CNT_FIXED - 1u;
     for (uint32_t i = threadIdx.x; i < n_clear; i += blockDim.x) p.cnt[1 + i] = 0u;
     sf37_stage_exp_tab(tab);
     __syncthreads();
@@ -491,25 +502,24 @@ __global__ void __launch_bounds__(256) dec_mid_kernel(dec_params p) {
 // down + combine
 // ---------------------------------------------------------------------------
 
-// Wave-level arrival: the wave's stores are acknowledged, then lane 0 adds n
-// to the counter.  True in every lane of the wave that completed target.
-__device__ __forceinline__ bool wave_arrive(uint32_t *counter, uint32_t n, uint32_t target) {
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    uint32_t old = 0;
-    if ((threadIdx.x & 63u) == 0) old = atomicAdd(counter, n);
-    old = __shfl(old, 0, 64);
-    return old + n == target;
+// Per-wave LDS tile copy: bytes [src, src + n) with direct global->LDS
+// dwordx4 loads (one contiguous KiB per instruction), starting at the
+// 16-byte boundary at or below src.  Returns the offset of src in dst; the
+// caller waits with wave_lds_wait() before reading.
+__device__ __forceinline__ uint32_t wave_lds_copy(uint8_t *dst, const uint8_t *src, uint32_t n) {
+    const uintptr_t a0 = (uintptr_t)src & ~(uintptr_t)15;
+    const uint32_t off = (uint32_t)((uintptr_t)src - a0);
+    const uint32_t chunks = (off + n + 15u) >> 4, lane = threadIdx.x & 63u;
+    for (uint32_t c0 = 0; c0 < chunks; c0 += 64u) {
+        if (c0 + lane < chunks)
+            __builtin_amdgcn_global_load_lds((const void *)(a0 + 16u * (uintptr_t)(c0 + lane)), dst + 16u * c0, 16, 0, 0);
+    }
+    return off;
 }
 
-// out = [shared +] sum over slots, for the 64 rows of one tile; lane = row.
-__device__ void tile_combine(const dec_params &p, uint32_t tile) {
-    const uint32_t r = tile * DN_TILE + (threadIdx.x & 63u);
-    for (uint32_t t = 0; t < p.T; t++) {
-        float acc = 0.0f;
-        for (uint32_t s = 0; s < p.topk; s++) acc = acc + ld_shared(p.down_pair + ((uint64_t)t * p.topk + s) * p.K + r);
-        const uint64_t o = (uint64_t)t * p.K + r;
-        p.out[o] = (p.flags & SF37_DEC_SHARED) ? ld_shared(p.sh_out + o) + acc : acc;
-    }
+__device__ __forceinline__ void wave_lds_wait() {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __builtin_amdgcn_wave_barrier();
 }
 
 // Block values of one Q2 block (21 dwords in a) against NT activation blocks
@@ -532,148 +542,212 @@ __device__ __forceinline__ void q2_block_dots(const uint32_t *a, c_act *const *x
             for (int k = 0; k < 16; k++) acc = sdot4(c[k], x[t]->qs[16 * g + k], acc);
             bs[t] = __builtin_fmaf(sc, (float)(acc - __mul24(zp, x[t]->gs[g])), bs[t]);
         }
+        __builtin_amdgcn_sched_barrier(0);            // one group's codes live at a time
     }
 }
 
-// NT pairs sorted[c0 ..] against a row's NB blocks in w: canonical block
-// order acc = fma(d_b, blk_b, acc), result to down_pair.
-template <int NB, int NT>
-__device__ __forceinline__ void down_pass(const dec_params &p, const uint32_t *w, uint32_t c0, uint32_t row) {
-    uint32_t pr[NT];
+// 21 dwords of a Q2 block (dword aligned) as five 16-byte loads and one dword.
+__device__ __forceinline__ void load_q2(uint32_t w[21], const uint8_t *p) {
+    const u32x4a4 *q = (const u32x4a4 *)p;
 #pragma unroll
-    for (int t = 0; t < NT; t++) pr[t] = __builtin_amdgcn_readfirstlane(p.sorted[c0 + t]);
-    float acc[DEC_TPC] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-    for (int b = 0; b < NB; b++) {
-        c_act *x[DEC_TPC];
-#pragma unroll
-        for (int t = 0; t < NT; t++) x[t] = (c_act *)((const act_t *)p.midq + (uint64_t)pr[t] * NB + b);
-        float bs[DEC_TPC];
-        q2_block_dots<NT>(w + 21 * b, x, bs);
-#pragma unroll
-        for (int t = 0; t < NT; t++) acc[t] = __builtin_fmaf(x[t]->d, bs[t], acc[t]);
-    }
-#pragma unroll
-    for (int t = 0; t < NT; t++) st_shared(p.down_pair + (uint64_t)pr[t] * p.K + row, acc[t]);
-}
-
-// Routed down of one (group, 64-row tile): lane = row, the row's NB blocks
-// loaded at once (a wave reads one contiguous 64-row span), pairs of the
-// group in passes of up to four.
-template <int NB>
-__device__ void down_item(const dec_params &p, uint32_t g, uint32_t tile) {
-    const uint32_t lane = threadIdx.x & 63u;
-    const uint32_t p0 = p.ginfo[1u + g], p1 = p.ginfo[2u + g], e = p.ginfo[2u + p.G + g];
-    const uint32_t row = tile * DN_TILE + lane;
-    const uint64_t row_bytes = (uint64_t)NB * SF37_Q2_BYTES;
-    const uint32_t *src = (const uint32_t *)(p.down_w + ((uint64_t)e * p.K + row) * row_bytes);
-    constexpr int N = NB * 21, N4 = N / 4;
-    uint32_t w[N];
-    const u32x4a4 *s4 = (const u32x4a4 *)src;
-#pragma unroll
-    for (int i = 0; i < N4; i++) {
-        const u32x4a4 v = s4[i];
+    for (int i = 0; i < 5; i++) {
+        const u32x4a4 v = q[i];
         w[4 * i] = v.x;
         w[4 * i + 1] = v.y;
         w[4 * i + 2] = v.z;
         w[4 * i + 3] = v.w;
     }
-#pragma unroll
-    for (int i = 4 * N4; i < N; i++) w[i] = src[i];
-    for (uint32_t c0 = p0; c0 < p1; c0 += DEC_TPC) {
-        const uint32_t nt = p1 - c0 < DEC_TPC ? p1 - c0 : DEC_TPC;
-        opaque<N>(w);
-        switch (nt) {
-            case 1: down_pass<NB, 1>(p, w, c0, row); break;
-            case 2: down_pass<NB, 2>(p, w, c0, row); break;
-            case 3: down_pass<NB, 3>(p, w, c0, row); break;
-            default: down_pass<NB, 4>(p, w, c0, row); break;
-        }
-    }
+    w[20] = ((const uint32_t *)p)[20];
 }
 
-// Shared down rows for every token: lane = (row, token), the reference's
-// block order acc = acc + (isum * ws) * xs, with the loads of 8 blocks
-// issued before their terms are added.
-__device__ void down_shared_item(const dec_params &p, uint32_t r0, uint32_t nrows) {
-    const uint32_t lane = threadIdx.x & 63u;
-    const uint32_t t = lane % p.T, rl = lane / p.T;
-    const uint32_t row = r0 + (rl < nrows ? rl : 0u), nb8 = p.F / 32u;
-    const uint8_t *wr = p.sh_down + (uint64_t)row * nb8 * SF37_Q8_0_BYTES;
-    const int8_t *xq = p.sh_mq + (uint64_t)t * p.F;
-    const float *xs = p.sh_ms + (uint64_t)t * nb8;
-    float acc = 0.0f;
-    for (uint32_t b0 = 0; b0 < nb8; b0 += 8u) {
-        uint32_t raw[8][10], xv[8][8];
-        float xsc[8];
+// Block values of one Q2 block (21 dwords in a) against NT activation blocks
+// in LDS (Q2 act layout): bs[t] = sum_g fma(s_g, I_g).
+template <int NT>
+__device__ __forceinline__ void q2_block_dots_lds(const uint32_t *a, const act_t *const *x, float bs[4]) {
 #pragma unroll
-        for (int j = 0; j < 8; j++) {
-            const uint32_t b = b0 + j < nb8 ? b0 + j : nb8 - 1u;
-            const uint8_t *blk = wr + (uint64_t)b * SF37_Q8_0_BYTES;
-            const uint32_t *wp = (const uint32_t *)(blk - ((uintptr_t)blk & 3u));
+    for (int t = 0; t < NT; t++) bs[t] = 0.0f;
 #pragma unroll
-            for (int k = 0; k < 10; k++) raw[j][k] = wp[k];
-            const u32x4 *xp = (const u32x4 *)(xq + (uint64_t)b * 32u);
-            const u32x4 x0 = xp[0], x1 = xp[1];
-            xv[j][0] = x0.x; xv[j][1] = x0.y; xv[j][2] = x0.z; xv[j][3] = x0.w;
-            xv[j][4] = x1.x; xv[j][5] = x1.y; xv[j][6] = x1.z; xv[j][7] = x1.w;
-            xsc[j] = xs[b];
-        }
+    for (int g = 0; g < 4; g++) {
+        uint32_t c[16];
 #pragma unroll
-        for (int j = 0; j < 8; j++) {
-            if (b0 + j < nb8) {
-                const uint32_t o = (uint32_t)((uintptr_t)(wr + (uint64_t)(b0 + j) * SF37_Q8_0_BYTES) & 3u);
-                uint32_t a[9];
+        for (int j = 0; j < 4; j++) q2_unpack16(a[3 + 4 * g + j], c[4 * j], c[4 * j + 1], c[4 * j + 2], c[4 * j + 3]);
+        const int32_t zp = (int32_t)((a[2] >> (8 * g)) & 3u);
+        const float sc = sf37_f16(a[g >> 1] >> (16 * (g & 1)));
 #pragma unroll
-                for (int k = 0; k < 9; k++) a[k] = align_bytes(raw[j][k + 1], raw[j][k], o);
-                int32_t isum = 0;
+        for (int t = 0; t < NT; t++) {
+            const u32x4 *xq = (const u32x4 *)&x[t]->qs[16 * g];
+            int32_t acc = 0;
 #pragma unroll
-                for (int k = 0; k < 8; k++) isum = sdot4(align_bytes(a[k + 1], a[k], 2), xv[j][k], isum);
-                acc = acc + (float)isum * sf37_f16(a[0]) * xsc[j];
+            for (int h = 0; h < 4; h++) {
+                const u32x4 v = xq[h];
+                acc = sdot4(c[4 * h], v.x, acc);
+                acc = sdot4(c[4 * h + 1], v.y, acc);
+                acc = sdot4(c[4 * h + 2], v.z, acc);
+                acc = sdot4(c[4 * h + 3], v.w, acc);
             }
+            bs[t] = __builtin_fmaf(sc, (float)(acc - __mul24(zp, x[t]->gs[g])), bs[t]);
         }
+        __builtin_amdgcn_sched_barrier(0);            // one group's codes live at a time
     }
-    if (rl < nrows) st_shared(p.sh_out + (uint64_t)t * p.K + row, acc);
 }
 
-// Waves take items in order: [0, n_sh) shared-down spans of rpw rows, then
-// ng * K/64 routed (group, tile) items.  Arrivals count rows; a tile is
-// complete at 64 rows per group (+ 64 for the shared expert), and its last
-// wave writes out.
+// acc = fma(d_b, bs_b, acc) along the nb lanes of each row segment (lane
+// blocks 0..nb-1 of one row are consecutive lanes inside a 16-lane DPP
+// row); the row's total ends in the lane of block nb-1.
+__device__ __forceinline__ float seg_chain(float d, float bs, uint32_t b, uint32_t nb) {
+    float acc = __builtin_fmaf(d, bs, 0.0f);
+    for (uint32_t st = 1; st < nb; st++) {
+        const float prev =
+            __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, acc), 0x111, 0xf, 0xf, true));
+        acc = __builtin_fmaf(d, bs, b == 0u ? 0.0f : prev);
+    }
+    return acc;
+}
+
+// Routed down.  Lane = (row, block): each 16-lane DPP row holds 16/nb rows
+// with their nb blocks on consecutive lanes, so a wave reads 64/nb*4 rows
+// (12 for F = 1280) as one contiguous span.  A wave owns a contiguous range
+// of these sub-items (mostly inside one group); the group's activation
+// blocks for up to four pairs sit in the wave's LDS slice.  The next
+// sub-item's blocks are loaded while the current one is computed.
 __global__ void __launch_bounds__(256) dec_down_kernel(dec_params p) {
-    const uint32_t tiles = p.K / DN_TILE, ng = p.ginfo[0];
-    const bool sh = (p.flags & SF37_DEC_SHARED) != 0;
-    const uint32_t rpw = 64u / p.T;                                 // shared rows per wave
-    const uint32_t spt = (DN_TILE + rpw - 1u) / rpw;                // shared items per tile
-    const uint32_t n_sh = sh ? tiles * spt : 0u;
-    const uint32_t n_items = n_sh + ng * tiles;
-    const uint32_t target = DN_TILE * (ng + (sh ? 1u : 0u));
-    const uint32_t nbF = p.F / SF37_QK;
-    const uint32_t nw = gridDim.x * (blockDim.x >> 6);
-    for (uint32_t item = blockIdx.x * (blockDim.x >> 6) + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-         item < n_items; item += nw) {
-        uint32_t tile, rows;
-        if (item < n_sh) {
-            tile = item / spt;
-            const uint32_t k = item - tile * spt, r0 = k * rpw;
-            rows = DN_TILE - r0 < rpw ? DN_TILE - r0 : rpw;
-            down_shared_item(p, tile * DN_TILE + r0, rows);
-        } else {
-            const uint32_t it = item - n_sh, g = it / tiles;
-            tile = it - g * tiles;
-            rows = DN_TILE;
-            switch (nbF) {
-                case 1: down_item<1>(p, g, tile); break;
-                case 2: down_item<2>(p, g, tile); break;
-                case 3: down_item<3>(p, g, tile); break;
-                case 4: down_item<4>(p, g, tile); break;
-                default: down_item<5>(p, g, tile); break;
+    __shared__ uint32_t meta[3u + 2u * 256u + 256u];
+    __shared__ __align__(16) act_t xsl[4][DN_TPC * DN_MAX_NB];
+    const uint32_t P = p.T * p.topk;
+    uint32_t *gi = meta;
+    uint32_t *so = gi + 3u + 2u * p.G;
+    for (uint32_t i = threadIdx.x; i < 3u + 2u * p.G; i += blockDim.x) gi[i] = p.ginfo[i];
+    for (uint32_t i = threadIdx.x; i < P; i += blockDim.x) so[i] = p.sorted[i];
+    __syncthreads();
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63u;
+    act_t *xw = xsl[wave];
+    const uint32_t nb = p.F / SF37_QK, rpd = 16u / nb, rpw = 4u * rpd;     // rows per DPP row / wave
+    const uint32_t q = lane & 15u, r_in = q / nb, b = q - r_in * nb;
+    const bool active = r_in < rpd;
+    const uint32_t rl = (lane >> 4) * rpd + (active ? r_in : 0u);          // row within the sub-item
+    const uint32_t spg = (p.K + rpw - 1u) / rpw, n_sub = gi[0] * spg;
+    const uint32_t nw = gridDim.x * (blockDim.x >> 6), gw = blockIdx.x * (blockDim.x >> 6) + wave;
+    const uint32_t lo = (uint32_t)((uint64_t)n_sub * gw / nw), hi = (uint32_t)((uint64_t)n_sub * (gw + 1u) / nw);
+    if (lo >= hi) return;
+    const uint64_t row_bytes = (uint64_t)nb * SF37_Q2_BYTES;
+    auto blk_ptr = [&](uint32_t sidx) -> const uint8_t * {
+        const uint32_t g = sidx / spg, sub = sidx - g * spg;
+        uint32_t row = sub * rpw + rl;
+        row = row < p.K ? row : p.K - 1u;                                    // keep tail lanes in bounds
+        return p.down_w + ((uint64_t)gi[2u + p.G + g] * p.K + row) * row_bytes + (uint64_t)b * SF37_Q2_BYTES;
+    };
+    uint32_t staged_g = 0xffffffffu, staged_c0 = 0xffffffffu;
+    uint32_t nxt[21];
+    load_q2(nxt, blk_ptr(lo));
+    for (uint32_t sidx = lo; sidx < hi; sidx++) {
+        uint32_t w[21];
+#pragma unroll
+        for (int i = 0; i < 21; i++) w[i] = nxt[i];
+        if (sidx + 1u < hi) load_q2(nxt, blk_ptr(sidx + 1u));
+        const uint32_t g = sidx / spg, sub = sidx - g * spg;
+        const uint32_t row = sub * rpw + rl;
+        const bool out_lane = active && b == nb - 1u && row < p.K;
+        const uint32_t p0 = gi[1u + g], p1 = gi[2u + g];
+        for (uint32_t c0 = p0; c0 < p1; c0 += DN_TPC) {
+            const uint32_t nt = p1 - c0 < DN_TPC ? p1 - c0 : DN_TPC;
+            if (g != staged_g || c0 != staged_c0) {
+                // stage this pass's activation blocks (nt pairs x nb blocks)
+                __builtin_amdgcn_wave_barrier();
+                const uint32_t words = nt * nb * (uint32_t)(sizeof(act_t) / 16u);
+                for (uint32_t i = lane; i < words; i += 64u) {
+                    const uint32_t per = nb * (uint32_t)(sizeof(act_t) / 16u);
+                    const uint32_t t = i / per, k = i - t * per;
+                    ((u32x4 *)xw)[i] = ((const u32x4 *)((const act_t *)p.midq + (uint64_t)so[c0 + t] * nb))[k];
+                }
+                asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+                __builtin_amdgcn_wave_barrier();
+                staged_g = g;
+                staged_c0 = c0;
+            }
+            opaque<21>(w);
+            const act_t *x[DEC_TPC];
+#pragma unroll
+            for (uint32_t t = 0; t < DEC_TPC; t++) x[t] = xw + (t < nt ? t : 0u) * nb + b;
+            float bs[DEC_TPC];
+            if (nt == 1) q2_block_dots_lds<1>(w, x, bs);
+            else q2_block_dots_lds<2>(w, x, bs);
+#pragma unroll
+            for (uint32_t t = 0; t < DN_TPC; t++) {
+                if (t < nt) {
+                    const float acc = seg_chain(x[t]->d, bs[t], b, nb);
+                    if (out_lane) p.down_pair[(uint64_t)so[c0 + t] * p.K + row] = acc;
+                }
             }
         }
-        if (wave_arrive(cnt_dn(p) + tile, rows, target)) {
-            tile_combine(p, tile);
-            if ((threadIdx.x & 63u) == 0) cnt_dn(p)[tile] = 0u;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// combine: out = shared + sum over slots (slot order); lane = (row, token).
+// With the shared expert the lane first runs its shared-down row: the span's
+// rows are copied to the wave's LDS buffer and the reference's block order
+// acc = acc + (isum * ws) * xs is followed (sf37_ops.c:92-108).
+// ---------------------------------------------------------------------------
+__global__ void __launch_bounds__(DN_WG_WAVES * 64) dec_combine_kernel(dec_params p) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63u;
+    uint8_t *buf = smem + wave * dn_buf_bytes(p.F);
+    const bool sh = (p.flags & SF37_DEC_SHARED) != 0;
+    const uint32_t rpw = sh_dn_rows(p.F, p.T);
+    const uint32_t n_items = (p.K + rpw - 1u) / rpw;
+    const uint32_t nw = gridDim.x * (blockDim.x >> 6);
+    const uint32_t t = lane % p.T, rl = lane / p.T;
+    const uint32_t nb8 = p.F / 32u, row_bytes = nb8 * SF37_Q8_0_BYTES;
+    for (uint32_t item = blockIdx.x * (blockDim.x >> 6) + wave; item < n_items; item += nw) {
+        const uint32_t r0 = item * rpw, nrows = p.K - r0 < rpw ? p.K - r0 : rpw;
+        const uint32_t rc = rl < nrows ? rl : 0u, row = r0 + rc;
+        // slot values first (independent loads, issued together)
+        float v[16];
+#pragma unroll
+        for (int s = 0; s < 16; s++) {
+            const uint32_t sc = (uint32_t)s < p.topk ? (uint32_t)s : 0u;   // every read in bounds
+            v[s] = p.down_pair[((uint64_t)t * p.topk + sc) * p.K + row];
         }
+        float acc = 0.0f;
+        if (sh) {
+            const uint32_t off = wave_lds_copy(buf, p.sh_down + (uint64_t)r0 * row_bytes, nrows * row_bytes);
+            wave_lds_wait();
+            const int8_t *xq = p.sh_mq + (uint64_t)t * p.F;
+            const float *xs = p.sh_ms + (uint64_t)t * nb8;
+            const uint32_t base = off + rc * row_bytes;
+            for (uint32_t b0 = 0; b0 < nb8; b0 += 8u) {
+                uint32_t xv[8][8];
+                float xsc[8];
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    const uint32_t b = b0 + j < nb8 ? b0 + j : nb8 - 1u;
+                    const u32x4 *xp = (const u32x4 *)(xq + (uint64_t)b * 32u);
+                    const u32x4 x0 = xp[0], x1 = xp[1];
+                    xv[j][0] = x0.x; xv[j][1] = x0.y; xv[j][2] = x0.z; xv[j][3] = x0.w;
+                    xv[j][4] = x1.x; xv[j][5] = x1.y; xv[j][6] = x1.z; xv[j][7] = x1.w;
+                    xsc[j] = xs[b];
+                }
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    if (b0 + j < nb8) {
+                        uint32_t q[8];
+                        const float wsc = q8_0_lds(buf, base + (b0 + j) * SF37_Q8_0_BYTES, q);
+                        int32_t isum = 0;
+#pragma unroll
+                        for (int k = 0; k < 8; k++) isum = sdot4(q[k], xv[j][k], isum);
+                        acc = acc + (float)isum * wsc * xsc[j];
+                    }
+                }
+            }
+            // the next item's copy must not overwrite rows still being read
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            __builtin_amdgcn_wave_barrier();
+        }
+        float r = 0.0f;
+#pragma unroll
+        for (int s = 0; s < 16; s++)
+            if ((uint32_t)s < p.topk) r = r + v[s];
+        if (rl < nrows) p.out[(uint64_t)t * p.K + row] = sh ? acc + r : r;
     }
 }
 
@@ -682,8 +756,8 @@ __global__ void __launch_bounds__(256) dec_down_kernel(dec_params p) {
 namespace {
 
 struct dec_shape {
-    uint32_t n_router, n_xq, n_shup, n_up, n_mid, n_dn;
-    size_t lds_up, lds_shup;
+    uint32_t n_router, n_xq, n_shup, n_up, n_mid, n_dn, n_cb;
+    size_t lds_up, lds_shup, lds_dn;
 };
 
 uint32_t device_cus() {
@@ -708,7 +782,22 @@ uint32_t device_max_lds() {
     return (uint32_t)lds;
 }
 
-constexpr uint32_t LDS_PER_CU = 160u * 1024u;
+// Workgroups of this kernel one CU holds at once (from the occupancy
+// calculator, at least 1), cached per (kernel, block size, LDS bytes).
+// Dynamic LDS above 64 KiB is opted into first.
+uint32_t resident_wgs(const void *fn, int threads, size_t lds) {
+    struct entry { const void *fn; int threads; size_t lds; uint32_t n; };
+    static entry cache[16];
+    static int used = 0;
+    for (int i = 0; i < used; i++)
+        if (cache[i].fn == fn && cache[i].threads == threads && cache[i].lds == lds) return cache[i].n;
+    if (lds > 65536u) (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, threads, lds) != hipSuccess || n < 1) n = 1;
+    (void)hipGetLastError();
+    if (used < 16) cache[used++] = {fn, threads, lds, (uint32_t)n};
+    return (uint32_t)n;
+}
 
 dec_shape dec_plan(const dec_params &p) {
     dec_shape d;
@@ -721,20 +810,22 @@ dec_shape dec_plan(const dec_params &p) {
     d.lds_shup = lds_up_shared(p.K, p.T);
     d.n_shup = sh ? p.F / SH_RS : 0u;
     // every up workgroup resident at once: at most 3 per CU, fewer if LDS-bound
-    uint32_t per_cu = (uint32_t)(LDS_PER_CU / (d.lds_up + 512u));
-    per_cu = per_cu > 3u ? 3u : per_cu < 1u ? 1u : per_cu;
-    d.n_up = per_cu * cus;
+    // persistent kernels: exactly as many workgroups as can be resident
+    d.n_up = resident_wgs((const void *)dec_up_kernel, 256, d.lds_up) * cus;
     const uint32_t n_mid_waves = p.T * p.topk * (p.F / SF37_QK) + (sh ? (p.T * (p.F / 32u) + 1u) / 2u : 0u);
     d.n_mid = (n_mid_waves + 3u) / 4u;
-    d.n_dn = 2u * cus;
+    d.lds_dn = 0;
+    d.n_dn = resident_wgs((const void *)dec_down_kernel, 256, 0) * cus;
+    const uint32_t cb_items = (p.K + sh_dn_rows(p.F, p.T) - 1u) / sh_dn_rows(p.F, p.T);
+    d.n_cb = (cb_items + DN_WG_WAVES - 1u) / DN_WG_WAVES;
     return d;
 }
 
 }  // namespace
 
 extern "C" int sf37k_decode_counters(uint32_t T, uint32_t topk, uint32_t E, uint32_t K, uint32_t F) {
-    (void)T; (void)topk; (void)E; (void)F;
-    return (int)(CNT_FIXED + K / DN_TILE);
+    (void)T; (void)topk; (void)E; (void)F; (void)K;
+    return (int)CNT_FIXED;
 }
 
 extern "C" int sf37k_decode_supported(uint32_t T, uint32_t topk, uint32_t E, uint32_t K, uint32_t F, int shared) {
@@ -791,5 +882,15 @@ extern "C" int sf37k_decode_mid(const sf37_dec_params *pp, sf37_stream_t s) {
 extern "C" int sf37k_decode_down(const sf37_dec_params *pp, sf37_stream_t s) {
     const dec_shape d = dec_plan(*pp);
     hipLaunchKernelGGL(dec_down_kernel, dim3(d.n_dn), dim3(256), 0, (hipStream_t)s, *pp);
+    return (int)hipGetLastError();
+}
+
+extern "C" int sf37k_decode_combine(const sf37_dec_params *pp, sf37_stream_t s) {
+    const dec_shape d = dec_plan(*pp);
+    const size_t lds = (pp->flags & SF37_DEC_SHARED) ? (size_t)DN_WG_WAVES * dn_buf_bytes(pp->F) : 0u;
+    static size_t opted = 65536;
+    const int err = set_lds((const void *)dec_combine_kernel, lds, &opted);
+    if (err) return err;
+    hipLaunchKernelGGL(dec_combine_kernel, dim3(d.n_cb), dim3(DN_WG_WAVES * 64), lds, (hipStream_t)s, *pp);
     return (int)hipGetLastError();
 }

@@ -87,7 +87,7 @@ static hipEvent_t g_prof_open;
 
 static const char *const k_stage_names[SF37_HIP_N_STAGES] = {
     "router", "select", "q8_0_act", "q8_0_gemm", "swiglu", "q8k_x", "dispatch",
-    "gate_up", "q8k_mid", "down", "combine", "add", "other", "dec_route", "dec_up", "dec_down", "dec_shared_up", "dec_mid"};
+    "gate_up", "q8k_mid", "down", "combine", "add", "other", "dec_route", "dec_up", "dec_down", "dec_shared_up", "dec_mid", "dec_combine"};
 
 static void prof_begin(void) {
     if (!g_prof_on) return;
@@ -1013,7 +1013,8 @@ static int decode_run(const routed_args *a, const dec_extra *ex, float *out, flo
            (!sh || LAUNCH(SF37_HIP_STAGE_DEC_SHARED_UP, sf37k_decode_shared_up(&p, st), "decode shared up launch")) &&
            LAUNCH(SF37_HIP_STAGE_DEC_UP, sf37k_decode_up(&p, st), "decode up launch") &&
            LAUNCH(SF37_HIP_STAGE_DEC_MID, sf37k_decode_mid(&p, st), "decode mid launch") &&
-           LAUNCH(SF37_HIP_STAGE_DEC_DOWN, sf37k_decode_down(&p, st), "decode down launch");
+           LAUNCH(SF37_HIP_STAGE_DEC_DOWN, sf37k_decode_down(&p, st), "decode down launch") &&
+           LAUNCH(SF37_HIP_STAGE_DEC_COMBINE, sf37k_decode_combine(&p, st), "decode combine launch");
 }
 
 /* fp32-activation path for one token (sf37_cuda.cu:5382-5446). */

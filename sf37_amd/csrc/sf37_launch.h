@@ -94,8 +94,8 @@ int sf37k_synth_quant_rows(int type, uint8_t *dst, uint64_t row0, uint64_t nrows
 /* Elementwise exp/sigmoid of a float array (for exhaustive parity tests). */
 int sf37k_sigmoid_array(float *out, const float *x, uint64_t n, int mode, sf37_stream_t s);
 
-/* Fused decode layer (up to 16 tokens): route, shared_up, up, mid, down
- * (k_decode.hip).  Pointers are device addresses; flags select the parts
+/* Fused decode layer (up to 16 tokens): route, shared_up, up, mid, down,
+ * combine (k_decode.hip).  Pointers are device addresses; flags select the parts
  * that run.  cnt holds sf37k_decode_counters(...) zero-initialised words
  * that the kernels leave zero again when they finish. */
 #define SF37_DEC_MAX_TOK 16u
@@ -139,6 +139,7 @@ int sf37k_decode_shared_up(const sf37_dec_params *p, sf37_stream_t s);
 int sf37k_decode_up(const sf37_dec_params *p, sf37_stream_t s);
 int sf37k_decode_mid(const sf37_dec_params *p, sf37_stream_t s);
 int sf37k_decode_down(const sf37_dec_params *p, sf37_stream_t s);
+int sf37k_decode_combine(const sf37_dec_params *p, sf37_stream_t s);
 
 #ifdef __cplusplus
 }
