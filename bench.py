@@ -7,7 +7,8 @@ Q8_0 shared expert, router logits injected i.i.d. N(0,1) (uniform routing).
 A step is the whole layer on device-resident inputs: router GEMV over the 8
 tokens (computed although the injected logits drive the selection), top-8
 selection, shared expert, routed experts, shared + routed.  With the fused
-decode path that is three kernel launches.
+decode path that is six kernel launches (route, select, up, mid, down,
+combine).
 
 Steps rotate over --layers independently seeded layers (each with its own
 input tokens), so consecutive steps never reuse weights and the 256 MB
@@ -131,18 +132,23 @@ def main():
         sh_gu = lay.sh_gate.nbytes + lay.sh_up.nbytes
         nb, nbf = K // 256, F // 256
         kern_bytes.append({
-            # router weights + x in; logits, x activation blocks (288 B) and Q8_0 of x out
-            "dec_route": lay.router_bytes() + n_tok * K * 4 + n_tok * E * 4 + n_tok * nb * 288
+            # router weights + x in; logits, selection candidates (12 B), x activation
+            # blocks (288 B) and Q8_0 of x out
+            "dec_route": lay.router_bytes() + n_tok * K * 4 + n_tok * E * (4 + 12) + n_tok * nb * 288
                          + n_tok * K + n_tok * (K // 32) * 4,
-            # shared gate/up weights + Q8_0 x in, gate/up rows out
-            "dec_shared_up": sh_gu + n_tok * K + n_tok * (K // 32) * 4 + 2 * n_tok * F * 4,
-            # routed gate/up weights of the distinct experts + x blocks in, mid out
-            "dec_up": distinct * GATE_UP_EXPERT_BYTES + n_tok * nb * 288 + P * F * 4,
-            # mid in, activation blocks out; shared gate/up in, Q8_0 mid out
-            "dec_mid": P * F * 4 + P * nbf * 288 + 2 * n_tok * F * 4 + n_tok * F + n_tok * (F // 32) * 4,
-            # routed + shared down weights, mid blocks in, per-pair rows out and back, out
-            "dec_down": distinct * DOWN_EXPERT_BYTES + lay.sh_down.nbytes + P * nbf * 288 + n_tok * F
-                        + P * K * 4 * 2 + n_tok * K * 4 * 3,
+            # candidates in, selections out; shared gate/up weights + Q8_0 x in, gate/up rows out
+            "dec_select": n_tok * E * 12 + P * 8 + sh_gu + n_tok * K + n_tok * (K // 32) * 4
+                          + 2 * n_tok * F * 4,
+            # routed gate/up weights of the distinct experts + x blocks in, gate/up rows out
+            "dec_up": distinct * GATE_UP_EXPERT_BYTES + n_tok * nb * 288 + 2 * P * F * 4,
+            # gate/up rows in, mid and its activation blocks out
+            "dec_mid": 2 * P * F * 4 + P * F * 4 + P * nbf * 288,
+            # shared gate/up in, Q8_0 shared mid out; routed down weights + mid blocks in,
+            # per-pair rows out
+            "dec_down": 2 * n_tok * F * 4 + n_tok * F + n_tok * (F // 32) * 4
+                        + distinct * DOWN_EXPERT_BYTES + P * nbf * 288 + P * K * 4,
+            # shared down weights + Q8_0 shared mid in, per-pair rows in, out
+            "dec_combine": lay.sh_down.nbytes + n_tok * F + n_tok * (F // 32) * 4 + P * K * 4 + n_tok * K * 4,
         })
     hip.synchronize()
 
@@ -167,7 +173,7 @@ def main():
         step(i)
     prof = hip.profile_read()
     L.sf37_hip_profile_enable(0)
-    kern = max(("dec_route", "dec_shared_up", "dec_up", "dec_mid", "dec_down"), key=lambda k: prof[k][0])
+    kern = max(("dec_route", "dec_select", "dec_up", "dec_mid", "dec_down", "dec_combine"), key=lambda k: prof[k][0])
     k_ms, k_n = prof[kern]
     if k_n == 0:
         raise SystemExit("bench.py: the fused decode kernels did not run")

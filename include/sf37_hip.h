@@ -284,12 +284,13 @@ enum {
     SF37_HIP_STAGE_SWIGLU, SF37_HIP_STAGE_Q8K_X, SF37_HIP_STAGE_DISPATCH, SF37_HIP_STAGE_GATE_UP,
     SF37_HIP_STAGE_Q8K_MID, SF37_HIP_STAGE_DOWN, SF37_HIP_STAGE_COMBINE, SF37_HIP_STAGE_ADD,
     SF37_HIP_STAGE_OTHER,
-    /* the fused decode layer (up to 16 tokens): route = router GEMV + x
-     * quantisation + top-k + grouping, up = routed gate/up with SwiGLU,
-     * down = routed down, shared_up = shared gate/up, mid = quantisation of
-     * the routed and shared mid, combine = shared down + slot-order sum */
+    /* the fused decode layer (up to 16 tokens): route = router GEMV +
+     * selection candidates + x quantisation, select = top-k + grouping and
+     * the shared gate/up, up = routed gate/up, mid = SwiGLU + Q8_K of the
+     * routed mid, down = Q8_0 of the shared mid + routed down, combine =
+     * shared down + slot-order sum */
     SF37_HIP_STAGE_DEC_ROUTE, SF37_HIP_STAGE_DEC_UP, SF37_HIP_STAGE_DEC_DOWN,
-    SF37_HIP_STAGE_DEC_SHARED_UP, SF37_HIP_STAGE_DEC_MID, SF37_HIP_STAGE_DEC_COMBINE,
+    SF37_HIP_STAGE_DEC_SELECT, SF37_HIP_STAGE_DEC_COMBINE, SF37_HIP_STAGE_DEC_MID,
     SF37_HIP_N_STAGES
 };
 int sf37_hip_profile_enable(int on);

@@ -1,24 +1,25 @@
 // k_decode.hip - the MoE layer for decode batches (up to 16 tokens) on
-// gfx950, in five launches on one stream:
+// gfx950, in six launches on one stream:
 //
-//   route     : router GEMV (binary64 accumulation) and the Q8_K / Q8_0
-//               quantisation of x; the last workgroup to finish runs top-k
-//               for every token, groups the (token, slot) pairs by expert
-//               and clears the down kernel's tile counters.
-//   shared_up : the shared expert's Q8_0 gate/up rows (LDS tiles).
-//   up        : routed Q3 gate/up with SwiGLU * routing weight; a lane owns
-//               one 110-byte block, a wave two rows of gate and up, and the
-//               canonical block-order chain runs as a DPP scan.
-//   mid       : Q8_K of the routed mid, SwiGLU + Q8_0 of the shared mid.
-//   down      : routed Q2 down (lane = row, activations through the scalar
-//               cache) and the shared Q8_0 down; the last wave of each
-//               64-row tile forms out = shared + sum over slots in slot order.
+//   route   : router GEMV (binary64 accumulation) and each expert's
+//             selection candidate (sigmoid, key), the Q8_K / Q8_0
+//             quantisation of x.
+//   select  : one workgroup runs top-k for every token and groups the
+//             (token, slot) pairs by expert; the others compute the shared
+//             expert's Q8_0 gate/up rows (LDS tiles).
+//   up      : routed Q3 gate/up: a lane owns one 110-byte block, a wave two
+//             rows of gate and up, and the canonical block-order chain runs
+//             as a DPP scan; items come from atomic queues.
+//   mid     : SwiGLU * routing weight and the Q8_K of the routed mid.
+//   down    : the first waves apply SwiGLU to the shared gate/up and
+//             quantise the shared mid to Q8_0; then routed Q2 down, one row
+//             per pair and output row.
+//   combine : the shared expert's down rows (one wave per row group) and
+//             out = shared + sum over slots in slot order.
 //
-// Hand-offs inside a launch (logits to the top-k workgroup, per-pair down
-// rows to the combining wave) use agent-coherent stores and loads and an
-// atomic arrival counter; the workgroup or wave that completes a counter
-// does the dependent work and resets it.  Nothing waits on another
-// workgroup, so every wave always runs to completion.
+// Nothing waits on another wave, so every wave always runs to completion;
+// the up kernel's queues hand out each item once and every wave stops at
+// its first request past the end of its queue.
 //
 // Arithmetic is the canonical order of the oracle (sf37_blocks.h), the
 // reference CPU order for the Q8_0 shared expert (sf37_ops.c:92-108), and
@@ -32,45 +33,20 @@ namespace {
 constexpr uint32_t DEC_MAX_TOK = 16;
 constexpr uint32_t DEC_TPC = 4;      // pairs per pass in the routed kernels
 constexpr uint32_t SH_RS = 2;        // shared gate/up rows per workgroup
-constexpr uint32_t DN_TILE = 64;     // down rows per item (= combine tile)
+constexpr uint32_t RT_ROWS = 2;      // router rows (experts) per route workgroup
 constexpr uint32_t DN_MAX_NB = 5;    // down blocks per row held in registers (F <= 1280)
-constexpr uint32_t DN_WG_WAVES = 2;  // waves per combine workgroup (one LDS tile each)
 constexpr uint32_t DN_TPC = 2;       // pairs per pass in the routed down kernel
+constexpr uint32_t SHD_CHUNK = 4;    // shared-down Q8_0 blocks per load batch (even)
+constexpr uint32_t SHD_MAX_BPS = 12; // shared-down blocks per lane (a multiple of SHD_CHUNK)
+constexpr uint32_t UP_QUEUES = 64;   // queues of the up kernel's dynamic items, one per 128 bytes
+constexpr uint32_t UP_DYN_PCT = 25;  // share of the up items handed out dynamically (percent)
+constexpr uint32_t CB_PASSES = 2;    // shared-down row groups per combine wave
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4a4 __attribute__((ext_vector_type(4), aligned(4)));
-// Activation blocks read through the scalar cache (every lane of a wave
-// reads the same block): constant address space, so loads become s_load.
-typedef const __attribute__((address_space(4))) act_t c_act;
 
 __device__ __forceinline__ uint32_t clamp_expert(int32_t e, uint32_t n) {
     return (e < 0 || (uint32_t)e >= n) ? 0u : (uint32_t)e;
-}
-
-// Data that one workgroup hands to another inside a launch is written and
-// read with agent-scope accesses (global_store/load ... sc1): the store is
-// acknowledged once it is coherent across all XCDs and the load bypasses the
-// XCD-local caches, so no cache-wide writeback or invalidate is needed.
-__device__ __forceinline__ void st_shared(float *p, float v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float ld_shared(const float *p) {
-    return __hip_atomic_load(const_cast<float *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Arrival at a counter: every wave waits for its stores to be acknowledged,
-// then thread 0 counts the workgroup.  Returns true in every thread of the
-// workgroup that completed the count.  Loads after a true return that read
-// other workgroups' data go through ld_shared.
-__device__ __forceinline__ bool arrive_last(uint32_t *counter, uint32_t target, int *flag) {
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        const uint32_t old = atomicAdd(counter, 1u);
-        *flag = (old + 1u == target) ? 1 : 0;
-    }
-    __syncthreads();
-    return *flag != 0;
 }
 
 }  // namespace
@@ -79,26 +55,26 @@ using dec_params = sf37_dec_params;
 
 namespace {
 
-// counter layout: [0] route arrivals, [1..3) reserved
-constexpr uint32_t CNT_FIXED = 3;
+// Counters: the up kernel's item queues, 32 words apart (zeroed by the
+// select workgroup).
+__device__ __forceinline__ uint32_t *up_queue(const dec_params &p, uint32_t q) { return p.cnt + 32u * q; }
+
+// Shared-down lane layout: the Q8_0 blocks of a row are split into S slices
+// (a power of two <= 16 with S * T <= 64, so one token's slices sit in one
+// 16-lane DPP row); lane = (row, token, slice).
+__host__ __device__ constexpr uint32_t shd_slices(uint32_t T) { return T <= 4u ? 16u : (T <= 8u ? 8u : 4u); }
+// Blocks per shared-down slice: ceil(nb8 / S) rounded up to even, so every
+// slice and every load batch starts on a 4-byte boundary (rows are 4-byte
+// aligned: nb8 is even).
+__host__ __device__ constexpr uint32_t shd_bps(uint32_t nb8, uint32_t S) { return ((nb8 + S - 1u) / S + 1u) & ~1u; }
 
 // LDS layout sizes, shared by the kernels and the host-side launch plan.
 // A weight tile buffer holds the tile plus the copy's leading offset.
 __host__ __device__ constexpr uint32_t tile_buf(uint32_t bytes) { return (bytes + 31u + 15u) & ~15u; }
 __host__ __device__ constexpr uint32_t up_shared_tile(uint32_t K) { return SH_RS * (K / 32u) * SF37_Q8_0_BYTES; }
-// down: per-wave tile buffer holding a routed 64-row tile; shared-down
-// items take as many rows as fit (and as the 64 lanes allow for T tokens)
-__host__ __device__ constexpr uint32_t dn_buf_bytes(uint32_t F) {
-    return tile_buf(DN_TILE * (F / SF37_QK) * SF37_Q2_BYTES);
-}
-__host__ __device__ constexpr uint32_t sh_dn_rows(uint32_t F, uint32_t T) {
-    return (64u / T) < (DN_TILE * (F / SF37_QK) * SF37_Q2_BYTES) / ((F / 32u) * SF37_Q8_0_BYTES)
-               ? 64u / T
-               : (DN_TILE * (F / SF37_QK) * SF37_Q2_BYTES) / ((F / 32u) * SF37_Q8_0_BYTES);
-}
-// up workgroup: x of every token, then group info, sorted pairs, weights
+// up workgroup: x of every token, then group info and sorted pairs
 __host__ __device__ constexpr size_t lds_up_routed(uint32_t K, uint32_t T, uint32_t G, uint32_t P) {
-    return (size_t)T * (K / SF37_QK) * sizeof(act_t) + (size_t)(3u + 2u * G + 2u * P) * 4u;
+    return (size_t)T * (K / SF37_QK) * sizeof(act_t) + (size_t)(3u + 2u * G + P) * 4u;
 }
 __host__ __device__ constexpr size_t lds_up_shared(uint32_t K, uint32_t T) {
     return 2u * (size_t)tile_buf(up_shared_tile(K)) + (size_t)T * 2u * SH_RS * (K / 32u) * 4u;
@@ -122,87 +98,119 @@ __device__ __forceinline__ float q8_0_lds(const uint8_t *base, uint32_t L, uint3
 // route
 // ---------------------------------------------------------------------------
 
-__global__ void __launch_bounds__(256) dec_route_kernel(dec_params p, uint32_t n_router) {
-    __shared__ double part[DEC_MAX_TOK][4];
+// Route workgroups [0, n_rt): RT_ROWS experts each - router logits, then
+// each expert's selection candidate per token (p = sigmoid, key of
+// p + bias).  Then workgroups quantising x (one 256-block of one token per
+// wave) to Q8_K for the routed experts and Q8_0 for the shared expert.
+__global__ void __launch_bounds__(256) dec_route_kernel(dec_params p, uint32_t n_rt) {
+    __shared__ double part[RT_ROWS][DEC_MAX_TOK][4];
+    __shared__ float s_logit[RT_ROWS][DEC_MAX_TOK];
     __shared__ uint64_t tab[32];
-    __shared__ uint32_t s_e[DEC_MAX_TOK * 16];
-    __shared__ uint32_t s_less[DEC_MAX_TOK * 16];
-    __shared__ uint32_t s_first[DEC_MAX_TOK * 16];
-    __shared__ uint32_t s_ng;
-    __shared__ int flag;
     const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
     const uint32_t nb = p.K / SF37_QK;
-    if (blockIdx.x < n_router) {
-        const uint32_t e = blockIdx.x;
-        sf37_router_rows(p.router_w + (uint64_t)e * p.K, p.x, p.K, p.T, part);
-        __syncthreads();
-        if (threadIdx.x < p.T) {
-            const uint32_t t = threadIdx.x;
-            st_shared(p.logits + (uint64_t)t * p.E + e, sf37_router_combine(part[t]));
-        }
-    } else {
-        // Q8_K (and Q8_0) of one 256-block of one token per wave
-        const uint32_t wq = (blockIdx.x - n_router) * 4u + wave;
-        if (wq < p.T * nb) {
-            const uint32_t t = wq / nb, b = wq - t * nb;
-            const float *xb = p.x + (uint64_t)t * p.K + (uint64_t)b * SF37_QK + 4u * lane;
-            float v[4];
+    if (blockIdx.x >= n_rt) {
+        const uint32_t wq = (blockIdx.x - n_rt) * 4u + wave;
+        if (wq >= p.T * nb) return;
+        const uint32_t t = wq / nb, b = wq - t * nb;
+        const float *xb = p.x + (uint64_t)t * p.K + (uint64_t)b * SF37_QK + 4u * lane;
+        float v[4];
 #pragma unroll
-            for (int k = 0; k < 4; k++) v[k] = xb[k];
-            int8_t qk[4];
-            int gsum;
-            const float d = q8k_codes4(v, qk, gsum);
-            act_t *y = (act_t *)p.xq + wq;
-            uint8_t *qb = (uint8_t *)y->qs;
+        for (int k = 0; k < 4; k++) v[k] = xb[k];
+        int8_t qk[4];
+        int gsum;
+        const float d = q8k_codes4(v, qk, gsum);
+        act_t *y = (act_t *)p.xq + wq;
+        uint8_t *qb = (uint8_t *)y->qs;
 #pragma unroll
-            for (int k = 0; k < 4; k++) qb[q3x_pos(4u * lane + k)] = (uint8_t)qk[k];
-            if (lane == 0) y->d = d;
-            if ((lane & 15u) == 0) y->gs[lane >> 4] = gsum;
-            if (p.flags & SF37_DEC_SHARED) {
-                // Q8_0 (sf37_ops.c:57-90): a 32-wide block is 8 lanes
-                float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-                amax = fmaxf(amax, __shfl_xor(amax, 4, 64));
-                amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
-                amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
-                float d8 = 0.0f;
-                uint32_t packed = 0;
-                if (amax != 0.0f) {
-                    d8 = amax / 127.0f;
-                    const float is = 1.0f / d8;
+        for (int k = 0; k < 4; k++) qb[q3x_pos(4u * lane + k)] = (uint8_t)qk[k];
+        if (lane == 0) y->d = d;
+        if ((lane & 15u) == 0) y->gs[lane >> 4] = gsum;
+        if (p.flags & SF37_DEC_SHARED) {
+            // Q8_0 (sf37_ops.c:57-90): a 32-wide block is 8 lanes
+            float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+            amax = fmaxf(amax, __shfl_xor(amax, 4, 64));
+            amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+            amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+            float d8 = 0.0f;
+            uint32_t packed = 0;
+            if (amax != 0.0f) {
+                d8 = amax / 127.0f;
+                const float is = 1.0f / d8;
 #pragma unroll
-                    for (int k = 0; k < 4; k++) {
-                        const float r = fminf(fmaxf(__builtin_rintf(is * v[k]), -128.0f), 127.0f);
-                        packed |= (uint32_t)(uint8_t)(int8_t)(int)r << (8 * k);
-                    }
+                for (int k = 0; k < 4; k++) {
+                    const float r = fminf(fmaxf(__builtin_rintf(is * v[k]), -128.0f), 127.0f);
+                    packed |= (uint32_t)(uint8_t)(int8_t)(int)r << (8 * k);
                 }
-                ((uint32_t *)(p.xq8 + (uint64_t)t * p.K + (uint64_t)b * SF37_QK))[lane] = packed;
-                if ((lane & 7u) == 0) p.xs8[(uint64_t)t * (p.K / 32u) + b * 8u + (lane >> 3)] = d8;
+            }
+            ((uint32_t *)(p.xq8 + (uint64_t)t * p.K + (uint64_t)b * SF37_QK))[lane] = packed;
+            if ((lane & 7u) == 0) p.xs8[(uint64_t)t * (p.K / 32u) + b * 8u + (lane >> 3)] = d8;
+        }
+        return;
+    }
+    sf37_stage_exp_tab(tab);
+    const uint32_t e0 = blockIdx.x * RT_ROWS;
+    if (p.flags & SF37_DEC_ROUTER) {
+        const uint32_t nr = p.E - e0 < RT_ROWS ? p.E - e0 : RT_ROWS;
+        sf37_router_rows_n<RT_ROWS>(p.router_w + (uint64_t)e0 * p.K, nr, p.x, p.K, p.T,
+                                    [](uint32_t r, uint32_t t, uint32_t w, double v) { part[r][t][w] = v; });
+        __syncthreads();
+        if (threadIdx.x < RT_ROWS * p.T) {
+            const uint32_t r = threadIdx.x / p.T, t = threadIdx.x - r * p.T;
+            if (e0 + r < p.E) {
+                const float l = sf37_router_combine(part[r][t]);
+                s_logit[r][t] = l;
+                p.logits[(uint64_t)t * p.E + e0 + r] = l;
             }
         }
     }
-    if (!arrive_last(p.cnt, gridDim.x, &flag)) return;
-
-    // ---- last workgroup: clear the next counters, top-k, groups ----------
-    const uint32_t n_clear = CNT_FIXED - 1u;
-    for (uint32_t i = threadIdx.x; i < n_clear; i += blockDim.x) p.cnt[1 + i] = 0u;
-    sf37_stage_exp_tab(tab);
     __syncthreads();
-    if (p.flags & SF37_DEC_SELECT) {
-        // wave w: tokens w, w + 4, ... two at a time
-        for (uint32_t t = wave; t < p.T; t += 8u) {
-            const uint32_t t2 = t + 4u < p.T ? t + 4u : t;
-            const float *lg0 = p.logits_sel + (uint64_t)t * p.E, *lg1 = p.logits_sel + (uint64_t)t2 * p.E;
-            int32_t *so[2] = {p.sel + (uint64_t)t * p.topk, p.sel + (uint64_t)t2 * p.topk};
-            float *wo[2] = {p.wts + (uint64_t)t * p.topk, p.wts + (uint64_t)t2 * p.topk};
-            float *po[2] = {nullptr, nullptr};
-            sf37_wave_topk<2>([lg0, lg1](uint32_t k, uint32_t e) { return ld_shared((k ? lg1 : lg0) + e); },
-                              p.router_bias, p.E, p.topk, p.scale, tab, so, wo, po);
+    if ((p.flags & SF37_DEC_SELECT) && threadIdx.x < RT_ROWS * p.T) {
+        const uint32_t r = threadIdx.x / p.T, t = threadIdx.x - r * p.T, e = e0 + r;
+        if (e < p.E) {
+            const bool own = (p.flags & SF37_DEC_ROUTER) && p.logits_sel == p.logits;
+            const float l = own ? s_logit[r][t] : p.logits_sel[(uint64_t)t * p.E + e];
+            float pr;
+            p.cand_key[(uint64_t)t * p.E + e] = sf37_topk_candidate(l, p.router_bias[e], e, tab, pr);
+            p.cand_p[(uint64_t)t * p.E + e] = pr;
         }
     }
-    __syncthreads();
+}
+
+// ---------------------------------------------------------------------------
+// select + shared gate/up
+// ---------------------------------------------------------------------------
+
+// Top-k of every token from the candidates (SELECT; else sel and wts are
+// inputs), then the (token, slot) pairs grouped by expert: ginfo and
+// sorted for the routed kernels.  One workgroup.
+__device__ void select_and_group(const dec_params &p) {
+    __shared__ uint32_t s_sel[DEC_MAX_TOK * 16];    // selected expert ids (raw)
+    __shared__ uint32_t s_e[DEC_MAX_TOK * 16];      // clamped ids, pair order
+    __shared__ uint32_t s_se[DEC_MAX_TOK * 16];     // clamped ids, sorted order
+    __shared__ uint32_t s_wcnt[4];
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
     const uint32_t P = p.T * p.topk;
-    if (threadIdx.x < P) s_e[threadIdx.x] = clamp_expert(p.sel[threadIdx.x], p.E);
-    if (threadIdx.x == 0) s_ng = 0u;
+    if (p.flags & SF37_DEC_SELECT) {
+        // wave w: tokens w, w + 4, ... two at a time; selections into LDS
+        for (uint32_t t = wave; t < p.T; t += 8u) {
+            const uint32_t t2 = t + 4u < p.T ? t + 4u : t;
+            const uint64_t *k0 = p.cand_key + (uint64_t)t * p.E, *k1 = p.cand_key + (uint64_t)t2 * p.E;
+            const float *p0 = p.cand_p + (uint64_t)t * p.E, *p1 = p.cand_p + (uint64_t)t2 * p.E;
+            int32_t *so[2] = {(int32_t *)s_sel + t * p.topk, (int32_t *)s_sel + t2 * p.topk};
+            float *wo[2] = {p.wts + (uint64_t)t * p.topk, p.wts + (uint64_t)t2 * p.topk};
+            sf37_wave_topk_cand<2>(
+                [k0, k1, p0, p1](uint32_t k, uint32_t e, float &pr) {
+                    pr = (k ? p1 : p0)[e];
+                    return (k ? k1 : k0)[e];
+                },
+                p.E, p.topk, p.scale, so, wo);
+        }
+        __syncthreads();
+        if (threadIdx.x < P) p.sel[threadIdx.x] = (int32_t)s_sel[threadIdx.x];
+    } else if (threadIdx.x < P) {
+        s_sel[threadIdx.x] = (uint32_t)p.sel[threadIdx.x];
+    }
+    if (threadIdx.x < P) s_e[threadIdx.x] = clamp_expert((int32_t)s_sel[threadIdx.x], p.E);
     __syncthreads();
     if (p.flags & SF37_DEC_SLOTS) {
         if (threadIdx.x < p.topk) {
@@ -215,69 +223,102 @@ __global__ void __launch_bounds__(256) dec_route_kernel(dec_params p, uint32_t n
             p.ginfo[0] = p.topk;
             p.ginfo[1u + p.topk] = p.topk;
         }
-    } else {
-        // stable grouping: pairs ordered by (expert, pair id); a group starts
-        // at the first pair of each expert
-        if (threadIdx.x < P) {
-            const uint32_t i = threadIdx.x, e = s_e[i];
-            uint32_t less = 0, eq_before = 0;
-#pragma unroll 8
-            for (uint32_t q = 0; q < P; q++) {
-                const uint32_t f = s_e[q];
-                less += f < e ? 1u : 0u;
-                eq_before += (f == e && q < i) ? 1u : 0u;
-            }
-            p.sorted[less + eq_before] = i;
-            s_less[i] = less;
-            s_first[i] = eq_before == 0u ? 1u : 0u;
-        }
-        __syncthreads();
-        if (threadIdx.x < P && s_first[threadIdx.x]) {
-            const uint32_t i = threadIdx.x, e = s_e[i];
-            uint32_t gi = 0;
-#pragma unroll 8
-            for (uint32_t q = 0; q < P; q++) gi += (s_first[q] && s_e[q] < e) ? 1u : 0u;
-            p.ginfo[1u + gi] = s_less[i];
-            p.ginfo[2u + p.G + gi] = e;
-            atomicAdd(&s_ng, 1u);
-        }
-        __syncthreads();
-        if (threadIdx.x == 0) {
-            p.ginfo[0] = s_ng;
-            p.ginfo[1u + s_ng] = P;
-        }
+        return;
     }
-    if (threadIdx.x == 0) p.cnt[0] = 0u;
+    // stable order by (expert, pair id): position = #pairs with a smaller
+    // expert + #earlier pairs with the same expert
+    if (threadIdx.x < P) {
+        const uint32_t i = threadIdx.x, e = s_e[i];
+        uint32_t pos = 0;
+#pragma unroll 8
+        for (uint32_t q = 0; q < P; q++) {
+            const uint32_t f = s_e[q];
+            pos += (uint32_t)(f < e) + ((uint32_t)(f == e) & (uint32_t)(q < i));
+        }
+        p.sorted[pos] = i;
+        s_se[pos] = e;
+    }
+    __syncthreads();
+    // groups start where the expert changes along the sorted order; the
+    // group index is the count of starts before (ballot prefix per wave)
+    const uint32_t i = threadIdx.x;
+    const bool act = i < P;
+    const uint32_t e = act ? s_se[i] : 0u;
+    const bool start = act && (i == 0u || s_se[i - 1u] != e);
+    const uint64_t m = __ballot(start);
+    const uint32_t below = (uint32_t)__builtin_popcountll(m & ((1ull << lane) - 1ull));
+    if (lane == 0) s_wcnt[wave] = (uint32_t)__builtin_popcountll(m);
+    __syncthreads();
+    uint32_t base = 0;
+    for (uint32_t w = 0; w < wave; w++) base += s_wcnt[w];
+    if (start) {
+        p.ginfo[1u + base + below] = i;
+        p.ginfo[2u + p.G + base + below] = e;
+    }
+    if (i == P - 1u) {
+        const uint32_t ng = base + below + (start ? 1u : 0u);
+        p.ginfo[0] = ng;
+        p.ginfo[1u + ng] = P;
+    }
 }
 
-// ---------------------------------------------------------------------------
-// shared gate/up: one workgroup per SH_RS rows, terms in LDS, then the
+// Workgroup 0: select_and_group.  Workgroups 1.. (with the shared expert):
+// SH_RS shared gate/up rows each - the weight tiles copied to LDS while the
+// x blocks of the first 8 tokens load, the terms in LDS, then the
 // reference's sequential block sum per (matrix, token, row)
-// ---------------------------------------------------------------------------
-__global__ void __launch_bounds__(256) dec_shup_kernel(dec_params p) {
+// (sf37_ops.c:92-108) into sh_gu.
+__global__ void __launch_bounds__(256) dec_select_kernel(dec_params p) {
+    if (blockIdx.x == 0) {
+        if (threadIdx.x < UP_QUEUES) *up_queue(p, threadIdx.x) = 0u;
+        select_and_group(p);
+        return;
+    }
     extern __shared__ __align__(16) unsigned char smem[];
     const uint32_t nb8 = p.K / 32u;
-    const uint32_t row0 = blockIdx.x * SH_RS;
+    const uint32_t row0 = (blockIdx.x - 1u) * SH_RS;
     const uint32_t tbytes = up_shared_tile(p.K), wbuf = tile_buf(tbytes);
     const uint64_t row_bytes = (uint64_t)nb8 * SF37_Q8_0_BYTES;
     uint8_t *wl = smem;                                             // gate tile | up tile
     float *red = (float *)(smem + 2u * wbuf);                       // [T][2][RS][nb8]
     const uint32_t og = lds_copy(wl, p.sh_gate + (uint64_t)row0 * row_bytes, tbytes);
     const uint32_t ou = wbuf + lds_copy(wl + wbuf, p.sh_up + (uint64_t)row0 * row_bytes, tbytes);
-    lds_copy_wait();
-    const uint32_t units = 2u * SH_RS * nb8;
-    for (uint32_t u = threadIdx.x; u < units; u += blockDim.x) {
-        const uint32_t m = u / (SH_RS * nb8);
-        const uint32_t rb = u - m * SH_RS * nb8;
-        const uint32_t r = rb / nb8, b = rb - r * nb8;
-        uint32_t q[8];
-        const float wsc = q8_0_lds(wl, (m ? ou : og) + (r * nb8 + b) * SF37_Q8_0_BYTES, q);
-        for (uint32_t t = 0; t < p.T; t++) {
-            const uint32_t *xv = (const uint32_t *)(p.xq8 + (uint64_t)t * p.K + (uint64_t)b * 32u);
-            int32_t isum = 0;
+    // thread = (row, block) for both matrices; x blocks of 8 tokens at a time
+    u32x4 xa[8], xb[8];
+    float xs[8];
+    auto load_x = [&](uint32_t b, uint32_t t0) {
 #pragma unroll
-            for (int k = 0; k < 8; k++) isum = sdot4(q[k], xv[k], isum);
-            red[((t * 2u + m) * SH_RS + r) * nb8 + b] = (float)isum * wsc * p.xs8[(uint64_t)t * nb8 + b];
+        for (uint32_t j = 0; j < 8u; j++) {
+            const uint32_t t = t0 + j < p.T ? t0 + j : p.T - 1u;
+            const u32x4 *xp = (const u32x4 *)(p.xq8 + (uint64_t)t * p.K + (uint64_t)b * 32u);
+            xa[j] = xp[0];
+            xb[j] = xp[1];
+            xs[j] = p.xs8[(uint64_t)t * nb8 + b];
+        }
+    };
+    if (threadIdx.x < SH_RS * nb8) load_x(threadIdx.x % nb8, 0);
+    lds_copy_wait();
+    for (uint32_t rb = threadIdx.x; rb < SH_RS * nb8; rb += blockDim.x) {
+        const uint32_t r = rb / nb8, b = rb - r * nb8;
+        uint32_t qg[8], qu[8];
+        const float wg = q8_0_lds(wl, og + rb * SF37_Q8_0_BYTES, qg);
+        const float wu = q8_0_lds(wl, ou + rb * SF37_Q8_0_BYTES, qu);
+        for (uint32_t t0 = 0; t0 < p.T; t0 += 8u) {
+            if (rb != threadIdx.x || t0 != 0u) load_x(b, t0);
+#pragma unroll
+            for (uint32_t j = 0; j < 8u; j++) {
+                if (t0 + j < p.T) {
+                    const uint32_t t = t0 + j;
+                    const uint32_t xv[8] = {xa[j].x, xa[j].y, xa[j].z, xa[j].w, xb[j].x, xb[j].y, xb[j].z, xb[j].w};
+                    int32_t ig = 0, iu = 0;
+#pragma unroll
+                    for (int k = 0; k < 8; k++) {
+                        ig = sdot4(qg[k], xv[k], ig);
+                        iu = sdot4(qu[k], xv[k], iu);
+                    }
+                    red[((t * 2u + 0u) * SH_RS + r) * nb8 + b] = (float)ig * wg * xs[j];
+                    red[((t * 2u + 1u) * SH_RS + r) * nb8 + b] = (float)iu * wu * xs[j];
+                }
+            }
         }
     }
     __syncthreads();
@@ -365,36 +406,140 @@ __device__ __forceinline__ void opaque(uint32_t *w) {
     for (int i = 0; i < N; i++) asm volatile("" : "+v"(w[i]));
 }
 
-// An item is 2 rows of one group's expert for both matrices: lane = matrix
-// (gate/up) | row | block, so each wave reads two contiguous 2-row spans.
-// Waves stride over the items (adjacent waves, adjacent rows) and load the
-// next item's blocks while computing the current one.  The x of every token
-// sits in LDS; the gate lane of each row applies SwiGLU * routing weight.
+// Shared down and combine: out[t][row] = shared + sum over slots in slot
+// order, where shared = sum over Q8_0 blocks b in order of
+// (isum_b * ws_b) * xs_b (sf37_ops.c:92-108), for R = 64 / (T * S) rows per
+// pass.  Lane = (row, token, slice): the slice holds bps consecutive blocks,
+// loaded as NB batches of SHD_CHUNK (all issued before the first is used),
+// and computes their terms; the sequential sum then walks the slices in
+// order with row_shr:1 (each slice adds its terms to the previous slice's
+// total).  The shared mid codes and scales of every token are in LDS (xq:
+// T x F codes, then T x F/32 scales).
+template <int NB>
+__device__ __forceinline__ void shared_down_pass(const dec_params &p, const int8_t *xq, const float *xsc, uint32_t r0) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t S = shd_slices(p.T), TS = p.T * S, R = 64u / TS;
+    const uint32_t nb8 = p.F / 32u, bps = shd_bps(nb8, S), ns = (nb8 + bps - 1u) / bps;
+    const uint32_t rsub = lane / TS, li = lane - rsub * TS, t = li / S, j = li - t * S;
+    const bool lane_ok = rsub < R;
+    const uint32_t tc = lane_ok ? t : 0u;
+    const uint64_t row_bytes = (uint64_t)nb8 * SF37_Q8_0_BYTES;
+    const uint32_t row = r0 + (lane_ok ? rsub : 0u);
+    const uint32_t rowc = row < p.K ? row : p.K - 1u;
+    // the routed slot values of (token, row), summed after the shared value
+    float v[16];
+#pragma unroll
+    for (uint32_t s = 0; s < 16u; s++) {
+        const uint32_t sc = s < p.topk ? s : 0u;                     // every read in bounds
+        v[s] = p.down_pair[((uint64_t)tc * p.topk + sc) * p.K + rowc];
+    }
+    uint32_t w[NB][36];
+#pragma unroll
+    for (int c = 0; c < NB; c++) {
+        // blocks [b0, b0 + nv) of this batch; nv = 0 past the slice or row
+        const uint32_t b0 = j * bps + c * SHD_CHUNK;
+        const uint32_t in_slice = bps > c * SHD_CHUNK ? bps - c * SHD_CHUNK : 0u;
+        const uint32_t in_row = nb8 > b0 ? nb8 - b0 : 0u;
+        uint32_t nv = in_slice < in_row ? in_slice : in_row;
+        nv = nv < SHD_CHUNK ? nv : SHD_CHUNK;
+        const u32x4a4 *q =
+            (const u32x4a4 *)(p.sh_down + (uint64_t)rowc * row_bytes + (uint64_t)(nv ? b0 : 0u) * SF37_Q8_0_BYTES);
+#pragma unroll
+        for (uint32_t i = 0; i < 9; i++) {
+            // dwords past the batch re-read its first 16 bytes: every load
+            // stays within the batch's blocks (+ < 16 bytes), unpredicated
+            const u32x4a4 v = q[16u * i < nv * SF37_Q8_0_BYTES ? i : 0u];
+            w[c][4 * i] = v.x;
+            w[c][4 * i + 1] = v.y;
+            w[c][4 * i + 2] = v.z;
+            w[c][4 * i + 3] = v.w;
+        }
+    }
+    float term[NB * SHD_CHUNK];
+#pragma unroll
+    for (int c = 0; c < NB; c++) {
+#pragma unroll
+        for (uint32_t i = 0; i < SHD_CHUNK; i++) {
+            const uint32_t B = 34u * i, d0 = B / 4u;                // compile-time offset in the batch
+            const uint32_t bg = j * bps + c * SHD_CHUNK + i;
+            const uint32_t b = bg < nb8 ? bg : 0u;
+            const u32x4 *xp = (const u32x4 *)(xq + (uint64_t)tc * p.F + (uint64_t)b * 32u);
+            const u32x4 x0 = xp[0], x1 = xp[1];
+            const uint32_t xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+            int32_t isum = 0;
+            float ws;
+            if ((B & 3u) == 0u) {
+                ws = sf37_f16(w[c][d0]);
+#pragma unroll
+                for (int k = 0; k < 8; k++) isum = sdot4(align_bytes(w[c][d0 + k + 1], w[c][d0 + k], 2), xv[k], isum);
+            } else {
+                ws = sf37_f16(w[c][d0] >> 16);
+#pragma unroll
+                for (int k = 0; k < 8; k++) isum = sdot4(w[c][d0 + 1 + k], xv[k], isum);
+            }
+            term[c * SHD_CHUNK + i] = (float)isum * ws * xsc[(uint64_t)tc * nb8 + b];
+        }
+        // this batch's terms are final here: its activation reads are not
+        // hoisted above the earlier batches' arithmetic
+#pragma unroll
+        for (uint32_t i = 0; i < SHD_CHUNK; i++) asm volatile("" : "+v"(term[c * SHD_CHUNK + i]));
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    // sequential sum over the slices of each (row, token)
+    float acc = 0.0f;
+    for (uint32_t st = 0; st < ns; st++) {
+        const float prev =
+            __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, acc), 0x111, 0xf, 0xf, true));
+        if (j == st) {
+            float a2 = st == 0u ? 0.0f : prev;
+#pragma unroll
+            for (uint32_t i = 0; i < NB * SHD_CHUNK; i++)
+                if (i < bps && j * bps + i < nb8) a2 = a2 + term[i];
+            acc = a2;
+        }
+    }
+    float r = 0.0f;
+#pragma unroll
+    for (uint32_t s = 0; s < 16u; s++)
+        if (s < p.topk) r = r + v[s];
+    if (lane_ok && j == ns - 1u && row < p.K) p.out[(uint64_t)t * p.K + row] = acc + r;
+}
+
+// Routed gate/up.  An item is 2 rows of one group's expert for both
+// matrices: lane = matrix (gate/up) | row | block, so each wave reads two
+// contiguous 2-row spans; the gate lane of each row stores gate and up.
+// The first (100 - UP_DYN_PCT)% of the items are split into equal contiguous
+// ranges, one per wave; the rest are handed out one at a time from
+// UP_QUEUES queues (wave w asks queue w % UP_QUEUES, which owns a contiguous
+// share), so waves that run faster - older waves win the issue arbitration -
+// take more of them and all finish together.  A wave asks for its first
+// dynamic item while computing its last static one; the next item's blocks
+// are always loaded while the current one is computed.
 __global__ void __launch_bounds__(256) dec_up_kernel(dec_params p) {
     extern __shared__ __align__(16) unsigned char smem[];
-    __shared__ uint64_t tab[32];
     const uint32_t nbK = p.K / SF37_QK, P = p.T * p.topk;
     act_t *xs = (act_t *)smem;
     uint32_t *gi = (uint32_t *)(xs + p.T * nbK);
     uint32_t *so = gi + 3u + 2u * p.G;
-    float *wt = (float *)(so + P);
-    sf37_stage_exp_tab(tab);
     const uint32_t n_x = p.T * nbK * (uint32_t)(sizeof(act_t) / 16u);
     for (uint32_t i = threadIdx.x; i < n_x; i += blockDim.x) ((u32x4 *)xs)[i] = ((const u32x4 *)p.xq)[i];
     for (uint32_t i = threadIdx.x; i < 3u + 2u * p.G; i += blockDim.x) gi[i] = p.ginfo[i];
-    for (uint32_t i = threadIdx.x; i < P; i += blockDim.x) {
-        so[i] = p.sorted[i];
-        wt[i] = p.wts[i];
-    }
+    for (uint32_t i = threadIdx.x; i < P; i += blockDim.x) so[i] = p.sorted[i];
     __syncthreads();
 
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t nw = gridDim.x * (blockDim.x >> 6), gw = blockIdx.x * (blockDim.x >> 6) + wave;
     const uint32_t m = lane >> 5, rr = (lane >> 4) & 1u, b = lane & 15u;
     const uint32_t bl = b < nbK ? b : nbK - 1u;                    // lanes past the row repeat its last block
     const bool out_lane = m == 0u && b == nbK - 1u;
     const uint32_t ipg = p.F / 2u, n_items = gi[0] * ipg;
-    const uint32_t nw = gridDim.x * (blockDim.x >> 6);
+    const uint32_t n_stat = n_items - (uint32_t)((uint64_t)n_items * UP_DYN_PCT / 100u);
+    const uint32_t lo = (uint32_t)((uint64_t)n_stat * gw / nw), hi = (uint32_t)((uint64_t)n_stat * (gw + 1u) / nw);
+    const uint32_t qi = gw % UP_QUEUES, n_dyn = n_items - n_stat;
+    const uint32_t q0 = n_stat + (uint32_t)((uint64_t)n_dyn * qi / UP_QUEUES);
+    const uint32_t q1 = n_stat + (uint32_t)((uint64_t)n_dyn * (qi + 1u) / UP_QUEUES);
+    uint32_t *queue = up_queue(p, qi);
     const uint64_t row_bytes = (uint64_t)nbK * SF37_Q3_BYTES, exp_bytes = (uint64_t)p.F * row_bytes;
     const uint8_t *W = m ? p.up_w : p.gate_w;
     auto block_ptr = [&](uint32_t item) -> const uint8_t * {
@@ -402,18 +547,42 @@ __global__ void __launch_bounds__(256) dec_up_kernel(dec_params p) {
         return W + (uint64_t)gi[2u + p.G + g] * exp_bytes + (uint64_t)(2u * rp + rr) * row_bytes +
                (uint64_t)bl * SF37_Q3_BYTES;
     };
-    uint32_t item = blockIdx.x * (blockDim.x >> 6) + wave;
-    if (item >= n_items) return;
+    // a dynamic request: lane 0's atomic; its index is read when needed
+    auto request = [&]() -> uint32_t {
+        uint32_t v = 0;
+        if (lane == 0) v = atomicAdd(queue, 1u);
+        return v;
+    };
+    auto answer = [&](uint32_t v) -> uint32_t { return q0 + (uint32_t)__builtin_amdgcn_readfirstlane((int)v); };
+    uint32_t pend = 0, cur;
+    if (lo < hi) {
+        cur = lo;
+        if (lo + 1u == hi) pend = request();
+    } else {
+        cur = answer(request());
+        if (cur >= q1) return;
+        pend = request();
+    }
     uint32_t nxt[28];
-    load_q3(nxt, block_ptr(item));
-    for (; item < n_items; item += nw) {
+    load_q3(nxt, block_ptr(cur));
+    for (;;) {
         uint32_t raw[28], a[27];
 #pragma unroll
         for (int k = 0; k < 28; k++) raw[k] = nxt[k];
-        const uint8_t *cur = block_ptr(item);
-        if (item + nw < n_items) load_q3(nxt, block_ptr(item + nw));
-        q3_realign(a, raw, (uint32_t)((uintptr_t)cur & 3u));
-        const uint32_t g = item / ipg, row = 2u * (item - g * ipg) + rr;
+        const uint8_t *curp = block_ptr(cur);
+        // the next item: the static successor, else the pending request's answer
+        uint32_t nx;
+        if (cur + 1u < hi) {
+            nx = cur + 1u;
+            if (nx + 1u == hi) pend = request();
+        } else {
+            nx = answer(pend);
+            if (nx < q1) pend = request();
+        }
+        const bool more = nx < hi || (nx >= q0 && nx < q1);
+        if (more) load_q3(nxt, block_ptr(nx));
+        q3_realign(a, raw, (uint32_t)((uintptr_t)curp & 3u));
+        const uint32_t g = cur / ipg, row = 2u * (cur - g * ipg) + rr;
         const uint32_t p0 = gi[1u + g], p1 = gi[2u + g];
         for (uint32_t c0 = p0; c0 < p1; c0 += DEC_TPC) {
             const uint32_t nt = p1 - c0 < DEC_TPC ? p1 - c0 : DEC_TPC;
@@ -434,117 +603,58 @@ __global__ void __launch_bounds__(256) dec_up_kernel(dec_params p) {
                     const float acc = block_chain(x[t]->d, bs[t], nbK);
                     const float up = __shfl_xor(acc, 32, 64);
                     if (out_lane) {
-                        const uint32_t pr = so[c0 + t];
-                        const uint64_t o = (uint64_t)pr * p.F + row;
-                        if (p.gate_out) {
-                            p.gate_out[o] = acc;
-                            p.up_out[o] = up;
-                        }
-                        p.mid[o] = sf37_swiglu_mid_t(acc, up, wt[pr], p.clamp_routed, tab);
+                        const uint64_t o = (uint64_t)so[c0 + t] * p.F + row;
+                        p.gate_out[o] = acc;
+                        p.up_out[o] = up;
                     }
                 }
             }
         }
+        if (!more) break;
+        cur = nx;
     }
 }
 
 // ---------------------------------------------------------------------------
-// mid: Q8_K of the routed mid (one wave per pair and 256-row block, Q2 act
-// layout) and, for the shared expert, SwiGLU + Q8_0 (one half-wave per token
-// and 32-row block)
+// mid: SwiGLU * routing weight (sf37.c:2179-2186) and its Q8_K in the Q2
+// activation layout, one wave per (pair, 256-row block); lane l owns rows
+// 4l .. 4l + 3
 // ---------------------------------------------------------------------------
 __global__ void __launch_bounds__(256) dec_mid_kernel(dec_params p) {
     __shared__ uint64_t tab[32];
     sf37_stage_exp_tab(tab);
     __syncthreads();
-    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t lane = threadIdx.x & 63u, nbm = p.F / SF37_QK;
     const uint32_t w = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-    const uint32_t nbm = p.F / SF37_QK, n_routed = p.T * p.topk * nbm;
-    if (w < n_routed) {
-        const uint32_t pr = w / nbm, blk = w - pr * nbm;
-        const float *mv = p.mid + (uint64_t)pr * p.F + (uint64_t)blk * SF37_QK + 4u * lane;
-        float v[4];
+    if (w >= p.T * p.topk * nbm) return;
+    const uint32_t pr = w / nbm, blk = w - pr * nbm;
+    const uint64_t o = (uint64_t)pr * p.F + (uint64_t)blk * SF37_QK + 4u * lane;
+    const float wt = p.wts[pr];
+    float gv[4], uv[4], v[4];
 #pragma unroll
-        for (int k = 0; k < 4; k++) v[k] = mv[k];
-        int8_t qk[4];
-        int gsum;
-        const float d = q8k_codes4(v, qk, gsum);
-        act_t *y = (act_t *)p.midq + w;
-        uint8_t *qb = (uint8_t *)y->qs;
-#pragma unroll
-        for (int k = 0; k < 4; k++) qb[q2_perm_pos(4u * lane + k)] = (uint8_t)qk[k];
-        if (lane == 0) y->d = d;
-        if ((lane & 15u) == 0) y->gs[lane >> 4] = gsum;
-        return;
+    for (int k = 0; k < 4; k++) {
+        gv[k] = p.gate_out[o + k];
+        uv[k] = p.up_out[o + k];
     }
-    if (!(p.flags & SF37_DEC_SHARED)) return;
-    const uint32_t nb8 = p.F / 32u;
-    const uint32_t hw = 2u * (w - n_routed) + (lane >> 5), l = lane & 31u;
-    if (hw >= p.T * nb8) return;
-    const uint32_t t = hw / nb8, blk = hw - t * nb8;
-    const uint64_t o = (uint64_t)t * p.F + (uint64_t)blk * 32u + l;
-    const float v = sf37_swiglu_mid_t(p.sh_gu[o], p.sh_gu[(uint64_t)p.T * p.F + o], 1.0f, p.clamp_shared, tab);
-    float amax = fabsf(v);
 #pragma unroll
-    for (int off = 16; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 32));
-    int8_t qv = 0;
-    float d = 0.0f;
-    if (amax != 0.0f) {
-        d = amax / 127.0f;
-        const float is = 1.0f / d;
-        qv = (int8_t)(int)fminf(fmaxf(__builtin_rintf(is * v), -128.0f), 127.0f);
+    for (int k = 0; k < 4; k++) {
+        v[k] = sf37_swiglu_mid_t(gv[k], uv[k], wt, p.clamp_routed, tab);
+        p.mid[o + k] = v[k];
     }
-    p.sh_mq[o] = qv;
-    if (l == 0) p.sh_ms[(uint64_t)t * nb8 + blk] = d;
+    int8_t qk[4];
+    int gsum;
+    const float d = q8k_codes4(v, qk, gsum);
+    act_t *y = (act_t *)p.midq + w;
+    uint8_t *qb = (uint8_t *)y->qs;
+#pragma unroll
+    for (int k = 0; k < 4; k++) qb[q2_perm_pos(4u * lane + k)] = (uint8_t)qk[k];
+    if (lane == 0) y->d = d;
+    if ((lane & 15u) == 0) y->gs[lane >> 4] = gsum;
 }
 
 // ---------------------------------------------------------------------------
-// down + combine
+// routed down
 // ---------------------------------------------------------------------------
-
-// Per-wave LDS tile copy: bytes [src, src + n) with direct global->LDS
-// dwordx4 loads (one contiguous KiB per instruction), starting at the
-// 16-byte boundary at or below src.  Returns the offset of src in dst; the
-// caller waits with wave_lds_wait() before reading.
-__device__ __forceinline__ uint32_t wave_lds_copy(uint8_t *dst, const uint8_t *src, uint32_t n) {
-    const uintptr_t a0 = (uintptr_t)src & ~(uintptr_t)15;
-    const uint32_t off = (uint32_t)((uintptr_t)src - a0);
-    const uint32_t chunks = (off + n + 15u) >> 4, lane = threadIdx.x & 63u;
-    for (uint32_t c0 = 0; c0 < chunks; c0 += 64u) {
-        if (c0 + lane < chunks)
-            __builtin_amdgcn_global_load_lds((const void *)(a0 + 16u * (uintptr_t)(c0 + lane)), dst + 16u * c0, 16, 0, 0);
-    }
-    return off;
-}
-
-__device__ __forceinline__ void wave_lds_wait() {
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __builtin_amdgcn_wave_barrier();
-}
-
-// Block values of one Q2 block (21 dwords in a) against NT activation blocks
-// read through the scalar cache: bs[t] = sum_g fma(s_g, I_g).
-template <int NT>
-__device__ __forceinline__ void q2_block_dots(const uint32_t *a, c_act *const *x, float bs[4]) {
-#pragma unroll
-    for (int t = 0; t < NT; t++) bs[t] = 0.0f;
-#pragma unroll
-    for (int g = 0; g < 4; g++) {
-        uint32_t c[16];
-#pragma unroll
-        for (int j = 0; j < 4; j++) q2_unpack16(a[3 + 4 * g + j], c[4 * j], c[4 * j + 1], c[4 * j + 2], c[4 * j + 3]);
-        const int32_t zp = (int32_t)((a[2] >> (8 * g)) & 3u);
-        const float sc = sf37_f16(a[g >> 1] >> (16 * (g & 1)));
-#pragma unroll
-        for (int t = 0; t < NT; t++) {
-            int32_t acc = 0;
-#pragma unroll
-            for (int k = 0; k < 16; k++) acc = sdot4(c[k], x[t]->qs[16 * g + k], acc);
-            bs[t] = __builtin_fmaf(sc, (float)(acc - __mul24(zp, x[t]->gs[g])), bs[t]);
-        }
-        __builtin_amdgcn_sched_barrier(0);            // one group's codes live at a time
-    }
-}
 
 // 21 dwords of a Q2 block (dword aligned) as five 16-byte loads and one dword.
 __device__ __forceinline__ void load_q2(uint32_t w[21], const uint8_t *p) {
@@ -604,7 +714,8 @@ __device__ __forceinline__ float seg_chain(float d, float bs, uint32_t b, uint32
     return acc;
 }
 
-// Routed down.  Lane = (row, block): each 16-lane DPP row holds 16/nb rows
+// Down.  With the shared expert the first waves quantise the shared mid.
+// Routed down: lane = (row, block): each 16-lane DPP row holds 16/nb rows
 // with their nb blocks on consecutive lanes, so a wave reads 64/nb*4 rows
 // (12 for F = 1280) as one contiguous span.  A wave owns a contiguous range
 // of these sub-items (mostly inside one group); the group's activation
@@ -613,13 +724,38 @@ __device__ __forceinline__ float seg_chain(float d, float bs, uint32_t b, uint32
 __global__ void __launch_bounds__(256) dec_down_kernel(dec_params p) {
     __shared__ uint32_t meta[3u + 2u * 256u + 256u];
     __shared__ __align__(16) act_t xsl[4][DN_TPC * DN_MAX_NB];
+    __shared__ uint64_t tab[32];
     const uint32_t P = p.T * p.topk;
     uint32_t *gi = meta;
     uint32_t *so = gi + 3u + 2u * p.G;
     for (uint32_t i = threadIdx.x; i < 3u + 2u * p.G; i += blockDim.x) gi[i] = p.ginfo[i];
     for (uint32_t i = threadIdx.x; i < P; i += blockDim.x) so[i] = p.sorted[i];
+    sf37_stage_exp_tab(tab);
     __syncthreads();
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63u;
+    if (p.flags & SF37_DEC_SHARED) {
+        // shared mid: SwiGLU (clamp_shared) and Q8_0 (sf37_ops.c:57-90), one
+        // half-wave per (token, 32-row block), on the first waves
+        const uint32_t nb32 = p.F / 32u;
+        const uint32_t hw = 2u * (blockIdx.x * (blockDim.x >> 6) + wave) + (lane >> 5), l = lane & 31u;
+        if (hw < p.T * nb32) {
+            const uint32_t t = hw / nb32, blk = hw - t * nb32;
+            const uint64_t o = (uint64_t)t * p.F + (uint64_t)blk * 32u + l;
+            const float v = sf37_swiglu_mid_t(p.sh_gu[o], p.sh_gu[(uint64_t)p.T * p.F + o], 1.0f, p.clamp_shared, tab);
+            float amax = fabsf(v);
+#pragma unroll
+            for (int off = 16; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 32));
+            int8_t qv = 0;
+            float d = 0.0f;
+            if (amax != 0.0f) {
+                d = amax / 127.0f;
+                const float is = 1.0f / d;
+                qv = (int8_t)(int)fminf(fmaxf(__builtin_rintf(is * v), -128.0f), 127.0f);
+            }
+            p.sh_mq[o] = qv;
+            if (l == 0) p.sh_ms[(uint64_t)t * nb32 + blk] = d;
+        }
+    }
     act_t *xw = xsl[wave];
     const uint32_t nb = p.F / SF37_QK, rpd = 16u / nb, rpw = 4u * rpd;     // rows per DPP row / wave
     const uint32_t q = lane & 15u, r_in = q / nb, b = q - r_in * nb;
@@ -628,7 +764,6 @@ __global__ void __launch_bounds__(256) dec_down_kernel(dec_params p) {
     const uint32_t spg = (p.K + rpw - 1u) / rpw, n_sub = gi[0] * spg;
     const uint32_t nw = gridDim.x * (blockDim.x >> 6), gw = blockIdx.x * (blockDim.x >> 6) + wave;
     const uint32_t lo = (uint32_t)((uint64_t)n_sub * gw / nw), hi = (uint32_t)((uint64_t)n_sub * (gw + 1u) / nw);
-    if (lo >= hi) return;
     const uint64_t row_bytes = (uint64_t)nb * SF37_Q2_BYTES;
     auto blk_ptr = [&](uint32_t sidx) -> const uint8_t * {
         const uint32_t g = sidx / spg, sub = sidx - g * spg;
@@ -637,6 +772,7 @@ __global__ void __launch_bounds__(256) dec_down_kernel(dec_params p) {
         return p.down_w + ((uint64_t)gi[2u + p.G + g] * p.K + row) * row_bytes + (uint64_t)b * SF37_Q2_BYTES;
     };
     uint32_t staged_g = 0xffffffffu, staged_c0 = 0xffffffffu;
+    if (lo >= hi) return;
     uint32_t nxt[21];
     load_q2(nxt, blk_ptr(lo));
     for (uint32_t sidx = lo; sidx < hi; sidx++) {
@@ -683,71 +819,42 @@ __global__ void __launch_bounds__(256) dec_down_kernel(dec_params p) {
 }
 
 // ---------------------------------------------------------------------------
-// combine: out = shared + sum over slots (slot order); lane = (row, token).
-// With the shared expert the lane first runs its shared-down row: the span's
-// rows are copied to the wave's LDS buffer and the reference's block order
-// acc = acc + (isum * ws) * xs is followed (sf37_ops.c:92-108).
+// combine: out = [shared +] sum over slots in slot order.  With the shared
+// expert one wave per CB_PASSES shared_down_pass row groups (mid codes
+// staged in LDS), else one thread per output.
 // ---------------------------------------------------------------------------
-__global__ void __launch_bounds__(DN_WG_WAVES * 64) dec_combine_kernel(dec_params p) {
-    extern __shared__ __align__(16) unsigned char smem[];
-    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63u;
-    uint8_t *buf = smem + wave * dn_buf_bytes(p.F);
-    const bool sh = (p.flags & SF37_DEC_SHARED) != 0;
-    const uint32_t rpw = sh_dn_rows(p.F, p.T);
-    const uint32_t n_items = (p.K + rpw - 1u) / rpw;
-    const uint32_t nw = gridDim.x * (blockDim.x >> 6);
-    const uint32_t t = lane % p.T, rl = lane / p.T;
-    const uint32_t nb8 = p.F / 32u, row_bytes = nb8 * SF37_Q8_0_BYTES;
-    for (uint32_t item = blockIdx.x * (blockDim.x >> 6) + wave; item < n_items; item += nw) {
-        const uint32_t r0 = item * rpw, nrows = p.K - r0 < rpw ? p.K - r0 : rpw;
-        const uint32_t rc = rl < nrows ? rl : 0u, row = r0 + rc;
-        // slot values first (independent loads, issued together)
-        float v[16];
+__global__ void __launch_bounds__(256) dec_combine_kernel(dec_params p) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= p.T * p.K) return;
+    const uint32_t t = i / p.K, r = i - t * p.K;
+    float v[16];
 #pragma unroll
-        for (int s = 0; s < 16; s++) {
-            const uint32_t sc = (uint32_t)s < p.topk ? (uint32_t)s : 0u;   // every read in bounds
-            v[s] = p.down_pair[((uint64_t)t * p.topk + sc) * p.K + row];
-        }
-        float acc = 0.0f;
-        if (sh) {
-            const uint32_t off = wave_lds_copy(buf, p.sh_down + (uint64_t)r0 * row_bytes, nrows * row_bytes);
-            wave_lds_wait();
-            const int8_t *xq = p.sh_mq + (uint64_t)t * p.F;
-            const float *xs = p.sh_ms + (uint64_t)t * nb8;
-            const uint32_t base = off + rc * row_bytes;
-            for (uint32_t b0 = 0; b0 < nb8; b0 += 8u) {
-                uint32_t xv[8][8];
-                float xsc[8];
+    for (int s = 0; s < 16; s++) {
+        const uint32_t sc = (uint32_t)s < p.topk ? (uint32_t)s : 0u;   // every read in bounds
+        v[s] = p.down_pair[((uint64_t)t * p.topk + sc) * p.K + r];
+    }
+    float acc = 0.0f;
 #pragma unroll
-                for (int j = 0; j < 8; j++) {
-                    const uint32_t b = b0 + j < nb8 ? b0 + j : nb8 - 1u;
-                    const u32x4 *xp = (const u32x4 *)(xq + (uint64_t)b * 32u);
-                    const u32x4 x0 = xp[0], x1 = xp[1];
-                    xv[j][0] = x0.x; xv[j][1] = x0.y; xv[j][2] = x0.z; xv[j][3] = x0.w;
-                    xv[j][4] = x1.x; xv[j][5] = x1.y; xv[j][6] = x1.z; xv[j][7] = x1.w;
-                    xsc[j] = xs[b];
-                }
-#pragma unroll
-                for (int j = 0; j < 8; j++) {
-                    if (b0 + j < nb8) {
-                        uint32_t q[8];
-                        const float wsc = q8_0_lds(buf, base + (b0 + j) * SF37_Q8_0_BYTES, q);
-                        int32_t isum = 0;
-#pragma unroll
-                        for (int k = 0; k < 8; k++) isum = sdot4(q[k], xv[j][k], isum);
-                        acc = acc + (float)isum * wsc * xsc[j];
-                    }
-                }
-            }
-            // the next item's copy must not overwrite rows still being read
-            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-            __builtin_amdgcn_wave_barrier();
-        }
-        float r = 0.0f;
-#pragma unroll
-        for (int s = 0; s < 16; s++)
-            if ((uint32_t)s < p.topk) r = r + v[s];
-        if (rl < nrows) p.out[(uint64_t)t * p.K + row] = sh ? acc + r : r;
+    for (int s = 0; s < 16; s++)
+        if ((uint32_t)s < p.topk) acc = acc + v[s];
+    p.out[i] = acc;
+}
+
+template <int NB>
+__global__ void __launch_bounds__(256) dec_combine_shared_kernel(dec_params p) {
+    extern __shared__ __align__(16) unsigned char smem[];        // shared mid codes, then scales
+    int8_t *shq = (int8_t *)smem;
+    float *shs = (float *)(smem + p.T * p.F);
+    for (uint32_t i = threadIdx.x; i < p.T * p.F / 16u; i += blockDim.x) ((u32x4 *)shq)[i] = ((const u32x4 *)p.sh_mq)[i];
+    for (uint32_t i = threadIdx.x; i < p.T * (p.F / 32u); i += blockDim.x) shs[i] = p.sh_ms[i];
+    __syncthreads();
+    const uint32_t S = shd_slices(p.T), R = 64u / (p.T * S);
+    const uint32_t gw = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+#pragma unroll 1
+    for (uint32_t i = 0; i < CB_PASSES; i++) {
+        const uint32_t r0 = (gw * CB_PASSES + i) * R;
+        if (r0 >= p.K) return;
+        shared_down_pass<NB>(p, shq, shs, r0);
     }
 }
 
@@ -756,7 +863,7 @@ __global__ void __launch_bounds__(DN_WG_WAVES * 64) dec_combine_kernel(dec_param
 namespace {
 
 struct dec_shape {
-    uint32_t n_router, n_xq, n_shup, n_up, n_mid, n_dn, n_cb;
+    uint32_t n_rt, n_xq, n_shup, n_up, n_mid, n_dn, n_cb;
     size_t lds_up, lds_shup, lds_dn;
 };
 
@@ -804,34 +911,40 @@ dec_shape dec_plan(const dec_params &p) {
     const uint32_t nb = p.K / SF37_QK;
     const bool sh = (p.flags & SF37_DEC_SHARED) != 0;
     const uint32_t cus = device_cus();
-    d.n_router = (p.flags & SF37_DEC_ROUTER) ? p.E : 0u;
+    d.n_rt = (p.flags & (SF37_DEC_ROUTER | SF37_DEC_SELECT)) ? (p.E + RT_ROWS - 1u) / RT_ROWS : 0u;
     d.n_xq = (p.T * nb + 3u) / 4u;
     d.lds_up = lds_up_routed(p.K, p.T, p.G, p.T * p.topk);
     d.lds_shup = lds_up_shared(p.K, p.T);
-    d.n_shup = sh ? p.F / SH_RS : 0u;
-    // every up workgroup resident at once: at most 3 per CU, fewer if LDS-bound
+    d.n_shup = 1u + (sh ? p.F / SH_RS : 0u);           // select workgroup + shared rows
     // persistent kernels: exactly as many workgroups as can be resident
     d.n_up = resident_wgs((const void *)dec_up_kernel, 256, d.lds_up) * cus;
-    const uint32_t n_mid_waves = p.T * p.topk * (p.F / SF37_QK) + (sh ? (p.T * (p.F / 32u) + 1u) / 2u : 0u);
-    d.n_mid = (n_mid_waves + 3u) / 4u;
+    d.n_mid = (p.T * p.topk * (p.F / SF37_QK) + 3u) / 4u;
     d.lds_dn = 0;
     d.n_dn = resident_wgs((const void *)dec_down_kernel, 256, 0) * cus;
-    const uint32_t cb_items = (p.K + sh_dn_rows(p.F, p.T) - 1u) / sh_dn_rows(p.F, p.T);
-    d.n_cb = (cb_items + DN_WG_WAVES - 1u) / DN_WG_WAVES;
+    if (sh) {
+        const uint32_t R = 64u / (p.T * shd_slices(p.T));
+        d.n_cb = ((p.K + R * CB_PASSES - 1u) / (R * CB_PASSES) + 3u) / 4u;
+    } else {
+        d.n_cb = (p.T * p.K + 255u) / 256u;
+    }
     return d;
 }
 
 }  // namespace
 
 extern "C" int sf37k_decode_counters(uint32_t T, uint32_t topk, uint32_t E, uint32_t K, uint32_t F) {
-    (void)T; (void)topk; (void)E; (void)F; (void)K;
-    return (int)CNT_FIXED;
+    (void)K;
+    const uint32_t P = T * topk, G = P < E ? P : E;
+    (void)T; (void)topk; (void)E; (void)F;
+    return (int)(32u * UP_QUEUES);
 }
 
 extern "C" int sf37k_decode_supported(uint32_t T, uint32_t topk, uint32_t E, uint32_t K, uint32_t F, int shared) {
     if (T == 0 || T > DEC_MAX_TOK || topk == 0 || K % SF37_QK || F % SF37_QK || K / SF37_QK > 16u ||
-        F / SF37_QK > DN_MAX_NB || K % DN_TILE)
+        F / SF37_QK > DN_MAX_NB)
         return 0;
+    // shared down: the shared mid fits in the x area, a lane's slice in registers
+    if (shared && shd_bps(F / 32u, shd_slices(T)) > SHD_MAX_BPS) return 0;
     const uint32_t P = T * topk, G = P < E ? P : E;
     if (lds_up_routed(K, T, G, P) > device_max_lds()) return 0;
     if (shared && lds_up_shared(K, T) > device_max_lds()) return 0;
@@ -850,17 +963,17 @@ int set_lds(const void *fn, size_t bytes, size_t *opted) {
 
 extern "C" int sf37k_decode_route(const sf37_dec_params *pp, sf37_stream_t s) {
     const dec_shape d = dec_plan(*pp);
-    hipLaunchKernelGGL(dec_route_kernel, dim3(d.n_router + d.n_xq), dim3(256), 0, (hipStream_t)s, *pp, d.n_router);
+    hipLaunchKernelGGL(dec_route_kernel, dim3(d.n_rt + d.n_xq), dim3(256), 0, (hipStream_t)s, *pp, d.n_rt);
     return (int)hipGetLastError();
 }
 
-extern "C" int sf37k_decode_shared_up(const sf37_dec_params *pp, sf37_stream_t s) {
+extern "C" int sf37k_decode_select(const sf37_dec_params *pp, sf37_stream_t s) {
     const dec_shape d = dec_plan(*pp);
-    if (!d.n_shup) return 0;
+    const size_t lds = (pp->flags & SF37_DEC_SHARED) ? d.lds_shup : 0u;
     static size_t opted = 65536;
-    const int err = set_lds((const void *)dec_shup_kernel, d.lds_shup, &opted);
+    const int err = set_lds((const void *)dec_select_kernel, lds, &opted);
     if (err) return err;
-    hipLaunchKernelGGL(dec_shup_kernel, dim3(d.n_shup), dim3(256), d.lds_shup, (hipStream_t)s, *pp);
+    hipLaunchKernelGGL(dec_select_kernel, dim3(d.n_shup), dim3(256), lds, (hipStream_t)s, *pp);
     return (int)hipGetLastError();
 }
 
@@ -887,10 +1000,22 @@ extern "C" int sf37k_decode_down(const sf37_dec_params *pp, sf37_stream_t s) {
 
 extern "C" int sf37k_decode_combine(const sf37_dec_params *pp, sf37_stream_t s) {
     const dec_shape d = dec_plan(*pp);
-    const size_t lds = (pp->flags & SF37_DEC_SHARED) ? (size_t)DN_WG_WAVES * dn_buf_bytes(pp->F) : 0u;
-    static size_t opted = 65536;
-    const int err = set_lds((const void *)dec_combine_kernel, lds, &opted);
-    if (err) return err;
-    hipLaunchKernelGGL(dec_combine_kernel, dim3(d.n_cb), dim3(DN_WG_WAVES * 64), lds, (hipStream_t)s, *pp);
+    if (!(pp->flags & SF37_DEC_SHARED)) {
+        hipLaunchKernelGGL(dec_combine_kernel, dim3(d.n_cb), dim3(256), 0, (hipStream_t)s, *pp);
+        return (int)hipGetLastError();
+    }
+    // one kernel per number of load batches (registers follow the batches)
+    const uint32_t nbat = (shd_bps(pp->F / 32u, shd_slices(pp->T)) + SHD_CHUNK - 1u) / SHD_CHUNK;
+    const void *fn = nbat == 1u ? (const void *)dec_combine_shared_kernel<1>
+                   : nbat == 2u ? (const void *)dec_combine_shared_kernel<2>
+                                : (const void *)dec_combine_shared_kernel<3>;
+    const size_t lds = (size_t)pp->T * pp->F + (size_t)pp->T * (pp->F / 32u) * 4u;
+    if (lds > 65536u) {
+        const hipError_t err = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (err != hipSuccess) return (int)err;
+    }
+    if (nbat == 1u) hipLaunchKernelGGL(dec_combine_shared_kernel<1>, dim3(d.n_cb), dim3(256), lds, (hipStream_t)s, *pp);
+    else if (nbat == 2u) hipLaunchKernelGGL(dec_combine_shared_kernel<2>, dim3(d.n_cb), dim3(256), lds, (hipStream_t)s, *pp);
+    else hipLaunchKernelGGL(dec_combine_shared_kernel<3>, dim3(d.n_cb), dim3(256), lds, (hipStream_t)s, *pp);
     return (int)hipGetLastError();
 }

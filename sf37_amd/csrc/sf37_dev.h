@@ -41,11 +41,13 @@ __host__ __device__ inline uint64_t sf37_exp2_tab(uint32_t i) {
     return tab[i & 31u];
 }
 
-// tab: the 32 table words (sf37_exp2_tab), e.g. staged in LDS by the caller.
-// Branch-free: the reduction runs for every input and the special cases
-// (|x| >= 88 that overflow or underflow, infinities, NaN) are selected at the
-// end, so unrolled calls stay straight-line code on the GPU.
-__host__ __device__ inline float sf37_expf_t(float x, const uint64_t *tab) {
+// LDS_TAB: the 32 table words (sf37_exp2_tab) are read from tab, a copy the
+// caller staged in LDS; otherwise from the constant table.  Branch-free: the
+// reduction runs for every input and the special cases (|x| >= 88 that
+// overflow or underflow, infinities, NaN) are selected at the end, so
+// unrolled calls stay straight-line code on the GPU.
+template <bool LDS_TAB>
+__host__ __device__ inline float sf37_expf_impl(float x, const uint64_t *tab) {
     const uint32_t ux = __builtin_bit_cast(uint32_t, x);
     const uint32_t abstop = (ux >> 20) & 0x7ffu;
     const double inv_ln2_n = 0x1.71547652b82fep+0 * 32.0;   // 32 / ln 2
@@ -58,7 +60,7 @@ __host__ __device__ inline float sf37_expf_t(float x, const uint64_t *tab) {
     const uint64_t ki = __builtin_bit_cast(uint64_t, kd);
     kd = kd - shift;
     const double r = __builtin_fma(inv_ln2_n, xd, -kd);
-    uint64_t t = tab ? tab[ki & 31u] : sf37_exp2_tab((uint32_t)(ki & 31u));
+    uint64_t t = LDS_TAB ? tab[ki & 31u] : sf37_exp2_tab((uint32_t)(ki & 31u));
     t += ki << 47;
     const double s = __builtin_bit_cast(double, t);
     const double z = __builtin_fma(c0, r, c1);
@@ -76,16 +78,19 @@ __host__ __device__ inline float sf37_expf_t(float x, const uint64_t *tab) {
     return res;
 }
 
-__host__ __device__ inline float sf37_expf(float x) { return sf37_expf_t(x, nullptr); }
+__host__ __device__ inline float sf37_expf(float x) { return sf37_expf_impl<false>(x, nullptr); }
 
 // sf37_ops.c:9-16: x >= 0 ? 1 / (1 + e^-x) : e^x / (1 + e^x), branch-free.
-__host__ __device__ inline float sf37_sigmoid_t(float x, const uint64_t *tab) {
+template <bool LDS_TAB>
+__host__ __device__ inline float sf37_sigmoid_impl(float x, const uint64_t *tab) {
     const bool pos = x >= 0.0f;
-    const float z = sf37_expf_t(pos ? -x : x, tab);
+    const float z = sf37_expf_impl<LDS_TAB>(pos ? -x : x, tab);
     return (pos ? 1.0f : z) / (1.0f + z);
 }
 
-__host__ __device__ inline float sf37_sigmoid(float x) { return sf37_sigmoid_t(x, nullptr); }
+__host__ __device__ inline float sf37_sigmoid(float x) { return sf37_sigmoid_impl<false>(x, nullptr); }
+// tab: the table staged in LDS (sf37_stage_exp_tab), never null
+__host__ __device__ inline float sf37_sigmoid_t(float x, const uint64_t *tab) { return sf37_sigmoid_impl<true>(x, tab); }
 
 // Stage the exp table into LDS (all threads may call; caller syncs).
 __device__ inline void sf37_stage_exp_tab(uint64_t *lds_tab) {
@@ -93,18 +98,23 @@ __device__ inline void sf37_stage_exp_tab(uint64_t *lds_tab) {
 }
 
 // ((g * sigmoid(g)) * u) * w with the routed/shared clamp (sf37_cuda.cu:4444-4456).
-__device__ __forceinline__ float sf37_swiglu_mid_t(float g, float u, float w, float clamp,
-                                                  const uint64_t *tab) {
+template <bool LDS_TAB>
+__device__ __forceinline__ float sf37_swiglu_mid_impl(float g, float u, float w, float clamp, const uint64_t *tab) {
     if (clamp > 1.0e-6f) {
         if (g > clamp) g = clamp;
         if (u > clamp) u = clamp;
         if (u < -clamp) u = -clamp;
     }
-    return g * sf37_sigmoid_t(g, tab) * u * w;
+    return g * sf37_sigmoid_impl<LDS_TAB>(g, tab) * u * w;
+}
+
+// tab: the table staged in LDS, never null
+__device__ __forceinline__ float sf37_swiglu_mid_t(float g, float u, float w, float clamp, const uint64_t *tab) {
+    return sf37_swiglu_mid_impl<true>(g, u, w, clamp, tab);
 }
 
 __device__ __forceinline__ float sf37_swiglu_mid(float g, float u, float w, float clamp) {
-    return sf37_swiglu_mid_t(g, u, w, clamp, nullptr);
+    return sf37_swiglu_mid_impl<false>(g, u, w, clamp, nullptr);
 }
 
 __device__ __forceinline__ float sf37_f16(uint32_t h16) {

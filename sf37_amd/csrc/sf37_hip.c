@@ -87,7 +87,7 @@ static hipEvent_t g_prof_open;
 
 static const char *const k_stage_names[SF37_HIP_N_STAGES] = {
     "router", "select", "q8_0_act", "q8_0_gemm", "swiglu", "q8k_x", "dispatch",
-    "gate_up", "q8k_mid", "down", "combine", "add", "other", "dec_route", "dec_up", "dec_down", "dec_shared_up", "dec_mid", "dec_combine"};
+    "gate_up", "q8k_mid", "down", "combine", "add", "other", "dec_route", "dec_up", "dec_down", "dec_select", "dec_combine", "dec_mid"};
 
 static void prof_begin(void) {
     if (!g_prof_on) return;
@@ -921,7 +921,8 @@ static int decode_eligible(const routed_args *a, uint32_t flags) {
 static int decode_run(const routed_args *a, const dec_extra *ex, float *out, float *mid, float *down_pair,
                       float *gate_out, float *up_out) {
     if (!aligned4(a->gate_w) || !aligned4(a->up_w) || !aligned4(a->down_w) || !aligned4(a->x) ||
-        !aligned4(out) || (mid && !aligned4(mid)) || (down_pair && !aligned4(down_pair)))
+        !aligned4(out) || (mid && !aligned4(mid)) || (down_pair && !aligned4(down_pair)) ||
+        (gate_out && !aligned4(gate_out)) || (up_out && !aligned4(up_out)))
         return 0;
     const uint32_t T = a->n_tok, E = a->n_expert, K = a->in_dim, F = a->mid_dim, TK = a->topk;
     const uint64_t P = (uint64_t)T * TK;
@@ -949,12 +950,10 @@ static int decode_run(const routed_args *a, const dec_extra *ex, float *out, flo
     p.sh_gate = ex->sh_gate;
     p.sh_up = ex->sh_up;
     p.sh_down = ex->sh_down;
-    p.gate_out = gate_out;
-    p.up_out = up_out;
     p.out = out;
     /* scratch layout */
     uint64_t off = 0, o_xq, o_xq8, o_xs8, o_gi, o_so, o_mid = 0, o_mq, o_gu = 0, o_smq = 0, o_sms = 0, o_dp = 0,
-                      o_sho = 0, o_lg = 0, o_sel = 0, o_wts = 0;
+                      o_lg = 0, o_ck = 0, o_cp = 0, o_sel = 0, o_wts = 0, o_go = 0, o_uo = 0;
 #define TAKE(var, bytes)            \
     do {                            \
         var = off;                  \
@@ -966,15 +965,20 @@ static int decode_run(const routed_args *a, const dec_extra *ex, float *out, flo
     TAKE(o_gi, (3u + 2u * (uint64_t)G) * 4u);
     TAKE(o_so, P * 4u);
     if (!mid) TAKE(o_mid, P * F * 4u);
+    if (!gate_out) TAKE(o_go, P * F * 4u);
+    if (!up_out) TAKE(o_uo, P * F * 4u);
     TAKE(o_mq, P * (F / QK) * SF37_DEC_ACT_BYTES);
     if (sh) {
         TAKE(o_gu, 2u * (uint64_t)T * F * 4u);
         TAKE(o_smq, (uint64_t)T * F);
         TAKE(o_sms, (uint64_t)T * (F / 32u) * 4u);
-        TAKE(o_sho, (uint64_t)T * K * 4u);
     }
     if (!down_pair) TAKE(o_dp, P * K * 4u);
     if (ex->flags & SF37_DEC_ROUTER) TAKE(o_lg, (uint64_t)T * E * 4u);
+    if (ex->flags & SF37_DEC_SELECT) {
+        TAKE(o_ck, (uint64_t)T * E * 8u);
+        TAKE(o_cp, (uint64_t)T * E * 4u);
+    }
     if ((ex->flags & SF37_DEC_SELECT) && !ex->sel) TAKE(o_sel, P * 4u);
     if ((ex->flags & SF37_DEC_SELECT) && !ex->wts) TAKE(o_wts, P * 4u);
 #undef TAKE
@@ -987,16 +991,19 @@ static int decode_run(const routed_args *a, const dec_extra *ex, float *out, flo
     p.ginfo = (uint32_t *)(base + o_gi);
     p.sorted = (uint32_t *)(base + o_so);
     p.mid = mid ? mid : (float *)(base + o_mid);
+    p.gate_out = gate_out ? gate_out : (float *)(base + o_go);
+    p.up_out = up_out ? up_out : (float *)(base + o_uo);
     p.midq = base + o_mq;
     if (sh) {
         p.sh_gu = (float *)(base + o_gu);
         p.sh_mq = (int8_t *)(base + o_smq);
         p.sh_ms = (float *)(base + o_sms);
-        p.sh_out = (float *)(base + o_sho);
     }
     p.down_pair = down_pair ? down_pair : (float *)(base + o_dp);
     p.logits = (ex->flags & SF37_DEC_ROUTER) ? (float *)(base + o_lg) : NULL;
     if (ex->flags & SF37_DEC_SELECT) {
+        p.cand_key = (uint64_t *)(base + o_ck);
+        p.cand_p = (float *)(base + o_cp);
         p.sel = ex->sel ? ex->sel : (int32_t *)(base + o_sel);
         p.wts = ex->wts ? ex->wts : (float *)(base + o_wts);
         if (!p.logits_sel) p.logits_sel = p.logits;
@@ -1010,7 +1017,7 @@ static int decode_run(const routed_args *a, const dec_extra *ex, float *out, flo
     p.cnt = cnt;
     const sf37_stream_t st = (sf37_stream_t)g_stream;
     return LAUNCH(SF37_HIP_STAGE_DEC_ROUTE, sf37k_decode_route(&p, st), "decode route launch") &&
-           (!sh || LAUNCH(SF37_HIP_STAGE_DEC_SHARED_UP, sf37k_decode_shared_up(&p, st), "decode shared up launch")) &&
+           LAUNCH(SF37_HIP_STAGE_DEC_SELECT, sf37k_decode_select(&p, st), "decode select launch") &&
            LAUNCH(SF37_HIP_STAGE_DEC_UP, sf37k_decode_up(&p, st), "decode up launch") &&
            LAUNCH(SF37_HIP_STAGE_DEC_MID, sf37k_decode_mid(&p, st), "decode mid launch") &&
            LAUNCH(SF37_HIP_STAGE_DEC_DOWN, sf37k_decode_down(&p, st), "decode down launch") &&

@@ -94,7 +94,7 @@ int sf37k_synth_quant_rows(int type, uint8_t *dst, uint64_t row0, uint64_t nrows
 /* Elementwise exp/sigmoid of a float array (for exhaustive parity tests). */
 int sf37k_sigmoid_array(float *out, const float *x, uint64_t n, int mode, sf37_stream_t s);
 
-/* Fused decode layer (up to 16 tokens): route, shared_up, up, mid, down,
+/* Fused decode layer (up to 16 tokens): route, select, up, mid, down,
  * combine (k_decode.hip).  Pointers are device addresses; flags select the parts
  * that run.  cnt holds sf37k_decode_counters(...) zero-initialised words
  * that the kernels leave zero again when they finish. */
@@ -110,7 +110,9 @@ typedef struct sf37_dec_params {
     uint32_t flags;
     const float *x, *router_w, *router_bias, *logits_sel;
     const uint8_t *gate_w, *up_w, *down_w, *sh_gate, *sh_up, *sh_down;
-    float *logits;
+    float *logits;       /* T x E router logits (ROUTER) */
+    uint64_t *cand_key;  /* T x E selection keys (SELECT) */
+    float *cand_p;       /* T x E sigmoid of the selecting logits (SELECT) */
     int32_t *sel;
     float *wts;
     void *xq;            /* T x K/256 activation blocks (Q3 order) */
@@ -120,22 +122,20 @@ typedef struct sf37_dec_params {
     uint32_t *sorted;    /* pairs ordered by (expert, pair) */
     float *mid;          /* pairs x F SwiGLU * weight */
     void *midq;          /* pairs x F/256 activation blocks (Q2 order) */
-    float *gate_out, *up_out;   /* optional pairs x F */
+    float *gate_out, *up_out;   /* pairs x F gate / up rows */
     float *sh_gu;        /* 2 x T x F shared gate | up */
     int8_t *sh_mq;       /* T x F Q8_0 codes of the shared mid */
     float *sh_ms;        /* T x F/32 scales */
     float *down_pair;    /* pairs x K */
-    float *sh_out;       /* T x K */
     float *out;          /* T x K */
     uint32_t *cnt;
 } sf37_dec_params;
 int sf37k_decode_counters(uint32_t T, uint32_t topk, uint32_t E, uint32_t K, uint32_t F);
 /* 1 if the fused kernels take this shape (token count, dims, LDS). */
 int sf37k_decode_supported(uint32_t T, uint32_t topk, uint32_t E, uint32_t K, uint32_t F, int shared);
-/* The launches, in this order on one stream (shared_up only with
- * SF37_DEC_SHARED). */
+/* The launches, in this order on one stream. */
 int sf37k_decode_route(const sf37_dec_params *p, sf37_stream_t s);
-int sf37k_decode_shared_up(const sf37_dec_params *p, sf37_stream_t s);
+int sf37k_decode_select(const sf37_dec_params *p, sf37_stream_t s);
 int sf37k_decode_up(const sf37_dec_params *p, sf37_stream_t s);
 int sf37k_decode_mid(const sf37_dec_params *p, sf37_stream_t s);
 int sf37k_decode_down(const sf37_dec_params *p, sf37_stream_t s);
