@@ -53,7 +53,24 @@ def parse():
     ap.add_argument("--seed", type=int, default=1234)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--copy-calib", type=int, default=0, metavar="MIB",
+                    help="only run 10 device-to-device copies of MIB MiB (calibrates the HBM counters)")
     return ap.parse_args()
+
+
+def copy_calibration(mib):
+    """10 device-to-device copies of mib MiB each (the runtime's copy kernel):
+    FETCH_SIZE / WRITE_SIZE per dispatch of this run against the known size
+    give the scale that turns those counters into HBM bytes."""
+    from sf37_amd import hip
+    hip.init()
+    n = mib << 20
+    a, b = hip.Tensor.alloc(n), hip.Tensor.alloc(n)
+    L = hip.lib()
+    for _ in range(10):
+        hip.check(L.sf37_hip_tensor_copy(b, 0, a, 0, n), "copy")
+    hip.synchronize()
+    print(json.dumps({"copy_calibration_bytes_per_dispatch": n, "dispatches": 10}), flush=True)
 
 
 class Hip:
@@ -87,6 +104,9 @@ class Hip:
 
 def main():
     args = parse()
+    if args.copy_calib:
+        copy_calibration(args.copy_calib)
+        return
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only; --gpus {args.gpus} is not supported "
               "(expert parallelism across GPUs is described in DESIGN.md, not built)", file=sys.stderr)
@@ -180,10 +200,7 @@ def main():
     k_avg_ms = k_ms / k_n
     k_mean_bytes = float(np.mean([kern_bytes[i % args.layers][kern] for i in range(args.steps)]))
     achieved = k_mean_bytes / (k_avg_ms * 1e-3) / 1e9
-    traffic = None
-    tpath = os.path.join(ROOT, "profiles", f"{kern}_decode8_traffic.json")
-    if os.path.exists(tpath):
-        traffic = json.load(open(tpath)).get("hbm_bytes_per_launch")
+    traffic = measured_traffic(kern)
 
     cpu = None
     if not args.no_cpu:
@@ -216,6 +233,19 @@ def main():
         "stages": stages,
     }
     print(json.dumps(line), flush=True)
+
+
+def measured_traffic(kern):
+    """HBM bytes per launch of kern from the counter summary in profiles/
+    (rocprofv3 FETCH_SIZE / WRITE_SIZE scaled by a copy calibration), or None."""
+    path = os.path.join(ROOT, "profiles", "decode8_hbm_traffic.md")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        cells = [c.strip() for c in line.strip().strip("|").split("|")]
+        if len(cells) == 4 and cells[0] == kern and cells[3].isdigit():
+            return int(cells[3])
+    return None
 
 
 def cpu_baseline(layer, x_dev, sel, step_bytes, n_tok, budget_s):
