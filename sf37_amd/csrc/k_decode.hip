@@ -10,16 +10,16 @@
 //   up      : routed Q3 gate/up: a lane owns one 110-byte block, a wave two
 //             rows of gate and up, and the canonical block-order chain runs
 //             as a DPP scan; items come from atomic queues.
-//   mid     : SwiGLU * routing weight and the Q8_K of the routed mid.
-//   down    : the first waves apply SwiGLU to the shared gate/up and
-//             quantise the shared mid to Q8_0; then routed Q2 down, one row
-//             per pair and output row.
-//   combine : the shared expert's down rows (one wave per row group) and
-//             out = shared + sum over slots in slot order.
+//   mid     : SwiGLU * routing weight and the Q8_K of the routed mid; SwiGLU
+//             and Q8_0 of the shared mid.
+//   down    : routed Q2 down, one row per pair and output row, then the
+//             shared expert's down rows from atomic queues (they fill the
+//             routed part's tail).
+//   combine : out = shared + sum over slots in slot order.
 //
 // Nothing waits on another wave, so every wave always runs to completion;
-// the up kernel's queues hand out each item once and every wave stops at
-// its first request past the end of its queue.
+// the up and down kernels' queues hand out each item once and every wave
+// stops at its first request past the end of its queue.
 //
 // Arithmetic is the canonical order of the oracle (sf37_blocks.h), the
 // reference CPU order for the Q8_0 shared expert (sf37_ops.c:92-108), and
@@ -36,11 +36,13 @@ constexpr uint32_t SH_RS = 2;        // shared gate/up rows per workgroup
 constexpr uint32_t RT_ROWS = 2;      // router rows (experts) per route workgroup
 constexpr uint32_t DN_MAX_NB = 5;    // down blocks per row held in registers (F <= 1280)
 constexpr uint32_t DN_TPC = 2;       // pairs per pass in the routed down kernel
+constexpr uint32_t DN_STAGE = 4;     // pairs whose activation blocks a down wave keeps in LDS
+static_assert(DN_STAGE % DN_TPC == 0, "a down pass stays inside one staged chunk");
 constexpr uint32_t SHD_CHUNK = 4;    // shared-down Q8_0 blocks per load batch (even)
 constexpr uint32_t SHD_MAX_BPS = 12; // shared-down blocks per lane (a multiple of SHD_CHUNK)
 constexpr uint32_t UP_QUEUES = 64;   // queues of the up kernel's dynamic items, one per 128 bytes
 constexpr uint32_t UP_DYN_PCT = 25;  // share of the up items handed out dynamically (percent)
-constexpr uint32_t CB_PASSES = 2;    // shared-down row groups per combine wave
+constexpr uint32_t DN_QUEUES = 64;   // queues of the down kernel's shared-down rows, one per 128 bytes
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4a4 __attribute__((ext_vector_type(4), aligned(4)));
@@ -55,9 +57,12 @@ using dec_params = sf37_dec_params;
 
 namespace {
 
-// Counters: the up kernel's item queues, 32 words apart (zeroed by the
-// select workgroup).
+// Counters: the up kernel's item queues, then the down kernel's, 32 words
+// apart (zeroed by the select workgroup).
 __device__ __forceinline__ uint32_t *up_queue(const dec_params &p, uint32_t q) { return p.cnt + 32u * q; }
+__device__ __forceinline__ uint32_t *dn_queue(const dec_params &p, uint32_t q) {
+    return p.cnt + 32u * (UP_QUEUES + q);
+}
 
 // Shared-down lane layout: the Q8_0 blocks of a row are split into S slices
 // (a power of two <= 16 with S * T <= 64, so one token's slices sit in one
@@ -73,8 +78,16 @@ __host__ __device__ constexpr uint32_t shd_bps(uint32_t nb8, uint32_t S) { retur
 __host__ __device__ constexpr uint32_t tile_buf(uint32_t bytes) { return (bytes + 31u + 15u) & ~15u; }
 __host__ __device__ constexpr uint32_t up_shared_tile(uint32_t K) { return SH_RS * (K / 32u) * SF37_Q8_0_BYTES; }
 // up workgroup: x of every token, then group info and sorted pairs
+// An activation block in the up kernel's LDS, padded to 304 bytes so the 16
+// blocks a wave reads at once spread over the LDS banks (a 288-byte stride
+// puts every fourth block on the same banks).
+struct act_lds_t {
+    act_t a;
+    uint32_t pad[4];
+};
+static_assert(sizeof(act_lds_t) == 304, "act_lds_t is 304 bytes");
 __host__ __device__ constexpr size_t lds_up_routed(uint32_t K, uint32_t T, uint32_t G, uint32_t P) {
-    return (size_t)T * (K / SF37_QK) * sizeof(act_t) + (size_t)(3u + 2u * G + P) * 4u;
+    return (size_t)T * (K / SF37_QK) * sizeof(act_lds_t) + (size_t)(3u + 2u * G + 2u * P) * 4u;
 }
 __host__ __device__ constexpr size_t lds_up_shared(uint32_t K, uint32_t T) {
     return 2u * (size_t)tile_buf(up_shared_tile(K)) + (size_t)T * 2u * SH_RS * (K / 32u) * 4u;
@@ -270,6 +283,7 @@ __device__ void select_and_group(const dec_params &p) {
 __global__ void __launch_bounds__(256) dec_select_kernel(dec_params p) {
     if (blockIdx.x == 0) {
         if (threadIdx.x < UP_QUEUES) *up_queue(p, threadIdx.x) = 0u;
+        if (threadIdx.x < DN_QUEUES) *dn_queue(p, threadIdx.x) = 0u;
         select_and_group(p);
         return;
     }
@@ -386,16 +400,27 @@ __device__ __forceinline__ void q3_block_dots(const uint32_t *a, const act_t *co
 }
 
 // acc = fma(d_b, bs_b, acc) over the blocks b = 0..nb-1 held by lanes 0..nb-1
-// of each 16-lane row: a scan with row_shr:1, exact canonical order.  The
-// row's total ends in lane nb-1.
-__device__ __forceinline__ float block_chain(float d, float bs, uint32_t nb) {
-    float acc = __builtin_fmaf(d, bs, 0.0f);
-    for (uint32_t st = 1; st < nb; st++) {
-        const float prev =
-            __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, acc), 0x111, 0xf, 0xf, true));
-        acc = __builtin_fmaf(d, bs, prev);
+// of each 16-lane row: a scan with row_shr:1, exact canonical order, for NT
+// tokens at once (their steps interleave).  The row's total ends in lane
+// nb-1.  Unrolled for 16 blocks (K = 4096).
+template <int NT>
+__device__ __forceinline__ void block_chains(const float *d, const float *bs, float *acc, uint32_t nb) {
+    auto step = [&]() {
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+            const float prev = __builtin_bit_cast(
+                float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, acc[t]), 0x111, 0xf, 0xf, true));
+            acc[t] = __builtin_fmaf(d[t], bs[t], prev);
+        }
+    };
+#pragma unroll
+    for (int t = 0; t < NT; t++) acc[t] = __builtin_fmaf(d[t], bs[t], 0.0f);
+    if (nb == 16u) {
+#pragma unroll
+        for (int st = 1; st < 16; st++) step();
+    } else {
+        for (uint32_t st = 1; st < nb; st++) step();
     }
-    return acc;
 }
 
 // Keeps the compiler from hoisting work on w out of a loop (an empty asm
@@ -406,84 +431,70 @@ __device__ __forceinline__ void opaque(uint32_t *w) {
     for (int i = 0; i < N; i++) asm volatile("" : "+v"(w[i]));
 }
 
-// Shared down and combine: out[t][row] = shared + sum over slots in slot
-// order, where shared = sum over Q8_0 blocks b in order of
-// (isum_b * ws_b) * xs_b (sf37_ops.c:92-108), for R = 64 / (T * S) rows per
-// pass.  Lane = (row, token, slice): the slice holds bps consecutive blocks,
-// loaded as NB batches of SHD_CHUNK (all issued before the first is used),
-// and computes their terms; the sequential sum then walks the slices in
-// order with row_shr:1 (each slice adds its terms to the previous slice's
-// total).  The shared mid codes and scales of every token are in LDS (xq:
-// T x F codes, then T x F/32 scales).
-template <int NB>
-__device__ __forceinline__ void shared_down_pass(const dec_params &p, const int8_t *xq, const float *xsc, uint32_t r0) {
+// Shared down: sh_out[t][row] = sum over Q8_0 blocks b in order of
+// (isum_b * ws_b) * xs_b (sf37_ops.c:92-108) for R = 64 / (T * S) rows.
+// Lane = (row, token, slice): the slice holds bps consecutive blocks, loaded
+// in batches of SHD_CHUNK (one batch in registers at a time), and computes
+// their terms; the sequential sum then walks the slices in order with
+// row_shr:1 (each slice adds its terms to the previous slice's total).  The
+// shared mid codes and scales of every token are in LDS (xq: T x F codes,
+// xsc: T x F/32 scales).
+__device__ void shared_down_pass(const dec_params &p, const int8_t *xq, const float *xsc, uint32_t r0) {
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t S = shd_slices(p.T), TS = p.T * S, R = 64u / TS;
     const uint32_t nb8 = p.F / 32u, bps = shd_bps(nb8, S), ns = (nb8 + bps - 1u) / bps;
+    const uint32_t nbat = (bps + SHD_CHUNK - 1u) / SHD_CHUNK;
     const uint32_t rsub = lane / TS, li = lane - rsub * TS, t = li / S, j = li - t * S;
     const bool lane_ok = rsub < R;
     const uint32_t tc = lane_ok ? t : 0u;
     const uint64_t row_bytes = (uint64_t)nb8 * SF37_Q8_0_BYTES;
     const uint32_t row = r0 + (lane_ok ? rsub : 0u);
     const uint32_t rowc = row < p.K ? row : p.K - 1u;
-    // the routed slot values of (token, row), summed after the shared value
-    float v[16];
+    float term[SHD_MAX_BPS];
 #pragma unroll
-    for (uint32_t s = 0; s < 16u; s++) {
-        const uint32_t sc = s < p.topk ? s : 0u;                     // every read in bounds
-        v[s] = p.down_pair[((uint64_t)tc * p.topk + sc) * p.K + rowc];
-    }
-    uint32_t w[NB][36];
+    for (uint32_t c = 0; c < SHD_MAX_BPS / SHD_CHUNK; c++) {
+        if (c < nbat) {
+            // blocks [b0, b0 + nv) of this batch; nv = 0 past the slice or row
+            const uint32_t b0 = j * bps + c * SHD_CHUNK;
+            const uint32_t in_slice = bps > c * SHD_CHUNK ? bps - c * SHD_CHUNK : 0u;
+            const uint32_t in_row = nb8 > b0 ? nb8 - b0 : 0u;
+            uint32_t nv = in_slice < in_row ? in_slice : in_row;
+            nv = nv < SHD_CHUNK ? nv : SHD_CHUNK;
+            const u32x4a4 *q = (const u32x4a4 *)(p.sh_down + (uint64_t)rowc * row_bytes +
+                                                 (uint64_t)(nv ? b0 : 0u) * SF37_Q8_0_BYTES);
+            uint32_t w[36];
 #pragma unroll
-    for (int c = 0; c < NB; c++) {
-        // blocks [b0, b0 + nv) of this batch; nv = 0 past the slice or row
-        const uint32_t b0 = j * bps + c * SHD_CHUNK;
-        const uint32_t in_slice = bps > c * SHD_CHUNK ? bps - c * SHD_CHUNK : 0u;
-        const uint32_t in_row = nb8 > b0 ? nb8 - b0 : 0u;
-        uint32_t nv = in_slice < in_row ? in_slice : in_row;
-        nv = nv < SHD_CHUNK ? nv : SHD_CHUNK;
-        const u32x4a4 *q =
-            (const u32x4a4 *)(p.sh_down + (uint64_t)rowc * row_bytes + (uint64_t)(nv ? b0 : 0u) * SF37_Q8_0_BYTES);
-#pragma unroll
-        for (uint32_t i = 0; i < 9; i++) {
-            // dwords past the batch re-read its first 16 bytes: every load
-            // stays within the batch's blocks (+ < 16 bytes), unpredicated
-            const u32x4a4 v = q[16u * i < nv * SF37_Q8_0_BYTES ? i : 0u];
-            w[c][4 * i] = v.x;
-            w[c][4 * i + 1] = v.y;
-            w[c][4 * i + 2] = v.z;
-            w[c][4 * i + 3] = v.w;
-        }
-    }
-    float term[NB * SHD_CHUNK];
-#pragma unroll
-    for (int c = 0; c < NB; c++) {
-#pragma unroll
-        for (uint32_t i = 0; i < SHD_CHUNK; i++) {
-            const uint32_t B = 34u * i, d0 = B / 4u;                // compile-time offset in the batch
-            const uint32_t bg = j * bps + c * SHD_CHUNK + i;
-            const uint32_t b = bg < nb8 ? bg : 0u;
-            const u32x4 *xp = (const u32x4 *)(xq + (uint64_t)tc * p.F + (uint64_t)b * 32u);
-            const u32x4 x0 = xp[0], x1 = xp[1];
-            const uint32_t xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-            int32_t isum = 0;
-            float ws;
-            if ((B & 3u) == 0u) {
-                ws = sf37_f16(w[c][d0]);
-#pragma unroll
-                for (int k = 0; k < 8; k++) isum = sdot4(align_bytes(w[c][d0 + k + 1], w[c][d0 + k], 2), xv[k], isum);
-            } else {
-                ws = sf37_f16(w[c][d0] >> 16);
-#pragma unroll
-                for (int k = 0; k < 8; k++) isum = sdot4(w[c][d0 + 1 + k], xv[k], isum);
+            for (uint32_t i = 0; i < 9; i++) {
+                // dwords past the batch re-read its first 16 bytes: every load
+                // stays within the batch's blocks (+ < 16 bytes), unpredicated
+                const u32x4a4 v = q[16u * i < nv * SF37_Q8_0_BYTES ? i : 0u];
+                w[4 * i] = v.x;
+                w[4 * i + 1] = v.y;
+                w[4 * i + 2] = v.z;
+                w[4 * i + 3] = v.w;
             }
-            term[c * SHD_CHUNK + i] = (float)isum * ws * xsc[(uint64_t)tc * nb8 + b];
-        }
-        // this batch's terms are final here: its activation reads are not
-        // hoisted above the earlier batches' arithmetic
 #pragma unroll
-        for (uint32_t i = 0; i < SHD_CHUNK; i++) asm volatile("" : "+v"(term[c * SHD_CHUNK + i]));
-        __builtin_amdgcn_sched_barrier(0);
+            for (uint32_t i = 0; i < SHD_CHUNK; i++) {
+                const uint32_t B = 34u * i, d0 = B / 4u;            // compile-time offset in the batch
+                const uint32_t bg = b0 + i;
+                const uint32_t b = bg < nb8 ? bg : 0u;
+                const u32x4 *xp = (const u32x4 *)(xq + (uint64_t)tc * p.F + (uint64_t)b * 32u);
+                const u32x4 x0 = xp[0], x1 = xp[1];
+                const uint32_t xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+                int32_t isum = 0;
+                float ws;
+                if ((B & 3u) == 0u) {
+                    ws = sf37_f16(w[d0]);
+#pragma unroll
+                    for (int k = 0; k < 8; k++) isum = sdot4(align_bytes(w[d0 + k + 1], w[d0 + k], 2), xv[k], isum);
+                } else {
+                    ws = sf37_f16(w[d0] >> 16);
+#pragma unroll
+                    for (int k = 0; k < 8; k++) isum = sdot4(w[d0 + 1 + k], xv[k], isum);
+                }
+                term[c * SHD_CHUNK + i] = (float)isum * ws * xsc[(uint64_t)tc * nb8 + b];
+            }
+        }
     }
     // sequential sum over the slices of each (row, token)
     float acc = 0.0f;
@@ -493,16 +504,12 @@ __device__ __forceinline__ void shared_down_pass(const dec_params &p, const int8
         if (j == st) {
             float a2 = st == 0u ? 0.0f : prev;
 #pragma unroll
-            for (uint32_t i = 0; i < NB * SHD_CHUNK; i++)
+            for (uint32_t i = 0; i < SHD_MAX_BPS; i++)
                 if (i < bps && j * bps + i < nb8) a2 = a2 + term[i];
             acc = a2;
         }
     }
-    float r = 0.0f;
-#pragma unroll
-    for (uint32_t s = 0; s < 16u; s++)
-        if (s < p.topk) r = r + v[s];
-    if (lane_ok && j == ns - 1u && row < p.K) p.out[(uint64_t)t * p.K + row] = acc + r;
+    if (lane_ok && j == ns - 1u && row < p.K) p.sh_out[(uint64_t)t * p.K + row] = acc;
 }
 
 // Routed gate/up.  An item is 2 rows of one group's expert for both
@@ -518,13 +525,21 @@ __device__ __forceinline__ void shared_down_pass(const dec_params &p, const int8
 __global__ void __launch_bounds__(256) dec_up_kernel(dec_params p) {
     extern __shared__ __align__(16) unsigned char smem[];
     const uint32_t nbK = p.K / SF37_QK, P = p.T * p.topk;
-    act_t *xs = (act_t *)smem;
+    act_lds_t *xs = (act_lds_t *)smem;
     uint32_t *gi = (uint32_t *)(xs + p.T * nbK);
     uint32_t *so = gi + 3u + 2u * p.G;
-    const uint32_t n_x = p.T * nbK * (uint32_t)(sizeof(act_t) / 16u);
-    for (uint32_t i = threadIdx.x; i < n_x; i += blockDim.x) ((u32x4 *)xs)[i] = ((const u32x4 *)p.xq)[i];
+    uint32_t *xo = so + P;                                        // first x block of each sorted pair's token
+    constexpr uint32_t A16 = sizeof(act_t) / 16u, L16 = sizeof(act_lds_t) / 16u;
+    for (uint32_t i = threadIdx.x; i < p.T * nbK * A16; i += blockDim.x) {
+        const uint32_t blk = i / A16, c = i - blk * A16;
+        ((u32x4 *)xs)[blk * L16 + c] = ((const u32x4 *)p.xq)[i];
+    }
     for (uint32_t i = threadIdx.x; i < 3u + 2u * p.G; i += blockDim.x) gi[i] = p.ginfo[i];
-    for (uint32_t i = threadIdx.x; i < P; i += blockDim.x) so[i] = p.sorted[i];
+    for (uint32_t i = threadIdx.x; i < P; i += blockDim.x) {
+        const uint32_t pr = p.sorted[i];
+        so[i] = pr;
+        xo[i] = (pr / p.topk) * nbK;
+    }
     __syncthreads();
 
     const uint32_t lane = threadIdx.x & 63u;
@@ -532,7 +547,8 @@ __global__ void __launch_bounds__(256) dec_up_kernel(dec_params p) {
     const uint32_t nw = gridDim.x * (blockDim.x >> 6), gw = blockIdx.x * (blockDim.x >> 6) + wave;
     const uint32_t m = lane >> 5, rr = (lane >> 4) & 1u, b = lane & 15u;
     const uint32_t bl = b < nbK ? b : nbK - 1u;                    // lanes past the row repeat its last block
-    const bool out_lane = m == 0u && b == nbK - 1u;
+    const bool out_lane = b == nbK - 1u;
+    float *const out_rows = m ? p.up_out : p.gate_out;
     const uint32_t ipg = p.F / 2u, n_items = gi[0] * ipg;
     const uint32_t n_stat = n_items - (uint32_t)((uint64_t)n_items * UP_DYN_PCT / 100u);
     const uint32_t lo = (uint32_t)((uint64_t)n_stat * gw / nw), hi = (uint32_t)((uint64_t)n_stat * (gw + 1u) / nw);
@@ -542,8 +558,9 @@ __global__ void __launch_bounds__(256) dec_up_kernel(dec_params p) {
     uint32_t *queue = up_queue(p, qi);
     const uint64_t row_bytes = (uint64_t)nbK * SF37_Q3_BYTES, exp_bytes = (uint64_t)p.F * row_bytes;
     const uint8_t *W = m ? p.up_w : p.gate_w;
-    auto block_ptr = [&](uint32_t item) -> const uint8_t * {
-        const uint32_t g = item / ipg, rp = item - g * ipg;
+    // an item is carried as (group, row pair): static successors step it,
+    // dynamic answers divide once
+    auto block_ptr = [&](uint32_t g, uint32_t rp) -> const uint8_t * {
         return W + (uint64_t)gi[2u + p.G + g] * exp_bytes + (uint64_t)(2u * rp + rr) * row_bytes +
                (uint64_t)bl * SF37_Q3_BYTES;
     };
@@ -563,70 +580,98 @@ __global__ void __launch_bounds__(256) dec_up_kernel(dec_params p) {
         if (cur >= q1) return;
         pend = request();
     }
+    uint32_t g = cur / ipg, rp = cur - g * ipg;
     uint32_t nxt[28];
-    load_q3(nxt, block_ptr(cur));
+    const uint8_t *curp = block_ptr(g, rp);
+    load_q3(nxt, curp);
     for (;;) {
         uint32_t raw[28], a[27];
 #pragma unroll
         for (int k = 0; k < 28; k++) raw[k] = nxt[k];
-        const uint8_t *curp = block_ptr(cur);
         // the next item: the static successor, else the pending request's answer
-        uint32_t nx;
+        uint32_t nx, ng, nrp;
         if (cur + 1u < hi) {
             nx = cur + 1u;
+            ng = rp + 1u == ipg ? g + 1u : g;
+            nrp = rp + 1u == ipg ? 0u : rp + 1u;
             if (nx + 1u == hi) pend = request();
         } else {
             nx = answer(pend);
+            ng = nx / ipg;
+            nrp = nx - ng * ipg;
             if (nx < q1) pend = request();
         }
         const bool more = nx < hi || (nx >= q0 && nx < q1);
-        if (more) load_q3(nxt, block_ptr(nx));
+        const uint8_t *nxp = more ? block_ptr(ng, nrp) : curp;
+        if (more) load_q3(nxt, nxp);
         q3_realign(a, raw, (uint32_t)((uintptr_t)curp & 3u));
-        const uint32_t g = cur / ipg, row = 2u * (cur - g * ipg) + rr;
+        const uint32_t row = 2u * rp + rr;
         const uint32_t p0 = gi[1u + g], p1 = gi[2u + g];
         for (uint32_t c0 = p0; c0 < p1; c0 += DEC_TPC) {
             const uint32_t nt = p1 - c0 < DEC_TPC ? p1 - c0 : DEC_TPC;
             opaque<27>(a);
             const act_t *x[DEC_TPC];
 #pragma unroll
-            for (uint32_t t = 0; t < DEC_TPC; t++) x[t] = xs + (so[c0 + (t < nt ? t : 0u)] / p.topk) * nbK + bl;
-            float bs[DEC_TPC];
-            switch (nt) {
-                case 1: q3_block_dots<1>(a, x, bs); break;
-                case 2: q3_block_dots<2>(a, x, bs); break;
-                case 3: q3_block_dots<3>(a, x, bs); break;
-                default: q3_block_dots<4>(a, x, bs); break;
-            }
+            for (uint32_t t = 0; t < DEC_TPC; t++) x[t] = &xs[xo[c0 + (t < nt ? t : 0u)] + bl].a;
+            float bs[DEC_TPC], dd[DEC_TPC], acc[DEC_TPC];
 #pragma unroll
-            for (uint32_t t = 0; t < DEC_TPC; t++) {
-                if (t < nt) {
-                    const float acc = block_chain(x[t]->d, bs[t], nbK);
-                    const float up = __shfl_xor(acc, 32, 64);
-                    if (out_lane) {
-                        const uint64_t o = (uint64_t)so[c0 + t] * p.F + row;
-                        p.gate_out[o] = acc;
-                        p.up_out[o] = up;
-                    }
-                }
+            for (uint32_t t = 0; t < DEC_TPC; t++) dd[t] = x[t]->d;
+            switch (nt) {
+                case 1: q3_block_dots<1>(a, x, bs); block_chains<1>(dd, bs, acc, nbK); break;
+                case 2: q3_block_dots<2>(a, x, bs); block_chains<2>(dd, bs, acc, nbK); break;
+                case 3: q3_block_dots<3>(a, x, bs); block_chains<3>(dd, bs, acc, nbK); break;
+                default: q3_block_dots<4>(a, x, bs); block_chains<4>(dd, bs, acc, nbK); break;
+            }
+            // the last block's lane of each (matrix, row) stores its row
+            if (out_lane) {
+#pragma unroll
+                for (uint32_t t = 0; t < DEC_TPC; t++)
+                    if (t < nt) out_rows[(uint64_t)so[c0 + t] * p.F + row] = acc[t];
             }
         }
         if (!more) break;
         cur = nx;
+        g = ng;
+        rp = nrp;
+        curp = nxp;
     }
 }
 
 // ---------------------------------------------------------------------------
 // mid: SwiGLU * routing weight (sf37.c:2179-2186) and its Q8_K in the Q2
-// activation layout, one wave per (pair, 256-row block); lane l owns rows
-// 4l .. 4l + 3
+// activation layout, one wave per (pair, 256-row block), lane l owning rows
+// 4l .. 4l + 3; then, with the shared expert, the shared mid
 // ---------------------------------------------------------------------------
 __global__ void __launch_bounds__(256) dec_mid_kernel(dec_params p) {
     __shared__ uint64_t tab[32];
     sf37_stage_exp_tab(tab);
     __syncthreads();
     const uint32_t lane = threadIdx.x & 63u, nbm = p.F / SF37_QK;
-    const uint32_t w = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-    if (w >= p.T * p.topk * nbm) return;
+    const uint32_t w = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6), n_routed = p.T * p.topk * nbm;
+    if (w >= n_routed) {
+        if (!(p.flags & SF37_DEC_SHARED)) return;
+        // shared mid: SwiGLU (clamp_shared) and Q8_0 (sf37_ops.c:57-90), one
+        // half-wave per (token, 32-row block)
+        const uint32_t nb32 = p.F / 32u;
+        const uint32_t hw = 2u * (w - n_routed) + (lane >> 5), l = lane & 31u;
+        if (hw >= p.T * nb32) return;
+        const uint32_t t = hw / nb32, blk = hw - t * nb32;
+        const uint64_t o = (uint64_t)t * p.F + (uint64_t)blk * 32u + l;
+        const float v = sf37_swiglu_mid_t(p.sh_gu[o], p.sh_gu[(uint64_t)p.T * p.F + o], 1.0f, p.clamp_shared, tab);
+        float amax = fabsf(v);
+#pragma unroll
+        for (int off = 16; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 32));
+        int8_t qv = 0;
+        float d = 0.0f;
+        if (amax != 0.0f) {
+            d = amax / 127.0f;
+            const float is = 1.0f / d;
+            qv = (int8_t)(int)fminf(fmaxf(__builtin_rintf(is * v), -128.0f), 127.0f);
+        }
+        p.sh_mq[o] = qv;
+        if (l == 0) p.sh_ms[(uint64_t)t * nb32 + blk] = d;
+        return;
+    }
     const uint32_t pr = w / nbm, blk = w - pr * nbm;
     const uint64_t o = (uint64_t)pr * p.F + (uint64_t)blk * SF37_QK + 4u * lane;
     const float wt = p.wts[pr];
@@ -704,58 +749,53 @@ __device__ __forceinline__ void q2_block_dots_lds(const uint32_t *a, const act_t
 // acc = fma(d_b, bs_b, acc) along the nb lanes of each row segment (lane
 // blocks 0..nb-1 of one row are consecutive lanes inside a 16-lane DPP
 // row); the row's total ends in the lane of block nb-1.
-__device__ __forceinline__ float seg_chain(float d, float bs, uint32_t b, uint32_t nb) {
-    float acc = __builtin_fmaf(d, bs, 0.0f);
-    for (uint32_t st = 1; st < nb; st++) {
-        const float prev =
-            __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, acc), 0x111, 0xf, 0xf, true));
-        acc = __builtin_fmaf(d, bs, b == 0u ? 0.0f : prev);
+// NT tokens at once (their steps interleave); unrolled for 5 blocks
+// (F = 1280).
+template <int NT>
+__device__ __forceinline__ void seg_chains(const float *d, const float *bs, float *acc, uint32_t b, uint32_t nb) {
+    auto step = [&]() {
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+            const float prev = __builtin_bit_cast(
+                float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, acc[t]), 0x111, 0xf, 0xf, true));
+            acc[t] = __builtin_fmaf(d[t], bs[t], b == 0u ? 0.0f : prev);
+        }
+    };
+#pragma unroll
+    for (int t = 0; t < NT; t++) acc[t] = __builtin_fmaf(d[t], bs[t], 0.0f);
+    if (nb == 5u) {
+#pragma unroll
+        for (int st = 1; st < 5; st++) step();
+    } else {
+        for (uint32_t st = 1; st < nb; st++) step();
     }
-    return acc;
 }
 
-// Down.  With the shared expert the first waves quantise the shared mid.
-// Routed down: lane = (row, block): each 16-lane DPP row holds 16/nb rows
+// Down.  Routed down: lane = (row, block): each 16-lane DPP row holds 16/nb rows
 // with their nb blocks on consecutive lanes, so a wave reads 64/nb*4 rows
 // (12 for F = 1280) as one contiguous span.  A wave owns a contiguous range
 // of these sub-items (mostly inside one group); the group's activation
 // blocks for up to four pairs sit in the wave's LDS slice.  The next
 // sub-item's blocks are loaded while the current one is computed.
 __global__ void __launch_bounds__(256) dec_down_kernel(dec_params p) {
+    extern __shared__ __align__(16) unsigned char smem[];        // shared mid codes, then scales
     __shared__ uint32_t meta[3u + 2u * 256u + 256u];
-    __shared__ __align__(16) act_t xsl[4][DN_TPC * DN_MAX_NB];
-    __shared__ uint64_t tab[32];
+    __shared__ __align__(16) act_t xsl[4][DN_STAGE * DN_MAX_NB];
     const uint32_t P = p.T * p.topk;
+    const bool sh = (p.flags & SF37_DEC_SHARED) != 0;
     uint32_t *gi = meta;
     uint32_t *so = gi + 3u + 2u * p.G;
+    int8_t *shq = (int8_t *)smem;
+    float *shs = (float *)(smem + p.T * p.F);
     for (uint32_t i = threadIdx.x; i < 3u + 2u * p.G; i += blockDim.x) gi[i] = p.ginfo[i];
     for (uint32_t i = threadIdx.x; i < P; i += blockDim.x) so[i] = p.sorted[i];
-    sf37_stage_exp_tab(tab);
+    if (sh) {
+        for (uint32_t i = threadIdx.x; i < p.T * p.F / 16u; i += blockDim.x)
+            ((u32x4 *)shq)[i] = ((const u32x4 *)p.sh_mq)[i];
+        for (uint32_t i = threadIdx.x; i < p.T * (p.F / 32u); i += blockDim.x) shs[i] = p.sh_ms[i];
+    }
     __syncthreads();
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63u;
-    if (p.flags & SF37_DEC_SHARED) {
-        // shared mid: SwiGLU (clamp_shared) and Q8_0 (sf37_ops.c:57-90), one
-        // half-wave per (token, 32-row block), on the first waves
-        const uint32_t nb32 = p.F / 32u;
-        const uint32_t hw = 2u * (blockIdx.x * (blockDim.x >> 6) + wave) + (lane >> 5), l = lane & 31u;
-        if (hw < p.T * nb32) {
-            const uint32_t t = hw / nb32, blk = hw - t * nb32;
-            const uint64_t o = (uint64_t)t * p.F + (uint64_t)blk * 32u + l;
-            const float v = sf37_swiglu_mid_t(p.sh_gu[o], p.sh_gu[(uint64_t)p.T * p.F + o], 1.0f, p.clamp_shared, tab);
-            float amax = fabsf(v);
-#pragma unroll
-            for (int off = 16; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 32));
-            int8_t qv = 0;
-            float d = 0.0f;
-            if (amax != 0.0f) {
-                d = amax / 127.0f;
-                const float is = 1.0f / d;
-                qv = (int8_t)(int)fminf(fmaxf(__builtin_rintf(is * v), -128.0f), 127.0f);
-            }
-            p.sh_mq[o] = qv;
-            if (l == 0) p.sh_ms[(uint64_t)t * nb32 + blk] = d;
-        }
-    }
     act_t *xw = xsl[wave];
     const uint32_t nb = p.F / SF37_QK, rpd = 16u / nb, rpw = 4u * rpd;     // rows per DPP row / wave
     const uint32_t q = lane & 15u, r_in = q / nb, b = q - r_in * nb;
@@ -765,63 +805,92 @@ __global__ void __launch_bounds__(256) dec_down_kernel(dec_params p) {
     const uint32_t nw = gridDim.x * (blockDim.x >> 6), gw = blockIdx.x * (blockDim.x >> 6) + wave;
     const uint32_t lo = (uint32_t)((uint64_t)n_sub * gw / nw), hi = (uint32_t)((uint64_t)n_sub * (gw + 1u) / nw);
     const uint64_t row_bytes = (uint64_t)nb * SF37_Q2_BYTES;
-    auto blk_ptr = [&](uint32_t sidx) -> const uint8_t * {
-        const uint32_t g = sidx / spg, sub = sidx - g * spg;
-        uint32_t row = sub * rpw + rl;
+    // a sub-item is carried as (group, sub-item in group), stepped in order
+    auto blk_ptr = [&](uint32_t g_, uint32_t sub_) -> const uint8_t * {
+        uint32_t row = sub_ * rpw + rl;
         row = row < p.K ? row : p.K - 1u;                                    // keep tail lanes in bounds
-        return p.down_w + ((uint64_t)gi[2u + p.G + g] * p.K + row) * row_bytes + (uint64_t)b * SF37_Q2_BYTES;
+        return p.down_w + ((uint64_t)gi[2u + p.G + g_] * p.K + row) * row_bytes + (uint64_t)b * SF37_Q2_BYTES;
     };
     uint32_t staged_g = 0xffffffffu, staged_c0 = 0xffffffffu;
-    if (lo >= hi) return;
+    uint32_t g = lo / spg, sub = lo - g * spg;
     uint32_t nxt[21];
-    load_q2(nxt, blk_ptr(lo));
+    if (lo < hi) load_q2(nxt, blk_ptr(g, sub));
     for (uint32_t sidx = lo; sidx < hi; sidx++) {
         uint32_t w[21];
 #pragma unroll
         for (int i = 0; i < 21; i++) w[i] = nxt[i];
-        if (sidx + 1u < hi) load_q2(nxt, blk_ptr(sidx + 1u));
-        const uint32_t g = sidx / spg, sub = sidx - g * spg;
+        const uint32_t ng = sub + 1u == spg ? g + 1u : g, nsub = sub + 1u == spg ? 0u : sub + 1u;
+        if (sidx + 1u < hi) load_q2(nxt, blk_ptr(ng, nsub));
         const uint32_t row = sub * rpw + rl;
         const bool out_lane = active && b == nb - 1u && row < p.K;
         const uint32_t p0 = gi[1u + g], p1 = gi[2u + g];
         for (uint32_t c0 = p0; c0 < p1; c0 += DN_TPC) {
             const uint32_t nt = p1 - c0 < DN_TPC ? p1 - c0 : DN_TPC;
-            if (g != staged_g || c0 != staged_c0) {
-                // stage this pass's activation blocks (nt pairs x nb blocks)
+            // the activation blocks of up to DN_STAGE pairs stay staged, so a
+            // group of that many pairs is staged once for the wave's range
+            const uint32_t cs = p0 + ((c0 - p0) / DN_STAGE) * DN_STAGE;
+            if (g != staged_g || cs != staged_c0) {
+                const uint32_t ns = p1 - cs < DN_STAGE ? p1 - cs : DN_STAGE;
                 __builtin_amdgcn_wave_barrier();
-                const uint32_t words = nt * nb * (uint32_t)(sizeof(act_t) / 16u);
-                for (uint32_t i = lane; i < words; i += 64u) {
-                    const uint32_t per = nb * (uint32_t)(sizeof(act_t) / 16u);
+                const uint32_t per = nb * (uint32_t)(sizeof(act_t) / 16u);
+                for (uint32_t i = lane; i < ns * per; i += 64u) {
                     const uint32_t t = i / per, k = i - t * per;
-                    ((u32x4 *)xw)[i] = ((const u32x4 *)((const act_t *)p.midq + (uint64_t)so[c0 + t] * nb))[k];
+                    ((u32x4 *)xw)[i] = ((const u32x4 *)((const act_t *)p.midq + (uint64_t)so[cs + t] * nb))[k];
                 }
                 asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
                 __builtin_amdgcn_wave_barrier();
                 staged_g = g;
-                staged_c0 = c0;
+                staged_c0 = cs;
             }
             opaque<21>(w);
             const act_t *x[DEC_TPC];
 #pragma unroll
-            for (uint32_t t = 0; t < DEC_TPC; t++) x[t] = xw + (t < nt ? t : 0u) * nb + b;
-            float bs[DEC_TPC];
-            if (nt == 1) q2_block_dots_lds<1>(w, x, bs);
-            else q2_block_dots_lds<2>(w, x, bs);
+            for (uint32_t t = 0; t < DEC_TPC; t++) x[t] = xw + (c0 - cs + (t < nt ? t : 0u)) * nb + b;
+            float bs[DEC_TPC], dd[DN_TPC], acc[DN_TPC];
 #pragma unroll
-            for (uint32_t t = 0; t < DN_TPC; t++) {
-                if (t < nt) {
-                    const float acc = seg_chain(x[t]->d, bs[t], b, nb);
-                    if (out_lane) p.down_pair[(uint64_t)so[c0 + t] * p.K + row] = acc;
-                }
+            for (uint32_t t = 0; t < DN_TPC; t++) dd[t] = x[t]->d;
+            if (nt == 1) {
+                q2_block_dots_lds<1>(w, x, bs);
+                seg_chains<1>(dd, bs, acc, b, nb);
+            } else {
+                q2_block_dots_lds<2>(w, x, bs);
+                seg_chains<2>(dd, bs, acc, b, nb);
+            }
+            if (out_lane) {
+#pragma unroll
+                for (uint32_t t = 0; t < DN_TPC; t++)
+                    if (t < nt) p.down_pair[(uint64_t)so[c0 + t] * p.K + row] = acc[t];
             }
         }
+        g = ng;
+        sub = nsub;
+    }
+    if (!sh) return;
+    // Then the shared expert's down rows, handed out one row group at a time
+    // from DN_QUEUES queues (wave w asks queue w % DN_QUEUES, which owns a
+    // contiguous share): waves that finish their routed range early take
+    // more.  The next request is issued before the current group is computed.
+    const uint32_t R = 64u / (p.T * shd_slices(p.T)), n_sp = (p.K + R - 1u) / R;
+    const uint32_t qi = gw % DN_QUEUES;
+    const uint32_t q0 = (uint32_t)((uint64_t)n_sp * qi / DN_QUEUES), q1 = (uint32_t)((uint64_t)n_sp * (qi + 1u) / DN_QUEUES);
+    uint32_t *queue = dn_queue(p, qi);
+    auto request = [&]() -> uint32_t {
+        uint32_t v = 0;
+        if (lane == 0) v = atomicAdd(queue, 1u);
+        return v;
+    };
+    uint32_t pend = request();
+    for (;;) {
+        const uint32_t idx = q0 + (uint32_t)__builtin_amdgcn_readfirstlane((int)pend);
+        if (idx >= q1) break;
+        pend = request();
+        shared_down_pass(p, shq, shs, idx * R);
     }
 }
 
 // ---------------------------------------------------------------------------
-// combine: out = [shared +] sum over slots in slot order.  With the shared
-// expert one wave per CB_PASSES shared_down_pass row groups (mid codes
-// staged in LDS), else one thread per output.
+// combine: out = [shared +] sum over slots in slot order, one thread per
+// output
 // ---------------------------------------------------------------------------
 __global__ void __launch_bounds__(256) dec_combine_kernel(dec_params p) {
     const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
@@ -837,25 +906,7 @@ __global__ void __launch_bounds__(256) dec_combine_kernel(dec_params p) {
 #pragma unroll
     for (int s = 0; s < 16; s++)
         if ((uint32_t)s < p.topk) acc = acc + v[s];
-    p.out[i] = acc;
-}
-
-template <int NB>
-__global__ void __launch_bounds__(256) dec_combine_shared_kernel(dec_params p) {
-    extern __shared__ __align__(16) unsigned char smem[];        // shared mid codes, then scales
-    int8_t *shq = (int8_t *)smem;
-    float *shs = (float *)(smem + p.T * p.F);
-    for (uint32_t i = threadIdx.x; i < p.T * p.F / 16u; i += blockDim.x) ((u32x4 *)shq)[i] = ((const u32x4 *)p.sh_mq)[i];
-    for (uint32_t i = threadIdx.x; i < p.T * (p.F / 32u); i += blockDim.x) shs[i] = p.sh_ms[i];
-    __syncthreads();
-    const uint32_t S = shd_slices(p.T), R = 64u / (p.T * S);
-    const uint32_t gw = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-#pragma unroll 1
-    for (uint32_t i = 0; i < CB_PASSES; i++) {
-        const uint32_t r0 = (gw * CB_PASSES + i) * R;
-        if (r0 >= p.K) return;
-        shared_down_pass<NB>(p, shq, shs, r0);
-    }
+    p.out[i] = (p.flags & SF37_DEC_SHARED) ? p.sh_out[i] + acc : acc;
 }
 
 }  // namespace
@@ -918,15 +969,10 @@ dec_shape dec_plan(const dec_params &p) {
     d.n_shup = 1u + (sh ? p.F / SH_RS : 0u);           // select workgroup + shared rows
     // persistent kernels: exactly as many workgroups as can be resident
     d.n_up = resident_wgs((const void *)dec_up_kernel, 256, d.lds_up) * cus;
-    d.n_mid = (p.T * p.topk * (p.F / SF37_QK) + 3u) / 4u;
-    d.lds_dn = 0;
-    d.n_dn = resident_wgs((const void *)dec_down_kernel, 256, 0) * cus;
-    if (sh) {
-        const uint32_t R = 64u / (p.T * shd_slices(p.T));
-        d.n_cb = ((p.K + R * CB_PASSES - 1u) / (R * CB_PASSES) + 3u) / 4u;
-    } else {
-        d.n_cb = (p.T * p.K + 255u) / 256u;
-    }
+    d.n_mid = (p.T * p.topk * (p.F / SF37_QK) + (sh ? (p.T * (p.F / 32u) + 1u) / 2u : 0u) + 3u) / 4u;
+    d.lds_dn = sh ? (size_t)p.T * p.F + (size_t)p.T * (p.F / 32u) * 4u : 0u;
+    d.n_dn = resident_wgs((const void *)dec_down_kernel, 256, d.lds_dn) * cus;
+    d.n_cb = (p.T * p.K + 255u) / 256u;
     return d;
 }
 
@@ -936,7 +982,7 @@ extern "C" int sf37k_decode_counters(uint32_t T, uint32_t topk, uint32_t E, uint
     (void)K;
     const uint32_t P = T * topk, G = P < E ? P : E;
     (void)T; (void)topk; (void)E; (void)F;
-    return (int)(32u * UP_QUEUES);
+    return (int)(32u * (UP_QUEUES + DN_QUEUES));
 }
 
 extern "C" int sf37k_decode_supported(uint32_t T, uint32_t topk, uint32_t E, uint32_t K, uint32_t F, int shared) {
@@ -994,28 +1040,12 @@ extern "C" int sf37k_decode_mid(const sf37_dec_params *pp, sf37_stream_t s) {
 
 extern "C" int sf37k_decode_down(const sf37_dec_params *pp, sf37_stream_t s) {
     const dec_shape d = dec_plan(*pp);
-    hipLaunchKernelGGL(dec_down_kernel, dim3(d.n_dn), dim3(256), 0, (hipStream_t)s, *pp);
+    hipLaunchKernelGGL(dec_down_kernel, dim3(d.n_dn), dim3(256), d.lds_dn, (hipStream_t)s, *pp);
     return (int)hipGetLastError();
 }
 
 extern "C" int sf37k_decode_combine(const sf37_dec_params *pp, sf37_stream_t s) {
     const dec_shape d = dec_plan(*pp);
-    if (!(pp->flags & SF37_DEC_SHARED)) {
-        hipLaunchKernelGGL(dec_combine_kernel, dim3(d.n_cb), dim3(256), 0, (hipStream_t)s, *pp);
-        return (int)hipGetLastError();
-    }
-    // one kernel per number of load batches (registers follow the batches)
-    const uint32_t nbat = (shd_bps(pp->F / 32u, shd_slices(pp->T)) + SHD_CHUNK - 1u) / SHD_CHUNK;
-    const void *fn = nbat == 1u ? (const void *)dec_combine_shared_kernel<1>
-                   : nbat == 2u ? (const void *)dec_combine_shared_kernel<2>
-                                : (const void *)dec_combine_shared_kernel<3>;
-    const size_t lds = (size_t)pp->T * pp->F + (size_t)pp->T * (pp->F / 32u) * 4u;
-    if (lds > 65536u) {
-        const hipError_t err = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        if (err != hipSuccess) return (int)err;
-    }
-    if (nbat == 1u) hipLaunchKernelGGL(dec_combine_shared_kernel<1>, dim3(d.n_cb), dim3(256), lds, (hipStream_t)s, *pp);
-    else if (nbat == 2u) hipLaunchKernelGGL(dec_combine_shared_kernel<2>, dim3(d.n_cb), dim3(256), lds, (hipStream_t)s, *pp);
-    else hipLaunchKernelGGL(dec_combine_shared_kernel<3>, dim3(d.n_cb), dim3(256), lds, (hipStream_t)s, *pp);
+    hipLaunchKernelGGL(dec_combine_kernel, dim3(d.n_cb), dim3(256), 0, (hipStream_t)s, *pp);
     return (int)hipGetLastError();
 }

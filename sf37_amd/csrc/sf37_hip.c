@@ -953,7 +953,7 @@ static int decode_run(const routed_args *a, const dec_extra *ex, float *out, flo
     p.out = out;
     /* scratch layout */
     uint64_t off = 0, o_xq, o_xq8, o_xs8, o_gi, o_so, o_mid = 0, o_mq, o_gu = 0, o_smq = 0, o_sms = 0, o_dp = 0,
-                      o_lg = 0, o_ck = 0, o_cp = 0, o_sel = 0, o_wts = 0, o_go = 0, o_uo = 0;
+                      o_sho = 0, o_lg = 0, o_ck = 0, o_cp = 0, o_sel = 0, o_wts = 0, o_go = 0, o_uo = 0;
 #define TAKE(var, bytes)            \
     do {                            \
         var = off;                  \
@@ -972,6 +972,7 @@ static int decode_run(const routed_args *a, const dec_extra *ex, float *out, flo
         TAKE(o_gu, 2u * (uint64_t)T * F * 4u);
         TAKE(o_smq, (uint64_t)T * F);
         TAKE(o_sms, (uint64_t)T * (F / 32u) * 4u);
+        TAKE(o_sho, (uint64_t)T * K * 4u);
     }
     if (!down_pair) TAKE(o_dp, P * K * 4u);
     if (ex->flags & SF37_DEC_ROUTER) TAKE(o_lg, (uint64_t)T * E * 4u);
@@ -998,6 +999,7 @@ static int decode_run(const routed_args *a, const dec_extra *ex, float *out, flo
         p.sh_gu = (float *)(base + o_gu);
         p.sh_mq = (int8_t *)(base + o_smq);
         p.sh_ms = (float *)(base + o_sms);
+        p.sh_out = (float *)(base + o_sho);
     }
     p.down_pair = down_pair ? down_pair : (float *)(base + o_dp);
     p.logits = (ex->flags & SF37_DEC_ROUTER) ? (float *)(base + o_lg) : NULL;

@@ -126,6 +126,7 @@ typedef struct sf37_dec_params {
     float *sh_gu;        /* 2 x T x F shared gate | up */
     int8_t *sh_mq;       /* T x F Q8_0 codes of the shared mid */
     float *sh_ms;        /* T x F/32 scales */
+    float *sh_out;       /* T x K shared expert output */
     float *down_pair;    /* pairs x K */
     float *out;          /* T x K */
     uint32_t *cnt;
