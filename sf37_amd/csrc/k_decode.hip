@@ -434,11 +434,12 @@ __device__ __forceinline__ void opaque(uint32_t *w) {
 // Shared down: sh_out[t][row] = sum over Q8_0 blocks b in order of
 // (isum_b * ws_b) * xs_b (sf37_ops.c:92-108) for R = 64 / (T * S) rows.
 // Lane = (row, token, slice): the slice holds bps consecutive blocks, loaded
-// in batches of SHD_CHUNK (one batch in registers at a time), and computes
-// their terms; the sequential sum then walks the slices in order with
+// in NB batches of SHD_CHUNK (up to two batches in registers at a time), and
+// computes their terms; the sequential sum then walks the slices in order with
 // row_shr:1 (each slice adds its terms to the previous slice's total).  The
 // shared mid codes and scales of every token are in LDS (xq: T x F codes,
 // xsc: T x F/32 scales).
+template <int NB>
 __device__ void shared_down_pass(const dec_params &p, const int8_t *xq, const float *xsc, uint32_t r0) {
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t S = shd_slices(p.T), TS = p.T * S, R = 64u / TS;
@@ -450,51 +451,71 @@ __device__ void shared_down_pass(const dec_params &p, const int8_t *xq, const fl
     const uint64_t row_bytes = (uint64_t)nb8 * SF37_Q8_0_BYTES;
     const uint32_t row = r0 + (lane_ok ? rsub : 0u);
     const uint32_t rowc = row < p.K ? row : p.K - 1u;
+    (void)nbat;
+    // batches in groups of GR, each group's loads issued before its first
+    // block is used: all batches together when there are at most 2, one at
+    // a time when 3 (registers)
+    constexpr uint32_t GR = NB <= 2 ? (uint32_t)NB : 1u;
     float term[SHD_MAX_BPS];
 #pragma unroll
-    for (uint32_t c = 0; c < SHD_MAX_BPS / SHD_CHUNK; c++) {
-        if (c < nbat) {
-            // blocks [b0, b0 + nv) of this batch; nv = 0 past the slice or row
-            const uint32_t b0 = j * bps + c * SHD_CHUNK;
-            const uint32_t in_slice = bps > c * SHD_CHUNK ? bps - c * SHD_CHUNK : 0u;
-            const uint32_t in_row = nb8 > b0 ? nb8 - b0 : 0u;
-            uint32_t nv = in_slice < in_row ? in_slice : in_row;
-            nv = nv < SHD_CHUNK ? nv : SHD_CHUNK;
-            const u32x4a4 *q = (const u32x4a4 *)(p.sh_down + (uint64_t)rowc * row_bytes +
-                                                 (uint64_t)(nv ? b0 : 0u) * SF37_Q8_0_BYTES);
-            uint32_t w[36];
+    for (uint32_t c0 = 0; c0 < (uint32_t)NB; c0 += GR) {
+        uint32_t w[GR][36];
 #pragma unroll
-            for (uint32_t i = 0; i < 9; i++) {
-                // dwords past the batch re-read its first 16 bytes: every load
-                // stays within the batch's blocks (+ < 16 bytes), unpredicated
-                const u32x4a4 v = q[16u * i < nv * SF37_Q8_0_BYTES ? i : 0u];
-                w[4 * i] = v.x;
-                w[4 * i + 1] = v.y;
-                w[4 * i + 2] = v.z;
-                w[4 * i + 3] = v.w;
-            }
+        for (uint32_t cc = 0; cc < GR; cc++) {
+            if (c0 + cc < (uint32_t)NB) {
+                const uint32_t c = c0 + cc;
+                // blocks [b0, b0 + nv) of this batch; nv = 0 past the slice or row
+                const uint32_t b0 = j * bps + c * SHD_CHUNK;
+                const uint32_t in_slice = bps > c * SHD_CHUNK ? bps - c * SHD_CHUNK : 0u;
+                const uint32_t in_row = nb8 > b0 ? nb8 - b0 : 0u;
+                uint32_t nv = in_slice < in_row ? in_slice : in_row;
+                nv = nv < SHD_CHUNK ? nv : SHD_CHUNK;
+                const u32x4a4 *q = (const u32x4a4 *)(p.sh_down + (uint64_t)rowc * row_bytes +
+                                                     (uint64_t)(nv ? b0 : 0u) * SF37_Q8_0_BYTES);
 #pragma unroll
-            for (uint32_t i = 0; i < SHD_CHUNK; i++) {
-                const uint32_t B = 34u * i, d0 = B / 4u;            // compile-time offset in the batch
-                const uint32_t bg = b0 + i;
-                const uint32_t b = bg < nb8 ? bg : 0u;
-                const u32x4 *xp = (const u32x4 *)(xq + (uint64_t)tc * p.F + (uint64_t)b * 32u);
-                const u32x4 x0 = xp[0], x1 = xp[1];
-                const uint32_t xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-                int32_t isum = 0;
-                float ws;
-                if ((B & 3u) == 0u) {
-                    ws = sf37_f16(w[d0]);
-#pragma unroll
-                    for (int k = 0; k < 8; k++) isum = sdot4(align_bytes(w[d0 + k + 1], w[d0 + k], 2), xv[k], isum);
-                } else {
-                    ws = sf37_f16(w[d0] >> 16);
-#pragma unroll
-                    for (int k = 0; k < 8; k++) isum = sdot4(w[d0 + 1 + k], xv[k], isum);
+                for (uint32_t i = 0; i < 9; i++) {
+                    // dwords past the batch re-read its first 16 bytes: every load
+                    // stays within the batch's blocks (+ < 16 bytes), unpredicated
+                    const u32x4a4 v = q[16u * i < nv * SF37_Q8_0_BYTES ? i : 0u];
+                    w[cc][4 * i] = v.x;
+                    w[cc][4 * i + 1] = v.y;
+                    w[cc][4 * i + 2] = v.z;
+                    w[cc][4 * i + 3] = v.w;
                 }
-                term[c * SHD_CHUNK + i] = (float)isum * ws * xsc[(uint64_t)tc * nb8 + b];
             }
         }
+#pragma unroll
+        for (uint32_t cc = 0; cc < GR; cc++) {
+            if (c0 + cc < (uint32_t)NB) {
+                const uint32_t c = c0 + cc, b0 = j * bps + c * SHD_CHUNK;
+#pragma unroll
+                for (uint32_t i = 0; i < SHD_CHUNK; i++) {
+                    const uint32_t B = 34u * i, d0 = B / 4u;            // compile-time offset in the batch
+                    const uint32_t bg = b0 + i;
+                    const uint32_t b = bg < nb8 ? bg : 0u;
+                    const u32x4 *xp = (const u32x4 *)(xq + (uint64_t)tc * p.F + (uint64_t)b * 32u);
+                    const u32x4 x0 = xp[0], x1 = xp[1];
+                    const uint32_t xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+                    int32_t isum = 0;
+                    float ws;
+                    if ((B & 3u) == 0u) {
+                        ws = sf37_f16(w[cc][d0]);
+#pragma unroll
+                        for (int k = 0; k < 8; k++) isum = sdot4(align_bytes(w[cc][d0 + k + 1], w[cc][d0 + k], 2), xv[k], isum);
+                    } else {
+                        ws = sf37_f16(w[cc][d0] >> 16);
+#pragma unroll
+                        for (int k = 0; k < 8; k++) isum = sdot4(w[cc][d0 + 1 + k], xv[k], isum);
+                    }
+                    term[c * SHD_CHUNK + i] = (float)isum * ws * xsc[(uint64_t)tc * nb8 + b];
+                }
+            }
+        }
+        // the next group's loads are not hoisted above these terms
+#pragma unroll
+        for (uint32_t i = 0; i < GR * SHD_CHUNK; i++)
+            if (c0 * SHD_CHUNK + i < (uint32_t)NB * SHD_CHUNK) asm volatile("" : "+v"(term[c0 * SHD_CHUNK + i]));
+        __builtin_amdgcn_sched_barrier(0);
     }
     // sequential sum over the slices of each (row, token)
     float acc = 0.0f;
@@ -504,7 +525,7 @@ __device__ void shared_down_pass(const dec_params &p, const int8_t *xq, const fl
         if (j == st) {
             float a2 = st == 0u ? 0.0f : prev;
 #pragma unroll
-            for (uint32_t i = 0; i < SHD_MAX_BPS; i++)
+            for (uint32_t i = 0; i < (uint32_t)NB * SHD_CHUNK; i++)
                 if (i < bps && j * bps + i < nb8) a2 = a2 + term[i];
             acc = a2;
         }
@@ -529,17 +550,7 @@ __global__ void __launch_bounds__(256) dec_up_kernel(dec_params p) {
     uint32_t *gi = (uint32_t *)(xs + p.T * nbK);
     uint32_t *so = gi + 3u + 2u * p.G;
     uint32_t *xo = so + P;                                        // first x block of each sorted pair's token
-    constexpr uint32_t A16 = sizeof(act_t) / 16u, L16 = sizeof(act_lds_t) / 16u;
-    for (uint32_t i = threadIdx.x; i < p.T * nbK * A16; i += blockDim.x) {
-        const uint32_t blk = i / A16, c = i - blk * A16;
-        ((u32x4 *)xs)[blk * L16 + c] = ((const u32x4 *)p.xq)[i];
-    }
     for (uint32_t i = threadIdx.x; i < 3u + 2u * p.G; i += blockDim.x) gi[i] = p.ginfo[i];
-    for (uint32_t i = threadIdx.x; i < P; i += blockDim.x) {
-        const uint32_t pr = p.sorted[i];
-        so[i] = pr;
-        xo[i] = (pr / p.topk) * nbK;
-    }
     __syncthreads();
 
     const uint32_t lane = threadIdx.x & 63u;
@@ -571,19 +582,31 @@ __global__ void __launch_bounds__(256) dec_up_kernel(dec_params p) {
         return v;
     };
     auto answer = [&](uint32_t v) -> uint32_t { return q0 + (uint32_t)__builtin_amdgcn_readfirstlane((int)v); };
+    // the first item and its loads are started before x is staged
     uint32_t pend = 0, cur;
     if (lo < hi) {
         cur = lo;
         if (lo + 1u == hi) pend = request();
     } else {
         cur = answer(request());
-        if (cur >= q1) return;
-        pend = request();
+        if (cur < q1) pend = request();
     }
     uint32_t g = cur / ipg, rp = cur - g * ipg;
     uint32_t nxt[28];
-    const uint8_t *curp = block_ptr(g, rp);
-    load_q3(nxt, curp);
+    const uint8_t *curp = block_ptr(cur < q1 ? g : 0u, cur < q1 ? rp : 0u);
+    if (cur < q1) load_q3(nxt, curp);
+    constexpr uint32_t A16 = sizeof(act_t) / 16u, L16 = sizeof(act_lds_t) / 16u;
+    for (uint32_t i = threadIdx.x; i < p.T * nbK * A16; i += blockDim.x) {
+        const uint32_t blk = i / A16, c = i - blk * A16;
+        ((u32x4 *)xs)[blk * L16 + c] = ((const u32x4 *)p.xq)[i];
+    }
+    for (uint32_t i = threadIdx.x; i < P; i += blockDim.x) {
+        const uint32_t pr = p.sorted[i];
+        so[i] = pr;
+        xo[i] = (pr / p.topk) * nbK;
+    }
+    __syncthreads();
+    if (cur >= q1) return;
     for (;;) {
         uint32_t raw[28], a[27];
 #pragma unroll
@@ -777,6 +800,7 @@ __device__ __forceinline__ void seg_chains(const float *d, const float *bs, floa
 // of these sub-items (mostly inside one group); the group's activation
 // blocks for up to four pairs sit in the wave's LDS slice.  The next
 // sub-item's blocks are loaded while the current one is computed.
+template <int SHNB>
 __global__ void __launch_bounds__(256) dec_down_kernel(dec_params p) {
     extern __shared__ __align__(16) unsigned char smem[];        // shared mid codes, then scales
     __shared__ uint32_t meta[3u + 2u * 256u + 256u];
@@ -884,7 +908,7 @@ __global__ void __launch_bounds__(256) dec_down_kernel(dec_params p) {
         const uint32_t idx = q0 + (uint32_t)__builtin_amdgcn_readfirstlane((int)pend);
         if (idx >= q1) break;
         pend = request();
-        shared_down_pass(p, shq, shs, idx * R);
+        shared_down_pass<SHNB>(p, shq, shs, idx * R);
     }
 }
 
@@ -916,6 +940,7 @@ namespace {
 struct dec_shape {
     uint32_t n_rt, n_xq, n_shup, n_up, n_mid, n_dn, n_cb;
     size_t lds_up, lds_shup, lds_dn;
+    const void *dn_kernel;
 };
 
 uint32_t device_cus() {
@@ -957,6 +982,14 @@ uint32_t resident_wgs(const void *fn, int threads, size_t lds) {
     return (uint32_t)n;
 }
 
+// One instance of the down kernel per shared-down batch count (registers:
+// each instance stays at 3 waves per SIMD, a kernel holding all would not).
+const void *down_kernel_for(const dec_params &p) {
+    const uint32_t nbat = (shd_bps(p.F / 32u, shd_slices(p.T)) + SHD_CHUNK - 1u) / SHD_CHUNK;
+    if ((p.flags & SF37_DEC_SHARED) == 0u || nbat <= 1u) return (const void *)dec_down_kernel<1>;
+    return nbat == 2u ? (const void *)dec_down_kernel<2> : (const void *)dec_down_kernel<3>;
+}
+
 dec_shape dec_plan(const dec_params &p) {
     dec_shape d;
     const uint32_t nb = p.K / SF37_QK;
@@ -971,7 +1004,8 @@ dec_shape dec_plan(const dec_params &p) {
     d.n_up = resident_wgs((const void *)dec_up_kernel, 256, d.lds_up) * cus;
     d.n_mid = (p.T * p.topk * (p.F / SF37_QK) + (sh ? (p.T * (p.F / 32u) + 1u) / 2u : 0u) + 3u) / 4u;
     d.lds_dn = sh ? (size_t)p.T * p.F + (size_t)p.T * (p.F / 32u) * 4u : 0u;
-    d.n_dn = resident_wgs((const void *)dec_down_kernel, 256, d.lds_dn) * cus;
+    d.dn_kernel = down_kernel_for(p);
+    d.n_dn = resident_wgs(d.dn_kernel, 256, d.lds_dn) * cus;
     d.n_cb = (p.T * p.K + 255u) / 256u;
     return d;
 }
@@ -1040,8 +1074,9 @@ extern "C" int sf37k_decode_mid(const sf37_dec_params *pp, sf37_stream_t s) {
 
 extern "C" int sf37k_decode_down(const sf37_dec_params *pp, sf37_stream_t s) {
     const dec_shape d = dec_plan(*pp);
-    hipLaunchKernelGGL(dec_down_kernel, dim3(d.n_dn), dim3(256), d.lds_dn, (hipStream_t)s, *pp);
-    return (int)hipGetLastError();
+    void *args[] = {(void *)pp};
+    const hipError_t e = hipLaunchKernel(d.dn_kernel, dim3(d.n_dn), dim3(256), args, d.lds_dn, (hipStream_t)s);
+    return (int)(e != hipSuccess ? e : hipGetLastError());
 }
 
 extern "C" int sf37k_decode_combine(const sf37_dec_params *pp, sf37_stream_t s) {
