@@ -291,6 +291,11 @@ enum {
      * shared down + slot-order sum */
     SF37_HIP_STAGE_DEC_ROUTE, SF37_HIP_STAGE_DEC_UP, SF37_HIP_STAGE_DEC_DOWN,
     SF37_HIP_STAGE_DEC_SELECT, SF37_HIP_STAGE_DEC_COMBINE, SF37_HIP_STAGE_DEC_MID,
+    /* the matrix-core prefill path (many pairs per expert): activations
+     * re-quantised into the MFMA operand order (x, then the routed mid),
+     * the per-expert tile list, gate/up + SwiGLU, down */
+    SF37_HIP_STAGE_PF_ACT_X, SF37_HIP_STAGE_PF_TILES, SF37_HIP_STAGE_PF_GATE_UP,
+    SF37_HIP_STAGE_PF_ACT_MID, SF37_HIP_STAGE_PF_DOWN,
     SF37_HIP_N_STAGES
 };
 int sf37_hip_profile_enable(int on);

@@ -1,0 +1,564 @@
+// k_prefill.hip - routed experts for many tokens per expert (prefill) on
+// the gfx950 matrix cores.
+//
+// Same results as the grouped dot-product kernels of k_moe.hip, bit for bit:
+// the integer group sums I_g = sum (q - zp) * qs are formed by
+// v_mfma_f32_32x32x16_f16 on operands that hold small integers exactly, and
+// the float epilogue is the canonical chain of the Q8_K path
+//   blk = fma(s3,I3, fma(s2,I2, fma(s1,I1, fma(s0,I0,0))));  acc = fma(d_b, blk, acc)
+// (sf37_cuda.cu:4226-4274 sums the same integers; this build fixes the order).
+//
+// Exactness.  A weight code pair is turned into one dword of two fp16 values
+// with a mask and an add: the codes sit in the mantissas under a fixed
+// exponent, so each half equals  B + (q - zp)  for a power-of-two bias B that
+// depends only on the element's position (fp16 exponent 25 - p for a code at
+// mantissa bit p).  Activation codes qs are int8, exact in fp16.  The MFMA
+// accumulator starts at  C = -sum_e B_e * qs_e  (a per-token, per-group
+// integer the activation kernel precomputes), so it ends at exactly I_g; all
+// partial sums are integers below 2^24 in magnitude, hence exact in fp32 in
+// any summation order.
+//
+// Layouts.  Activations are re-quantised to Q8_K (sf37_cuda.cu:4168-4205,
+// bit-exact) and written as fp16 codes in the MFMA lane order of the weight
+// format, plus a table per (row, 256-block): C of the four 64-groups and d.
+// A workgroup owns (tile of <= 128 pairs of one expert, row tile); it stages
+// the tile's activation blocks in LDS by direct global->LDS loads (two
+// buffers, one block ahead) and each wave streams its own weight rows into
+// registers one block ahead, dequantises them in registers and runs the
+// MFMAs: 4 token blocks x one 32-column weight block per wave.
+#include "sf37_blocks.h"
+#include "sf37_launch.h"
+
+namespace {
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef float f16v __attribute__((ext_vector_type(16)));
+
+constexpr uint32_t PF_T = 128;          // pairs per tile
+constexpr uint32_t PF_TB = PF_T / 32u;  // 32-pair MFMA blocks per tile
+constexpr uint32_t PF_GU_R = 64;        // F rows (gate and up) per gate/up workgroup
+constexpr uint32_t PF_DN_R = 128;       // output rows per down workgroup
+constexpr uint32_t PF_TAB = 8;          // floats per (row, block) table entry: C0..C3, d
+constexpr uint32_t PF_ACT_BUF = 32u * PF_T * 16u;   // bytes of one LDS activation block
+
+// ---------------------------------------------------------------------------
+// Pair layouts.  Lane half kh of an MFMA holds 32 codes of every 64-group
+// (codes 32kh .. 32kh+31) as 16 pairs; pair P feeds MFMA P/4, dword P%4.
+// ---------------------------------------------------------------------------
+// Q3 (3-bit codes at bit 3c of the lane's 96-bit string).  Window = the
+// string shifted right by the window offset; type = where the two codes sit
+// in the window: A1 bits 0 / 18, A2 bits 3 / 21, B1 bits 1 / 16, B2 bits 4 / 19.
+__constant__ uint8_t q3_lo_c[16] = {0, 1, 2, 3, 4, 5, 12, 13, 14, 15, 16, 22, 23, 24, 25, 26};
+__constant__ uint8_t q3_hi_c[16] = {6, 7, 8, 9, 10, 11, 17, 18, 19, 20, 21, 27, 28, 29, 30, 31};
+__constant__ uint8_t q3_ty_c[16] = {0, 1, 0, 1, 0, 1, 2, 3, 2, 3, 2, 2, 3, 2, 3, 2};
+// mantissa bit of the low / high code of each type (high relative to bit 16)
+__host__ __device__ constexpr uint32_t q3_plo(uint32_t ty) { return ty == 0 ? 0u : ty == 1 ? 3u : ty == 2 ? 1u : 4u; }
+__host__ __device__ constexpr uint32_t q3_phi(uint32_t ty) { return ty == 0 ? 2u : ty == 1 ? 5u : ty == 2 ? 0u : 3u; }
+__host__ __device__ constexpr uint32_t q3_mask(uint32_t ty) {
+    return (7u << q3_plo(ty)) | (7u << (16u + q3_phi(ty)));
+}
+__host__ __device__ constexpr uint32_t pf_exp(uint32_t plo, uint32_t phi) {
+    return ((25u - plo) << 10) | ((25u - phi) << 26);
+}
+__host__ __device__ constexpr uint32_t pf_mul(uint32_t plo, uint32_t phi) {
+    return (1u << plo) | (1u << (16u + phi));
+}
+
+// ---------------------------------------------------------------------------
+// Activation kernel: Q8_K of one (row, 256-block) per wave, then the codes
+// in MFMA order as fp16, C per 64-group and d.
+// MFMA order of a block: position 64g + 32kh + 8m + e holds the code of
+// pair P = 4m + e/2 (low code if e even, high if odd) of lane half kh.
+// ---------------------------------------------------------------------------
+template <bool Q3>
+__device__ __forceinline__ void pf_pos_code(uint32_t pos, uint32_t &code, int32_t &bias) {
+    const uint32_t kh = (pos >> 5) & 1u, m = (pos >> 3) & 3u, e = pos & 7u;
+    const uint32_t P = 4u * m + (e >> 1), half = e & 1u;
+    if (Q3) {
+        const uint32_t ty = q3_ty_c[P];
+        code = 32u * kh + (half ? q3_hi_c[P] : q3_lo_c[P]);
+        bias = (int32_t)(1u << (10u - (half ? q3_phi(ty) : q3_plo(ty)))) + 8;
+    } else {
+        const uint32_t k = P & 3u, qd = P >> 2;
+        code = 32u * kh + 16u * (qd >> 1) + 4u * (qd & 1u) + k + 8u * half;
+        bias = (int32_t)(1u << (10u - 2u * k)) + 4;
+    }
+}
+
+template <bool Q3>
+__global__ void __launch_bounds__(256) pf_act_kernel(_Float16 *__restrict__ codes, float *__restrict__ tab,
+                                                     const float *__restrict__ x, uint32_t nblk,
+                                                     uint32_t n_rows) {
+    __shared__ int8_t qs[4][SF37_QK];
+    const uint32_t wv = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+    const uint32_t unit = blockIdx.x * 4u + wv;
+    const bool live = unit < nblk * n_rows;
+    const uint32_t u = live ? unit : 0u;
+    const float *xb = x + (uint64_t)u * SF37_QK + 4u * lane;
+    float v[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) v[k] = xb[k];
+    int8_t q[4];
+    int gs;
+    const float d = q8k_codes4(v, q, gs);
+    (void)gs;
+#pragma unroll
+    for (int k = 0; k < 4; k++) qs[wv][4u * lane + k] = q[k];
+    __syncthreads();
+    // lane produces positions 4*lane .. 4*lane+3, all in group lane/16
+    const uint32_t g = lane >> 4;
+    int32_t s = 0;
+    _Float16 h[4];
+#pragma unroll
+    for (uint32_t c = 0; c < 4u; c++) {
+        uint32_t code;
+        int32_t bias;
+        pf_pos_code<Q3>(4u * (lane & 15u) + c, code, bias);
+        const int32_t a = qs[wv][64u * g + code];
+        h[c] = (_Float16)a;
+        s += bias * a;
+    }
+    s = wave_sum_i32_width(s, 16);
+    if (!live) return;
+    typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+    const h4 hv = {h[0], h[1], h[2], h[3]};
+    *(h4 *)(codes + (uint64_t)u * SF37_QK + 4u * lane) = hv;
+    float *tb = tab + (uint64_t)u * PF_TAB;
+    if ((lane & 15u) == 0u) tb[g] = (float)(-s);
+    if (lane == 0u) tb[4] = d;
+}
+
+// ---------------------------------------------------------------------------
+// Tile list: every group split into tiles of <= PF_T pairs.
+// tiles[0] = count; tile t at uint4 index 1 + t = {expert, first pair, count, 0}.
+// ---------------------------------------------------------------------------
+__global__ void __launch_bounds__(1024) pf_tiles_kernel(uint32_t *__restrict__ tiles,
+                                                        const uint32_t *__restrict__ ginfo,
+                                                        uint32_t max_groups) {
+    __shared__ uint32_t wsum[16];
+    const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63u;
+    const uint32_t ng = ginfo[0];
+    uint32_t base = 0;
+    for (uint32_t g0 = 0; g0 < ng; g0 += 1024u) {
+        const uint32_t g = g0 + tid;
+        uint32_t nt = 0, p0 = 0, cnt = 0;
+        if (g < ng) {
+            p0 = ginfo[1 + g];
+            cnt = ginfo[2 + g] - p0;
+            nt = (cnt + PF_T - 1u) / PF_T;
+        }
+        uint32_t sc = nt;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const uint32_t a = __shfl_up(sc, o, 64);
+            if (lane >= (uint32_t)o) sc += a;
+        }
+        if (lane == 63u) wsum[wave] = sc;
+        __syncthreads();
+        uint32_t before = base, all = 0;
+        for (uint32_t w = 0; w < 16u; w++) {
+            if (w < wave) before += wsum[w];
+            all += wsum[w];
+        }
+        const uint32_t first = before + sc - nt;
+        if (g < ng) {
+            const uint32_t e = ginfo[2 + max_groups + g];
+            for (uint32_t k = 0; k < nt; k++) {
+                const uint32_t c = cnt - k * PF_T < PF_T ? cnt - k * PF_T : PF_T;
+                ((uint4 *)tiles)[1 + first + k] = make_uint4(e, p0 + k * PF_T, c, 0u);
+            }
+        }
+        base += all;
+        __syncthreads();
+    }
+    if (tid == 0) tiles[0] = base;
+}
+
+// ---------------------------------------------------------------------------
+// LDS direct loads (global -> LDS, no registers).  Issued through inline asm
+// so the compiler does not wait for them before unrelated LDS reads; the
+// kernel waits with s_waitcnt vmcnt(0) + barrier before reading the buffer.
+// Lane i of a dwordx4 load writes LDS bytes [m0 + 16 i, m0 + 16 i + 16).
+// ---------------------------------------------------------------------------
+// sbase must be wave-uniform; it is moved to SGPRs with readfirstlane.
+__device__ __forceinline__ uint64_t sgpr_ptr(const void *p) {
+    const uint64_t v = (uint64_t)(uintptr_t)p;
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return ((uint64_t)hi << 32) | lo;
+}
+__device__ __forceinline__ void lds_dma16(uint32_t lds, uint32_t voff, const void *sbase) {
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds), "v"(voff), "s"(sgpr_ptr(sbase))
+                 : "memory", "m0");
+}
+__device__ __forceinline__ void lds_dma4(uint32_t lds, uint32_t voff, const void *sbase) {
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, %2" ::"s"(lds), "v"(voff), "s"(sgpr_ptr(sbase))
+                 : "memory", "m0");
+}
+__device__ __forceinline__ void wait_vm0() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+__device__ __forceinline__ uint32_t lds_addr(const void *p) { return (uint32_t)(uintptr_t)p; }
+
+struct pf_params {
+    float *mid, *gate_out, *up_out, *down_pair;
+    const uint8_t *w0, *w1;        // gate / up (Q3) or down (Q2)
+    const _Float16 *act;           // [rows][nblk * 256] codes in MFMA order
+    const float *tab;              // [rows][nblk][PF_TAB]
+    const uint32_t *tiles;
+    const uint32_t *sorted;
+    const float *weights;
+    uint32_t topk, nblk, out_rows, n_rt;
+    float clamp;
+};
+
+// Weight bytes of one lane for one block.
+struct q3_raw {
+    uint32_t h[4];      // header dwords (scales, zero points)
+    uint32_t w[4][4];   // per group: 16 aligned bytes holding the lane's 12
+};
+struct q2_raw {
+    uint32_t h[3];
+    uint32_t w[4][2];
+};
+
+typedef uint32_t u32x4a __attribute__((ext_vector_type(4), aligned(4)));
+typedef uint32_t u32x3a __attribute__((ext_vector_type(3), aligned(4)));
+typedef uint32_t u32x2a __attribute__((ext_vector_type(2), aligned(4)));
+
+__device__ __forceinline__ void q3_load(q3_raw &r, const uint8_t *hp, const uint8_t *pp) {
+    const u32x4a v = *(const u32x4a *)hp;
+    r.h[0] = v.x; r.h[1] = v.y; r.h[2] = v.z; r.h[3] = v.w;
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+        const u32x4a q = *(const u32x4a *)(pp + 24 * g);
+        r.w[g][0] = q.x; r.w[g][1] = q.y; r.w[g][2] = q.z; r.w[g][3] = q.w;
+    }
+}
+__device__ __forceinline__ void q2_load(q2_raw &r, const uint8_t *hp, const uint8_t *pp) {
+    const u32x3a v = *(const u32x3a *)hp;
+    r.h[0] = v.x; r.h[1] = v.y; r.h[2] = v.z;
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+        const u32x2a q = *(const u32x2a *)(pp + 16 * g);
+        r.w[g][0] = q.x; r.w[g][1] = q.y;
+    }
+}
+
+// 32 bits of the lane's string starting at bit SH + o of the loaded words.
+template <int SH, int O>
+__device__ __forceinline__ uint32_t q3_win(const uint32_t *w) {
+    constexpr int a = SH + O, k = a >> 5, s = a & 31;
+    if constexpr (s == 0) return w[k];
+    else return align_bits(w[k + 1], w[k], (uint32_t)s);
+}
+
+// Dequantise group g of a Q3 block into 16 fp16 pair words.  k = 8 - zp.
+template <int SH>
+__device__ __forceinline__ void q3_dequant(const uint32_t *w, uint32_t k, uint32_t out[16]) {
+    const uint32_t cA1 = pf_exp(0, 2) + k * pf_mul(0, 2), cA2 = pf_exp(3, 5) + k * pf_mul(3, 5);
+    const uint32_t cB1 = pf_exp(1, 0) + k * pf_mul(1, 0), cB2 = pf_exp(4, 3) + k * pf_mul(4, 3);
+    constexpr uint32_t mA1 = q3_mask(0), mA2 = q3_mask(1), mB1 = q3_mask(2), mB2 = q3_mask(3);
+    uint32_t x;
+    x = q3_win<SH, 0>(w);  out[0] = (x & mA1) + cA1;  out[1] = (x & mA2) + cA2;
+    x = q3_win<SH, 6>(w);  out[2] = (x & mA1) + cA1;  out[3] = (x & mA2) + cA2;
+    x = q3_win<SH, 12>(w); out[4] = (x & mA1) + cA1;  out[5] = (x & mA2) + cA2;
+    x = q3_win<SH, 35>(w); out[6] = (x & mB1) + cB1;  out[7] = (x & mB2) + cB2;
+    x = q3_win<SH, 41>(w); out[8] = (x & mB1) + cB1;  out[9] = (x & mB2) + cB2;
+    x = q3_win<SH, 47>(w); out[10] = (x & mB1) + cB1;
+    x = q3_win<SH, 65>(w); out[11] = (x & mB1) + cB1; out[12] = (x & mB2) + cB2;
+    x = q3_win<SH, 71>(w); out[13] = (x & mB1) + cB1; out[14] = (x & mB2) + cB2;
+    x = q3_win<SH, 77>(w); out[15] = (x & mB1) + cB1;
+}
+
+// Dequantise group g of a Q2 block (two dwords of the lane) into 16 words.  k = 4 - zp.
+__device__ __forceinline__ void q2_dequant(const uint32_t *w, uint32_t k, uint32_t out[16]) {
+    uint32_t c[4];
+#pragma unroll
+    for (uint32_t j = 0; j < 4u; j++) c[j] = pf_exp(2u * j, 2u * j) + k * pf_mul(2u * j, 2u * j);
+#pragma unroll
+    for (uint32_t q = 0; q < 4u; q++) {
+        const uint32_t x = (q & 1u) ? (w[q >> 1] >> 8) : w[q >> 1];
+#pragma unroll
+        for (uint32_t j = 0; j < 4u; j++) out[4u * q + j] = (x & (0x00030003u << (2u * j))) + c[j];
+    }
+}
+
+// f16 scale of group g, zero point of group g from the header bits at SH.
+template <int SH>
+__device__ __forceinline__ float hdr_scale(const uint32_t *h, int g) {
+    const int a = SH + 16 * g;
+    return sf37_f16(h[a >> 5] >> (a & 31));
+}
+template <int SH>
+__device__ __forceinline__ uint32_t hdr_zp(const uint32_t *h, int g) {
+    const int a = SH + 64 + 8 * g;
+    return (h[a >> 5] >> (a & 31)) & 0xffu;
+}
+
+// One 256-block of the tile: 4 groups x (dequant + 4 token blocks x 4 MFMAs),
+// the canonical chain into blk, then acc = fma(d, blk, acc).
+template <bool Q3, int SH, typename RAW>
+__device__ __forceinline__ void pf_block(const RAW &r, const uint8_t *act_lds, const float *cd_lds,
+                                         uint32_t kh, uint32_t col, uint32_t ntb, f16v acc[PF_TB],
+                                         f16v blk[PF_TB]) {
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+        uint32_t bw[16];
+        if constexpr (Q3) q3_dequant<SH>(r.w[g], 8u - (hdr_zp<SH>(r.h, g) & 7u), bw);
+        else q2_dequant(r.w[g], 4u - (hdr_zp<0>(r.h, g) & 3u), bw);
+        const float s = hdr_scale<Q3 ? SH : 0>(r.h, g);
+        h8 B[4];
+#pragma unroll
+        for (int m = 0; m < 4; m++) {
+            typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+            const u4 t = {bw[4 * m], bw[4 * m + 1], bw[4 * m + 2], bw[4 * m + 3]};
+            B[m] = __builtin_bit_cast(h8, t);
+        }
+#pragma unroll
+        for (uint32_t i = 0; i < PF_TB; i++) {
+            if (i < ntb) {
+                f16v D;
+#pragma unroll
+                for (int jj = 0; jj < 4; jj++) {
+                    const float4 c = *(const float4 *)(cd_lds + g * PF_T + 32u * i + 8u * jj + 4u * kh);
+                    D[4 * jj] = c.x; D[4 * jj + 1] = c.y; D[4 * jj + 2] = c.z; D[4 * jj + 3] = c.w;
+                }
+#pragma unroll
+                for (int m = 0; m < 4; m++) {
+                    const h8 A = *(const h8 *)(act_lds + ((uint32_t)(8 * g + m) * PF_T + 4u * kh * PF_T + 32u * i + col) * 16u);
+                    D = __builtin_amdgcn_mfma_f32_32x32x16_f16(A, B[m], D, 0, 0, 0);
+                }
+#pragma unroll
+                for (int r2 = 0; r2 < 16; r2++) blk[i][r2] = __builtin_fmaf(s, D[r2], g == 0 ? 0.0f : blk[i][r2]);
+            }
+        }
+    }
+#pragma unroll
+    for (uint32_t i = 0; i < PF_TB; i++) {
+        if (i < ntb) {
+#pragma unroll
+            for (int jj = 0; jj < 4; jj++) {
+                const float4 d = *(const float4 *)(cd_lds + 4 * PF_T + 32u * i + 8u * jj + 4u * kh);
+                acc[i][4 * jj] = __builtin_fmaf(d.x, blk[i][4 * jj], acc[i][4 * jj]);
+                acc[i][4 * jj + 1] = __builtin_fmaf(d.y, blk[i][4 * jj + 1], acc[i][4 * jj + 1]);
+                acc[i][4 * jj + 2] = __builtin_fmaf(d.z, blk[i][4 * jj + 2], acc[i][4 * jj + 2]);
+                acc[i][4 * jj + 3] = __builtin_fmaf(d.w, blk[i][4 * jj + 3], acc[i][4 * jj + 3]);
+            }
+        }
+    }
+}
+
+// Gate/up (Q3 = true): row tile = 64 F rows, wave w has gate rows
+// rt*64 + 16w + c and up rows (c < 16: gate, else up) as its 32 columns;
+// epilogue mid = ((g*sig(g))*u)*w per pair.  Down (Q3 = false): row tile =
+// 128 output rows, 32 per wave; epilogue down_pair[pair][row].
+template <bool Q3>
+__global__ void __launch_bounds__(256, 1) pf_expert_kernel(pf_params p) {
+    __shared__ __align__(16) uint8_t s_act[2][PF_ACT_BUF];
+    __shared__ __align__(16) float s_cd[2][5 * PF_T];
+    __shared__ uint32_t s_pair[PF_T];
+    __shared__ float s_w[PF_T];
+    const uint32_t wg = blockIdx.x, xcd = wg & 7u, slot = wg >> 3;
+    const uint32_t t = xcd + 8u * (slot / p.n_rt), rt = slot % p.n_rt;
+    if (t >= p.tiles[0]) return;
+    const uint4 ti = ((const uint4 *)p.tiles)[1 + t];
+    const uint32_t e = ti.x, p0 = ti.y, cnt = ti.z;
+    const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63u, kh = lane >> 5, col = lane & 31u;
+    const uint32_t ntb = (cnt + 31u) / 32u;
+    const uint32_t nblk = p.nblk;
+    if (tid < PF_T) {
+        const uint32_t pr = p.sorted[p0 + (tid < cnt ? tid : cnt - 1u)];
+        s_pair[tid] = pr;
+        if (Q3) s_w[tid] = p.weights[pr];
+    }
+    // activation rows of tile slots `lane` and 64 + lane (pad slots repeat the last pair)
+    uint32_t voff_c[2], voff_t[2];
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        const uint32_t sl = 64u * h + lane;
+        const uint32_t pr = p.sorted[p0 + (sl < cnt ? sl : cnt - 1u)];
+        const uint32_t row = Q3 ? pr / p.topk : pr;
+        voff_c[h] = row * nblk * (SF37_QK * 2u);
+        voff_t[h] = row * nblk * (PF_TAB * 4u);
+    }
+    const uint32_t act_l = lds_addr(&s_act[0][0]), cd_l = lds_addr(&s_cd[0][0]);
+    auto issue_act = [&](uint32_t b) {
+        const uint32_t bf = b & 1u;
+        const uint8_t *cb = (const uint8_t *)p.act + (uint64_t)b * (SF37_QK * 2u);
+#pragma unroll
+        for (uint32_t j = 0; j < 8u; j++) {
+            const uint32_t pc = 8u * wave + j;
+#pragma unroll
+            for (uint32_t h = 0; h < 2u; h++)
+                lds_dma16(__builtin_amdgcn_readfirstlane(act_l + bf * PF_ACT_BUF + (pc * PF_T + 64u * h) * 16u),
+                          voff_c[h], cb + 16u * pc);
+        }
+        const uint8_t *tb = (const uint8_t *)p.tab + (uint64_t)b * (PF_TAB * 4u);
+#pragma unroll
+        for (uint32_t j = 0; j < 3u; j++) {
+            const uint32_t it = wave + 4u * j;
+            if (it < 10u) {
+                const uint32_t a = it >> 1, h = it & 1u;
+                lds_dma4(__builtin_amdgcn_readfirstlane(cd_l + bf * (5u * PF_T * 4u) + (a * PF_T + 64u * h) * 4u),
+                         voff_t[h], tb + 4u * a);
+            }
+        }
+    };
+    // this lane's weight row
+    const uint32_t wcol = Q3 ? rt * PF_GU_R + 16u * wave + (col & 15u) : rt * PF_DN_R + 32u * wave + col;
+    const uint32_t blk_bytes = Q3 ? SF37_Q3_BYTES : SF37_Q2_BYTES;
+    const uint64_t row_bytes = (uint64_t)nblk * blk_bytes;
+    const uint8_t *wrow = (Q3 && col >= 16u ? p.w1 : p.w0) + ((uint64_t)e * p.out_rows + wcol) * row_bytes;
+
+    f16v acc[PF_TB], blk[PF_TB];
+#pragma unroll
+    for (uint32_t i = 0; i < PF_TB; i++)
+#pragma unroll
+        for (int r2 = 0; r2 < 16; r2++) acc[i][r2] = 0.0f;
+
+    issue_act(0);
+    if constexpr (Q3) {
+        // blocks in pairs: even blocks start dword-aligned, odd blocks 2 bytes in
+        q3_raw ra, rb;
+        q3_load(ra, wrow, wrow + 12u + 12u * kh);
+        for (uint32_t b = 0; b < nblk; b += 2u) {
+            const uint8_t *base = wrow + (uint64_t)b * SF37_Q3_BYTES;
+            wait_vm0();
+            __syncthreads();
+            if (b + 1u < nblk) {
+                issue_act(b + 1u);
+                q3_load(rb, base + 108u, base + 108u + 12u + 12u * kh);
+            }
+            pf_block<true, 0>(ra, s_act[b & 1u], s_cd[b & 1u], kh, col, ntb, acc, blk);
+            if (b + 1u < nblk) {
+                wait_vm0();
+                __syncthreads();
+                if (b + 2u < nblk) {
+                    issue_act(b + 2u);
+                    q3_load(ra, base + 220u, base + 220u + 12u + 12u * kh);
+                }
+                pf_block<true, 16>(rb, s_act[(b + 1u) & 1u], s_cd[(b + 1u) & 1u], kh, col, ntb, acc, blk);
+            }
+        }
+    } else {
+        q2_raw ra, rb;
+        q2_load(ra, wrow, wrow + 12u + 8u * kh);
+        for (uint32_t b = 0; b < nblk; b += 2u) {
+            const uint8_t *base = wrow + (uint64_t)b * SF37_Q2_BYTES;
+            wait_vm0();
+            __syncthreads();
+            if (b + 1u < nblk) {
+                issue_act(b + 1u);
+                q2_load(rb, base + 84u, base + 84u + 12u + 8u * kh);
+            }
+            pf_block<false, 0>(ra, s_act[b & 1u], s_cd[b & 1u], kh, col, ntb, acc, blk);
+            if (b + 1u < nblk) {
+                wait_vm0();
+                __syncthreads();
+                if (b + 2u < nblk) {
+                    issue_act(b + 2u);
+                    q2_load(ra, base + 168u, base + 168u + 12u + 8u * kh);
+                }
+                pf_block<false, 0>(rb, s_act[(b + 1u) & 1u], s_cd[(b + 1u) & 1u], kh, col, ntb, acc, blk);
+            }
+        }
+    }
+
+    // epilogue: D layout - lane holds column col, tokens 8*(r/4) + 4*kh + r%4
+#pragma unroll
+    for (uint32_t i = 0; i < PF_TB; i++) {
+        if (i < ntb) {
+#pragma unroll
+            for (int r2 = 0; r2 < 16; r2++) {
+                const uint32_t tl = 32u * i + 8u * (r2 >> 2) + 4u * kh + (r2 & 3);
+                const float v = acc[i][r2];
+                if constexpr (Q3) {
+                    const float o = __shfl_xor(v, 16, 64);
+                    if (col < 16u && tl < cnt) {
+                        const uint64_t at = (uint64_t)s_pair[tl] * p.out_rows + wcol;
+                        p.mid[at] = sf37_swiglu_mid(v, o, s_w[tl], p.clamp);
+                        if (p.gate_out) p.gate_out[at] = v;
+                        if (p.up_out) p.up_out[at] = o;
+                    }
+                } else {
+                    if (tl < cnt) p.down_pair[(uint64_t)s_pair[tl] * p.out_rows + wcol] = v;
+                }
+            }
+        }
+    }
+}
+
+uint32_t pf_grid(uint32_t max_tiles, uint32_t n_rt) { return 8u * ((max_tiles + 7u) / 8u) * n_rt; }
+
+}  // namespace
+
+extern "C" uint32_t sf37k_pf_max_tiles(uint32_t n_pairs, uint32_t max_groups) {
+    return (n_pairs + PF_T - 1u) / PF_T + max_groups;
+}
+
+extern "C" int sf37k_pf_supported(uint32_t in_dim, uint32_t mid_dim, uint32_t out_dim) {
+    return in_dim % SF37_QK == 0 && mid_dim % SF37_QK == 0 && mid_dim % PF_GU_R == 0 &&
+           out_dim % PF_DN_R == 0 && in_dim > 0 && mid_dim > 0;
+}
+
+extern "C" int sf37k_pf_act(int q3, void *codes_v, float *tab, const float *x, uint32_t dim,
+                            uint32_t n_rows, sf37_stream_t s) {
+    _Float16 *codes = (_Float16 *)codes_v;
+    const uint32_t nblk = dim / SF37_QK;
+    const uint64_t units = (uint64_t)nblk * n_rows;
+    if (units == 0) return 0;
+    const dim3 grid((unsigned)((units + 3u) / 4u));
+    if (q3)
+        hipLaunchKernelGGL(pf_act_kernel<true>, grid, dim3(256), 0, (hipStream_t)s, codes, tab, x, nblk, n_rows);
+    else
+        hipLaunchKernelGGL(pf_act_kernel<false>, grid, dim3(256), 0, (hipStream_t)s, codes, tab, x, nblk, n_rows);
+    return (int)hipGetLastError();
+}
+
+extern "C" int sf37k_pf_tiles(uint32_t *tiles, const uint32_t *group_info, uint32_t max_groups,
+                              sf37_stream_t s) {
+    hipLaunchKernelGGL(pf_tiles_kernel, dim3(1), dim3(1024), 0, (hipStream_t)s, tiles, group_info, max_groups);
+    return (int)hipGetLastError();
+}
+
+extern "C" int sf37k_pf_gate_up(float *mid, float *gate_out, float *up_out, const uint8_t *gate_w,
+                                const uint8_t *up_w, const void *act, const float *tab,
+                                const uint32_t *tiles, const uint32_t *sorted_pairs, const float *weights,
+                                uint32_t max_tiles, uint32_t topk, uint32_t in_dim, uint32_t mid_dim,
+                                float clamp, sf37_stream_t s) {
+    pf_params p = {};
+    p.mid = mid;
+    p.gate_out = gate_out;
+    p.up_out = up_out;
+    p.w0 = gate_w;
+    p.w1 = up_w;
+    p.act = (const _Float16 *)act;
+    p.tab = tab;
+    p.tiles = tiles;
+    p.sorted = sorted_pairs;
+    p.weights = weights;
+    p.topk = topk;
+    p.nblk = in_dim / SF37_QK;
+    p.out_rows = mid_dim;
+    p.n_rt = mid_dim / PF_GU_R;
+    p.clamp = clamp;
+    hipLaunchKernelGGL(pf_expert_kernel<true>, dim3(pf_grid(max_tiles, p.n_rt)), dim3(256), 0, (hipStream_t)s, p);
+    return (int)hipGetLastError();
+}
+
+extern "C" int sf37k_pf_down(float *down_pair, const uint8_t *down_w, const void *act, const float *tab,
+                             const uint32_t *tiles, const uint32_t *sorted_pairs, uint32_t max_tiles,
+                             uint32_t mid_dim, uint32_t out_dim, sf37_stream_t s) {
+    pf_params p = {};
+    p.down_pair = down_pair;
+    p.w0 = down_w;
+    p.act = (const _Float16 *)act;
+    p.tab = tab;
+    p.tiles = tiles;
+    p.sorted = sorted_pairs;
+    p.nblk = mid_dim / SF37_QK;
+    p.out_rows = out_dim;
+    p.n_rt = out_dim / PF_DN_R;
+    hipLaunchKernelGGL(pf_expert_kernel<false>, dim3(pf_grid(max_tiles, p.n_rt)), dim3(256), 0, (hipStream_t)s, p);
+    return (int)hipGetLastError();
+}

@@ -50,6 +50,8 @@ static int64_t g_opt_q8k_min_rows = 512;
 static int64_t g_opt_write_gate_up = 0;
 static int64_t g_opt_decode = 1;
 static int64_t g_opt_router_always = 0;
+static int64_t g_opt_prefill = 1;
+static int64_t g_opt_prefill_min_pairs = 256;
 
 /* arrival counters of the fused decode kernels: zeroed once, left zero by
  * every completed launch */
@@ -87,7 +89,8 @@ static hipEvent_t g_prof_open;
 
 static const char *const k_stage_names[SF37_HIP_N_STAGES] = {
     "router", "select", "q8_0_act", "q8_0_gemm", "swiglu", "q8k_x", "dispatch",
-    "gate_up", "q8k_mid", "down", "combine", "add", "other", "dec_route", "dec_up", "dec_down", "dec_select", "dec_combine", "dec_mid"};
+    "gate_up", "q8k_mid", "down", "combine", "add", "other", "dec_route", "dec_up", "dec_down", "dec_select", "dec_combine", "dec_mid",
+    "pf_act_x", "pf_tiles", "pf_gate_up", "pf_act_mid", "pf_down"};
 
 static void prof_begin(void) {
     if (!g_prof_on) return;
@@ -299,6 +302,8 @@ int sf37_hip_set_option(const char *name, int64_t value) {
     else if (!strcmp(name, "moe_write_gate_up")) g_opt_write_gate_up = value ? 1 : 0;
     else if (!strcmp(name, "decode_fused")) g_opt_decode = value ? 1 : 0;
     else if (!strcmp(name, "router_with_logits")) g_opt_router_always = value ? 1 : 0;
+    else if (!strcmp(name, "prefill_mfma")) g_opt_prefill = value ? 1 : 0;
+    else if (!strcmp(name, "prefill_min_pairs")) g_opt_prefill_min_pairs = value < 0 ? 0 : value;
     else return 0;
     return 1;
 }
@@ -310,6 +315,8 @@ int64_t sf37_hip_get_option(const char *name) {
     if (!strcmp(name, "moe_write_gate_up")) return g_opt_write_gate_up;
     if (!strcmp(name, "decode_fused")) return g_opt_decode;
     if (!strcmp(name, "router_with_logits")) return g_opt_router_always;
+    if (!strcmp(name, "prefill_mfma")) return g_opt_prefill;
+    if (!strcmp(name, "prefill_min_pairs")) return g_opt_prefill_min_pairs;
     return -1;
 }
 
@@ -802,10 +809,15 @@ typedef struct {
     void *xq, *midq;
     uint32_t *ginfo, *sorted, *counts, *offsets;
     float *mid, *down_pair;
+    void *x16, *m16;        /* matrix-core path: fp16 codes in MFMA order */
+    float *xtab, *mtab;     /* their per-block tables */
+    uint32_t *tiles;
 } routed_scratch;
 
-static uint64_t routed_layout(const routed_args *a, int slots, int need_mid, int need_down, char *base,
-                              routed_scratch *s) {
+#define PF_TAB_BYTES 32u
+
+static uint64_t routed_layout(const routed_args *a, int slots, int pf, int need_mid, int need_down,
+                              char *base, routed_scratch *s) {
     const uint64_t pairs = (uint64_t)a->n_tok * a->topk;
     const uint64_t groups = slots ? a->topk : a->n_expert;
     uint64_t off = 0;
@@ -814,8 +826,16 @@ static uint64_t routed_layout(const routed_args *a, int slots, int need_mid, int
         if (base) s->field = (type)(base + off);                       \
         off = align256(off + (bytes));                                 \
     } while (0)
-    RESERVE(xq, void *, (uint64_t)a->n_tok * (a->in_dim / QK) * Q8KB);
-    RESERVE(midq, void *, pairs * (a->mid_dim / QK) * Q8KB);
+    if (pf) {
+        RESERVE(x16, void *, (uint64_t)a->n_tok * a->in_dim * 2u);
+        RESERVE(xtab, float *, (uint64_t)a->n_tok * (a->in_dim / QK) * PF_TAB_BYTES);
+        RESERVE(m16, void *, pairs * a->mid_dim * 2u);
+        RESERVE(mtab, float *, pairs * (a->mid_dim / QK) * PF_TAB_BYTES);
+        RESERVE(tiles, uint32_t *, ((uint64_t)sf37k_pf_max_tiles((uint32_t)pairs, (uint32_t)groups) + 1u) * 16u);
+    } else {
+        RESERVE(xq, void *, (uint64_t)a->n_tok * (a->in_dim / QK) * Q8KB);
+        RESERVE(midq, void *, pairs * (a->mid_dim / QK) * Q8KB);
+    }
     RESERVE(ginfo, uint32_t *, (3u + 2u * groups) * 4u);
     RESERVE(sorted, uint32_t *, pairs * 4u);
     RESERVE(counts, uint32_t *, (uint64_t)a->n_expert * 4u);
@@ -824,6 +844,42 @@ static uint64_t routed_layout(const routed_args *a, int slots, int need_mid, int
     if (need_down) RESERVE(down_pair, float *, pairs * a->out_dim * 4u);
 #undef RESERVE
     return off;
+}
+
+/* The matrix-core path takes grouped (not per-slot) batches with enough
+ * pairs, dims it tiles, and operand offsets that fit 32 bits. */
+static int prefill_eligible(const routed_args *a, int slots) {
+    const uint64_t pairs = (uint64_t)a->n_tok * a->topk;
+    return !slots && g_opt_prefill && pairs >= (uint64_t)g_opt_prefill_min_pairs &&
+           sf37k_pf_supported(a->in_dim, a->mid_dim, a->out_dim) &&
+           (uint64_t)a->n_tok * a->in_dim * 2u < (1ull << 32) && pairs * a->mid_dim * 2u < (1ull << 32);
+}
+
+/* Matrix-core pipeline (k_prefill.hip): x to fp16 MFMA codes, dispatch,
+ * tiles, gate/up + SwiGLU*w, mid to fp16 MFMA codes, down, combine. */
+static int routed_pf(const routed_args *a, const routed_scratch *s, float *out, float *mid, float *down_pair,
+                     float *gate_out, float *up_out) {
+    const sf37_stream_t st = (sf37_stream_t)g_stream;
+    const uint32_t pairs = a->n_tok * a->topk;
+    const uint32_t groups = a->n_expert;
+    const uint32_t max_tiles = sf37k_pf_max_tiles(pairs, groups);
+    return LAUNCH(SF37_HIP_STAGE_PF_ACT_X, sf37k_pf_act(1, s->x16, s->xtab, a->x, a->in_dim, a->n_tok, st),
+                  "routed_moe mfma input codes launch") &&
+           LAUNCH(SF37_HIP_STAGE_DISPATCH, sf37k_moe_dispatch(s->ginfo, s->sorted, s->counts, s->offsets, a->selected,
+                                                              pairs, a->n_expert, st),
+                  "routed_moe dispatch launch") &&
+           LAUNCH(SF37_HIP_STAGE_PF_TILES, sf37k_pf_tiles(s->tiles, s->ginfo, groups, st), "routed_moe tiles launch") &&
+           LAUNCH(SF37_HIP_STAGE_PF_GATE_UP, sf37k_pf_gate_up(mid, gate_out, up_out, a->gate_w, a->up_w, s->x16, s->xtab,
+                                                             s->tiles, s->sorted, a->weights, max_tiles, a->topk,
+                                                             a->in_dim, a->mid_dim, a->clamp, st),
+                  "routed_moe mfma gate/up launch") &&
+           LAUNCH(SF37_HIP_STAGE_PF_ACT_MID, sf37k_pf_act(0, s->m16, s->mtab, mid, a->mid_dim, pairs, st),
+                  "routed_moe mfma mid codes launch") &&
+           LAUNCH(SF37_HIP_STAGE_PF_DOWN, sf37k_pf_down(down_pair, a->down_w, s->m16, s->mtab, s->tiles, s->sorted,
+                                                       max_tiles, a->mid_dim, a->out_dim, st),
+                  "routed_moe mfma down launch") &&
+           LAUNCH(SF37_HIP_STAGE_COMBINE, sf37k_moe_combine(out, down_pair, a->topk, a->out_dim, a->n_tok, st),
+                  "routed_moe combine launch");
 }
 
 /* Q8_K pipeline: quantize x, group pairs by expert (slots = one group per
@@ -835,12 +891,14 @@ static int routed_q8k(const routed_args *a, float *out, float *mid, float *down_
         return 0;
     routed_scratch s;
     memset(&s, 0, sizeof(s));
-    const uint64_t bytes = routed_layout(a, slots, mid == NULL, down_pair == NULL, NULL, &s);
+    const int pf = prefill_eligible(a, slots);
+    const uint64_t bytes = routed_layout(a, slots, pf, mid == NULL, down_pair == NULL, NULL, &s);
     char *base = scratch_get(bytes, "routed moe scratch");
     if (!base) return 0;
-    routed_layout(a, slots, mid == NULL, down_pair == NULL, base, &s);
+    routed_layout(a, slots, pf, mid == NULL, down_pair == NULL, base, &s);
     if (!mid) mid = s.mid;
     if (!down_pair) down_pair = s.down_pair;
+    if (pf) return routed_pf(a, &s, out, mid, down_pair, gate_out, up_out);
     const sf37_stream_t st = (sf37_stream_t)g_stream;
     const uint32_t pairs = a->n_tok * a->topk;
     const uint32_t groups = slots ? a->topk : a->n_expert;

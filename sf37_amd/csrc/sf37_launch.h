@@ -94,6 +94,25 @@ int sf37k_synth_quant_rows(int type, uint8_t *dst, uint64_t row0, uint64_t nrows
 /* Elementwise exp/sigmoid of a float array (for exhaustive parity tests). */
 int sf37k_sigmoid_array(float *out, const float *x, uint64_t n, int mode, sf37_stream_t s);
 
+/* Routed experts on the matrix cores for many pairs per expert
+ * (k_prefill.hip).  Activations are re-quantised to Q8_K and written as fp16
+ * codes in the MFMA operand order of the weight format (q3 = 1: Q3 gate/up,
+ * 0: Q2 down) with a table of 8 floats per (row, 256-block); groups are cut
+ * into tiles of <= 128 pairs; gate/up and down read them.  codes: rows x dim
+ * halves; tab: rows x dim/256 x 8 floats; tiles: (max_tiles + 1) x 4 words. */
+uint32_t sf37k_pf_max_tiles(uint32_t n_pairs, uint32_t max_groups);
+int sf37k_pf_supported(uint32_t in_dim, uint32_t mid_dim, uint32_t out_dim);
+int sf37k_pf_act(int q3, void *codes, float *tab, const float *x, uint32_t dim, uint32_t n_rows,
+                 sf37_stream_t s);
+int sf37k_pf_tiles(uint32_t *tiles, const uint32_t *group_info, uint32_t max_groups, sf37_stream_t s);
+int sf37k_pf_gate_up(float *mid, float *gate_out, float *up_out, const uint8_t *gate_w,
+                     const uint8_t *up_w, const void *act, const float *tab, const uint32_t *tiles,
+                     const uint32_t *sorted_pairs, const float *weights, uint32_t max_tiles,
+                     uint32_t topk, uint32_t in_dim, uint32_t mid_dim, float clamp, sf37_stream_t s);
+int sf37k_pf_down(float *down_pair, const uint8_t *down_w, const void *act, const float *tab,
+                  const uint32_t *tiles, const uint32_t *sorted_pairs, uint32_t max_tiles,
+                  uint32_t mid_dim, uint32_t out_dim, sf37_stream_t s);
+
 /* Fused decode layer (up to 16 tokens): route, select, up, mid, down,
  * combine (k_decode.hip).  Pointers are device addresses; flags select the parts
  * that run.  cnt holds sf37k_decode_counters(...) zero-initialised words
