@@ -38,6 +38,7 @@ sys.path.insert(0, ROOT)
 import numpy as np  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
+MFMA_F16_PEAK_TFLOPS = 2500.0     # MI355X dense fp16/bf16 matrix peak
 EXPERT_BYTES = 6_225_920
 GATE_UP_EXPERT_BYTES = 2 * 2_252_800
 DOWN_EXPERT_BYTES = 1_720_320
@@ -55,6 +56,8 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--copy-calib", type=int, default=0, metavar="MIB",
                     help="only run 10 device-to-device copies of MIB MiB (calibrates the HBM counters)")
+    ap.add_argument("--prefill-steps", type=int, default=5, help="timed layers per prefill config (0 = skip)")
+    ap.add_argument("--prefill-only", action="store_true", help="only the prefill configs (2 and 3)")
     return ap.parse_args()
 
 
@@ -117,6 +120,10 @@ def main():
     hip.init()
     H = Hip()
     n_tok, E, K, F, TOPK = 8, moe.EXPERTS, moe.EMBD, moe.EXPERT_FF, moe.EXPERT_USED
+    if args.prefill_only:
+        lay = moe.SynthLayer(seed=moe.layer_seed(args.seed, 0))
+        print(json.dumps({"prefill": [prefill_bench(args, H, lay, c) for c in (3, 2)]}), flush=True)
+        return
 
     layers, xs, lgs, sels = [], [], [], []
     for l in range(args.layers):
@@ -202,6 +209,8 @@ def main():
     achieved = k_mean_bytes / (k_avg_ms * 1e-3) / 1e9
     traffic = measured_traffic(kern)
 
+    prefill = [prefill_bench(args, H, layers[0], c) for c in (3, 2)] if args.prefill_steps > 0 else None
+
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(layers[0], xs[0], sels[0], step_bytes[0], n_tok, args.cpu_seconds)
@@ -231,8 +240,66 @@ def main():
                      "kernel": kern, "bytes_per_launch": int(k_mean_bytes), "ms_per_launch": round(k_avg_ms, 5)},
         "cpu_baseline": cpu,
         "stages": stages,
+        "prefill": prefill,
     }
     print(json.dumps(line), flush=True)
+
+
+def prefill_bench(args, H, layer, config):
+    """One MoE layer over a prefill chunk (512 tokens,
+    Zipf-skewed routing; configs[3]: 4096 tokens, uniform): router GEMM,
+    top-8, shared expert, routed experts on the matrix cores, add.  Reports
+    tokens/s/layer and, for the two matrix-core kernels, achieved fp16 MFMA
+    TFLOP/s (algorithmic 2*M*N*K per pair) from HIP-event stage times."""
+    from sf37_amd import configs, hip
+    n_tok = configs.CONFIG_TOKENS[config]
+    K, F, E, TOPK = layer.in_dim, layer.mid_dim, layer.n_expert, layer.topk
+    seed = args.seed + 1000 * config
+    x = configs.x_device(config, seed, n_tok)
+    lg = hip.Tensor.from_array(configs.logits_for(config, seed, n_tok))
+    out, sel, wts = hip.Tensor.alloc(n_tok * K * 4), hip.Tensor.alloc(n_tok * TOPK * 4), \
+        hip.Tensor.alloc(n_tok * TOPK * 4)
+    L = hip.lib()
+    st = layer.weights_struct()
+
+    def step():
+        hip.check(L.sf37_hip_moe_layer(out, sel, wts, st, lg, x, n_tok), "moe layer (prefill)")
+
+    step()
+    H.sync()
+    a, b = H.event(), H.event()
+    H.record(a)
+    for _ in range(args.prefill_steps):
+        step()
+    H.record(b)
+    ms = H.elapsed_ms(a, b) / args.prefill_steps
+    L.sf37_hip_profile_enable(1)
+    hip.profile_read()
+    for _ in range(args.prefill_steps):
+        step()
+    prof = hip.profile_read()
+    L.sf37_hip_profile_enable(0)
+    P = n_tok * TOPK
+    flops = {"pf_gate_up": 2.0 * P * (2 * F) * K, "pf_down": 2.0 * P * F * K}
+    mfma = {}
+    for k, f in flops.items():
+        k_ms, k_n = prof[k]
+        if k_n == 0:
+            raise SystemExit(f"bench.py: {k} did not run for config {config}")
+        t = f / (k_ms / k_n * 1e-3) / 1e12
+        mfma[k] = {"achieved": round(t, 1), "ms_per_launch": round(k_ms / k_n, 4),
+                   "frac": round(t / MFMA_F16_PEAK_TFLOPS, 4)}
+    routed_ms = sum(prof[k][0] / prof[k][1] for k in flops)
+    routed_t = sum(flops.values()) / (routed_ms * 1e-3) / 1e12
+    counts = np.bincount(sel.read(np.int32).ravel(), minlength=E)
+    stages = {k: round(v[0] / v[1], 4) for k, v in prof.items() if v[1]}
+    return {"config": config, "tokens": n_tok, "ms_per_layer": round(ms, 4),
+            "tokens_per_s_per_layer": round(n_tok / (ms * 1e-3), 1),
+            "routed_mfma": {"bound": "mfma", "achieved": round(routed_t, 1), "peak": MFMA_F16_PEAK_TFLOPS,
+                            "unit": "TFLOP/s", "frac": round(routed_t / MFMA_F16_PEAK_TFLOPS, 4),
+                            "dtype": "f16 operands holding exact small integers, fp32 accumulate"},
+            "kernels": mfma, "max_pairs_per_expert": int(counts.max()), "idle_experts": int((counts == 0).sum()),
+            "stage_ms": stages}
 
 
 def measured_traffic(kern):

@@ -39,7 +39,13 @@ constexpr uint32_t PF_TB = PF_T / 32u;  // 32-pair MFMA blocks per tile
 constexpr uint32_t PF_GU_R = 64;        // F rows (gate and up) per gate/up workgroup
 constexpr uint32_t PF_DN_R = 128;       // output rows per down workgroup
 constexpr uint32_t PF_TAB = 8;          // floats per (row, block) table entry: C0..C3, d
-constexpr uint32_t PF_ACT_BUF = 32u * PF_T * 16u;   // bytes of one LDS activation block
+// LDS layout of one activation block: 4 groups of 32 tile slots; in a group
+// slot t (0..31) starts at PF_RS * (t % 16) + 512 * (t / 16), so one 64-lane
+// load fills slots t and t + 16 (512 contiguous bytes each) and 16
+// consecutive slots sit 16 bytes apart modulo 256 (no bank conflicts).
+constexpr uint32_t PF_RS = 2u * SF37_QK * 2u + 16u;  // 1040
+constexpr uint32_t PF_GRP = 16u * PF_RS;             // bytes of 32 slots
+constexpr uint32_t PF_ACT_BUF = PF_TB * PF_GRP;      // bytes of one LDS activation block
 
 // ---------------------------------------------------------------------------
 // Pair layouts.  Lane half kh of an MFMA holds 32 codes of every 64-group
@@ -178,7 +184,8 @@ __global__ void __launch_bounds__(1024) pf_tiles_kernel(uint32_t *__restrict__ t
 // LDS direct loads (global -> LDS, no registers).  Issued through inline asm
 // so the compiler does not wait for them before unrelated LDS reads; the
 // kernel waits with s_waitcnt vmcnt(0) + barrier before reading the buffer.
-// Lane i of a dwordx4 load writes LDS bytes [m0 + 16 i, m0 + 16 i + 16).
+// Lane i of a dwordx4 load writes LDS bytes [m0 + 16 i, m0 + 16 i + 16);
+// one wait state separates the M0 write from the load.
 // ---------------------------------------------------------------------------
 // sbase must be wave-uniform; it is moved to SGPRs with readfirstlane.
 __device__ __forceinline__ uint64_t sgpr_ptr(const void *p) {
@@ -188,14 +195,23 @@ __device__ __forceinline__ uint64_t sgpr_ptr(const void *p) {
     return ((uint64_t)hi << 32) | lo;
 }
 __device__ __forceinline__ void lds_dma16(uint32_t lds, uint32_t voff, const void *sbase) {
-    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds), "v"(voff), "s"(sgpr_ptr(sbase))
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(__builtin_amdgcn_readfirstlane(lds)),
+                 "v"(voff), "s"(sgpr_ptr(sbase))
                  : "memory", "m0");
 }
 __device__ __forceinline__ void lds_dma4(uint32_t lds, uint32_t voff, const void *sbase) {
-    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, %2" ::"s"(lds), "v"(voff), "s"(sgpr_ptr(sbase))
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, %2" ::"s"(__builtin_amdgcn_readfirstlane(lds)),
+                 "v"(voff), "s"(sgpr_ptr(sbase))
                  : "memory", "m0");
 }
 __device__ __forceinline__ void wait_vm0() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// After wait_vm0, mark a block's weight words as just defined: the compiler
+// then knows no load is pending on them and does not place its own
+// s_waitcnt vmcnt inside the compute (which would also wait for the next
+// block's LDS direct loads, issued earlier in program order).
+struct q3_raw;
+struct q2_raw;
 
 __device__ __forceinline__ uint32_t lds_addr(const void *p) { return (uint32_t)(uintptr_t)p; }
 
@@ -221,26 +237,43 @@ struct q2_raw {
     uint32_t w[4][2];
 };
 
+__device__ __forceinline__ void raw_ready(q3_raw &r) {
+    asm volatile("" : "+v"(r.h[0]), "+v"(r.h[1]), "+v"(r.h[2]), "+v"(r.h[3]), "+v"(r.w[0][0]), "+v"(r.w[0][1]),
+                 "+v"(r.w[0][2]), "+v"(r.w[0][3]), "+v"(r.w[1][0]), "+v"(r.w[1][1]), "+v"(r.w[1][2]),
+                 "+v"(r.w[1][3]), "+v"(r.w[2][0]), "+v"(r.w[2][1]), "+v"(r.w[2][2]), "+v"(r.w[2][3]),
+                 "+v"(r.w[3][0]), "+v"(r.w[3][1]), "+v"(r.w[3][2]), "+v"(r.w[3][3]));
+}
+__device__ __forceinline__ void raw_ready(q2_raw &r) {
+    asm volatile("" : "+v"(r.h[0]), "+v"(r.h[1]), "+v"(r.h[2]), "+v"(r.w[0][0]), "+v"(r.w[0][1]), "+v"(r.w[1][0]),
+                 "+v"(r.w[1][1]), "+v"(r.w[2][0]), "+v"(r.w[2][1]), "+v"(r.w[3][0]), "+v"(r.w[3][1]));
+}
+
 typedef uint32_t u32x4a __attribute__((ext_vector_type(4), aligned(4)));
 typedef uint32_t u32x3a __attribute__((ext_vector_type(3), aligned(4)));
 typedef uint32_t u32x2a __attribute__((ext_vector_type(2), aligned(4)));
 
+// Dword loads (no register tuples): the words go straight into the
+// registers the loop carries them in, so no copy waits for the data.
 __device__ __forceinline__ void q3_load(q3_raw &r, const uint8_t *hp, const uint8_t *pp) {
-    const u32x4a v = *(const u32x4a *)hp;
-    r.h[0] = v.x; r.h[1] = v.y; r.h[2] = v.z; r.h[3] = v.w;
+    const uint32_t *h = (const uint32_t *)hp;
+#pragma unroll
+    for (int i = 0; i < 4; i++) r.h[i] = h[i];
 #pragma unroll
     for (int g = 0; g < 4; g++) {
-        const u32x4a q = *(const u32x4a *)(pp + 24 * g);
-        r.w[g][0] = q.x; r.w[g][1] = q.y; r.w[g][2] = q.z; r.w[g][3] = q.w;
+        const uint32_t *q = (const uint32_t *)(pp + 24 * g);
+#pragma unroll
+        for (int i = 0; i < 4; i++) r.w[g][i] = q[i];
     }
 }
 __device__ __forceinline__ void q2_load(q2_raw &r, const uint8_t *hp, const uint8_t *pp) {
-    const u32x3a v = *(const u32x3a *)hp;
-    r.h[0] = v.x; r.h[1] = v.y; r.h[2] = v.z;
+    const uint32_t *h = (const uint32_t *)hp;
+#pragma unroll
+    for (int i = 0; i < 3; i++) r.h[i] = h[i];
 #pragma unroll
     for (int g = 0; g < 4; g++) {
-        const u32x2a q = *(const u32x2a *)(pp + 16 * g);
-        r.w[g][0] = q.x; r.w[g][1] = q.y;
+        const uint32_t *q = (const uint32_t *)(pp + 16 * g);
+        r.w[g][0] = q[0];
+        r.w[g][1] = q[1];
     }
 }
 
@@ -295,55 +328,125 @@ __device__ __forceinline__ uint32_t hdr_zp(const uint32_t *h, int g) {
     return (h[a >> 5] >> (a & 31)) & 0xffu;
 }
 
-// One 256-block of the tile: 4 groups x (dequant + 4 token blocks x 4 MFMAs),
-// the canonical chain into blk, then acc = fma(d, blk, acc).
-template <bool Q3, int SH, typename RAW>
-__device__ __forceinline__ void pf_block(const RAW &r, const uint8_t *act_lds, const float *cd_lds,
-                                         uint32_t kh, uint32_t col, uint32_t ntb, f16v acc[PF_TB],
-                                         f16v blk[PF_TB]) {
-#pragma unroll
-    for (int g = 0; g < 4; g++) {
-        uint32_t bw[16];
-        if constexpr (Q3) q3_dequant<SH>(r.w[g], 8u - (hdr_zp<SH>(r.h, g) & 7u), bw);
-        else q2_dequant(r.w[g], 4u - (hdr_zp<0>(r.h, g) & 3u), bw);
-        const float s = hdr_scale<Q3 ? SH : 0>(r.h, g);
-        h8 B[4];
-#pragma unroll
-        for (int m = 0; m < 4; m++) {
-            typedef uint32_t u4 __attribute__((ext_vector_type(4)));
-            const u4 t = {bw[4 * m], bw[4 * m + 1], bw[4 * m + 2], bw[4 * m + 3]};
-            B[m] = __builtin_bit_cast(h8, t);
+// Running sums live in AGPRs (the VGPRs hold the block sums, MFMA
+// accumulators and operands); acc = fma(d, blk, acc) goes through a VGPR.
+__device__ __forceinline__ void acc_fma_agpr(float &acc, float d, float b) {
+    float t;
+    asm("v_accvgpr_read_b32 %1, %0\n\tv_fma_f32 %1, %2, %3, %1\n\tv_accvgpr_write_b32 %0, %1"
+        : "+a"(acc), "=&v"(t)
+        : "v"(d), "v"(b));
+}
+
+// Q3 / Q2 dequantisation of part (0: pair words 0..7, 1: words 8..15) of group g.
+template <bool Q3, int SH, int PART, typename RAW>
+__device__ __forceinline__ void pf_dequant(const RAW &r, int g, uint32_t out[16]) {
+    if constexpr (Q3) {
+        const uint32_t k = 8u - (hdr_zp<SH>(r.h, g) & 7u);
+        const uint32_t *w = r.w[g];
+        constexpr uint32_t mA1 = q3_mask(0), mA2 = q3_mask(1), mB1 = q3_mask(2), mB2 = q3_mask(3);
+        const uint32_t cB1 = pf_exp(1, 0) + k * pf_mul(1, 0), cB2 = pf_exp(4, 3) + k * pf_mul(4, 3);
+        uint32_t x;
+        if constexpr (PART == 0) {
+            const uint32_t cA1 = pf_exp(0, 2) + k * pf_mul(0, 2), cA2 = pf_exp(3, 5) + k * pf_mul(3, 5);
+            x = q3_win<SH, 0>(w);  out[0] = (x & mA1) + cA1;  out[1] = (x & mA2) + cA2;
+            x = q3_win<SH, 6>(w);  out[2] = (x & mA1) + cA1;  out[3] = (x & mA2) + cA2;
+            x = q3_win<SH, 12>(w); out[4] = (x & mA1) + cA1;  out[5] = (x & mA2) + cA2;
+            x = q3_win<SH, 35>(w); out[6] = (x & mB1) + cB1;  out[7] = (x & mB2) + cB2;
+        } else {
+            x = q3_win<SH, 41>(w); out[8] = (x & mB1) + cB1;  out[9] = (x & mB2) + cB2;
+            x = q3_win<SH, 47>(w); out[10] = (x & mB1) + cB1;
+            x = q3_win<SH, 65>(w); out[11] = (x & mB1) + cB1; out[12] = (x & mB2) + cB2;
+            x = q3_win<SH, 71>(w); out[13] = (x & mB1) + cB1; out[14] = (x & mB2) + cB2;
+            x = q3_win<SH, 77>(w); out[15] = (x & mB1) + cB1;
         }
+    } else {
+        const uint32_t k = 4u - (hdr_zp<0>(r.h, g) & 3u);
+        const uint32_t u = r.w[g][PART];
 #pragma unroll
-        for (uint32_t i = 0; i < PF_TB; i++) {
-            if (i < ntb) {
-                f16v D;
+        for (uint32_t h = 0; h < 2u; h++) {
+            const uint32_t x = h ? (u >> 8) : u;
 #pragma unroll
-                for (int jj = 0; jj < 4; jj++) {
-                    const float4 c = *(const float4 *)(cd_lds + g * PF_T + 32u * i + 8u * jj + 4u * kh);
-                    D[4 * jj] = c.x; D[4 * jj + 1] = c.y; D[4 * jj + 2] = c.z; D[4 * jj + 3] = c.w;
-                }
-#pragma unroll
-                for (int m = 0; m < 4; m++) {
-                    const h8 A = *(const h8 *)(act_lds + ((uint32_t)(8 * g + m) * PF_T + 4u * kh * PF_T + 32u * i + col) * 16u);
-                    D = __builtin_amdgcn_mfma_f32_32x32x16_f16(A, B[m], D, 0, 0, 0);
-                }
-#pragma unroll
-                for (int r2 = 0; r2 < 16; r2++) blk[i][r2] = __builtin_fmaf(s, D[r2], g == 0 ? 0.0f : blk[i][r2]);
-            }
+            for (uint32_t j = 0; j < 4u; j++)
+                out[8 * PART + 4u * h + j] =
+                    (x & (0x00030003u << (2u * j))) + pf_exp(2u * j, 2u * j) + k * pf_mul(2u * j, 2u * j);
         }
     }
+}
+
+// One 256-block of the tile.  Chains c = (group g, token block i), 4*NTB of
+// them, each = 4 MFMAs on accumulator D = C(g, i).  Stage c calls pre(c)
+// (a slice of the next block's global loads, so a stalled memory issue
+// overlaps MFMAs already in flight), issues the LDS loads of chain c+1,
+// part of the next group's dequantisation, the MFMAs of chain c and the
+// epilogue blk = fma(s_g, D, blk) of chain c-1; stages are fenced so the
+// compiler interleaves within a stage only.  Then acc = fma(d, blk, acc)
+// per token block.
+template <bool Q3, int SH, int NTB, typename RAW, typename PRE>
+__device__ __forceinline__ void pf_block(const RAW &r, const uint8_t *act_lds, const float *cd_lds,
+                                         uint32_t kh, uint32_t col, float (*acc)[16], f16v blk[PF_TB],
+                                         PRE &&pre) {
+    constexpr int NC = 4 * NTB;
+    const uint8_t *a_lane = act_lds + (col & 15u) * PF_RS + (col >> 4) * 512u + 64u * kh;
+    const float *c_lane = cd_lds + 4u * kh;
+    uint32_t bw[2][16];
+    float s[4];
 #pragma unroll
-    for (uint32_t i = 0; i < PF_TB; i++) {
-        if (i < ntb) {
+    for (int g = 0; g < 4; g++) s[g] = hdr_scale<Q3 ? SH : 0>(r.h, g);
+    pf_dequant<Q3, SH, 0>(r, 0, bw[0]);
+    pf_dequant<Q3, SH, 1>(r, 0, bw[0]);
+    f16v D[3];
+    h8 A[2][4];
+    auto load = [&](int c, f16v &d, h8 *a) {
+        const int g = c / NTB, i = c % NTB;
 #pragma unroll
-            for (int jj = 0; jj < 4; jj++) {
-                const float4 d = *(const float4 *)(cd_lds + 4 * PF_T + 32u * i + 8u * jj + 4u * kh);
-                acc[i][4 * jj] = __builtin_fmaf(d.x, blk[i][4 * jj], acc[i][4 * jj]);
-                acc[i][4 * jj + 1] = __builtin_fmaf(d.y, blk[i][4 * jj + 1], acc[i][4 * jj + 1]);
-                acc[i][4 * jj + 2] = __builtin_fmaf(d.z, blk[i][4 * jj + 2], acc[i][4 * jj + 2]);
-                acc[i][4 * jj + 3] = __builtin_fmaf(d.w, blk[i][4 * jj + 3], acc[i][4 * jj + 3]);
+        for (int jj = 0; jj < 4; jj++) {
+            const float4 v = *(const float4 *)(c_lane + g * PF_T + 32 * i + 8 * jj);
+            d[4 * jj] = v.x; d[4 * jj + 1] = v.y; d[4 * jj + 2] = v.z; d[4 * jj + 3] = v.w;
+        }
+#pragma unroll
+        for (int m = 0; m < 4; m++) a[m] = *(const h8 *)(a_lane + i * PF_GRP + (8 * g + m) * 16);
+    };
+    load(0, D[0], A[0]);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int c = 0; c < NC; c++) {
+        const int g = c / NTB, i = c % NTB;
+        pre(c, NC);
+        if (c + 1 < NC) load(c + 1, D[(c + 1) % 3], A[(c + 1) & 1]);
+        if (g < 3) {
+            constexpr int P0 = NTB >= 3 ? 1 : 0, P1 = NTB >= 3 ? 2 : NTB - 1;
+            if (i == P0) pf_dequant<Q3, SH, 0>(r, g + 1, bw[(g + 1) & 1]);
+            if (i == P1) pf_dequant<Q3, SH, 1>(r, g + 1, bw[(g + 1) & 1]);
+        }
+        {
+            const uint32_t *bb = bw[g & 1];
+#pragma unroll
+            for (int m = 0; m < 4; m++) {
+                typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+                const u4 t = {bb[4 * m], bb[4 * m + 1], bb[4 * m + 2], bb[4 * m + 3]};
+                D[c % 3] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[c & 1][m], __builtin_bit_cast(h8, t), D[c % 3], 0, 0, 0);
             }
+        }
+        if (c > 0) {
+            const int gp = (c - 1) / NTB, ip = (c - 1) % NTB;
+#pragma unroll
+            for (int r2 = 0; r2 < 16; r2++)
+                blk[ip][r2] = __builtin_fmaf(s[gp], D[(c - 1) % 3][r2], gp == 0 ? 0.0f : blk[ip][r2]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int r2 = 0; r2 < 16; r2++)
+        blk[NTB - 1][r2] = __builtin_fmaf(s[3], D[(NC - 1) % 3][r2], blk[NTB - 1][r2]);
+#pragma unroll
+    for (int i = 0; i < NTB; i++) {
+#pragma unroll
+        for (int jj = 0; jj < 4; jj++) {
+            const float4 d = *(const float4 *)(c_lane + 4 * PF_T + 32 * i + 8 * jj);
+            acc_fma_agpr(acc[i][4 * jj], d.x, blk[i][4 * jj]);
+            acc_fma_agpr(acc[i][4 * jj + 1], d.y, blk[i][4 * jj + 1]);
+            acc_fma_agpr(acc[i][4 * jj + 2], d.z, blk[i][4 * jj + 2]);
+            acc_fma_agpr(acc[i][4 * jj + 3], d.w, blk[i][4 * jj + 3]);
         }
     }
 }
@@ -352,6 +455,12 @@ __device__ __forceinline__ void pf_block(const RAW &r, const uint8_t *act_lds, c
 // rt*64 + 16w + c and up rows (c < 16: gate, else up) as its 32 columns;
 // epilogue mid = ((g*sig(g))*u)*w per pair.  Down (Q3 = false): row tile =
 // 128 output rows, 32 per wave; epilogue down_pair[pair][row].
+template <bool Q3, int NTB, typename ISSUE>
+__device__ __forceinline__ void pf_body(const pf_params &p, const uint8_t *wrow, ISSUE &issue_act,
+                                        uint8_t (*s_act)[PF_ACT_BUF], float (*s_cd)[5 * PF_T],
+                                        const uint32_t *s_pair, const float *s_w, uint32_t kh, uint32_t col,
+                                        uint32_t wcol, uint32_t cnt);
+
 template <bool Q3>
 __global__ void __launch_bounds__(256, 1) pf_expert_kernel(pf_params p) {
     __shared__ __align__(16) uint8_t s_act[2][PF_ACT_BUF];
@@ -363,7 +472,8 @@ __global__ void __launch_bounds__(256, 1) pf_expert_kernel(pf_params p) {
     if (t >= p.tiles[0]) return;
     const uint4 ti = ((const uint4 *)p.tiles)[1 + t];
     const uint32_t e = ti.x, p0 = ti.y, cnt = ti.z;
-    const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63u, kh = lane >> 5, col = lane & 31u;
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, kh = lane >> 5, col = lane & 31u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t ntb = (cnt + 31u) / 32u;
     const uint32_t nblk = p.nblk;
     if (tid < PF_T) {
@@ -371,36 +481,44 @@ __global__ void __launch_bounds__(256, 1) pf_expert_kernel(pf_params p) {
         s_pair[tid] = pr;
         if (Q3) s_w[tid] = p.weights[pr];
     }
-    // activation rows of tile slots `lane` and 64 + lane (pad slots repeat the last pair)
-    uint32_t voff_c[2], voff_t[2];
+    // activation rows: tile slots `lane` and 64 + lane for the tables; slot
+    // 32*wave + lane (lanes 0..31) for the codes (pad slots repeat the last pair)
+    uint32_t voff_t[2], rowoff_c;
 #pragma unroll
     for (int h = 0; h < 2; h++) {
         const uint32_t sl = 64u * h + lane;
         const uint32_t pr = p.sorted[p0 + (sl < cnt ? sl : cnt - 1u)];
         const uint32_t row = Q3 ? pr / p.topk : pr;
-        voff_c[h] = row * nblk * (SF37_QK * 2u);
         voff_t[h] = row * nblk * (PF_TAB * 4u);
     }
+    {
+        const uint32_t sl = 32u * wave + (lane & 31u);
+        const uint32_t pr = p.sorted[p0 + (sl < cnt ? sl : cnt - 1u)];
+        rowoff_c = (Q3 ? pr / p.topk : pr) * nblk * (SF37_QK * 2u);
+    }
     const uint32_t act_l = lds_addr(&s_act[0][0]), cd_l = lds_addr(&s_cd[0][0]);
-    auto issue_act = [&](uint32_t b) {
+    // codes: wave w copies tile slots 32w .. 32w+31, one load per slot pair
+    // (t, t + 16): lanes 0..31 read slot t's 512-byte row, lanes 32..63 slot t + 16's
+    // slice `part` of `nparts` (compile-time after inlining) of block b's loads
+    auto issue_act = [&](uint32_t b, int part, int nparts) {
         const uint32_t bf = b & 1u;
         const uint8_t *cb = (const uint8_t *)p.act + (uint64_t)b * (SF37_QK * 2u);
+        const int j0 = 16 * part / nparts, j1 = 16 * (part + 1) / nparts;
 #pragma unroll
-        for (uint32_t j = 0; j < 8u; j++) {
-            const uint32_t pc = 8u * wave + j;
-#pragma unroll
-            for (uint32_t h = 0; h < 2u; h++)
-                lds_dma16(__builtin_amdgcn_readfirstlane(act_l + bf * PF_ACT_BUF + (pc * PF_T + 64u * h) * 16u),
-                          voff_c[h], cb + 16u * pc);
+        for (int j = j0; j < j1; j++) {
+            const uint32_t r0 = (uint32_t)__builtin_amdgcn_readlane((int)rowoff_c, j);
+            const uint32_t r1 = (uint32_t)__builtin_amdgcn_readlane((int)rowoff_c, j + 16);
+            lds_dma16(act_l + bf * PF_ACT_BUF + wave * PF_GRP + (uint32_t)j * PF_RS, (kh ? r1 : r0) + 16u * col, cb);
         }
-        const uint8_t *tb = (const uint8_t *)p.tab + (uint64_t)b * (PF_TAB * 4u);
+        if (part == 0) {
+            const uint8_t *tb = (const uint8_t *)p.tab + (uint64_t)b * (PF_TAB * 4u);
 #pragma unroll
-        for (uint32_t j = 0; j < 3u; j++) {
-            const uint32_t it = wave + 4u * j;
-            if (it < 10u) {
-                const uint32_t a = it >> 1, h = it & 1u;
-                lds_dma4(__builtin_amdgcn_readfirstlane(cd_l + bf * (5u * PF_T * 4u) + (a * PF_T + 64u * h) * 4u),
-                         voff_t[h], tb + 4u * a);
+            for (uint32_t j = 0; j < 3u; j++) {
+                const uint32_t it = wave + 4u * j;
+                if (it < 10u) {
+                    const uint32_t a = it >> 1, h = it & 1u;
+                    lds_dma4(cd_l + bf * (5u * PF_T * 4u) + (a * PF_T + 64u * h) * 4u, voff_t[h], tb + 4u * a);
+                }
             }
         }
     };
@@ -409,65 +527,96 @@ __global__ void __launch_bounds__(256, 1) pf_expert_kernel(pf_params p) {
     const uint32_t blk_bytes = Q3 ? SF37_Q3_BYTES : SF37_Q2_BYTES;
     const uint64_t row_bytes = (uint64_t)nblk * blk_bytes;
     const uint8_t *wrow = (Q3 && col >= 16u ? p.w1 : p.w0) + ((uint64_t)e * p.out_rows + wcol) * row_bytes;
+    switch (ntb) {
+        case 1: pf_body<Q3, 1>(p, wrow, issue_act, s_act, s_cd, s_pair, s_w, kh, col, wcol, cnt); break;
+        case 2: pf_body<Q3, 2>(p, wrow, issue_act, s_act, s_cd, s_pair, s_w, kh, col, wcol, cnt); break;
+        case 3: pf_body<Q3, 3>(p, wrow, issue_act, s_act, s_cd, s_pair, s_w, kh, col, wcol, cnt); break;
+        default: pf_body<Q3, 4>(p, wrow, issue_act, s_act, s_cd, s_pair, s_w, kh, col, wcol, cnt); break;
+    }
+}
 
-    f16v acc[PF_TB], blk[PF_TB];
+// Main loop and epilogue for NTB 32-pair blocks (the tile's pair count rounded up).
+template <bool Q3, int NTB, typename ISSUE>
+__device__ __forceinline__ void pf_body(const pf_params &p, const uint8_t *wrow, ISSUE &issue_act,
+                                        uint8_t (*s_act)[PF_ACT_BUF], float (*s_cd)[5 * PF_T],
+                                        const uint32_t *s_pair, const float *s_w, uint32_t kh, uint32_t col,
+                                        uint32_t wcol, uint32_t cnt) {
+    const uint32_t nblk = p.nblk;
+    float acc[NTB][16];
+    f16v blk[PF_TB];
 #pragma unroll
-    for (uint32_t i = 0; i < PF_TB; i++)
+    for (int i = 0; i < NTB; i++)
 #pragma unroll
         for (int r2 = 0; r2 < 16; r2++) acc[i][r2] = 0.0f;
 
-    issue_act(0);
+    issue_act(0, 0, 1);
+    // Each block's compute carries the next block's loads.  Past the last
+    // block the loads repeat block nblk-1 into the buffer no longer read
+    // (uniform code, no branch inside the stages); the final wait below
+    // keeps no load in flight at the end of the workgroup.
+    const uint32_t last = nblk - 1u;
     if constexpr (Q3) {
         // blocks in pairs: even blocks start dword-aligned, odd blocks 2 bytes in
         q3_raw ra, rb;
-        q3_load(ra, wrow, wrow + 12u + 12u * kh);
+        auto wload = [&](q3_raw &r, uint32_t bn) {
+            const uint32_t o = SF37_Q3_BYTES * bn;
+            q3_load(r, wrow + (o & ~3u), wrow + ((o + 12u + 12u * kh) & ~3u));
+        };
+        wload(ra, 0);
         for (uint32_t b = 0; b < nblk; b += 2u) {
-            const uint8_t *base = wrow + (uint64_t)b * SF37_Q3_BYTES;
             wait_vm0();
+            raw_ready(ra);
             __syncthreads();
-            if (b + 1u < nblk) {
-                issue_act(b + 1u);
-                q3_load(rb, base + 108u, base + 108u + 12u + 12u * kh);
-            }
-            pf_block<true, 0>(ra, s_act[b & 1u], s_cd[b & 1u], kh, col, ntb, acc, blk);
+            const uint32_t b1 = b + 1u < nblk ? b + 1u : last, b2 = b + 2u < nblk ? b + 2u : last;
+            pf_block<true, 0, NTB>(ra, s_act[b & 1u], s_cd[b & 1u], kh, col, acc, blk, [&](int c, int nc) {
+                issue_act(b1, c, nc);
+                if (c == 0) wload(rb, b1);
+            });
             if (b + 1u < nblk) {
                 wait_vm0();
+                raw_ready(rb);
                 __syncthreads();
-                if (b + 2u < nblk) {
-                    issue_act(b + 2u);
-                    q3_load(ra, base + 220u, base + 220u + 12u + 12u * kh);
-                }
-                pf_block<true, 16>(rb, s_act[(b + 1u) & 1u], s_cd[(b + 1u) & 1u], kh, col, ntb, acc, blk);
+                pf_block<true, 16, NTB>(rb, s_act[(b + 1u) & 1u], s_cd[(b + 1u) & 1u], kh, col, acc, blk,
+                                        [&](int c, int nc) {
+                                            issue_act(b2, c, nc);
+                                            if (c == 0) wload(ra, b2);
+                                        });
             }
         }
     } else {
         q2_raw ra, rb;
-        q2_load(ra, wrow, wrow + 12u + 8u * kh);
+        auto wload = [&](q2_raw &r, uint32_t bn) {
+            const uint8_t *bp = wrow + (uint64_t)SF37_Q2_BYTES * bn;
+            q2_load(r, bp, bp + 12u + 8u * kh);
+        };
+        wload(ra, 0);
         for (uint32_t b = 0; b < nblk; b += 2u) {
-            const uint8_t *base = wrow + (uint64_t)b * SF37_Q2_BYTES;
             wait_vm0();
+            raw_ready(ra);
             __syncthreads();
-            if (b + 1u < nblk) {
-                issue_act(b + 1u);
-                q2_load(rb, base + 84u, base + 84u + 12u + 8u * kh);
-            }
-            pf_block<false, 0>(ra, s_act[b & 1u], s_cd[b & 1u], kh, col, ntb, acc, blk);
+            const uint32_t b1 = b + 1u < nblk ? b + 1u : last, b2 = b + 2u < nblk ? b + 2u : last;
+            pf_block<false, 0, NTB>(ra, s_act[b & 1u], s_cd[b & 1u], kh, col, acc, blk, [&](int c, int nc) {
+                issue_act(b1, c, nc);
+                if (c == 0) wload(rb, b1);
+            });
             if (b + 1u < nblk) {
                 wait_vm0();
+                raw_ready(rb);
                 __syncthreads();
-                if (b + 2u < nblk) {
-                    issue_act(b + 2u);
-                    q2_load(ra, base + 168u, base + 168u + 12u + 8u * kh);
-                }
-                pf_block<false, 0>(rb, s_act[(b + 1u) & 1u], s_cd[(b + 1u) & 1u], kh, col, ntb, acc, blk);
+                pf_block<false, 0, NTB>(rb, s_act[(b + 1u) & 1u], s_cd[(b + 1u) & 1u], kh, col, acc, blk,
+                                        [&](int c, int nc) {
+                                            issue_act(b2, c, nc);
+                                            if (c == 0) wload(ra, b2);
+                                        });
             }
         }
     }
+    wait_vm0();
 
     // epilogue: D layout - lane holds column col, tokens 8*(r/4) + 4*kh + r%4
 #pragma unroll
-    for (uint32_t i = 0; i < PF_TB; i++) {
-        if (i < ntb) {
+    for (uint32_t i = 0; i < (uint32_t)NTB; i++) {
+        {
 #pragma unroll
             for (int r2 = 0; r2 < 16; r2++) {
                 const uint32_t tl = 32u * i + 8u * (r2 >> 2) + 4u * kh + (r2 & 3);
