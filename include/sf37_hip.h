@@ -296,6 +296,10 @@ enum {
      * the per-expert tile list, gate/up + SwiGLU, down */
     SF37_HIP_STAGE_PF_ACT_X, SF37_HIP_STAGE_PF_TILES, SF37_HIP_STAGE_PF_GATE_UP,
     SF37_HIP_STAGE_PF_ACT_MID, SF37_HIP_STAGE_PF_DOWN,
+    /* the shared expert on the matrix cores (prefill batches): Q8_0 weights
+     * repacked to fp16 codes, Q8_0 activations (x, then the shared mid),
+     * gate/up + SwiGLU, down */
+    SF37_HIP_STAGE_SH_REPACK, SF37_HIP_STAGE_SH_ACT, SF37_HIP_STAGE_SH_GATE_UP, SF37_HIP_STAGE_SH_DOWN,
     SF37_HIP_N_STAGES
 };
 int sf37_hip_profile_enable(int on);

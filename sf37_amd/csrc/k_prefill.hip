@@ -637,6 +637,216 @@ __device__ __forceinline__ void pf_body(const pf_params &p, const uint8_t *wrow,
     }
 }
 
+// ---------------------------------------------------------------------------
+// Shared expert (Q8_0, every token) on the matrix cores.
+//
+// Canonical order of sf37_ops.c:92-108: acc = acc + ((float)isum_b * ws_b) * xs_b
+// per 32-block in block order.  isum_b comes from two 32x32x16 MFMAs on
+// fp16 operands holding the int8 codes exactly (|partial sums| < 2^20), so
+// it is exact; the epilogue is those three float operations per block.
+// The weights are repacked per call into fp16 codes in MFMA lane order
+// (position 16*kh + 8*m + e of a block holds code 16*m + 8*kh + e) with the
+// scales as floats; the activations are quantised straight into the same
+// order (bit-exact with sf37_ops.c:57-90).
+// ---------------------------------------------------------------------------
+constexpr uint32_t SH_T = 64;                  // tokens per tile
+constexpr uint32_t SH_TB = SH_T / 32u;         // 32-token blocks per tile
+constexpr uint32_t SH_CB = 4;                  // Q8_0 blocks per K chunk
+constexpr uint32_t SH_RS = SH_CB * 64u + 16u;  // LDS bytes per token row of a chunk (+16: banks)
+constexpr uint32_t SH_BUF = SH_T * SH_RS;
+
+__host__ __device__ constexpr uint32_t sh_pos(uint32_t k) {   // code index -> position in a block
+    return ((k >> 3) & 1u) * 16u + (k >> 4) * 8u + (k & 7u);
+}
+
+// one lane per Q8_0 block: 32 codes -> fp16 in lane order, scale -> float
+__global__ void __launch_bounds__(256) sh_w16_kernel(_Float16 *__restrict__ w16, float *__restrict__ ws,
+                                                     const uint8_t *__restrict__ w, uint64_t n_blocks) {
+    const uint64_t u = (uint64_t)blockIdx.x * 256u + threadIdx.x;
+    if (u >= n_blocks) return;
+    const uint8_t *b = w + u * SF37_Q8_0_BYTES;
+    ws[u] = sf37_f16((uint32_t)b[0] | ((uint32_t)b[1] << 8));
+    _Float16 h[32];
+#pragma unroll
+    for (uint32_t k = 0; k < 32u; k++) h[sh_pos(k)] = (_Float16)(int)(int8_t)b[2 + k];
+    typedef _Float16 h8v __attribute__((ext_vector_type(8)));
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        const h8v v = {h[8 * q], h[8 * q + 1], h[8 * q + 2], h[8 * q + 3],
+                       h[8 * q + 4], h[8 * q + 5], h[8 * q + 6], h[8 * q + 7]};
+        *(h8v *)(w16 + u * 32u + 8u * q) = v;
+    }
+}
+
+// Q8_0 activations (arithmetic of q8_0_quantize_kernel, k_q8_0.hip): one
+// half-wave per 32-block; codes as fp16 in lane order, scale as float.
+__global__ void __launch_bounds__(256) sh_act_kernel(_Float16 *__restrict__ a16, float *__restrict__ xs,
+                                                     const float *__restrict__ x, uint32_t nb, uint64_t n_tok) {
+    const uint64_t hw = (uint64_t)blockIdx.x * 8u + (threadIdx.x >> 5);
+    const uint32_t l = threadIdx.x & 31u;
+    const bool live = hw < nb * n_tok;
+    const uint64_t u = live ? hw : 0u;
+    const float v = x[u * 32u + l];
+    float amax = fabsf(v);
+#pragma unroll
+    for (int off = 16; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 32));
+    int q = 0;
+    float d = 0.0f;
+    if (amax != 0.0f) {
+        d = amax / 127.0f;
+        const float iscale = 1.0f / d;
+        q = (int)fminf(fmaxf(__builtin_rintf(iscale * v), -128.0f), 127.0f);
+    }
+    if (!live) return;
+    a16[u * 32u + sh_pos(l)] = (_Float16)q;
+    if (l == 0) xs[u] = d;
+}
+
+struct sh_params {
+    float *out0, *out1;            // gate/up: mid (SwiGLU) [tok][rows]; down: out [tok][rows]
+    const _Float16 *w0, *w1;       // gate, up (or down) in lane order
+    const float *ws0, *ws1;
+    const _Float16 *act;           // [tok][nb * 32]
+    const float *xs;               // [tok][nb]
+    uint32_t n_tok, nb, rows, n_ct, n_tt;
+    float clamp;
+};
+
+struct sh_raw {
+    uint32_t w[SH_CB][8];          // per block: the lane's 16 codes (two MFMA operands)
+    float s[SH_CB];
+};
+
+__device__ __forceinline__ void sh_ready(sh_raw &r) {
+    asm volatile("" : "+v"(r.w[0][0]), "+v"(r.w[0][1]), "+v"(r.w[0][2]), "+v"(r.w[0][3]), "+v"(r.w[0][4]),
+                 "+v"(r.w[0][5]), "+v"(r.w[0][6]), "+v"(r.w[0][7]), "+v"(r.w[1][0]), "+v"(r.w[1][1]),
+                 "+v"(r.w[1][2]), "+v"(r.w[1][3]), "+v"(r.w[1][4]), "+v"(r.w[1][5]), "+v"(r.w[1][6]),
+                 "+v"(r.w[1][7]), "+v"(r.s[0]), "+v"(r.s[1]));
+    asm volatile("" : "+v"(r.w[2][0]), "+v"(r.w[2][1]), "+v"(r.w[2][2]), "+v"(r.w[2][3]), "+v"(r.w[2][4]),
+                 "+v"(r.w[2][5]), "+v"(r.w[2][6]), "+v"(r.w[2][7]), "+v"(r.w[3][0]), "+v"(r.w[3][1]),
+                 "+v"(r.w[3][2]), "+v"(r.w[3][3]), "+v"(r.w[3][4]), "+v"(r.w[3][5]), "+v"(r.w[3][6]),
+                 "+v"(r.w[3][7]), "+v"(r.s[2]), "+v"(r.s[3]));
+}
+
+__device__ __forceinline__ void sh_load(sh_raw &r, const _Float16 *wrow, const float *wsrow, uint32_t c,
+                                        uint32_t kh) {
+#pragma unroll
+    for (uint32_t j = 0; j < SH_CB; j++) {
+        const uint32_t *q = (const uint32_t *)(wrow + (uint64_t)(c * SH_CB + j) * 32u + 16u * kh);
+#pragma unroll
+        for (int i = 0; i < 8; i++) r.w[j][i] = q[i];
+    }
+    const float4 sv = *(const float4 *)(wsrow + (uint64_t)c * SH_CB);
+    r.s[0] = sv.x; r.s[1] = sv.y; r.s[2] = sv.z; r.s[3] = sv.w;
+}
+
+// One K chunk (SH_CB Q8_0 blocks) for SH_TB token blocks.
+__device__ __forceinline__ void sh_chunk(const sh_raw &r, const uint8_t *act_lds, const float *xs_lds,
+                                         uint32_t kh, uint32_t col, float (*acc)[16]) {
+    const uint8_t *a_lane = act_lds + col * SH_RS + 32u * kh;
+    const float *x_lane = xs_lds + 4u * kh;
+#pragma unroll
+    for (uint32_t j = 0; j < SH_CB; j++) {
+        typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+        const u4 t0 = {r.w[j][0], r.w[j][1], r.w[j][2], r.w[j][3]};
+        const u4 t1 = {r.w[j][4], r.w[j][5], r.w[j][6], r.w[j][7]};
+#pragma unroll
+        for (uint32_t i = 0; i < SH_TB; i++) {
+            const uint8_t *ap = a_lane + i * 32u * SH_RS + j * 64u;
+            f16v D = {};
+            D = __builtin_amdgcn_mfma_f32_32x32x16_f16(*(const h8 *)ap, __builtin_bit_cast(h8, t0), D, 0, 0, 0);
+            D = __builtin_amdgcn_mfma_f32_32x32x16_f16(*(const h8 *)(ap + 16), __builtin_bit_cast(h8, t1), D, 0, 0, 0);
+#pragma unroll
+            for (int jj = 0; jj < 4; jj++) {
+                const float4 xv = *(const float4 *)(x_lane + j * SH_T + 32u * i + 8u * jj);
+                const float xa[4] = {xv.x, xv.y, xv.z, xv.w};
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const float t = D[4 * jj + q] * r.s[j] * xa[q];
+                    acc[i][4 * jj + q] = acc[i][4 * jj + q] + t;
+                }
+            }
+        }
+    }
+}
+
+// GU: gate/up, 128 weight columns per workgroup = 16 gate + 16 up rows per
+// wave, epilogue mid = (g*sig(g))*u (shared clamp).  Otherwise down: 32
+// output rows per wave, out written directly.
+template <bool GU>
+__global__ void __launch_bounds__(256, 2) sh_gemm_kernel(sh_params p) {
+    __shared__ __align__(16) uint8_t s_act[2][SH_BUF];
+    __shared__ __align__(16) float s_xs[2][SH_CB * SH_T];
+    const uint32_t tt = blockIdx.x % p.n_tt, ct = blockIdx.x / p.n_tt;
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, kh = lane >> 5, col = lane & 31u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t t0 = tt * SH_T;
+    const uint32_t nb = p.nb, nchunk = nb / SH_CB;
+    // this lane's weight row
+    const uint32_t wcol = GU ? ct * 64u + 16u * wave + (col & 15u) : ct * 128u + 32u * wave + col;
+    const bool second = GU && col >= 16u;
+    const _Float16 *wrow = (second ? p.w1 : p.w0) + (uint64_t)wcol * nb * 32u;
+    const float *wsrow = (second ? p.ws1 : p.ws0) + (uint64_t)wcol * nb;
+    // DMA: wave w copies token rows 16w .. 16w+15 (one 256-byte row per dword load);
+    // xs: one dword load per block (lane = token)
+    const uint32_t tl = t0 + (lane < SH_T ? lane : 0u);
+    const uint32_t tok_dma = tl < p.n_tok ? tl : p.n_tok - 1u;
+    const uint32_t act_l = lds_addr(&s_act[0][0]), xs_l = lds_addr(&s_xs[0][0]);
+    auto issue = [&](uint32_t c) {
+        const uint32_t bf = c & 1u;
+#pragma unroll
+        for (uint32_t j = 0; j < 16u; j++) {
+            const uint32_t t = 16u * wave + j;
+            const uint32_t tr = t0 + t < p.n_tok ? t0 + t : p.n_tok - 1u;
+            lds_dma4(act_l + bf * SH_BUF + t * SH_RS, 4u * lane,
+                     (const uint8_t *)p.act + ((uint64_t)tr * nb + (uint64_t)c * SH_CB) * 64u);
+        }
+        lds_dma4(xs_l + bf * (SH_CB * SH_T * 4u) + wave * SH_T * 4u, tok_dma * nb * 4u,
+                 (const uint8_t *)p.xs + ((uint64_t)c * SH_CB + wave) * 4u);
+    };
+    float acc[SH_TB][16];
+#pragma unroll
+    for (uint32_t i = 0; i < SH_TB; i++)
+#pragma unroll
+        for (int r2 = 0; r2 < 16; r2++) acc[i][r2] = 0.0f;
+    sh_raw ra, rb;
+    issue(0);
+    sh_load(ra, wrow, wsrow, 0, kh);
+    const uint32_t last = nchunk - 1u;
+    for (uint32_t c = 0; c < nchunk; c += 2u) {
+        const uint32_t c1 = c + 1u < nchunk ? c + 1u : last, c2 = c + 2u < nchunk ? c + 2u : last;
+        wait_vm0();
+        sh_ready(ra);
+        __syncthreads();
+        issue(c1);
+        sh_load(rb, wrow, wsrow, c1, kh);
+        sh_chunk(ra, s_act[c & 1u], s_xs[c & 1u], kh, col, acc);
+        if (c + 1u < nchunk) {
+            wait_vm0();
+            sh_ready(rb);
+            __syncthreads();
+            issue(c2);
+            sh_load(ra, wrow, wsrow, c2, kh);
+            sh_chunk(rb, s_act[(c + 1u) & 1u], s_xs[(c + 1u) & 1u], kh, col, acc);
+        }
+    }
+    wait_vm0();
+#pragma unroll
+    for (uint32_t i = 0; i < SH_TB; i++) {
+#pragma unroll
+        for (int r2 = 0; r2 < 16; r2++) {
+            const uint32_t t = t0 + 32u * i + 8u * (r2 >> 2) + 4u * kh + (r2 & 3);
+            const float v = acc[i][r2];
+            if constexpr (GU) {
+                const float o = __shfl_xor(v, 16, 64);
+                if (col < 16u && t < p.n_tok) p.out0[(uint64_t)t * p.rows + wcol] = sf37_swiglu_mid(v, o, 1.0f, p.clamp);
+            } else {
+                if (t < p.n_tok) p.out0[(uint64_t)t * p.rows + wcol] = v;
+            }
+        }
+    }
+}
+
 uint32_t pf_grid(uint32_t max_tiles, uint32_t n_rt) { return 8u * ((max_tiles + 7u) / 8u) * n_rt; }
 
 }  // namespace
@@ -711,3 +921,64 @@ extern "C" int sf37k_pf_down(float *down_pair, const uint8_t *down_w, const void
     hipLaunchKernelGGL(pf_expert_kernel<false>, dim3(pf_grid(max_tiles, p.n_rt)), dim3(256), 0, (hipStream_t)s, p);
     return (int)hipGetLastError();
 }
+
+extern "C" int sf37k_sh_supported(uint32_t in_dim, uint32_t mid_dim, uint32_t out_dim) {
+    return in_dim % (32u * SH_CB * 2u) == 0 && mid_dim % (32u * SH_CB * 2u) == 0 && mid_dim % 64u == 0 &&
+           out_dim % 128u == 0 && in_dim > 0 && mid_dim > 0;
+}
+
+extern "C" int sf37k_sh_repack(void *w16, float *ws, const uint8_t *w, uint64_t rows, uint32_t in_dim,
+                               sf37_stream_t s) {
+    const uint64_t n = rows * (in_dim / 32u);
+    if (n == 0) return 0;
+    hipLaunchKernelGGL(sh_w16_kernel, dim3((unsigned)((n + 255u) / 256u)), dim3(256), 0, (hipStream_t)s,
+                       (_Float16 *)w16, ws, w, n);
+    return (int)hipGetLastError();
+}
+
+extern "C" int sf37k_sh_act(void *a16, float *xs, const float *x, uint32_t dim, uint32_t n_tok, sf37_stream_t s) {
+    const uint64_t n = (uint64_t)(dim / 32u) * n_tok;
+    if (n == 0) return 0;
+    hipLaunchKernelGGL(sh_act_kernel, dim3((unsigned)((n + 7u) / 8u)), dim3(256), 0, (hipStream_t)s,
+                       (_Float16 *)a16, xs, x, dim / 32u, (uint64_t)n_tok);
+    return (int)hipGetLastError();
+}
+
+extern "C" int sf37k_sh_gate_up(float *mid, const void *g16, const float *gs, const void *u16, const float *us,
+                                const void *a16, const float *xs, uint32_t n_tok, uint32_t in_dim,
+                                uint32_t mid_dim, float clamp, sf37_stream_t s) {
+    sh_params p = {};
+    p.out0 = mid;
+    p.w0 = (const _Float16 *)g16;
+    p.w1 = (const _Float16 *)u16;
+    p.ws0 = gs;
+    p.ws1 = us;
+    p.act = (const _Float16 *)a16;
+    p.xs = xs;
+    p.n_tok = n_tok;
+    p.nb = in_dim / 32u;
+    p.rows = mid_dim;
+    p.n_ct = mid_dim / 64u;
+    p.n_tt = (n_tok + SH_T - 1u) / SH_T;
+    p.clamp = clamp;
+    hipLaunchKernelGGL(sh_gemm_kernel<true>, dim3(p.n_ct * p.n_tt), dim3(256), 0, (hipStream_t)s, p);
+    return (int)hipGetLastError();
+}
+
+extern "C" int sf37k_sh_down(float *out, const void *d16, const float *ds, const void *a16, const float *xs,
+                             uint32_t n_tok, uint32_t mid_dim, uint32_t out_dim, sf37_stream_t s) {
+    sh_params p = {};
+    p.out0 = out;
+    p.w0 = (const _Float16 *)d16;
+    p.ws0 = ds;
+    p.act = (const _Float16 *)a16;
+    p.xs = xs;
+    p.n_tok = n_tok;
+    p.nb = mid_dim / 32u;
+    p.rows = out_dim;
+    p.n_ct = out_dim / 128u;
+    p.n_tt = (n_tok + SH_T - 1u) / SH_T;
+    hipLaunchKernelGGL(sh_gemm_kernel<false>, dim3(p.n_ct * p.n_tt), dim3(256), 0, (hipStream_t)s, p);
+    return (int)hipGetLastError();
+}
+

@@ -52,6 +52,7 @@ static int64_t g_opt_decode = 1;
 static int64_t g_opt_router_always = 0;
 static int64_t g_opt_prefill = 1;
 static int64_t g_opt_prefill_min_pairs = 256;
+static int64_t g_opt_shared_min_tok = 64;
 
 /* arrival counters of the fused decode kernels: zeroed once, left zero by
  * every completed launch */
@@ -90,7 +91,8 @@ static hipEvent_t g_prof_open;
 static const char *const k_stage_names[SF37_HIP_N_STAGES] = {
     "router", "select", "q8_0_act", "q8_0_gemm", "swiglu", "q8k_x", "dispatch",
     "gate_up", "q8k_mid", "down", "combine", "add", "other", "dec_route", "dec_up", "dec_down", "dec_select", "dec_combine", "dec_mid",
-    "pf_act_x", "pf_tiles", "pf_gate_up", "pf_act_mid", "pf_down"};
+    "pf_act_x", "pf_tiles", "pf_gate_up", "pf_act_mid", "pf_down",
+    "sh_repack", "sh_act", "sh_gate_up", "sh_down"};
 
 static void prof_begin(void) {
     if (!g_prof_on) return;
@@ -304,6 +306,7 @@ int sf37_hip_set_option(const char *name, int64_t value) {
     else if (!strcmp(name, "router_with_logits")) g_opt_router_always = value ? 1 : 0;
     else if (!strcmp(name, "prefill_mfma")) g_opt_prefill = value ? 1 : 0;
     else if (!strcmp(name, "prefill_min_pairs")) g_opt_prefill_min_pairs = value < 0 ? 0 : value;
+    else if (!strcmp(name, "shared_min_tokens")) g_opt_shared_min_tok = value < 0 ? 0 : value;
     else return 0;
     return 1;
 }
@@ -317,6 +320,7 @@ int64_t sf37_hip_get_option(const char *name) {
     if (!strcmp(name, "router_with_logits")) return g_opt_router_always;
     if (!strcmp(name, "prefill_mfma")) return g_opt_prefill;
     if (!strcmp(name, "prefill_min_pairs")) return g_opt_prefill_min_pairs;
+    if (!strcmp(name, "shared_min_tokens")) return g_opt_shared_min_tok;
     return -1;
 }
 
@@ -855,6 +859,45 @@ static int prefill_eligible(const routed_args *a, int slots) {
            (uint64_t)a->n_tok * a->in_dim * 2u < (1ull << 32) && pairs * a->mid_dim * 2u < (1ull << 32);
 }
 
+/* Shared expert on the matrix cores for prefill batches (k_prefill.hip):
+ * out = down(SwiGLU(gate x, up x)) with the Q8_0 arithmetic of
+ * sf37_ops.c:57-141, bit-identical to the q8_0_matmul path. */
+static int shared_mfma_eligible(uint32_t n_tok, uint32_t D, uint32_t F) {
+    return g_opt_prefill && n_tok >= (uint64_t)g_opt_shared_min_tok && sf37k_sh_supported(D, F, D) &&
+           (uint64_t)n_tok * D * 2u < (1ull << 32) && (uint64_t)n_tok * F * 2u < (1ull << 32);
+}
+
+static int shared_mfma(float *out, float *mid, const uint8_t *gw, const uint8_t *uw, const uint8_t *dw, uint32_t D,
+                       uint32_t F, const float *x, uint32_t n_tok, float clamp) {
+    if (!aligned4(x) || !aligned4(out) || !aligned4(mid)) return 0;
+    const uint64_t wb = (uint64_t)F * D * 2u, sb = (uint64_t)F * (D / 32u) * 4u;
+    const uint64_t maxd = D > F ? D : F;
+    const uint64_t ab = (uint64_t)n_tok * maxd * 2u, xb = (uint64_t)n_tok * (maxd / 32u) * 4u;
+    uint64_t off = 0, o_g, o_u, o_d, o_gs, o_us, o_ds, o_a, o_x;
+    o_g = off; off = align256(off + wb);
+    o_u = off; off = align256(off + wb);
+    o_d = off; off = align256(off + wb);
+    o_gs = off; off = align256(off + sb);
+    o_us = off; off = align256(off + sb);
+    o_ds = off; off = align256(off + sb);
+    o_a = off; off = align256(off + ab);
+    o_x = off; off = align256(off + xb);
+    char *s = scratch_get(off, "shared expert scratch");
+    if (!s) return 0;
+    const sf37_stream_t st = (sf37_stream_t)g_stream;
+    float *gs = (float *)(s + o_gs), *us = (float *)(s + o_us), *ds = (float *)(s + o_ds), *xs = (float *)(s + o_x);
+    return LAUNCH(SF37_HIP_STAGE_SH_REPACK, sf37k_sh_repack(s + o_g, gs, gw, F, D, st), "shared repack launch") &&
+           LAUNCH(SF37_HIP_STAGE_SH_REPACK, sf37k_sh_repack(s + o_u, us, uw, F, D, st), "shared repack launch") &&
+           LAUNCH(SF37_HIP_STAGE_SH_REPACK, sf37k_sh_repack(s + o_d, ds, dw, D, F, st), "shared repack launch") &&
+           LAUNCH(SF37_HIP_STAGE_SH_ACT, sf37k_sh_act(s + o_a, xs, x, D, n_tok, st), "shared activation launch") &&
+           LAUNCH(SF37_HIP_STAGE_SH_GATE_UP, sf37k_sh_gate_up(mid, s + o_g, gs, s + o_u, us, s + o_a, xs, n_tok, D, F,
+                                                             clamp, st),
+                  "shared gate/up launch") &&
+           LAUNCH(SF37_HIP_STAGE_SH_ACT, sf37k_sh_act(s + o_a, xs, mid, F, n_tok, st), "shared mid activation launch") &&
+           LAUNCH(SF37_HIP_STAGE_SH_DOWN, sf37k_sh_down(out, s + o_d, ds, s + o_a, xs, n_tok, F, D, st),
+                  "shared down launch");
+}
+
 /* Matrix-core pipeline (k_prefill.hip): x to fp16 MFMA codes, dispatch,
  * tiles, gate/up + SwiGLU*w, mid to fp16 MFMA codes, down, combine. */
 static int routed_pf(const routed_args *a, const routed_scratch *s, float *out, float *mid, float *down_pair,
@@ -1319,7 +1362,12 @@ int sf37_hip_moe_layer(sf37_hip_tensor *out, sf37_hip_tensor *selected, sf37_hip
                    "moe_layer router_select launch"))
         return 0;
     /* shared expert: Q8_0 gate/up pair -> SwiGLU -> Q8_0 down into out */
-    if (!q8_0_run(sh, sh + (uint64_t)n_tok * F, (const uint8_t *)w->sh_gate->ptr, (const uint8_t *)w->sh_up->ptr, D,
+    if (shared_mfma_eligible(n_tok, D, F)) {
+        if (!shared_mfma((float *)out->ptr, sh + 2u * (uint64_t)n_tok * F, (const uint8_t *)w->sh_gate->ptr,
+                         (const uint8_t *)w->sh_up->ptr, (const uint8_t *)w->sh_down->ptr, D, F, (const float *)x->ptr,
+                         n_tok, w->clamp_shared))
+            return 0;
+    } else if (!q8_0_run(sh, sh + (uint64_t)n_tok * F, (const uint8_t *)w->sh_gate->ptr, (const uint8_t *)w->sh_up->ptr, D,
                   F, (const float *)x->ptr, n_tok) ||
         !LAUNCH(SF37_HIP_STAGE_SWIGLU, sf37k_swiglu(sh + 2u * (uint64_t)n_tok * F, sh, sh + (uint64_t)n_tok * F, (uint64_t)n_tok * F,
                                 w->clamp_shared, st),

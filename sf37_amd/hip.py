@@ -103,7 +103,7 @@ _SIGS = {
     "sf37_hip_profile_stage_name": (C.c_char_p, [u32]),
 }
 
-N_STAGES = 24
+N_STAGES = 28
 
 
 def profile_read() -> dict:

@@ -176,3 +176,31 @@ def test_config3_layer_sample_vs_oracle(H, O, layer):
                                     clamp_shared=layer.clamp_shared)
     assert np.array_equal(sel[idx], wsel)
     assert_bitexact(out[idx], want, "config 3 sample")
+
+
+@pytest.mark.parametrize("n_tok", [77, 300])
+def test_layer_mfma_equals_staged(H, layer, n_tok):
+    """Whole layer (router on the device, shared expert and routed experts on
+    the matrix cores) against the dot-product kernels (prefill_mfma=0), bit for
+    bit; token counts that leave partial 32- and 64-token tiles."""
+    from sf37_amd import moe
+    rng = np.random.default_rng(300 + n_tok)
+    x = rng.standard_normal((n_tok, K)).astype(np.float32)
+    res = []
+    for mfma in (1, 0):
+        H.set_option("prefill_mfma", mfma)
+        H.lib().sf37_hip_profile_enable(1)
+        H.profile_read()
+        try:
+            xt = H.Tensor.from_array(x)
+            out, sel, w = H.Tensor.alloc(n_tok * K * 4), H.Tensor.alloc(n_tok * 32), H.Tensor.alloc(n_tok * 32)
+            moe.moe_layer(layer, xt, n_tok, out, sel, w, None)
+            prof = H.profile_read()
+        finally:
+            H.lib().sf37_hip_profile_enable(0)
+            H.set_option("prefill_mfma", 1)
+        ran = prof["sh_gate_up"][1] + prof["pf_gate_up"][1]
+        assert ran == (2 if mfma else 0), f"matrix-core kernels ran {ran} times with prefill_mfma={mfma}"
+        res.append((out.read(np.float32), sel.read(np.int32)))
+    assert np.array_equal(res[0][1], res[1][1])
+    assert_bitexact(res[0][0], res[1][0], f"layer out, {n_tok} tokens")
