@@ -34,10 +34,11 @@ namespace {
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef float f16v __attribute__((ext_vector_type(16)));
 
-constexpr uint32_t PF_T = 128;          // pairs per tile
+constexpr uint32_t PF_T = 64;           // pairs per tile
 constexpr uint32_t PF_TB = PF_T / 32u;  // 32-pair MFMA blocks per tile
-constexpr uint32_t PF_GU_R = 64;        // F rows (gate and up) per gate/up workgroup
-constexpr uint32_t PF_DN_R = 128;       // output rows per down workgroup
+constexpr uint32_t PF_WAVES = 8;        // waves per workgroup (two per SIMD), 32 weight columns each
+constexpr uint32_t PF_GU_R = 128;       // F rows (gate and up) per gate/up workgroup
+constexpr uint32_t PF_DN_R = 256;       // output rows per down workgroup
 constexpr uint32_t PF_TAB = 8;          // floats per (row, block) table entry: C0..C3, d
 // LDS layout of one activation block: 4 groups of 32 tile slots; in a group
 // slot t (0..31) starts at PF_RS * (t % 16) + 512 * (t / 16), so one 64-lane
@@ -328,15 +329,6 @@ __device__ __forceinline__ uint32_t hdr_zp(const uint32_t *h, int g) {
     return (h[a >> 5] >> (a & 31)) & 0xffu;
 }
 
-// Running sums live in AGPRs (the VGPRs hold the block sums, MFMA
-// accumulators and operands); acc = fma(d, blk, acc) goes through a VGPR.
-__device__ __forceinline__ void acc_fma_agpr(float &acc, float d, float b) {
-    float t;
-    asm("v_accvgpr_read_b32 %1, %0\n\tv_fma_f32 %1, %2, %3, %1\n\tv_accvgpr_write_b32 %0, %1"
-        : "+a"(acc), "=&v"(t)
-        : "v"(d), "v"(b));
-}
-
 // Q3 / Q2 dequantisation of part (0: pair words 0..7, 1: words 8..15) of group g.
 template <bool Q3, int SH, int PART, typename RAW>
 __device__ __forceinline__ void pf_dequant(const RAW &r, int g, uint32_t out[16]) {
@@ -443,10 +435,10 @@ __device__ __forceinline__ void pf_block(const RAW &r, const uint8_t *act_lds, c
 #pragma unroll
         for (int jj = 0; jj < 4; jj++) {
             const float4 d = *(const float4 *)(c_lane + 4 * PF_T + 32 * i + 8 * jj);
-            acc_fma_agpr(acc[i][4 * jj], d.x, blk[i][4 * jj]);
-            acc_fma_agpr(acc[i][4 * jj + 1], d.y, blk[i][4 * jj + 1]);
-            acc_fma_agpr(acc[i][4 * jj + 2], d.z, blk[i][4 * jj + 2]);
-            acc_fma_agpr(acc[i][4 * jj + 3], d.w, blk[i][4 * jj + 3]);
+            acc[i][4 * jj] = __builtin_fmaf(d.x, blk[i][4 * jj], acc[i][4 * jj]);
+            acc[i][4 * jj + 1] = __builtin_fmaf(d.y, blk[i][4 * jj + 1], acc[i][4 * jj + 1]);
+            acc[i][4 * jj + 2] = __builtin_fmaf(d.z, blk[i][4 * jj + 2], acc[i][4 * jj + 2]);
+            acc[i][4 * jj + 3] = __builtin_fmaf(d.w, blk[i][4 * jj + 3], acc[i][4 * jj + 3]);
         }
     }
 }
@@ -462,7 +454,7 @@ __device__ __forceinline__ void pf_body(const pf_params &p, const uint8_t *wrow,
                                         uint32_t wcol, uint32_t cnt);
 
 template <bool Q3>
-__global__ void __launch_bounds__(256, 1) pf_expert_kernel(pf_params p) {
+__global__ void __launch_bounds__(PF_WAVES * 64, 1) pf_expert_kernel(pf_params p) {
     __shared__ __align__(16) uint8_t s_act[2][PF_ACT_BUF];
     __shared__ __align__(16) float s_cd[2][5 * PF_T];
     __shared__ uint32_t s_pair[PF_T];
@@ -481,58 +473,48 @@ __global__ void __launch_bounds__(256, 1) pf_expert_kernel(pf_params p) {
         s_pair[tid] = pr;
         if (Q3) s_w[tid] = p.weights[pr];
     }
-    // activation rows: tile slots `lane` and 64 + lane for the tables; slot
-    // 32*wave + lane (lanes 0..31) for the codes (pad slots repeat the last pair)
-    uint32_t voff_t[2], rowoff_c;
-#pragma unroll
-    for (int h = 0; h < 2; h++) {
-        const uint32_t sl = 64u * h + lane;
-        const uint32_t pr = p.sorted[p0 + (sl < cnt ? sl : cnt - 1u)];
-        const uint32_t row = Q3 ? pr / p.topk : pr;
-        voff_t[h] = row * nblk * (PF_TAB * 4u);
+    // activation rows: tile slot `lane` for the tables; slot 32*(wave/4) + lane%32
+    // for the codes (pad slots repeat the last pair)
+    const uint32_t gi = wave >> 2, wq = wave & 3u;
+    uint32_t voff_t, rowoff_c;
+    {
+        const uint32_t pr = p.sorted[p0 + (lane < cnt ? lane : cnt - 1u)];
+        voff_t = (Q3 ? pr / p.topk : pr) * nblk * (PF_TAB * 4u);
     }
     {
-        const uint32_t sl = 32u * wave + (lane & 31u);
+        const uint32_t sl = 32u * gi + (lane & 31u);
         const uint32_t pr = p.sorted[p0 + (sl < cnt ? sl : cnt - 1u)];
         rowoff_c = (Q3 ? pr / p.topk : pr) * nblk * (SF37_QK * 2u);
     }
     const uint32_t act_l = lds_addr(&s_act[0][0]), cd_l = lds_addr(&s_cd[0][0]);
-    // codes: wave w copies tile slots 32w .. 32w+31, one load per slot pair
-    // (t, t + 16): lanes 0..31 read slot t's 512-byte row, lanes 32..63 slot t + 16's
+    // codes: waves 4*gi .. 4*gi+3 copy slot group gi; wave 4*gi + q loads slot
+    // pairs (t, t + 16), t = 4q .. 4q+3: lanes 0..31 read slot t's 512-byte
+    // row, lanes 32..63 slot t + 16's
     // slice `part` of `nparts` (compile-time after inlining) of block b's loads
     auto issue_act = [&](uint32_t b, int part, int nparts) {
         const uint32_t bf = b & 1u;
         const uint8_t *cb = (const uint8_t *)p.act + (uint64_t)b * (SF37_QK * 2u);
-        const int j0 = 16 * part / nparts, j1 = 16 * (part + 1) / nparts;
+        const int j0 = 4 * part / nparts, j1 = 4 * (part + 1) / nparts;
 #pragma unroll
         for (int j = j0; j < j1; j++) {
-            const uint32_t r0 = (uint32_t)__builtin_amdgcn_readlane((int)rowoff_c, j);
-            const uint32_t r1 = (uint32_t)__builtin_amdgcn_readlane((int)rowoff_c, j + 16);
-            lds_dma16(act_l + bf * PF_ACT_BUF + wave * PF_GRP + (uint32_t)j * PF_RS, (kh ? r1 : r0) + 16u * col, cb);
+            const uint32_t t = 4u * wq + (uint32_t)j;
+            const uint32_t r0 = (uint32_t)__builtin_amdgcn_readlane((int)rowoff_c, (int)t);
+            const uint32_t r1 = (uint32_t)__builtin_amdgcn_readlane((int)rowoff_c, (int)t + 16);
+            lds_dma16(act_l + bf * PF_ACT_BUF + gi * PF_GRP + t * PF_RS, (kh ? r1 : r0) + 16u * col, cb);
         }
-        if (part == 0) {
+        if (part == 0 && wave < 5u) {   // tables: wave a loads C_a (a < 4) or d (a = 4) of all slots
             const uint8_t *tb = (const uint8_t *)p.tab + (uint64_t)b * (PF_TAB * 4u);
-#pragma unroll
-            for (uint32_t j = 0; j < 3u; j++) {
-                const uint32_t it = wave + 4u * j;
-                if (it < 10u) {
-                    const uint32_t a = it >> 1, h = it & 1u;
-                    lds_dma4(cd_l + bf * (5u * PF_T * 4u) + (a * PF_T + 64u * h) * 4u, voff_t[h], tb + 4u * a);
-                }
-            }
+            lds_dma4(cd_l + bf * (5u * PF_T * 4u) + wave * PF_T * 4u, voff_t, tb + 4u * wave);
         }
     };
     // this lane's weight row
     const uint32_t wcol = Q3 ? rt * PF_GU_R + 16u * wave + (col & 15u) : rt * PF_DN_R + 32u * wave + col;
+    static_assert(PF_GU_R == 16u * PF_WAVES && PF_DN_R == 32u * PF_WAVES, "32 columns per wave");
     const uint32_t blk_bytes = Q3 ? SF37_Q3_BYTES : SF37_Q2_BYTES;
     const uint64_t row_bytes = (uint64_t)nblk * blk_bytes;
     const uint8_t *wrow = (Q3 && col >= 16u ? p.w1 : p.w0) + ((uint64_t)e * p.out_rows + wcol) * row_bytes;
-    switch (ntb) {
-        case 1: pf_body<Q3, 1>(p, wrow, issue_act, s_act, s_cd, s_pair, s_w, kh, col, wcol, cnt); break;
-        case 2: pf_body<Q3, 2>(p, wrow, issue_act, s_act, s_cd, s_pair, s_w, kh, col, wcol, cnt); break;
-        case 3: pf_body<Q3, 3>(p, wrow, issue_act, s_act, s_cd, s_pair, s_w, kh, col, wcol, cnt); break;
-        default: pf_body<Q3, 4>(p, wrow, issue_act, s_act, s_cd, s_pair, s_w, kh, col, wcol, cnt); break;
-    }
+    if (ntb == 1) pf_body<Q3, 1>(p, wrow, issue_act, s_act, s_cd, s_pair, s_w, kh, col, wcol, cnt);
+    else pf_body<Q3, 2>(p, wrow, issue_act, s_act, s_cd, s_pair, s_w, kh, col, wcol, cnt);
 }
 
 // Main loop and epilogue for NTB 32-pair blocks (the tile's pair count rounded up).
@@ -857,7 +839,7 @@ extern "C" uint32_t sf37k_pf_max_tiles(uint32_t n_pairs, uint32_t max_groups) {
 
 extern "C" int sf37k_pf_supported(uint32_t in_dim, uint32_t mid_dim, uint32_t out_dim) {
     return in_dim % SF37_QK == 0 && mid_dim % SF37_QK == 0 && mid_dim % PF_GU_R == 0 &&
-           out_dim % PF_DN_R == 0 && in_dim > 0 && mid_dim > 0;
+           out_dim % PF_DN_R == 0 && in_dim > 0 && mid_dim > 0;   // 32 weight columns per wave
 }
 
 extern "C" int sf37k_pf_act(int q3, void *codes_v, float *tab, const float *x, uint32_t dim,
@@ -901,7 +883,7 @@ extern "C" int sf37k_pf_gate_up(float *mid, float *gate_out, float *up_out, cons
     p.out_rows = mid_dim;
     p.n_rt = mid_dim / PF_GU_R;
     p.clamp = clamp;
-    hipLaunchKernelGGL(pf_expert_kernel<true>, dim3(pf_grid(max_tiles, p.n_rt)), dim3(256), 0, (hipStream_t)s, p);
+    hipLaunchKernelGGL(pf_expert_kernel<true>, dim3(pf_grid(max_tiles, p.n_rt)), dim3(PF_WAVES * 64), 0, (hipStream_t)s, p);
     return (int)hipGetLastError();
 }
 
@@ -918,7 +900,7 @@ extern "C" int sf37k_pf_down(float *down_pair, const uint8_t *down_w, const void
     p.nblk = mid_dim / SF37_QK;
     p.out_rows = out_dim;
     p.n_rt = out_dim / PF_DN_R;
-    hipLaunchKernelGGL(pf_expert_kernel<false>, dim3(pf_grid(max_tiles, p.n_rt)), dim3(256), 0, (hipStream_t)s, p);
+    hipLaunchKernelGGL(pf_expert_kernel<false>, dim3(pf_grid(max_tiles, p.n_rt)), dim3(PF_WAVES * 64), 0, (hipStream_t)s, p);
     return (int)hipGetLastError();
 }
 
