@@ -182,6 +182,26 @@ __global__ void __launch_bounds__(1024) pf_tiles_kernel(uint32_t *__restrict__ t
 }
 
 // ---------------------------------------------------------------------------
+// Tables in dispatch order: tabs[(b * 5 + a) * stride + s] = tab[row(s)][b][a]
+// for sorted position s (row = pair / div: the token for x, the pair for the
+// mid), a = C0..C3, d.  A tile's entries are then contiguous.
+// ---------------------------------------------------------------------------
+__global__ void __launch_bounds__(256) pf_tab_sort_kernel(float *__restrict__ tabs, const float *__restrict__ tab,
+                                                          const uint32_t *__restrict__ sorted, uint32_t n_pairs,
+                                                          uint32_t nblk, uint32_t div, uint32_t stride) {
+    const uint32_t s = blockIdx.x * 256u + threadIdx.x, b = blockIdx.y;
+    if (s >= n_pairs) return;
+    const float *t = tab + ((uint64_t)(sorted[s] / div) * nblk + b) * PF_TAB;
+    const float4 c = *(const float4 *)t;
+    float *o = tabs + (uint64_t)b * 5u * stride + s;
+    o[0] = c.x;
+    o[(uint64_t)stride] = c.y;
+    o[2ull * stride] = c.z;
+    o[3ull * stride] = c.w;
+    o[4ull * stride] = t[4];
+}
+
+// ---------------------------------------------------------------------------
 // LDS direct loads (global -> LDS, no registers).  Issued through inline asm
 // so the compiler does not wait for them before unrelated LDS reads; the
 // kernel waits with s_waitcnt vmcnt(0) + barrier before reading the buffer.
@@ -220,11 +240,11 @@ struct pf_params {
     float *mid, *gate_out, *up_out, *down_pair;
     const uint8_t *w0, *w1;        // gate / up (Q3) or down (Q2)
     const _Float16 *act;           // [rows][nblk * 256] codes in MFMA order
-    const float *tab;              // [rows][nblk][PF_TAB]
+    const float *tab;              // [nblk][5][tab_stride] tables in dispatch order
     const uint32_t *tiles;
     const uint32_t *sorted;
     const float *weights;
-    uint32_t topk, nblk, out_rows, n_rt;
+    uint32_t topk, nblk, out_rows, n_rt, tab_stride;
     float clamp;
 };
 
@@ -449,14 +469,14 @@ __device__ __forceinline__ void pf_block(const RAW &r, const uint8_t *act_lds, c
 // 128 output rows, 32 per wave; epilogue down_pair[pair][row].
 template <bool Q3, int NTB, typename ISSUE>
 __device__ __forceinline__ void pf_body(const pf_params &p, const uint8_t *wrow, ISSUE &issue_act,
-                                        uint8_t (*s_act)[PF_ACT_BUF], float (*s_cd)[5 * PF_T],
+                                        uint8_t (*s_act)[PF_ACT_BUF], float (*s_cd)[PF_WAVES * PF_T],
                                         const uint32_t *s_pair, const float *s_w, uint32_t kh, uint32_t col,
                                         uint32_t wcol, uint32_t cnt);
 
 template <bool Q3>
 __global__ void __launch_bounds__(PF_WAVES * 64, 1) pf_expert_kernel(pf_params p) {
     __shared__ __align__(16) uint8_t s_act[2][PF_ACT_BUF];
-    __shared__ __align__(16) float s_cd[2][5 * PF_T];
+    __shared__ __align__(16) float s_cd[2][PF_WAVES * PF_T];
     __shared__ uint32_t s_pair[PF_T];
     __shared__ float s_w[PF_T];
     const uint32_t wg = blockIdx.x, xcd = wg & 7u, slot = wg >> 3;
@@ -476,11 +496,7 @@ __global__ void __launch_bounds__(PF_WAVES * 64, 1) pf_expert_kernel(pf_params p
     // activation rows: tile slot `lane` for the tables; slot 32*(wave/4) + lane%32
     // for the codes (pad slots repeat the last pair)
     const uint32_t gi = wave >> 2, wq = wave & 3u;
-    uint32_t voff_t, rowoff_c;
-    {
-        const uint32_t pr = p.sorted[p0 + (lane < cnt ? lane : cnt - 1u)];
-        voff_t = (Q3 ? pr / p.topk : pr) * nblk * (PF_TAB * 4u);
-    }
+    uint32_t rowoff_c;
     {
         const uint32_t sl = 32u * gi + (lane & 31u);
         const uint32_t pr = p.sorted[p0 + (sl < cnt ? sl : cnt - 1u)];
@@ -502,9 +518,11 @@ __global__ void __launch_bounds__(PF_WAVES * 64, 1) pf_expert_kernel(pf_params p
             const uint32_t r1 = (uint32_t)__builtin_amdgcn_readlane((int)rowoff_c, (int)t + 16);
             lds_dma16(act_l + bf * PF_ACT_BUF + gi * PF_GRP + t * PF_RS, (kh ? r1 : r0) + 16u * col, cb);
         }
-        if (part == 0 && wave < 5u) {   // tables: wave a loads C_a (a < 4) or d (a = 4) of all slots
-            const uint8_t *tb = (const uint8_t *)p.tab + (uint64_t)b * (PF_TAB * 4u);
-            lds_dma4(cd_l + bf * (5u * PF_T * 4u) + wave * PF_T * 4u, voff_t, tb + 4u * wave);
+        if (part == 0) {   // tables: wave a < 5 loads C_a (a < 4) or d (a = 4) of all slots;
+                           // waves 5..7 fill spare rows (no branch inside the stage)
+            const uint32_t a = wave < 5u ? wave : 4u;
+            const float *tb = p.tab + ((uint64_t)b * 5u + a) * p.tab_stride + p0;
+            lds_dma4(cd_l + bf * (PF_WAVES * PF_T * 4u) + wave * PF_T * 4u, 4u * lane, tb);
         }
     };
     // this lane's weight row
@@ -520,7 +538,7 @@ __global__ void __launch_bounds__(PF_WAVES * 64, 1) pf_expert_kernel(pf_params p
 // Main loop and epilogue for NTB 32-pair blocks (the tile's pair count rounded up).
 template <bool Q3, int NTB, typename ISSUE>
 __device__ __forceinline__ void pf_body(const pf_params &p, const uint8_t *wrow, ISSUE &issue_act,
-                                        uint8_t (*s_act)[PF_ACT_BUF], float (*s_cd)[5 * PF_T],
+                                        uint8_t (*s_act)[PF_ACT_BUF], float (*s_cd)[PF_WAVES * PF_T],
                                         const uint32_t *s_pair, const float *s_w, uint32_t kh, uint32_t col,
                                         uint32_t wcol, uint32_t cnt) {
     const uint32_t nblk = p.nblk;
@@ -856,6 +874,17 @@ extern "C" int sf37k_pf_act(int q3, void *codes_v, float *tab, const float *x, u
     return (int)hipGetLastError();
 }
 
+extern "C" uint32_t sf37k_pf_tab_stride(uint32_t n_pairs) { return (n_pairs + PF_T + 63u) & ~63u; }
+
+extern "C" int sf37k_pf_tab_sort(float *tabs, const float *tab, const uint32_t *sorted_pairs, uint32_t n_pairs,
+                                 uint32_t dim, uint32_t div, sf37_stream_t s) {
+    const uint32_t nblk = dim / SF37_QK;
+    if (n_pairs == 0) return 0;
+    hipLaunchKernelGGL(pf_tab_sort_kernel, dim3((n_pairs + 255u) / 256u, nblk), dim3(256), 0, (hipStream_t)s, tabs,
+                       tab, sorted_pairs, n_pairs, nblk, div, sf37k_pf_tab_stride(n_pairs));
+    return (int)hipGetLastError();
+}
+
 extern "C" int sf37k_pf_tiles(uint32_t *tiles, const uint32_t *group_info, uint32_t max_groups,
                               sf37_stream_t s) {
     hipLaunchKernelGGL(pf_tiles_kernel, dim3(1), dim3(1024), 0, (hipStream_t)s, tiles, group_info, max_groups);
@@ -865,8 +894,8 @@ extern "C" int sf37k_pf_tiles(uint32_t *tiles, const uint32_t *group_info, uint3
 extern "C" int sf37k_pf_gate_up(float *mid, float *gate_out, float *up_out, const uint8_t *gate_w,
                                 const uint8_t *up_w, const void *act, const float *tab,
                                 const uint32_t *tiles, const uint32_t *sorted_pairs, const float *weights,
-                                uint32_t max_tiles, uint32_t topk, uint32_t in_dim, uint32_t mid_dim,
-                                float clamp, sf37_stream_t s) {
+                                uint32_t max_tiles, uint32_t tab_stride, uint32_t topk, uint32_t in_dim,
+                                uint32_t mid_dim, float clamp, sf37_stream_t s) {
     pf_params p = {};
     p.mid = mid;
     p.gate_out = gate_out;
@@ -882,6 +911,7 @@ extern "C" int sf37k_pf_gate_up(float *mid, float *gate_out, float *up_out, cons
     p.nblk = in_dim / SF37_QK;
     p.out_rows = mid_dim;
     p.n_rt = mid_dim / PF_GU_R;
+    p.tab_stride = tab_stride;
     p.clamp = clamp;
     hipLaunchKernelGGL(pf_expert_kernel<true>, dim3(pf_grid(max_tiles, p.n_rt)), dim3(PF_WAVES * 64), 0, (hipStream_t)s, p);
     return (int)hipGetLastError();
@@ -889,7 +919,7 @@ extern "C" int sf37k_pf_gate_up(float *mid, float *gate_out, float *up_out, cons
 
 extern "C" int sf37k_pf_down(float *down_pair, const uint8_t *down_w, const void *act, const float *tab,
                              const uint32_t *tiles, const uint32_t *sorted_pairs, uint32_t max_tiles,
-                             uint32_t mid_dim, uint32_t out_dim, sf37_stream_t s) {
+                             uint32_t tab_stride, uint32_t mid_dim, uint32_t out_dim, sf37_stream_t s) {
     pf_params p = {};
     p.down_pair = down_pair;
     p.w0 = down_w;
@@ -900,6 +930,7 @@ extern "C" int sf37k_pf_down(float *down_pair, const uint8_t *down_w, const void
     p.nblk = mid_dim / SF37_QK;
     p.out_rows = out_dim;
     p.n_rt = out_dim / PF_DN_R;
+    p.tab_stride = tab_stride;
     hipLaunchKernelGGL(pf_expert_kernel<false>, dim3(pf_grid(max_tiles, p.n_rt)), dim3(PF_WAVES * 64), 0, (hipStream_t)s, p);
     return (int)hipGetLastError();
 }

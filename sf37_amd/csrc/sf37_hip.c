@@ -815,6 +815,7 @@ typedef struct {
     float *mid, *down_pair;
     void *x16, *m16;        /* matrix-core path: fp16 codes in MFMA order */
     float *xtab, *mtab;     /* their per-block tables */
+    float *xtabs, *mtabs;   /* the tables in dispatch order */
     uint32_t *tiles;
 } routed_scratch;
 
@@ -836,6 +837,8 @@ static uint64_t routed_layout(const routed_args *a, int slots, int pf, int need_
         RESERVE(m16, void *, pairs * a->mid_dim * 2u);
         RESERVE(mtab, float *, pairs * (a->mid_dim / QK) * PF_TAB_BYTES);
         RESERVE(tiles, uint32_t *, ((uint64_t)sf37k_pf_max_tiles((uint32_t)pairs, (uint32_t)groups) + 1u) * 16u);
+        RESERVE(xtabs, float *, (uint64_t)(a->in_dim / QK) * 5u * sf37k_pf_tab_stride((uint32_t)pairs) * 4u);
+        RESERVE(mtabs, float *, (uint64_t)(a->mid_dim / QK) * 5u * sf37k_pf_tab_stride((uint32_t)pairs) * 4u);
     } else {
         RESERVE(xq, void *, (uint64_t)a->n_tok * (a->in_dim / QK) * Q8KB);
         RESERVE(midq, void *, pairs * (a->mid_dim / QK) * Q8KB);
@@ -906,20 +909,25 @@ static int routed_pf(const routed_args *a, const routed_scratch *s, float *out, 
     const uint32_t pairs = a->n_tok * a->topk;
     const uint32_t groups = a->n_expert;
     const uint32_t max_tiles = sf37k_pf_max_tiles(pairs, groups);
+    const uint32_t tstride = sf37k_pf_tab_stride(pairs);
     return LAUNCH(SF37_HIP_STAGE_PF_ACT_X, sf37k_pf_act(1, s->x16, s->xtab, a->x, a->in_dim, a->n_tok, st),
                   "routed_moe mfma input codes launch") &&
            LAUNCH(SF37_HIP_STAGE_DISPATCH, sf37k_moe_dispatch(s->ginfo, s->sorted, s->counts, s->offsets, a->selected,
                                                               pairs, a->n_expert, st),
                   "routed_moe dispatch launch") &&
            LAUNCH(SF37_HIP_STAGE_PF_TILES, sf37k_pf_tiles(s->tiles, s->ginfo, groups, st), "routed_moe tiles launch") &&
-           LAUNCH(SF37_HIP_STAGE_PF_GATE_UP, sf37k_pf_gate_up(mid, gate_out, up_out, a->gate_w, a->up_w, s->x16, s->xtab,
-                                                             s->tiles, s->sorted, a->weights, max_tiles, a->topk,
-                                                             a->in_dim, a->mid_dim, a->clamp, st),
+           LAUNCH(SF37_HIP_STAGE_PF_TILES, sf37k_pf_tab_sort(s->xtabs, s->xtab, s->sorted, pairs, a->in_dim, a->topk, st),
+                  "routed_moe input tables launch") &&
+           LAUNCH(SF37_HIP_STAGE_PF_GATE_UP, sf37k_pf_gate_up(mid, gate_out, up_out, a->gate_w, a->up_w, s->x16, s->xtabs,
+                                                             s->tiles, s->sorted, a->weights, max_tiles, tstride,
+                                                             a->topk, a->in_dim, a->mid_dim, a->clamp, st),
                   "routed_moe mfma gate/up launch") &&
            LAUNCH(SF37_HIP_STAGE_PF_ACT_MID, sf37k_pf_act(0, s->m16, s->mtab, mid, a->mid_dim, pairs, st),
                   "routed_moe mfma mid codes launch") &&
-           LAUNCH(SF37_HIP_STAGE_PF_DOWN, sf37k_pf_down(down_pair, a->down_w, s->m16, s->mtab, s->tiles, s->sorted,
-                                                       max_tiles, a->mid_dim, a->out_dim, st),
+           LAUNCH(SF37_HIP_STAGE_PF_ACT_MID, sf37k_pf_tab_sort(s->mtabs, s->mtab, s->sorted, pairs, a->mid_dim, 1u, st),
+                  "routed_moe mid tables launch") &&
+           LAUNCH(SF37_HIP_STAGE_PF_DOWN, sf37k_pf_down(down_pair, a->down_w, s->m16, s->mtabs, s->tiles, s->sorted,
+                                                       max_tiles, tstride, a->mid_dim, a->out_dim, st),
                   "routed_moe mfma down launch") &&
            LAUNCH(SF37_HIP_STAGE_COMBINE, sf37k_moe_combine(out, down_pair, a->topk, a->out_dim, a->n_tok, st),
                   "routed_moe combine launch");

@@ -105,13 +105,19 @@ int sf37k_pf_supported(uint32_t in_dim, uint32_t mid_dim, uint32_t out_dim);
 int sf37k_pf_act(int q3, void *codes, float *tab, const float *x, uint32_t dim, uint32_t n_rows,
                  sf37_stream_t s);
 int sf37k_pf_tiles(uint32_t *tiles, const uint32_t *group_info, uint32_t max_groups, sf37_stream_t s);
+/* The per-block tables gathered into dispatch order (floats:
+ * dim/256 x 5 x sf37k_pf_tab_stride(n_pairs)); row = pair / div. */
+uint32_t sf37k_pf_tab_stride(uint32_t n_pairs);
+int sf37k_pf_tab_sort(float *tabs, const float *tab, const uint32_t *sorted_pairs, uint32_t n_pairs, uint32_t dim,
+                      uint32_t div, sf37_stream_t s);
 int sf37k_pf_gate_up(float *mid, float *gate_out, float *up_out, const uint8_t *gate_w,
                      const uint8_t *up_w, const void *act, const float *tab, const uint32_t *tiles,
                      const uint32_t *sorted_pairs, const float *weights, uint32_t max_tiles,
-                     uint32_t topk, uint32_t in_dim, uint32_t mid_dim, float clamp, sf37_stream_t s);
+                     uint32_t tab_stride, uint32_t topk, uint32_t in_dim, uint32_t mid_dim, float clamp,
+                     sf37_stream_t s);
 int sf37k_pf_down(float *down_pair, const uint8_t *down_w, const void *act, const float *tab,
                   const uint32_t *tiles, const uint32_t *sorted_pairs, uint32_t max_tiles,
-                  uint32_t mid_dim, uint32_t out_dim, sf37_stream_t s);
+                  uint32_t tab_stride, uint32_t mid_dim, uint32_t out_dim, sf37_stream_t s);
 
 /* Shared expert (Q8_0) on the matrix cores for many tokens (k_prefill.hip):
  * repack weight rows to fp16 codes in MFMA lane order + float scales
