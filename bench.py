@@ -58,6 +58,10 @@ def parse():
                     help="only run 10 device-to-device copies of MIB MiB (calibrates the HBM counters)")
     ap.add_argument("--prefill-steps", type=int, default=5, help="timed layers per prefill config (0 = skip)")
     ap.add_argument("--prefill-only", action="store_true", help="only the prefill configs (2 and 3)")
+    ap.add_argument("--stack-layers", type=int, default=45, help="layers of the config 4 stack (0 = skip)")
+    ap.add_argument("--stack-steps", type=int, default=20, help="timed decode tokens through the stack")
+    ap.add_argument("--stack-prefill-steps", type=int, default=2, help="timed 2048-token chunks through the stack")
+    ap.add_argument("--stack-only", action="store_true", help="only the config 4 stack")
     return ap.parse_args()
 
 
@@ -120,9 +124,14 @@ def main():
     hip.init()
     H = Hip()
     n_tok, E, K, F, TOPK = 8, moe.EXPERTS, moe.EMBD, moe.EXPERT_FF, moe.EXPERT_USED
+    # the router GEMV/GEMM runs inside the layer although injected logits select
+    hip.set_option("router_with_logits", 1)
     if args.prefill_only:
         lay = moe.SynthLayer(seed=moe.layer_seed(args.seed, 0))
         print(json.dumps({"prefill": [prefill_bench(args, H, lay, c) for c in (3, 2)]}), flush=True)
+        return
+    if args.stack_only:
+        print(json.dumps({"stack": stack_bench(args, H)}), flush=True)
         return
 
     layers, xs, lgs, sels = [], [], [], []
@@ -136,8 +145,6 @@ def main():
     sel = hip.Tensor.alloc(n_tok * TOPK * 4)
     wts = hip.Tensor.alloc(n_tok * TOPK * 4)
     L = hip.lib()
-    # the router GEMV runs inside the layer although injected logits select
-    hip.set_option("router_with_logits", 1)
     structs = [lay.weights_struct() for lay in layers]
 
     def step(i):
@@ -210,10 +217,15 @@ def main():
     traffic = measured_traffic(kern)
 
     prefill = [prefill_bench(args, H, layers[0], c) for c in (3, 2)] if args.prefill_steps > 0 else None
+    for lay in layers:
+        lay.free()
+    stack = stack_bench(args, H) if args.stack_layers > 0 else None
 
     cpu = None
     if not args.no_cpu:
-        cpu = cpu_baseline(layers[0], xs[0], sels[0], step_bytes[0], n_tok, args.cpu_seconds)
+        cpu_layer = moe.SynthLayer(seed=moe.layer_seed(args.seed, 0))
+        cpu = cpu_baseline(cpu_layer, xs[0], sels[0], step_bytes[0], n_tok, args.cpu_seconds)
+        cpu_layer.free()
 
     stages = {k: {"ms_per_launch": round(v[0] / max(v[1], 1), 5), "launches": v[1]} for k, v in prof.items() if v[1]}
     line = {
@@ -241,6 +253,7 @@ def main():
         "cpu_baseline": cpu,
         "stages": stages,
         "prefill": prefill,
+        "stack": stack,
     }
     print(json.dumps(line), flush=True)
 
@@ -300,6 +313,83 @@ def prefill_bench(args, H, layer, config):
                             "dtype": "f16 operands holding exact small integers, fp32 accumulate"},
             "kernels": mfma, "max_pairs_per_expert": int(counts.max()), "idle_experts": int((counts == 0).sum()),
             "stage_ms": stages}
+
+
+def stack_bench(args, H):
+    """--stack-layers independently seeded layers resident
+    in HBM, h <- h + MoE_l(RMSNorm_l(h)) through all of them, Zipf-skewed
+    injected router logits (the router still runs).  Decode: one token through
+    the stack per step; prefill: one 2048-token chunk per step.  Each step
+    starts from its own input rows (a device copy into h, inside the step) and
+    steps rotate over two logits sets per layer.  HBM bytes per step = over
+    the layers, distinct selected experts x 6,225,920 + shared + router + norm
+    weights + the fp32 activation rows the norm, layer and add read and write
+    (7 x tokens x 16 KiB)."""
+    from sf37_amd import configs, hip, moe
+    t0 = time.time()
+    S = moe.SynthStack(master=moe.layer_seed(args.seed, 4000), n_layers=args.stack_layers)
+    hip.synchronize()
+    gen_s = time.time() - t0
+    print(f"stack: {S.n_layers} layers generated in {gen_s:.1f} s", file=sys.stderr, flush=True)
+    Lh = hip.lib()
+    K, TOPK, NL = S.in_dim, moe.EXPERT_USED, S.n_layers
+    lay0 = S.layers[0]
+    fixed = lay0.shared_bytes() + lay0.router_bytes() + K * 2
+    resident = NL * (lay0.n_expert * EXPERT_BYTES + fixed)
+    res = {"workload": "BASELINE configs[4]: MoE stack, RMSNorm(w+1) + residual between layers, Zipf routing",
+           "layers": NL, "resident_weight_bytes": int(resident), "generate_s": round(gen_s, 1)}
+    for mode, n_tok, steps in (("decode", 1, args.stack_steps), ("prefill", 2048, args.stack_prefill_steps)):
+        if steps <= 0:
+            continue
+        n_sets = 2
+        xs = [configs.x_device(4, 4000 + 10 * s + n_tok, n_tok) for s in range(n_sets)]
+        lgs = [[hip.Tensor.from_array(configs.logits_for(4, moe.layer_seed(4000 + 10 * s + n_tok, l), n_tok))
+                for l in range(NL)] for s in range(n_sets)]
+        sels = [hip.Tensor.alloc(n_tok * TOPK * 4) for _ in range(NL)]
+        h, xn, y = (hip.Tensor.alloc(n_tok * K * 4) for _ in range(3))
+        wts = hip.Tensor.alloc(n_tok * TOPK * 4)
+
+        def step(i):
+            s = i % n_sets
+            hip.check(Lh.sf37_hip_tensor_copy(h, 0, xs[s], 0, n_tok * K * 4), "stack input copy")
+            S.forward(h, n_tok, xn, y, sels, wts, lgs[s])
+
+        step_bytes = []
+        for s in range(n_sets):
+            step(s)
+            b = 0
+            for l in range(NL):
+                distinct = len(np.unique(sels[l].read(np.int32)))
+                b += distinct * EXPERT_BYTES + fixed + 7 * n_tok * K * 4
+            step_bytes.append(b)
+        H.sync()
+        a, b = H.event(), H.event()
+        H.record(a)
+        for i in range(steps):
+            step(i)
+        H.record(b)
+        ms = H.elapsed_ms(a, b) / steps
+        H.sync()
+        Lh.sf37_hip_profile_enable(1)
+        hip.profile_read()
+        for i in range(steps):
+            step(i)
+        prof = hip.profile_read()
+        Lh.sf37_hip_profile_enable(0)
+        mean_bytes = float(np.mean([step_bytes[i % n_sets] for i in range(steps)]))
+        gbs = mean_bytes / (ms * 1e-3) / 1e9
+        kern_ms = sum(v[0] for v in prof.values()) / steps
+        res[mode] = {"tokens": n_tok, "steps": steps, "ms_per_step": round(ms, 4),
+                     "tokens_per_s": round(n_tok / (ms * 1e-3), 1), "hbm_bytes_per_step": int(mean_bytes),
+                     "hbm_gbs": round(gbs, 1), "pct_of_hbm_peak": round(100.0 * gbs / HBM_PEAK_GBS, 2),
+                     "ms_per_layer": round(ms / NL, 4), "kernel_ms_per_step": round(kern_ms, 4),
+                     "stage_ms_per_step": {k: round(v[0] / steps, 4) for k, v in prof.items() if v[1]}}
+        print(f"stack {mode}: {res[mode]['tokens_per_s']} tokens/s, {res[mode]['hbm_gbs']} GB/s",
+              file=sys.stderr, flush=True)
+        for t in xs + [x for ls in lgs for x in ls] + sels + [h, xn, y, wts]:
+            t.free()
+    S.free()
+    return res
 
 
 def measured_traffic(kern):

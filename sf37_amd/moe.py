@@ -101,3 +101,54 @@ def moe_layer(layer: SynthLayer, x: Tensor, n_tok: int, out: Tensor, selected: T
     w = layer.weights_struct(scale)
     check(lib().sf37_hip_moe_layer(out.h, selected.h if selected else None, weights.h if weights else None,
                                    w, logits.h if logits else None, x.h, n_tok), "moe_layer")
+
+
+def bf16_bits(a: np.ndarray) -> np.ndarray:
+    """fp32 -> bf16 bit patterns, round to nearest even (finite inputs)."""
+    u = np.ascontiguousarray(a, np.float32).view(np.uint32).astype(np.uint64)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+class SynthStack:
+    """n_layers independently seeded layers (layer il
+    has seed layer_seed(master, il) and the SwiGLU clamps of layer il), each
+    preceded by RMSNorm with (w + 1) weights, bf16 w ~ N(0, 0.02), as the
+    engine's h <- h + MoE_l(RMSNorm_l(h)) (sf37.c:2243-2250).  The norm
+    weights of all layers sit in one device range registered under a model-map
+    key, read by the batched bf16 RMSNorm entry point."""
+
+    EPS = 1e-5       # sf37.c:61
+
+    def __init__(self, master: int, n_layers: int = 45, il0: int = 0, **layer_kw):
+        self.layers = [SynthLayer(seed=layer_seed(master, il0 + l), il=il0 + l, **layer_kw)
+                       for l in range(n_layers)]
+        K = self.layers[0].in_dim
+        self.in_dim, self.n_layers = K, n_layers
+        w = np.stack([hip.synth_normal(K, layer_seed(master, il0 + l), STREAM["norm"], sigma=0.02).read(np.float32)
+                      for l in range(n_layers)])
+        self.norm_bits = bf16_bits(w)                    # [n_layers][K] bf16
+        self.norm = Tensor.from_array(self.norm_bits)
+        self._key = np.zeros(64, np.uint8)               # host address used as the map key
+        check(lib().sf37_hip_register_device_range(self._key.ctypes.data, self.norm.nbytes, 0, self.norm.nbytes,
+                                                   self.norm.h), "register norm weights")
+
+    def rms_norm(self, out: Tensor, x: Tensor, layer: int, n_tok: int) -> None:
+        K = self.in_dim
+        check(lib().sf37_hip_rms_norm_weight1_bf16_batch_mapped(out.h, x.h, self._key.ctypes.data, self.norm.nbytes,
+                                                                layer * K * 2, K, n_tok, self.EPS), "rms_norm")
+
+    def forward(self, h: Tensor, n_tok: int, xn: Tensor, y: Tensor, sel=None, wts: Tensor | None = None,
+                logits=None) -> None:
+        """h <- h + MoE_l(RMSNorm_l(h)) for every layer; logits[l] (optional)
+        are injected router logits of layer l; sel is one selection buffer or
+        a list of one per layer."""
+        for l, lay in enumerate(self.layers):
+            self.rms_norm(xn, h, l, n_tok)
+            s = sel[l] if isinstance(sel, (list, tuple)) else sel
+            moe_layer(lay, xn, n_tok, y, s, wts, logits[l] if logits is not None else None)
+            check(lib().sf37_hip_add_inplace_f32(h.h, y.h, n_tok * self.in_dim), "add_inplace")
+
+    def free(self) -> None:
+        for lay in self.layers:
+            lay.free()
+        self.norm.free()
