@@ -274,6 +274,29 @@ int sf37_hip_moe_layer(sf37_hip_tensor *out, sf37_hip_tensor *selected,
                        const sf37_hip_tensor *logits_in, const sf37_hip_tensor *x,
                        uint32_t n_tok);
 
+/* The FFN block of an MoE decoder layer as the engine runs it
+ * (sf37.c:2243-2250): hidden += moe_layer(rms_norm_weight1_bf16(hidden)),
+ * the bf16 norm weights (in_dim of them) at norm_offset of a registered
+ * model map, eps as sf37_hip_rms_norm_weight1_bf16_mapped.  Up to 16 tokens
+ * the fused decode launches normalise and add the residual themselves (six
+ * launches per block); larger batches run rms_norm, the layer and the add.
+ * normed (optional) receives the normalised rows.  Same bits either way. */
+int sf37_hip_moe_block(sf37_hip_tensor *hidden, sf37_hip_tensor *normed,
+                       sf37_hip_tensor *selected, sf37_hip_tensor *weights,
+                       const sf37_hip_moe_layer_weights *w, const void *model_map,
+                       uint64_t model_size, uint64_t norm_offset, float eps,
+                       const sf37_hip_tensor *logits_in, uint32_t n_tok);
+
+/* n_layers consecutive blocks (the engine's layer loop, sf37.c:2243-2250 per
+ * layer) in one call: layers[l], norm weights at norm_offsets[l], injected
+ * logits logits[l] and selection outputs selected[l] when those arrays are
+ * given (entries may be NULL). */
+int sf37_hip_moe_stack(sf37_hip_tensor *hidden, uint32_t n_layers,
+                       const sf37_hip_moe_layer_weights *layers, const void *model_map,
+                       uint64_t model_size, const uint64_t *norm_offsets, float eps,
+                       const sf37_hip_tensor *const *logits,
+                       sf37_hip_tensor *const *selected, uint32_t n_tok);
+
 /* Stage timing with HIP events, the counterpart of the reference's
  * SF37_CUDA_MOE_PROFILE (sf37_cuda.cu:345-449).  While enabled, every kernel
  * the library launches is bracketed by events on the launch stream;

@@ -26,6 +26,7 @@
 // slot-order combines, so results equal the staged kernels bit for bit.
 #include "sf37_blocks.h"
 #include "sf37_router.h"
+#include "sf37_norm.h"
 #include "sf37_launch.h"
 
 namespace {
@@ -115,20 +116,41 @@ __device__ __forceinline__ float q8_0_lds(const uint8_t *base, uint32_t L, uint3
 // each expert's selection candidate per token (p = sigmoid, key of
 // p + bias).  Then workgroups quantising x (one 256-block of one token per
 // wave) to Q8_K for the routed experts and Q8_0 for the shared expert.
+// With NORM, x is the hidden state and every workgroup first forms the
+// RMSNorm scale of each token (sf37_rms_scale_wave, one wave per token);
+// the x values are normalised as they are loaded.
 __global__ void __launch_bounds__(256) dec_route_kernel(dec_params p, uint32_t n_rt) {
     __shared__ double part[RT_ROWS][DEC_MAX_TOK][4];
     __shared__ float s_logit[RT_ROWS][DEC_MAX_TOK];
+    __shared__ float s_scale[DEC_MAX_TOK];
     __shared__ uint64_t tab[32];
     const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
     const uint32_t nb = p.K / SF37_QK;
+    const bool norm = (p.flags & SF37_DEC_NORM) != 0u;
+    if (norm) {
+        for (uint32_t t = wave; t < p.T; t += 4u) {
+            const float sc = sf37_rms_scale_wave(p.x + (uint64_t)t * p.K, p.K, p.eps);
+            if (lane == 0) s_scale[t] = sc;
+        }
+        __syncthreads();
+    }
     if (blockIdx.x >= n_rt) {
         const uint32_t wq = (blockIdx.x - n_rt) * 4u + wave;
         if (wq >= p.T * nb) return;
         const uint32_t t = wq / nb, b = wq - t * nb;
-        const float *xb = p.x + (uint64_t)t * p.K + (uint64_t)b * SF37_QK + 4u * lane;
+        const uint32_t k0 = b * SF37_QK + 4u * lane;
+        const float *xb = p.x + (uint64_t)t * p.K + k0;
         float v[4];
 #pragma unroll
         for (int k = 0; k < 4; k++) v[k] = xb[k];
+        if (norm) {
+#pragma unroll
+            for (int k = 0; k < 4; k++) v[k] = sf37_norm_w1_bf16(v[k], s_scale[t], p.norm_w[k0 + k]);
+            if (p.xn) {
+#pragma unroll
+                for (int k = 0; k < 4; k++) p.xn[(uint64_t)t * p.K + k0 + k] = v[k];
+            }
+        }
         int8_t qk[4];
         int gsum;
         const float d = q8k_codes4(v, qk, gsum);
@@ -164,8 +186,16 @@ __global__ void __launch_bounds__(256) dec_route_kernel(dec_params p, uint32_t n
     const uint32_t e0 = blockIdx.x * RT_ROWS;
     if (p.flags & SF37_DEC_ROUTER) {
         const uint32_t nr = p.E - e0 < RT_ROWS ? p.E - e0 : RT_ROWS;
-        sf37_router_rows_n<RT_ROWS>(p.router_w + (uint64_t)e0 * p.K, nr, p.x, p.K, p.T,
-                                    [](uint32_t r, uint32_t t, uint32_t w, double v) { part[r][t][w] = v; });
+        const auto store = [](uint32_t r, uint32_t t, uint32_t w, double v) { part[r][t][w] = v; };
+        if (norm) {
+            const uint16_t *nw = p.norm_w;
+            sf37_router_rows_n<RT_ROWS>(p.router_w + (uint64_t)e0 * p.K, nr, p.x, p.K, p.T, store,
+                                        [nw](uint32_t t, uint32_t k, float v) {
+                                            return sf37_norm_w1_bf16(v, s_scale[t], nw[k]);
+                                        });
+        } else {
+            sf37_router_rows_n<RT_ROWS>(p.router_w + (uint64_t)e0 * p.K, nr, p.x, p.K, p.T, store);
+        }
         __syncthreads();
         if (threadIdx.x < RT_ROWS * p.T) {
             const uint32_t r = threadIdx.x / p.T, t = threadIdx.x - r * p.T;
@@ -930,7 +960,8 @@ __global__ void __launch_bounds__(256) dec_combine_kernel(dec_params p) {
 #pragma unroll
     for (int s = 0; s < 16; s++)
         if ((uint32_t)s < p.topk) acc = acc + v[s];
-    p.out[i] = (p.flags & SF37_DEC_SHARED) ? p.sh_out[i] + acc : acc;
+    const float y = (p.flags & SF37_DEC_SHARED) ? p.sh_out[i] + acc : acc;
+    p.out[i] = (p.flags & SF37_DEC_RESID) ? p.out[i] + y : y;
 }
 
 }  // namespace

@@ -1,7 +1,8 @@
 // k_elem.hip - elementwise ops for gfx950: SwiGLU with clamp (sf37_ops.c:30-42),
 // in-place add (sf37_cuda.cu:2137-2151) and RMSNorm with (w + 1) weights
-// (sf37_ops.c:22-28: binary64 sum of squares, scale = 1 / sqrtf(mean + eps)).
+// (sf37_ops.c:22-28, computed by sf37_norm.h).
 #include "sf37_dev.h"
+#include "sf37_norm.h"
 #include "sf37_launch.h"
 
 namespace {
@@ -21,25 +22,20 @@ __global__ void __launch_bounds__(256) add_kernel(float *__restrict__ dst,
     if (i < n) dst[i] = dst[i] + src[i];
 }
 
+// One wave per row (four rows per workgroup): sf37_rms_scale_wave, then
+// the weighted scale of every element.
 __global__ void __launch_bounds__(256) rms_norm_kernel(float *__restrict__ out,
                                                        const float *__restrict__ x,
                                                        const void *__restrict__ w, int bf16,
-                                                       uint32_t n, float eps) {
-    __shared__ double part[4];
-    const float *xr = x + (uint64_t)blockIdx.x * n;
-    float *orow = out + (uint64_t)blockIdx.x * n;
-    double ss = 0.0;
-    for (uint32_t i = threadIdx.x; i < n; i += 256u) ss += (double)xr[i] * (double)xr[i];
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
-    if ((threadIdx.x & 63u) == 0) part[threadIdx.x >> 6] = ss;
-    __syncthreads();
-    const double tot = (part[0] + part[1]) + (part[2] + part[3]);
-    const float scale = 1.0f / __builtin_sqrtf((float)(tot / (double)n) + eps);
-    for (uint32_t i = threadIdx.x; i < n; i += 256u) {
-        const float wf = bf16 ? __uint_as_float((uint32_t)((const uint16_t *)w)[i] << 16)
-                              : ((const float *)w)[i];
-        orow[i] = xr[i] * scale * (wf + 1.0f);
+                                                       uint32_t n, uint32_t n_rows, float eps) {
+    const uint32_t row = blockIdx.x * 4u + (threadIdx.x >> 6), lane = threadIdx.x & 63u;
+    if (row >= n_rows) return;
+    const float *xr = x + (uint64_t)row * n;
+    float *orow = out + (uint64_t)row * n;
+    const float scale = sf37_rms_scale_wave(xr, n, eps);
+    for (uint32_t i = lane; i < n; i += 64u) {
+        orow[i] = bf16 ? sf37_norm_w1_bf16(xr[i], scale, ((const uint16_t *)w)[i])
+                       : xr[i] * scale * (((const float *)w)[i] + 1.0f);
     }
 }
 
@@ -63,7 +59,7 @@ extern "C" int sf37k_add_inplace(float *dst, const float *src, uint64_t n, sf37_
 extern "C" int sf37k_rms_norm(float *out, const float *x, const void *w, int w_is_bf16, uint32_t n,
                               uint32_t n_tok, float eps, sf37_stream_t s) {
     if (n_tok == 0) return 0;
-    hipLaunchKernelGGL(rms_norm_kernel, dim3(n_tok), dim3(256), 0, (hipStream_t)s, out, x, w,
-                       w_is_bf16, n, eps);
+    hipLaunchKernelGGL(rms_norm_kernel, dim3((n_tok + 3u) / 4u), dim3(256), 0, (hipStream_t)s, out, x, w,
+                       w_is_bf16, n, n_tok, eps);
     return (int)hipGetLastError();
 }

@@ -988,6 +988,9 @@ typedef struct {
     float scale, clamp_shared;
     int32_t *sel;   /* selection output when SELECT (NULL = scratch) */
     float *wts;
+    const uint16_t *norm_w;  /* NORM: bf16 norm weights, epsilon, normalised rows (or NULL) */
+    float eps;
+    float *xn;
 } dec_extra;
 
 static uint32_t *dec_counters(uint64_t words) {
@@ -1125,6 +1128,10 @@ static int decode_run(const routed_args *a, const dec_extra *ex, float *out, flo
     }
     if ((ex->flags & SF37_DEC_ROUTER) && !p.router_w) return 0;
     if (sh && (!p.sh_gate || !p.sh_up || !p.sh_down)) return 0;
+    if ((ex->flags & SF37_DEC_NORM) && !ex->norm_w) return 0;
+    p.norm_w = ex->norm_w;
+    p.eps = ex->eps;
+    p.xn = ex->xn;
     p.cnt = cnt;
     const sf37_stream_t st = (sf37_stream_t)g_stream;
     return LAUNCH(SF37_HIP_STAGE_DEC_ROUTE, sf37k_decode_route(&p, st), "decode route launch") &&
@@ -1308,9 +1315,33 @@ int sf37_hip_moe_dispatch(sf37_hip_tensor *counts, sf37_hip_tensor *offsets, sf3
 /* Whole layer: scratch holds logits, selection, the shared expert's
  * activations and the routed output; the routed pipeline then takes the
  * scratch area, so everything it needs from here lives in ls[]. */
+/* The RMSNorm and residual of an FFN block around the layer (sf37_hip_moe_block). */
+typedef struct {
+    const uint16_t *norm_w;
+    float eps;
+    float *xn;
+} block_norm;
+
+static int moe_layer_impl(sf37_hip_tensor *out, sf37_hip_tensor *selected, sf37_hip_tensor *weights,
+                          const sf37_hip_moe_layer_weights *w, const sf37_hip_tensor *logits_in,
+                          const sf37_hip_tensor *x, uint32_t n_tok, const block_norm *bn);
+
 int sf37_hip_moe_layer(sf37_hip_tensor *out, sf37_hip_tensor *selected, sf37_hip_tensor *weights,
                        const sf37_hip_moe_layer_weights *w, const sf37_hip_tensor *logits_in,
                        const sf37_hip_tensor *x, uint32_t n_tok) {
+    return moe_layer_impl(out, selected, weights, w, logits_in, x, n_tok, NULL);
+}
+
+static sf37_hip_tensor *g_block_buf[2];
+static uint64_t g_block_buf_bytes[2];
+
+/* With bn, out is the hidden state (and x the same tensor): out += layer(
+ * RMSNorm(out)).  The fused decode launches take the norm and residual
+ * themselves; otherwise rms_norm into a block buffer, the layer into
+ * another, then the add. */
+static int moe_layer_impl(sf37_hip_tensor *out, sf37_hip_tensor *selected, sf37_hip_tensor *weights,
+                          const sf37_hip_moe_layer_weights *w, const sf37_hip_tensor *logits_in,
+                          const sf37_hip_tensor *x, uint32_t n_tok, const block_norm *bn) {
     if (!out || !w || !x || n_tok == 0 || !ensure_init()) return 0;
     const uint32_t E = w->n_expert, K = w->topk, D = w->in_dim, F = w->mid_dim;
     if (!w->router_bias || !w->gate || !w->up || !w->down || !w->sh_gate || !w->sh_up || !w->sh_down || E == 0 ||
@@ -1339,10 +1370,35 @@ int sf37_hip_moe_layer(sf37_hip_tensor *out, sf37_hip_tensor *selected, sf37_hip
     const int run_router = !logits_in || (g_opt_router_always && w->router);
     routed_args a = {(const uint8_t *)w->gate->ptr, (const uint8_t *)w->up->ptr, (const uint8_t *)w->down->ptr, NULL,
                      NULL, E, K, D, F, D, w->clamp_routed, (const float *)x->ptr, n_tok};
-    if (decode_eligible(&a, SF37_DEC_SELECT | SF37_DEC_SHARED)) {
+    const int fused = decode_eligible(&a, SF37_DEC_SELECT | SF37_DEC_SHARED);
+    if (bn && !fused) {
+        const uint64_t bytes = (uint64_t)n_tok * D * 4u;
+        for (int i = 0; i < 2; i++) {
+            if (!g_block_buf[i] || g_block_buf_bytes[i] < bytes) {
+                if (g_block_buf[i]) sf37_hip_tensor_free(g_block_buf[i]);
+                g_block_buf[i] = sf37_hip_tensor_alloc(bytes);
+                g_block_buf_bytes[i] = bytes;
+                if (!g_block_buf[i]) return 0;
+            }
+        }
+        float *xn = bn->xn ? bn->xn : (float *)g_block_buf[0]->ptr;
+        sf37_hip_tensor xnt = {xn, bytes, 0}, *y = g_block_buf[1];
+        return LAUNCH(SF37_HIP_STAGE_OTHER, sf37k_rms_norm(xn, (const float *)x->ptr, bn->norm_w, 1, D, n_tok, bn->eps, st),
+                      "moe block rms_norm launch") &&
+               moe_layer_impl(y, selected, weights, w, logits_in, &xnt, n_tok, NULL) &&
+               LAUNCH(SF37_HIP_STAGE_ADD, sf37k_add_inplace((float *)out->ptr, (const float *)y->ptr, (uint64_t)n_tok * D, st),
+                      "moe block residual launch");
+    }
+    if (fused) {
         dec_extra ex;
         memset(&ex, 0, sizeof(ex));
         ex.flags = SF37_DEC_SELECT | SF37_DEC_SHARED | (run_router ? SF37_DEC_ROUTER : 0u);
+        if (bn) {
+            ex.flags |= SF37_DEC_NORM | SF37_DEC_RESID;
+            ex.norm_w = bn->norm_w;
+            ex.eps = bn->eps;
+            ex.xn = bn->xn;
+        }
         ex.router_w = w->router ? (const float *)w->router->ptr : NULL;
         ex.router_bias = (const float *)w->router_bias->ptr;
         ex.logits_sel = logits_in ? (const float *)logits_in->ptr : NULL;
@@ -1395,6 +1451,35 @@ int sf37_hip_moe_layer(sf37_hip_tensor *out, sf37_hip_tensor *selected, sf37_hip
         return 0;
     }
     return LAUNCH(SF37_HIP_STAGE_ADD, sf37k_add_inplace((float *)out->ptr, routed, (uint64_t)n_tok * D, st), "moe_layer add launch");
+}
+
+int sf37_hip_moe_block(sf37_hip_tensor *hidden, sf37_hip_tensor *normed, sf37_hip_tensor *selected,
+                       sf37_hip_tensor *weights, const sf37_hip_moe_layer_weights *w, const void *model_map,
+                       uint64_t model_size, uint64_t norm_offset, float eps, const sf37_hip_tensor *logits_in,
+                       uint32_t n_tok) {
+    if (!hidden || !w || !model_map || n_tok == 0 || !ensure_init()) return 0;
+    const uint64_t bytes = (uint64_t)n_tok * w->in_dim * 4u;
+    if (hidden->bytes < bytes || (normed && normed->bytes < bytes) ||
+        !mapped_range_ok(model_size, norm_offset, (uint64_t)w->in_dim * 2u))
+        return 0;
+    const void *nw = model_ptr(model_map, norm_offset, (uint64_t)w->in_dim * 2u, "ffn norm weight");
+    if (!nw) return 0;
+    const block_norm bn = {(const uint16_t *)nw, eps, normed ? (float *)normed->ptr : NULL};
+    return moe_layer_impl(hidden, selected, weights, w, logits_in, hidden, n_tok, &bn);
+}
+
+int sf37_hip_moe_stack(sf37_hip_tensor *hidden, uint32_t n_layers, const sf37_hip_moe_layer_weights *layers,
+                       const void *model_map, uint64_t model_size, const uint64_t *norm_offsets, float eps,
+                       const sf37_hip_tensor *const *logits, sf37_hip_tensor *const *selected, uint32_t n_tok) {
+    if (!hidden || !layers || !norm_offsets || n_layers == 0) return 0;
+    for (uint32_t l = 0; l < n_layers; l++) {
+        if (!sf37_hip_moe_block(hidden, NULL, selected ? selected[l] : NULL, NULL, &layers[l], model_map, model_size,
+                                norm_offsets[l], eps, logits ? logits[l] : NULL, n_tok)) {
+            fprintf(stderr, "sf37_hip: moe stack layer %u failed\n", l);
+            return 0;
+        }
+    }
+    return 1;
 }
 
 int sf37_hip_synth_normal(sf37_hip_tensor *dst, uint64_t n, uint64_t seed, uint64_t stream, uint64_t index0,

@@ -142,6 +142,8 @@ int sf37k_sh_down(float *out, const void *d16, const float *ds, const void *a16,
 #define SF37_DEC_SELECT 2u   /* top-k from logits_sel (else sel/wts are inputs) */
 #define SF37_DEC_SHARED 4u   /* shared expert, out = shared + routed */
 #define SF37_DEC_SLOTS 8u    /* one group per slot of a single token */
+#define SF37_DEC_NORM 16u    /* x is the hidden state: RMSNorm(w + 1) by the route kernel */
+#define SF37_DEC_RESID 32u   /* out += layer output (out is the hidden state) */
 #define SF37_DEC_ACT_BYTES 288u  /* activation block: 256 codes, d, 4 sums, pad */
 typedef struct sf37_dec_params {
     uint32_t T, E, K, F, topk, G;
@@ -169,6 +171,9 @@ typedef struct sf37_dec_params {
     float *down_pair;    /* pairs x K */
     float *out;          /* T x K */
     uint32_t *cnt;
+    const uint16_t *norm_w;  /* K bf16 norm weights (NORM) */
+    float eps;               /* RMSNorm epsilon (NORM) */
+    float *xn;               /* T x K normalised rows, or NULL (NORM) */
 } sf37_dec_params;
 int sf37k_decode_counters(uint32_t T, uint32_t topk, uint32_t E, uint32_t K, uint32_t F);
 /* 1 if the fused kernels take this shape (token count, dims, LDS). */

@@ -48,10 +48,15 @@ __device__ __forceinline__ double sf37_wave_sum_f64(double v) {
 // the x slice is read once for all rows), then a DPP sum per wave
 // (sf37_wave_sum_f64), and sf37_router_combine adds the four wave sums as
 // (w0 + w1) + (w2 + w3).  K must be a multiple of 256.  store(r, t, wave, v)
-// receives the wave sums.
-template <int NR, int NT, class STORE>
+// receives the wave sums; xf(t, k, v) maps each loaded x value (identity,
+// or the row's normalisation).
+struct sf37_x_identity {
+    __device__ float operator()(uint32_t, uint32_t, float v) const { return v; }
+};
+
+template <int NR, int NT, class STORE, class XF = sf37_x_identity>
 __device__ __forceinline__ void sf37_router_block(const float *wr, uint32_t nr, const float *x, uint32_t K,
-                                                  uint32_t t0, STORE store) {
+                                                  uint32_t t0, STORE store, XF xf = XF()) {
     const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
     const uint32_t c = K >> 8, k0 = threadIdx.x * c;
     double acc[NR][NT];
@@ -72,7 +77,12 @@ __device__ __forceinline__ void sf37_router_block(const float *wr, uint32_t nr, 
                     wv[r][j] = *(const sf37_f32x4 *)(wr + (uint64_t)rr * K + k0 + kk + 4u * jj);
                 }
 #pragma unroll
-                for (int t = 0; t < NT; t++) xv[t][j] = *(const sf37_f32x4 *)(x + (uint64_t)(t0 + t) * K + k0 + kk + 4u * jj);
+                for (int t = 0; t < NT; t++) {
+                    const uint32_t k = k0 + kk + 4u * jj;
+                    xv[t][j] = *(const sf37_f32x4 *)(x + (uint64_t)(t0 + t) * K + k);
+#pragma unroll
+                    for (int q = 0; q < 4; q++) xv[t][j][q] = xf(t0 + (uint32_t)t, k + (uint32_t)q, xv[t][j][q]);
+                }
             }
 #pragma unroll
             for (int j = 0; j < 4; j++) {
@@ -93,7 +103,9 @@ __device__ __forceinline__ void sf37_router_block(const float *wr, uint32_t nr, 
             for (int r = 0; r < NR; r++) {
                 const double wk = wr[(uint64_t)((uint32_t)r < nr ? r : 0) * K + k];
 #pragma unroll
-                for (int t = 0; t < NT; t++) acc[r][t] = __builtin_fma(wk, (double)x[(uint64_t)(t0 + t) * K + k], acc[r][t]);
+                for (int t = 0; t < NT; t++)
+                    acc[r][t] = __builtin_fma(wk, (double)xf(t0 + (uint32_t)t, k, x[(uint64_t)(t0 + t) * K + k]),
+                                              acc[r][t]);
             }
         }
     }
@@ -107,19 +119,19 @@ __device__ __forceinline__ void sf37_router_block(const float *wr, uint32_t nr, 
 }
 
 // NR rows, all T tokens, in passes of at most 8 tokens.
-template <int NR, class STORE>
+template <int NR, class STORE, class XF = sf37_x_identity>
 __device__ __forceinline__ void sf37_router_rows_n(const float *wr, uint32_t nr, const float *x, uint32_t K, uint32_t T,
-                                                   STORE store) {
+                                                   STORE store, XF xf = XF()) {
     for (uint32_t t0 = 0; t0 < T; t0 += 8u) {
         switch (T - t0 < 8u ? T - t0 : 8u) {
-            case 1: sf37_router_block<NR, 1>(wr, nr, x, K, t0, store); break;
-            case 2: sf37_router_block<NR, 2>(wr, nr, x, K, t0, store); break;
-            case 3: sf37_router_block<NR, 3>(wr, nr, x, K, t0, store); break;
-            case 4: sf37_router_block<NR, 4>(wr, nr, x, K, t0, store); break;
-            case 5: sf37_router_block<NR, 5>(wr, nr, x, K, t0, store); break;
-            case 6: sf37_router_block<NR, 6>(wr, nr, x, K, t0, store); break;
-            case 7: sf37_router_block<NR, 7>(wr, nr, x, K, t0, store); break;
-            default: sf37_router_block<NR, 8>(wr, nr, x, K, t0, store); break;
+            case 1: sf37_router_block<NR, 1>(wr, nr, x, K, t0, store, xf); break;
+            case 2: sf37_router_block<NR, 2>(wr, nr, x, K, t0, store, xf); break;
+            case 3: sf37_router_block<NR, 3>(wr, nr, x, K, t0, store, xf); break;
+            case 4: sf37_router_block<NR, 4>(wr, nr, x, K, t0, store, xf); break;
+            case 5: sf37_router_block<NR, 5>(wr, nr, x, K, t0, store, xf); break;
+            case 6: sf37_router_block<NR, 6>(wr, nr, x, K, t0, store, xf); break;
+            case 7: sf37_router_block<NR, 7>(wr, nr, x, K, t0, store, xf); break;
+            default: sf37_router_block<NR, 8>(wr, nr, x, K, t0, store, xf); break;
         }
     }
 }

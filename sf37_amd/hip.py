@@ -95,6 +95,9 @@ _SIGS = {
     "sf37_hip_q8k_quantize": (C.c_int, [T, T, u32, u32]),
     "sf37_hip_moe_dispatch": (C.c_int, [T, T, T, T, u32, u32]),
     "sf37_hip_moe_layer": (C.c_int, [T, T, T, C.POINTER(LayerWeights), T, T, u32]),
+    "sf37_hip_moe_block": (C.c_int, [T, T, T, T, C.POINTER(LayerWeights), vp, u64, u64, f32, T, u32]),
+    "sf37_hip_moe_stack": (C.c_int, [T, u32, C.POINTER(LayerWeights), vp, u64, C.POINTER(u64), f32, C.POINTER(T),
+                                     C.POINTER(T), u32]),
     "sf37_hip_synth_normal": (C.c_int, [T, u64, u64, u64, u64, f32]),
     "sf37_hip_synth_quant_rows": (C.c_int, [C.c_int, T, u64, u64, u64, u64, u64, f32]),
     "sf37_hip_sigmoid_array": (C.c_int, [T, T, u64, C.c_int]),

@@ -9,6 +9,8 @@ counter-based streams so any part can be regenerated bit-identically.
 """
 from __future__ import annotations
 
+import ctypes as C
+
 import numpy as np
 
 from . import hip
@@ -131,21 +133,33 @@ class SynthStack:
         self._key = np.zeros(64, np.uint8)               # host address used as the map key
         check(lib().sf37_hip_register_device_range(self._key.ctypes.data, self.norm.nbytes, 0, self.norm.nbytes,
                                                    self.norm.h), "register norm weights")
+        self._structs = (hip.LayerWeights * n_layers)(*[lay.weights_struct() for lay in self.layers])
+        self._offsets = (C.c_uint64 * n_layers)(*[l * K * 2 for l in range(n_layers)])
 
     def rms_norm(self, out: Tensor, x: Tensor, layer: int, n_tok: int) -> None:
         K = self.in_dim
         check(lib().sf37_hip_rms_norm_weight1_bf16_batch_mapped(out.h, x.h, self._key.ctypes.data, self.norm.nbytes,
                                                                 layer * K * 2, K, n_tok, self.EPS), "rms_norm")
 
-    def forward(self, h: Tensor, n_tok: int, xn: Tensor, y: Tensor, sel=None, wts: Tensor | None = None,
-                logits=None) -> None:
+    def forward(self, h: Tensor, n_tok: int, xn: Tensor | None = None, y: Tensor | None = None, sel=None,
+                wts: Tensor | None = None, logits=None, native: bool = True) -> None:
         """h <- h + MoE_l(RMSNorm_l(h)) for every layer; logits[l] (optional)
         are injected router logits of layer l; sel is one selection buffer or
-        a list of one per layer."""
+        a list of one per layer.  native: one sf37_hip_moe_stack call (the
+        decode launches normalise and add the residual themselves); else per
+        layer the rms_norm, moe_layer and add entry points (xn, y needed)."""
+        n = self.n_layers
+        sels = list(sel) if isinstance(sel, (list, tuple)) else [sel] * n
+        if native:
+            Ta = C.c_void_p * n
+            lg = Ta(*[t.h if t is not None else None for t in logits]) if logits is not None else None
+            sl = Ta(*[t.h if t is not None else None for t in sels])
+            check(lib().sf37_hip_moe_stack(h.h, n, self._structs, self._key.ctypes.data, self.norm.nbytes,
+                                           self._offsets, self.EPS, lg, sl, n_tok), "moe_stack")
+            return
         for l, lay in enumerate(self.layers):
             self.rms_norm(xn, h, l, n_tok)
-            s = sel[l] if isinstance(sel, (list, tuple)) else sel
-            moe_layer(lay, xn, n_tok, y, s, wts, logits[l] if logits is not None else None)
+            moe_layer(lay, xn, n_tok, y, sels[l], wts, logits[l] if logits is not None else None)
             check(lib().sf37_hip_add_inplace_f32(h.h, y.h, n_tok * self.in_dim), "add_inplace")
 
     def free(self) -> None:

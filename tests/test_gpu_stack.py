@@ -71,12 +71,12 @@ def oracle_stack(O, stack, h, logits):
     return h
 
 
-def run_stack(H, stack, h0, logits):
+def run_stack(H, stack, h0, logits, native=True):
     n_tok, K = h0.shape
     h = H.Tensor.from_array(h0)
     xn, y = H.Tensor.alloc(n_tok * K * 4), H.Tensor.alloc(n_tok * K * 4)
     lts = [H.Tensor.from_array(lg) for lg in logits]
-    stack.forward(h, n_tok, xn, y, None, None, lts)
+    stack.forward(h, n_tok, xn, y, None, None, lts, native=native)
     return h.read(np.float32).reshape(n_tok, K)
 
 
@@ -92,6 +92,9 @@ def small_stack(H):
 
 @pytest.mark.parametrize("n_tok", [3, 40])
 def test_small_stack_vs_oracle(H, O, small_stack, n_tok):
+    """sf37_hip_moe_stack (fused norm + residual at 3 tokens, rms_norm +
+    layer + add at 40) and the per-layer entry points, both against the
+    oracle."""
     from sf37_amd import configs
     S = small_stack
     for k in ("q8k_min_rows", "prefill_min_pairs", "shared_min_tokens"):
@@ -99,20 +102,42 @@ def test_small_stack_vs_oracle(H, O, small_stack, n_tok):
     rng = np.random.default_rng(40 + n_tok)
     h0 = rng.standard_normal((n_tok, S.in_dim)).astype(np.float32)
     logits = [configs.logits_for(4, 700 + l, n_tok, n_expert=16) for l in range(S.n_layers)]
-    H.lib().sf37_hip_profile_enable(1)
-    H.profile_read()
-    try:
-        got = run_stack(H, S, h0, logits)
-        prof = H.profile_read()
-    finally:
-        H.lib().sf37_hip_profile_enable(0)
-    if n_tok > 16:
-        assert prof["pf_gate_up"][1] == S.n_layers and prof["sh_gate_up"][1] == S.n_layers
-    else:
-        assert prof["dec_up"][1] == S.n_layers
+    got = {}
+    for native in (True, False):
+        H.lib().sf37_hip_profile_enable(1)
+        H.profile_read()
+        try:
+            got[native] = run_stack(H, S, h0, logits, native)
+            prof = H.profile_read()
+        finally:
+            H.lib().sf37_hip_profile_enable(0)
+        if n_tok > 16:
+            assert prof["pf_gate_up"][1] == S.n_layers and prof["sh_gate_up"][1] == S.n_layers
+        else:
+            assert prof["dec_up"][1] == S.n_layers
+            # the stack call's decode launches take the norm and the residual
+            assert prof["other"][1] == (0 if native else S.n_layers), prof["other"]
     say(f"oracle: {S.n_layers} layers x {n_tok} tokens")
     want = oracle_stack(O, S, h0, logits)
-    assert_bitexact(got, want, f"stack output, {n_tok} tokens")
+    assert_bitexact(got[True], want, f"stack call output, {n_tok} tokens")
+    assert_bitexact(got[False], want, f"per-layer calls output, {n_tok} tokens")
+
+
+def test_block_normed_rows(H, small_stack):
+    """sf37_hip_moe_block's optional normalised rows equal the standalone
+    rms_norm entry point's, on the fused (5 tokens) and staged (20) paths."""
+    import ctypes as C
+    S = small_stack
+    H.set_option("q8k_min_rows", 0)
+    for n_tok in (5, 20):
+        rng = np.random.default_rng(n_tok)
+        h0 = (rng.standard_normal((n_tok, S.in_dim)) * 3).astype(np.float32)
+        h, normed = H.Tensor.from_array(h0), H.Tensor.alloc(n_tok * S.in_dim * 4)
+        ref = H.Tensor.alloc(n_tok * S.in_dim * 4)
+        S.rms_norm(ref, H.Tensor.from_array(h0), 1, n_tok)
+        H.check(H.lib().sf37_hip_moe_block(h, normed, None, None, C.byref(S._structs[1]), S._key.ctypes.data,
+                                           S.norm.nbytes, S._offsets[1], S.EPS, None, n_tok), "moe_block")
+        assert_bitexact(normed.read(np.float32), ref.read(np.float32), f"normed rows, {n_tok} tokens")
 
 
 def test_baseline_shape_stack_layers_43_44(H, O):
