@@ -3,8 +3,8 @@
 // Logits: out[t][e] = sum_k W[e][k] * x[t][k], accumulated in binary64 as
 // the engine's CPU path does (sf37.c:1970-1976).  Tiled: a workgroup owns
 // 32 experts x 32 tokens, stages 64-wide K slices of both operands in LDS
-// and each thread accumulates a 2x2 patch in double.  The same kernel serves
-// decode (one token column) and prefill.
+// and each thread accumulates a 2x2 patch in double (shapes the matrix-core
+// kernel below does not take); up to 16 tokens a GEMV kernel.
 //
 // Selection (sf37.c:2144-2157, sf37_cuda.cu:4866-4997): one wave per token.
 // p = sigmoid(logit), score = p + bias, k rounds of a wave-wide arg-max under
@@ -56,6 +56,66 @@ __global__ void __launch_bounds__(256) f32_matmul_kernel(float *__restrict__ out
             const uint64_t e = e0 + te + i, t = t0 + tt + j;
             if (e < out_dim && t < n_tok) out[t * out_dim + e] = (float)acc[i][j];
         }
+}
+
+// Prefill logits on the fp64 matrix cores (v_mfma_f64_16x16x4f64): the
+// fp32 operands convert exactly to binary64, every product is exact and the
+// sums are binary64, so the logits stay within 1 ulp of the CPU's ordered
+// sum.  A wave owns 16 tokens x 16 experts, a workgroup four expert tiles
+// of the same tokens (they share the x rows in the caches).  Lane l loads
+// float4 runs x[t0 + l%16][k + 4(l/16) ..] and W[e0 + l%16][same k]; MFMA
+// step s of a 16-wide k slice takes element s of both, so the MFMA's k
+// index g = l/16 is k + 4g + s in both operands.  Chunks of 64 k are
+// double-buffered in registers.  K must be a multiple of 128.
+typedef double rt_f64x4 __attribute__((ext_vector_type(4)));
+constexpr uint32_t RM_CH = 4;   // 16-wide k slices per chunk
+
+__device__ __forceinline__ void rm_load(sf37_f32x4 (&a)[RM_CH], sf37_f32x4 (&b)[RM_CH], const float *xa,
+                                        const float *wb, uint32_t k) {
+#pragma unroll
+    for (uint32_t c = 0; c < RM_CH; c++) {
+        a[c] = *(const sf37_f32x4 *)(xa + k + 16u * c);
+        b[c] = *(const sf37_f32x4 *)(wb + k + 16u * c);
+    }
+}
+
+// Two accumulation chains (even / odd slices) so consecutive MFMAs of a
+// wave do not wait on each other; they are added once at the end.
+__device__ __forceinline__ void rm_mfma(rt_f64x4 (&acc)[2], const sf37_f32x4 (&a)[RM_CH],
+                                        const sf37_f32x4 (&b)[RM_CH]) {
+#pragma unroll
+    for (int s = 0; s < 4; s++)
+#pragma unroll
+        for (uint32_t c = 0; c < RM_CH; c++)
+            acc[c & 1u] = __builtin_amdgcn_mfma_f64_16x16x4f64((double)a[c][s], (double)b[c][s], acc[c & 1u], 0, 0, 0);
+}
+
+__global__ void __launch_bounds__(256) f64mm_router_kernel(float *__restrict__ out, const float *__restrict__ w,
+                                                           const float *__restrict__ x, uint32_t K, uint32_t E,
+                                                           uint32_t T) {
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t e0 = (blockIdx.y * 4u + wave) * 16u;
+    if (e0 >= E) return;
+    const uint32_t t0 = blockIdx.x * 16u, i = lane & 15u, g = lane >> 4;
+    const uint32_t tr = t0 + i < T ? t0 + i : T - 1u, er = e0 + i < E ? e0 + i : E - 1u;   // loads stay in bounds
+    const float *xa = x + (uint64_t)tr * K + 4u * g;
+    const float *wb = w + (uint64_t)er * K + 4u * g;
+    rt_f64x4 acc[2] = {{0.0, 0.0, 0.0, 0.0}, {0.0, 0.0, 0.0, 0.0}};
+    sf37_f32x4 a0[RM_CH], b0[RM_CH], a1[RM_CH], b1[RM_CH];
+    rm_load(a0, b0, xa, wb, 0);
+    for (uint32_t k = 0; k < K; k += 128u) {
+        rm_load(a1, b1, xa, wb, k + 64u);
+        rm_mfma(acc, a0, b0);
+        if (k + 128u < K) rm_load(a0, b0, xa, wb, k + 128u);
+        rm_mfma(acc, a1, b1);
+    }
+    // D: lane l holds rows l/16 + 4r (tokens), column l%16 (expert)
+    const uint32_t e = e0 + i;
+#pragma unroll
+    for (uint32_t r = 0; r < 4; r++) {
+        const uint32_t t = t0 + g + 4u * r;
+        if (t < T && e < E) out[(uint64_t)t * E + e] = (float)(acc[0][r] + acc[1][r]);
+    }
 }
 
 // Decode GEMV (n_tok small): one workgroup per expert row and 8 tokens.
@@ -128,6 +188,10 @@ extern "C" int sf37k_f32_matmul(float *out, const float *w, const float *x, uint
     if (n_tok <= 16) {
         hipLaunchKernelGGL(f32_matvec_kernel, dim3((unsigned)out_dim, (unsigned)((n_tok + 7) / 8)),
                            dim3(256), 0, (hipStream_t)s, out, w, x, in_dim, out_dim, (uint32_t)n_tok);
+    } else if (in_dim % 128u == 0 && in_dim <= 0xffffffffu && out_dim <= 0xffffffffu && n_tok <= 0xffffffffu) {
+        hipLaunchKernelGGL(f64mm_router_kernel, dim3((unsigned)((n_tok + 15) / 16), (unsigned)((out_dim + 63) / 64)),
+                           dim3(256), 0, (hipStream_t)s, out, w, x, (uint32_t)in_dim, (uint32_t)out_dim,
+                           (uint32_t)n_tok);
     } else {
         hipLaunchKernelGGL(f32_matmul_kernel,
                            dim3((unsigned)((out_dim + RT_E - 1) / RT_E), (unsigned)((n_tok + RT_T - 1) / RT_T)),
