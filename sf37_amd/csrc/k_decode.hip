@@ -42,7 +42,6 @@ static_assert(DN_STAGE % DN_TPC == 0, "a down pass stays inside one staged chunk
 constexpr uint32_t SHD_CHUNK = 4;    // shared-down Q8_0 blocks per load batch (even)
 constexpr uint32_t SHD_MAX_BPS = 12; // shared-down blocks per lane (a multiple of SHD_CHUNK)
 constexpr uint32_t UP_QUEUES = 64;   // queues of the up kernel's dynamic items, one per 128 bytes
-constexpr uint32_t UP_DYN_PCT = 25;  // share of the up items handed out dynamically (percent)
 constexpr uint32_t DN_QUEUES = 64;   // queues of the down kernel's shared-down rows, one per 128 bytes
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -371,7 +370,24 @@ __global__ void __launch_bounds__(256) dec_select_kernel(dec_params p) {
         const uint32_t m = mr / SH_RS, r = mr - m * SH_RS;
         const float *rv = red + (uint64_t)i * nb8;
         float acc = 0.0f;
-        for (uint32_t b = 0; b < nb8; b++) acc = acc + rv[b];
+        if ((nb8 & 15u) == 0) {
+            // the same sequential sum; 16 terms read per step so the LDS
+            // latency is paid once per step, not once per term
+            for (uint32_t b = 0; b < nb8; b += 16u) {
+                float4 v[4];
+#pragma unroll
+                for (int j = 0; j < 4; j++) v[j] = *(const float4 *)(rv + b + 4u * j);
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    acc = acc + v[j].x;
+                    acc = acc + v[j].y;
+                    acc = acc + v[j].z;
+                    acc = acc + v[j].w;
+                }
+            }
+        } else {
+            for (uint32_t b = 0; b < nb8; b++) acc = acc + rv[b];
+        }
         p.sh_gu[((uint64_t)m * p.T + t) * p.F + row0 + r] = acc;
     }
 }
@@ -566,7 +582,7 @@ __device__ void shared_down_pass(const dec_params &p, const int8_t *xq, const fl
 // Routed gate/up.  An item is 2 rows of one group's expert for both
 // matrices: lane = matrix (gate/up) | row | block, so each wave reads two
 // contiguous 2-row spans; the gate lane of each row stores gate and up.
-// The first (100 - UP_DYN_PCT)% of the items are split into equal contiguous
+// The first (100 - up_dyn_pct)% of the items are split into equal contiguous
 // ranges, one per wave; the rest are handed out one at a time from
 // UP_QUEUES queues (wave w asks queue w % UP_QUEUES, which owns a contiguous
 // share), so waves that run faster - older waves win the issue arbitration -
@@ -591,7 +607,8 @@ __global__ void __launch_bounds__(256) dec_up_kernel(dec_params p) {
     const bool out_lane = b == nbK - 1u;
     float *const out_rows = m ? p.up_out : p.gate_out;
     const uint32_t ipg = p.F / 2u, n_items = gi[0] * ipg;
-    const uint32_t n_stat = n_items - (uint32_t)((uint64_t)n_items * UP_DYN_PCT / 100u);
+    const uint32_t dyn_pct = p.up_dyn_pct < 100u ? p.up_dyn_pct : 100u;
+    const uint32_t n_stat = n_items - (uint32_t)((uint64_t)n_items * dyn_pct / 100u);
     const uint32_t lo = (uint32_t)((uint64_t)n_stat * gw / nw), hi = (uint32_t)((uint64_t)n_stat * (gw + 1u) / nw);
     const uint32_t qi = gw % UP_QUEUES, n_dyn = n_items - n_stat;
     const uint32_t q0 = n_stat + (uint32_t)((uint64_t)n_dyn * qi / UP_QUEUES);
@@ -1032,11 +1049,13 @@ dec_shape dec_plan(const dec_params &p) {
     d.lds_shup = lds_up_shared(p.K, p.T);
     d.n_shup = 1u + (sh ? p.F / SH_RS : 0u);           // select workgroup + shared rows
     // persistent kernels: exactly as many workgroups as can be resident
-    d.n_up = resident_wgs((const void *)dec_up_kernel, 256, d.lds_up) * cus;
+    const uint32_t up_res = resident_wgs((const void *)dec_up_kernel, 256, d.lds_up);
+    d.n_up = (p.up_wgs && p.up_wgs < up_res ? p.up_wgs : up_res) * cus;
     d.n_mid = (p.T * p.topk * (p.F / SF37_QK) + (sh ? (p.T * (p.F / 32u) + 1u) / 2u : 0u) + 3u) / 4u;
     d.lds_dn = sh ? (size_t)p.T * p.F + (size_t)p.T * (p.F / 32u) * 4u : 0u;
     d.dn_kernel = down_kernel_for(p);
-    d.n_dn = resident_wgs(d.dn_kernel, 256, d.lds_dn) * cus;
+    const uint32_t dn_res = resident_wgs(d.dn_kernel, 256, d.lds_dn);
+    d.n_dn = (p.dn_wgs && p.dn_wgs < dn_res ? p.dn_wgs : dn_res) * cus;
     d.n_cb = (p.T * p.K + 255u) / 256u;
     return d;
 }

@@ -50,6 +50,7 @@ static int64_t g_opt_q8k_min_rows = 512;
 static int64_t g_opt_write_gate_up = 0;
 static int64_t g_opt_decode = 1;
 static int64_t g_opt_router_always = 0;
+static int64_t g_opt_up_dyn_pct = 25, g_opt_up_wgs = 0, g_opt_dn_wgs = 0;
 static int64_t g_opt_prefill = 1;
 static int64_t g_opt_prefill_min_pairs = 256;
 static int64_t g_opt_shared_min_tok = 64;
@@ -304,6 +305,9 @@ int sf37_hip_set_option(const char *name, int64_t value) {
     else if (!strcmp(name, "moe_write_gate_up")) g_opt_write_gate_up = value ? 1 : 0;
     else if (!strcmp(name, "decode_fused")) g_opt_decode = value ? 1 : 0;
     else if (!strcmp(name, "router_with_logits")) g_opt_router_always = value ? 1 : 0;
+    else if (!strcmp(name, "decode_up_dyn_pct")) g_opt_up_dyn_pct = value < 0 ? 0 : (value > 100 ? 100 : value);
+    else if (!strcmp(name, "decode_up_wgs")) g_opt_up_wgs = value < 0 ? 0 : value;
+    else if (!strcmp(name, "decode_down_wgs")) g_opt_dn_wgs = value < 0 ? 0 : value;
     else if (!strcmp(name, "prefill_mfma")) g_opt_prefill = value ? 1 : 0;
     else if (!strcmp(name, "prefill_min_pairs")) g_opt_prefill_min_pairs = value < 0 ? 0 : value;
     else if (!strcmp(name, "shared_min_tokens")) g_opt_shared_min_tok = value < 0 ? 0 : value;
@@ -318,6 +322,9 @@ int64_t sf37_hip_get_option(const char *name) {
     if (!strcmp(name, "moe_write_gate_up")) return g_opt_write_gate_up;
     if (!strcmp(name, "decode_fused")) return g_opt_decode;
     if (!strcmp(name, "router_with_logits")) return g_opt_router_always;
+    if (!strcmp(name, "decode_up_dyn_pct")) return g_opt_up_dyn_pct;
+    if (!strcmp(name, "decode_up_wgs")) return g_opt_up_wgs;
+    if (!strcmp(name, "decode_down_wgs")) return g_opt_dn_wgs;
     if (!strcmp(name, "prefill_mfma")) return g_opt_prefill;
     if (!strcmp(name, "prefill_min_pairs")) return g_opt_prefill_min_pairs;
     if (!strcmp(name, "shared_min_tokens")) return g_opt_shared_min_tok;
@@ -1129,6 +1136,9 @@ static int decode_run(const routed_args *a, const dec_extra *ex, float *out, flo
     if ((ex->flags & SF37_DEC_ROUTER) && !p.router_w) return 0;
     if (sh && (!p.sh_gate || !p.sh_up || !p.sh_down)) return 0;
     if ((ex->flags & SF37_DEC_NORM) && !ex->norm_w) return 0;
+    p.up_dyn_pct = (uint32_t)g_opt_up_dyn_pct;
+    p.up_wgs = (uint32_t)g_opt_up_wgs;
+    p.dn_wgs = (uint32_t)g_opt_dn_wgs;
     p.norm_w = ex->norm_w;
     p.eps = ex->eps;
     p.xn = ex->xn;

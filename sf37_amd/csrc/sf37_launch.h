@@ -174,6 +174,8 @@ typedef struct sf37_dec_params {
     const uint16_t *norm_w;  /* K bf16 norm weights (NORM) */
     float eps;               /* RMSNorm epsilon (NORM) */
     float *xn;               /* T x K normalised rows, or NULL (NORM) */
+    uint32_t up_dyn_pct;     /* share of the up items handed out dynamically (percent) */
+    uint32_t up_wgs, dn_wgs; /* up / down workgroups per CU (0 = as many as fit) */
 } sf37_dec_params;
 int sf37k_decode_counters(uint32_t T, uint32_t topk, uint32_t E, uint32_t K, uint32_t F);
 /* 1 if the fused kernels take this shape (token count, dims, LDS). */
