@@ -1063,9 +1063,7 @@ dec_shape dec_plan(const dec_params &p) {
 }  // namespace
 
 extern "C" int sf37k_decode_counters(uint32_t T, uint32_t topk, uint32_t E, uint32_t K, uint32_t F) {
-    (void)K;
-    const uint32_t P = T * topk, G = P < E ? P : E;
-    (void)T; (void)topk; (void)E; (void)F;
+    (void)T; (void)topk; (void)E; (void)K; (void)F;
     return (int)(32u * (UP_QUEUES + DN_QUEUES));
 }
 

@@ -22,8 +22,16 @@ __global__ void __launch_bounds__(256) add_kernel(float *__restrict__ dst,
     if (i < n) dst[i] = dst[i] + src[i];
 }
 
+__global__ void __launch_bounds__(256) add2_kernel(float *__restrict__ dst, const float *__restrict__ a,
+                                                   const float *__restrict__ b, uint64_t n) {
+    const uint64_t i = (uint64_t)blockIdx.x * 256u + threadIdx.x;
+    if (i < n) dst[i] = dst[i] + (a[i] + b[i]);
+}
+
 // One wave per row (four rows per workgroup): sf37_rms_scale_wave, then
-// the weighted scale of every element.
+// the weighted scale of every element.  Rows of 256..4096 elements (a
+// multiple of 256) stay in registers between the two passes; the sum of
+// squares runs in sf37_rms_scale_wave's order.
 __global__ void __launch_bounds__(256) rms_norm_kernel(float *__restrict__ out,
                                                        const float *__restrict__ x,
                                                        const void *__restrict__ w, int bf16,
@@ -32,6 +40,34 @@ __global__ void __launch_bounds__(256) rms_norm_kernel(float *__restrict__ out,
     if (row >= n_rows) return;
     const float *xr = x + (uint64_t)row * n;
     float *orow = out + (uint64_t)row * n;
+    if (bf16 && (n & 255u) == 0 && n <= 4096u) {
+        constexpr uint32_t MAXJ = 16;
+        const uint32_t nj = n >> 8;
+        sf37_f32x4 v[MAXJ];
+#pragma unroll
+        for (uint32_t j = 0; j < MAXJ; j++)
+            if (j < nj) v[j] = *(const sf37_f32x4 *)(xr + 4u * lane + 256u * j);
+        double ss = 0.0;
+#pragma unroll
+        for (uint32_t j = 0; j < MAXJ; j++)
+            if (j < nj) {
+#pragma unroll
+                for (int q = 0; q < 4; q++) ss = __builtin_fma((double)v[j][q], (double)v[j][q], ss);
+            }
+        const double tot = sf37_wave_sum_f64(ss);
+        const float scale = 1.0f / __builtin_sqrtf((float)(tot / (double)n) + eps);
+        const uint16_t *wb = (const uint16_t *)w;
+#pragma unroll
+        for (uint32_t j = 0; j < MAXJ; j++)
+            if (j < nj) {
+                const uint32_t k = 4u * lane + 256u * j;
+                sf37_f32x4 o;
+#pragma unroll
+                for (int q = 0; q < 4; q++) o[q] = sf37_norm_w1_bf16(v[j][q], scale, wb[k + q]);
+                *(sf37_f32x4 *)(orow + k) = o;
+            }
+        return;
+    }
     const float scale = sf37_rms_scale_wave(xr, n, eps);
     for (uint32_t i = lane; i < n; i += 64u) {
         orow[i] = bf16 ? sf37_norm_w1_bf16(xr[i], scale, ((const uint16_t *)w)[i])
@@ -53,6 +89,12 @@ extern "C" int sf37k_add_inplace(float *dst, const float *src, uint64_t n, sf37_
     if (n == 0) return 0;
     hipLaunchKernelGGL(add_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)s,
                        dst, src, n);
+    return (int)hipGetLastError();
+}
+
+extern "C" int sf37k_add2_inplace(float *dst, const float *a, const float *b, uint64_t n, sf37_stream_t s) {
+    if (n == 0) return 0;
+    hipLaunchKernelGGL(add2_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)s, dst, a, b, n);
     return (int)hipGetLastError();
 }
 

@@ -306,37 +306,6 @@ __device__ __forceinline__ uint32_t q3_win(const uint32_t *w) {
     else return align_bits(w[k + 1], w[k], (uint32_t)s);
 }
 
-// Dequantise group g of a Q3 block into 16 fp16 pair words.  k = 8 - zp.
-template <int SH>
-__device__ __forceinline__ void q3_dequant(const uint32_t *w, uint32_t k, uint32_t out[16]) {
-    const uint32_t cA1 = pf_exp(0, 2) + k * pf_mul(0, 2), cA2 = pf_exp(3, 5) + k * pf_mul(3, 5);
-    const uint32_t cB1 = pf_exp(1, 0) + k * pf_mul(1, 0), cB2 = pf_exp(4, 3) + k * pf_mul(4, 3);
-    constexpr uint32_t mA1 = q3_mask(0), mA2 = q3_mask(1), mB1 = q3_mask(2), mB2 = q3_mask(3);
-    uint32_t x;
-    x = q3_win<SH, 0>(w);  out[0] = (x & mA1) + cA1;  out[1] = (x & mA2) + cA2;
-    x = q3_win<SH, 6>(w);  out[2] = (x & mA1) + cA1;  out[3] = (x & mA2) + cA2;
-    x = q3_win<SH, 12>(w); out[4] = (x & mA1) + cA1;  out[5] = (x & mA2) + cA2;
-    x = q3_win<SH, 35>(w); out[6] = (x & mB1) + cB1;  out[7] = (x & mB2) + cB2;
-    x = q3_win<SH, 41>(w); out[8] = (x & mB1) + cB1;  out[9] = (x & mB2) + cB2;
-    x = q3_win<SH, 47>(w); out[10] = (x & mB1) + cB1;
-    x = q3_win<SH, 65>(w); out[11] = (x & mB1) + cB1; out[12] = (x & mB2) + cB2;
-    x = q3_win<SH, 71>(w); out[13] = (x & mB1) + cB1; out[14] = (x & mB2) + cB2;
-    x = q3_win<SH, 77>(w); out[15] = (x & mB1) + cB1;
-}
-
-// Dequantise group g of a Q2 block (two dwords of the lane) into 16 words.  k = 4 - zp.
-__device__ __forceinline__ void q2_dequant(const uint32_t *w, uint32_t k, uint32_t out[16]) {
-    uint32_t c[4];
-#pragma unroll
-    for (uint32_t j = 0; j < 4u; j++) c[j] = pf_exp(2u * j, 2u * j) + k * pf_mul(2u * j, 2u * j);
-#pragma unroll
-    for (uint32_t q = 0; q < 4u; q++) {
-        const uint32_t x = (q & 1u) ? (w[q >> 1] >> 8) : w[q >> 1];
-#pragma unroll
-        for (uint32_t j = 0; j < 4u; j++) out[4u * q + j] = (x & (0x00030003u << (2u * j))) + c[j];
-    }
-}
-
 // f16 scale of group g, zero point of group g from the header bits at SH.
 template <int SH>
 __device__ __forceinline__ float hdr_scale(const uint32_t *h, int g) {

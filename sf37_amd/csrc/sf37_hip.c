@@ -1334,12 +1334,12 @@ typedef struct {
 
 static int moe_layer_impl(sf37_hip_tensor *out, sf37_hip_tensor *selected, sf37_hip_tensor *weights,
                           const sf37_hip_moe_layer_weights *w, const sf37_hip_tensor *logits_in,
-                          const sf37_hip_tensor *x, uint32_t n_tok, const block_norm *bn);
+                          const sf37_hip_tensor *x, uint32_t n_tok, const block_norm *bn, float *resid);
 
 int sf37_hip_moe_layer(sf37_hip_tensor *out, sf37_hip_tensor *selected, sf37_hip_tensor *weights,
                        const sf37_hip_moe_layer_weights *w, const sf37_hip_tensor *logits_in,
                        const sf37_hip_tensor *x, uint32_t n_tok) {
-    return moe_layer_impl(out, selected, weights, w, logits_in, x, n_tok, NULL);
+    return moe_layer_impl(out, selected, weights, w, logits_in, x, n_tok, NULL, NULL);
 }
 
 static sf37_hip_tensor *g_block_buf[2];
@@ -1347,11 +1347,12 @@ static uint64_t g_block_buf_bytes[2];
 
 /* With bn, out is the hidden state (and x the same tensor): out += layer(
  * RMSNorm(out)).  The fused decode launches take the norm and residual
- * themselves; otherwise rms_norm into a block buffer, the layer into
- * another, then the add. */
+ * themselves; otherwise rms_norm into a block buffer and the layer into
+ * another, whose last add then writes resid = resid + (shared + routed)
+ * (resid given: out keeps the shared expert's rows only). */
 static int moe_layer_impl(sf37_hip_tensor *out, sf37_hip_tensor *selected, sf37_hip_tensor *weights,
                           const sf37_hip_moe_layer_weights *w, const sf37_hip_tensor *logits_in,
-                          const sf37_hip_tensor *x, uint32_t n_tok, const block_norm *bn) {
+                          const sf37_hip_tensor *x, uint32_t n_tok, const block_norm *bn, float *resid) {
     if (!out || !w || !x || n_tok == 0 || !ensure_init()) return 0;
     const uint32_t E = w->n_expert, K = w->topk, D = w->in_dim, F = w->mid_dim;
     if (!w->router_bias || !w->gate || !w->up || !w->down || !w->sh_gate || !w->sh_up || !w->sh_down || E == 0 ||
@@ -1395,9 +1396,7 @@ static int moe_layer_impl(sf37_hip_tensor *out, sf37_hip_tensor *selected, sf37_
         sf37_hip_tensor xnt = {xn, bytes, 0}, *y = g_block_buf[1];
         return LAUNCH(SF37_HIP_STAGE_OTHER, sf37k_rms_norm(xn, (const float *)x->ptr, bn->norm_w, 1, D, n_tok, bn->eps, st),
                       "moe block rms_norm launch") &&
-               moe_layer_impl(y, selected, weights, w, logits_in, &xnt, n_tok, NULL) &&
-               LAUNCH(SF37_HIP_STAGE_ADD, sf37k_add_inplace((float *)out->ptr, (const float *)y->ptr, (uint64_t)n_tok * D, st),
-                      "moe block residual launch");
+               moe_layer_impl(y, selected, weights, w, logits_in, &xnt, n_tok, NULL, (float *)out->ptr);
     }
     if (fused) {
         dec_extra ex;
@@ -1460,6 +1459,9 @@ static int moe_layer_impl(sf37_hip_tensor *out, sf37_hip_tensor *selected, sf37_
     } else if (!routed_q8k(&a, routed, NULL, NULL, NULL, NULL, slots)) {
         return 0;
     }
+    if (resid)
+        return LAUNCH(SF37_HIP_STAGE_ADD, sf37k_add2_inplace(resid, (const float *)out->ptr, routed, (uint64_t)n_tok * D, st),
+                      "moe block residual launch");
     return LAUNCH(SF37_HIP_STAGE_ADD, sf37k_add_inplace((float *)out->ptr, routed, (uint64_t)n_tok * D, st), "moe_layer add launch");
 }
 
@@ -1475,7 +1477,7 @@ int sf37_hip_moe_block(sf37_hip_tensor *hidden, sf37_hip_tensor *normed, sf37_hi
     const void *nw = model_ptr(model_map, norm_offset, (uint64_t)w->in_dim * 2u, "ffn norm weight");
     if (!nw) return 0;
     const block_norm bn = {(const uint16_t *)nw, eps, normed ? (float *)normed->ptr : NULL};
-    return moe_layer_impl(hidden, selected, weights, w, logits_in, hidden, n_tok, &bn);
+    return moe_layer_impl(hidden, selected, weights, w, logits_in, hidden, n_tok, &bn, NULL);
 }
 
 int sf37_hip_moe_stack(sf37_hip_tensor *hidden, uint32_t n_layers, const sf37_hip_moe_layer_weights *layers,

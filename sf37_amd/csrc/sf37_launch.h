@@ -48,6 +48,8 @@ int sf37k_q8_0_matmul(float *out0, float *out1, const uint8_t *w0, const uint8_t
 int sf37k_swiglu(float *out, const float *gate, const float *up, uint64_t n, float clamp,
                  sf37_stream_t s);
 int sf37k_add_inplace(float *dst, const float *src, uint64_t n, sf37_stream_t s);
+/* dst = dst + (a + b): a layer's output (shared + routed) added to the hidden state. */
+int sf37k_add2_inplace(float *dst, const float *a, const float *b, uint64_t n, sf37_stream_t s);
 int sf37k_rms_norm(float *out, const float *x, const void *w, int w_is_bf16, uint32_t n,
                    uint32_t n_tok, float eps, sf37_stream_t s);
 
