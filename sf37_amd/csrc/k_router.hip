@@ -90,13 +90,21 @@ __device__ __forceinline__ void rm_mfma(rt_f64x4 (&acc)[2], const sf37_f32x4 (&a
             acc[c & 1u] = __builtin_amdgcn_mfma_f64_16x16x4f64((double)a[c][s], (double)b[c][s], acc[c & 1u], 0, 0, 0);
 }
 
+// Workgroups go to the 8 XCDs round-robin by id: XCD k takes the token
+// tiles t = k (mod 8) and walks them expert-tile by expert-tile, so its L2
+// holds one 64-row slice of W at a time and each x row is read by one XCD.
 __global__ void __launch_bounds__(256) f64mm_router_kernel(float *__restrict__ out, const float *__restrict__ w,
                                                            const float *__restrict__ x, uint32_t K, uint32_t E,
                                                            uint32_t T) {
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
-    const uint32_t e0 = (blockIdx.y * 4u + wave) * 16u;
+    const uint32_t nt = (T + 15u) / 16u, ne = (E + 63u) / 64u;
+    const uint32_t xcd = blockIdx.x & 7u, q = blockIdx.x >> 3;
+    const uint32_t ct = nt > xcd ? (nt - xcd + 7u) / 8u : 0u;      // token tiles of this XCD
+    if (q >= ct * ne) return;
+    const uint32_t et = q / ct, tt = xcd + 8u * (q - et * ct);
+    const uint32_t e0 = (et * 4u + wave) * 16u;
     if (e0 >= E) return;
-    const uint32_t t0 = blockIdx.x * 16u, i = lane & 15u, g = lane >> 4;
+    const uint32_t t0 = tt * 16u, i = lane & 15u, g = lane >> 4;
     const uint32_t tr = t0 + i < T ? t0 + i : T - 1u, er = e0 + i < E ? e0 + i : E - 1u;   // loads stay in bounds
     const float *xa = x + (uint64_t)tr * K + 4u * g;
     const float *wb = w + (uint64_t)er * K + 4u * g;
@@ -189,9 +197,9 @@ extern "C" int sf37k_f32_matmul(float *out, const float *w, const float *x, uint
         hipLaunchKernelGGL(f32_matvec_kernel, dim3((unsigned)out_dim, (unsigned)((n_tok + 7) / 8)),
                            dim3(256), 0, (hipStream_t)s, out, w, x, in_dim, out_dim, (uint32_t)n_tok);
     } else if (in_dim % 128u == 0 && in_dim <= 0xffffffffu && out_dim <= 0xffffffffu && n_tok <= 0xffffffffu) {
-        hipLaunchKernelGGL(f64mm_router_kernel, dim3((unsigned)((n_tok + 15) / 16), (unsigned)((out_dim + 63) / 64)),
-                           dim3(256), 0, (hipStream_t)s, out, w, x, (uint32_t)in_dim, (uint32_t)out_dim,
-                           (uint32_t)n_tok);
+        const uint64_t nt = (n_tok + 15) / 16, ne = (out_dim + 63) / 64;
+        hipLaunchKernelGGL(f64mm_router_kernel, dim3((unsigned)(8u * ((nt + 7) / 8) * ne)), dim3(256), 0,
+                           (hipStream_t)s, out, w, x, (uint32_t)in_dim, (uint32_t)out_dim, (uint32_t)n_tok);
     } else {
         hipLaunchKernelGGL(f32_matmul_kernel,
                            dim3((unsigned)((out_dim + RT_E - 1) / RT_E), (unsigned)((n_tok + RT_T - 1) / RT_T)),
