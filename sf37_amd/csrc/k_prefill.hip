@@ -226,6 +226,11 @@ __device__ __forceinline__ void lds_dma4(uint32_t lds, uint32_t voff, const void
                  : "memory", "m0");
 }
 __device__ __forceinline__ void wait_vm0() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+// All but the newest PF_DMA_PER_BLOCK vector-memory operations of the wave
+// done: the activation loads issued for the block after next stay in flight.
+constexpr int PF_DMA_PER_BLOCK = 5;   // 4 code rows + 1 table row per wave and block
+static_assert(PF_DMA_PER_BLOCK == 5, "the count in wait_vm_keep_next");
+__device__ __forceinline__ void wait_vm_keep_next() { asm volatile("s_waitcnt vmcnt(5)" ::: "memory"); }
 
 // After wait_vm0, mark a block's weight words as just defined: the compiler
 // then knows no load is pending on them and does not place its own
@@ -444,8 +449,8 @@ __device__ __forceinline__ void pf_body(const pf_params &p, const uint8_t *wrow,
 
 template <bool Q3>
 __global__ void __launch_bounds__(PF_WAVES * 64, 1) pf_expert_kernel(pf_params p) {
-    __shared__ __align__(16) uint8_t s_act[2][PF_ACT_BUF];
-    __shared__ __align__(16) float s_cd[2][PF_WAVES * PF_T];
+    __shared__ __align__(16) uint8_t s_act[3][PF_ACT_BUF];
+    __shared__ __align__(16) float s_cd[3][PF_WAVES * PF_T];
     __shared__ uint32_t s_pair[PF_T];
     __shared__ float s_w[PF_T];
     const uint32_t wg = blockIdx.x, xcd = wg & 7u, slot = wg >> 3;
@@ -477,7 +482,7 @@ __global__ void __launch_bounds__(PF_WAVES * 64, 1) pf_expert_kernel(pf_params p
     // row, lanes 32..63 slot t + 16's
     // slice `part` of `nparts` (compile-time after inlining) of block b's loads
     auto issue_act = [&](uint32_t b, int part, int nparts) {
-        const uint32_t bf = b & 1u;
+        const uint32_t bf = b % 3u;
         const uint8_t *cb = (const uint8_t *)p.act + (uint64_t)b * (SF37_QK * 2u);
         const int j0 = 4 * part / nparts, j1 = 4 * (part + 1) / nparts;
 #pragma unroll
@@ -518,12 +523,16 @@ __device__ __forceinline__ void pf_body(const pf_params &p, const uint8_t *wrow,
 #pragma unroll
         for (int r2 = 0; r2 < 16; r2++) acc[i][r2] = 0.0f;
 
-    issue_act(0, 0, 1);
-    // Each block's compute carries the next block's loads.  Past the last
-    // block the loads repeat block nblk-1 into the buffer no longer read
-    // (uniform code, no branch inside the stages); the final wait below
-    // keeps no load in flight at the end of the workgroup.
+    // Pipeline: a block's weight words (registers) are loaded one block
+    // ahead, its activation rows and tables (LDS, three buffers) two blocks
+    // ahead.  During block b: first the weights of b+1, then the activation
+    // loads of b+2 spread over the stages; at the top of block b+1 the wave
+    // waits for all but those newest PF_DMA_PER_BLOCK loads.  Past the last
+    // block the loads repeat block nblk-1 (its buffer then receives the same
+    // bytes again; uniform code, no branch inside the stages); the final
+    // wait below keeps no load in flight at the end of the workgroup.
     const uint32_t last = nblk - 1u;
+    auto clampb = [&](uint32_t x) { return x < nblk ? x : last; };
     if constexpr (Q3) {
         // blocks in pairs: even blocks start dword-aligned, odd blocks 2 bytes in
         q3_raw ra, rb;
@@ -531,24 +540,26 @@ __device__ __forceinline__ void pf_body(const pf_params &p, const uint8_t *wrow,
             const uint32_t o = SF37_Q3_BYTES * bn;
             q3_load(r, wrow + (o & ~3u), wrow + ((o + 12u + 12u * kh) & ~3u));
         };
+        issue_act(0, 0, 1);
         wload(ra, 0);
+        issue_act(clampb(1u), 0, 1);
         for (uint32_t b = 0; b < nblk; b += 2u) {
-            wait_vm0();
+            wait_vm_keep_next();
             raw_ready(ra);
             __syncthreads();
-            const uint32_t b1 = b + 1u < nblk ? b + 1u : last, b2 = b + 2u < nblk ? b + 2u : last;
-            pf_block<true, 0, NTB>(ra, s_act[b & 1u], s_cd[b & 1u], kh, col, acc, blk, [&](int c, int nc) {
-                issue_act(b1, c, nc);
+            const uint32_t b1 = clampb(b + 1u), b2 = clampb(b + 2u), b3 = clampb(b + 3u);
+            pf_block<true, 0, NTB>(ra, s_act[b % 3u], s_cd[b % 3u], kh, col, acc, blk, [&](int c, int nc) {
                 if (c == 0) wload(rb, b1);
+                issue_act(b2, c, nc);
             });
             if (b + 1u < nblk) {
-                wait_vm0();
+                wait_vm_keep_next();
                 raw_ready(rb);
                 __syncthreads();
-                pf_block<true, 16, NTB>(rb, s_act[(b + 1u) & 1u], s_cd[(b + 1u) & 1u], kh, col, acc, blk,
+                pf_block<true, 16, NTB>(rb, s_act[(b + 1u) % 3u], s_cd[(b + 1u) % 3u], kh, col, acc, blk,
                                         [&](int c, int nc) {
-                                            issue_act(b2, c, nc);
                                             if (c == 0) wload(ra, b2);
+                                            issue_act(b3, c, nc);
                                         });
             }
         }
@@ -558,24 +569,26 @@ __device__ __forceinline__ void pf_body(const pf_params &p, const uint8_t *wrow,
             const uint8_t *bp = wrow + (uint64_t)SF37_Q2_BYTES * bn;
             q2_load(r, bp, bp + 12u + 8u * kh);
         };
+        issue_act(0, 0, 1);
         wload(ra, 0);
+        issue_act(clampb(1u), 0, 1);
         for (uint32_t b = 0; b < nblk; b += 2u) {
-            wait_vm0();
+            wait_vm_keep_next();
             raw_ready(ra);
             __syncthreads();
-            const uint32_t b1 = b + 1u < nblk ? b + 1u : last, b2 = b + 2u < nblk ? b + 2u : last;
-            pf_block<false, 0, NTB>(ra, s_act[b & 1u], s_cd[b & 1u], kh, col, acc, blk, [&](int c, int nc) {
-                issue_act(b1, c, nc);
+            const uint32_t b1 = clampb(b + 1u), b2 = clampb(b + 2u), b3 = clampb(b + 3u);
+            pf_block<false, 0, NTB>(ra, s_act[b % 3u], s_cd[b % 3u], kh, col, acc, blk, [&](int c, int nc) {
                 if (c == 0) wload(rb, b1);
+                issue_act(b2, c, nc);
             });
             if (b + 1u < nblk) {
-                wait_vm0();
+                wait_vm_keep_next();
                 raw_ready(rb);
                 __syncthreads();
-                pf_block<false, 0, NTB>(rb, s_act[(b + 1u) & 1u], s_cd[(b + 1u) & 1u], kh, col, acc, blk,
+                pf_block<false, 0, NTB>(rb, s_act[(b + 1u) % 3u], s_cd[(b + 1u) % 3u], kh, col, acc, blk,
                                         [&](int c, int nc) {
-                                            issue_act(b2, c, nc);
                                             if (c == 0) wload(ra, b2);
+                                            issue_act(b3, c, nc);
                                         });
             }
         }
