@@ -58,7 +58,7 @@ using dec_params = sf37_dec_params;
 namespace {
 
 // Counters: the up kernel's item queues, then the down kernel's, 32 words
-// apart (zeroed by the select workgroup).
+// apart (zeroed by the route kernel's first workgroup).
 __device__ __forceinline__ uint32_t *up_queue(const dec_params &p, uint32_t q) { return p.cnt + 32u * q; }
 __device__ __forceinline__ uint32_t *dn_queue(const dec_params &p, uint32_t q) {
     return p.cnt + 32u * (UP_QUEUES + q);
@@ -126,6 +126,10 @@ __global__ void __launch_bounds__(256) dec_route_kernel(dec_params p, uint32_t n
     const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
     const uint32_t nb = p.K / SF37_QK;
     const bool norm = (p.flags & SF37_DEC_NORM) != 0u;
+    if (blockIdx.x == 0) {   // the up and down kernels' item queues
+        if (threadIdx.x < UP_QUEUES) *up_queue(p, threadIdx.x) = 0u;
+        if (threadIdx.x < DN_QUEUES) *dn_queue(p, threadIdx.x) = 0u;
+    }
     if (norm) {
         for (uint32_t t = wave; t < p.T; t += 4u) {
             const float sc = sf37_rms_scale_wave(p.x + (uint64_t)t * p.K, p.K, p.eps);
@@ -223,12 +227,16 @@ __global__ void __launch_bounds__(256) dec_route_kernel(dec_params p, uint32_t n
 // ---------------------------------------------------------------------------
 
 // Top-k of every token from the candidates (SELECT; else sel and wts are
-// inputs), then the (token, slot) pairs grouped by expert: ginfo and
-// sorted for the routed kernels.  One workgroup.
-__device__ void select_and_group(const dec_params &p) {
+// inputs), then the (token, slot) pairs grouped by expert: the group table
+// gi ([0] groups, [1..G+1] pair offsets, [G+2..2G+2) experts) and the
+// sorted pairs so, in the caller's LDS.  Every routed up workgroup runs it;
+// the one with publish also writes sel, wts, ginfo and sorted for the later
+// kernels.  All threads of the workgroup take part.
+__device__ void select_and_group(const dec_params &p, uint32_t *gi, uint32_t *so, bool publish) {
     __shared__ uint32_t s_sel[DEC_MAX_TOK * 16];    // selected expert ids (raw)
     __shared__ uint32_t s_e[DEC_MAX_TOK * 16];      // clamped ids, pair order
     __shared__ uint32_t s_se[DEC_MAX_TOK * 16];     // clamped ids, sorted order
+    __shared__ float s_wts[DEC_MAX_TOK * 16];
     __shared__ uint32_t s_wcnt[4];
     const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
     const uint32_t P = p.T * p.topk;
@@ -238,17 +246,20 @@ __device__ void select_and_group(const dec_params &p) {
             const uint32_t t2 = t + 4u < p.T ? t + 4u : t;
             const uint64_t *k0 = p.cand_key + (uint64_t)t * p.E, *k1 = p.cand_key + (uint64_t)t2 * p.E;
             const float *p0 = p.cand_p + (uint64_t)t * p.E, *p1 = p.cand_p + (uint64_t)t2 * p.E;
-            int32_t *so[2] = {(int32_t *)s_sel + t * p.topk, (int32_t *)s_sel + t2 * p.topk};
-            float *wo[2] = {p.wts + (uint64_t)t * p.topk, p.wts + (uint64_t)t2 * p.topk};
+            int32_t *sl[2] = {(int32_t *)s_sel + t * p.topk, (int32_t *)s_sel + t2 * p.topk};
+            float *wo[2] = {s_wts + t * p.topk, s_wts + t2 * p.topk};
             sf37_wave_topk_cand<2>(
                 [k0, k1, p0, p1](uint32_t k, uint32_t e, float &pr) {
                     pr = (k ? p1 : p0)[e];
                     return (k ? k1 : k0)[e];
                 },
-                p.E, p.topk, p.scale, so, wo);
+                p.E, p.topk, p.scale, sl, wo);
         }
         __syncthreads();
-        if (threadIdx.x < P) p.sel[threadIdx.x] = (int32_t)s_sel[threadIdx.x];
+        if (publish && threadIdx.x < P) {
+            p.sel[threadIdx.x] = (int32_t)s_sel[threadIdx.x];
+            p.wts[threadIdx.x] = s_wts[threadIdx.x];
+        }
     } else if (threadIdx.x < P) {
         s_sel[threadIdx.x] = (uint32_t)p.sel[threadIdx.x];
     }
@@ -257,13 +268,22 @@ __device__ void select_and_group(const dec_params &p) {
     if (p.flags & SF37_DEC_SLOTS) {
         if (threadIdx.x < p.topk) {
             const uint32_t s = threadIdx.x;
-            p.sorted[s] = s;
-            p.ginfo[1u + s] = s;
-            p.ginfo[2u + p.G + s] = s_e[s];
+            so[s] = s;
+            gi[1u + s] = s;
+            gi[2u + p.G + s] = s_e[s];
+            if (publish) {
+                p.sorted[s] = s;
+                p.ginfo[1u + s] = s;
+                p.ginfo[2u + p.G + s] = s_e[s];
+            }
         }
         if (threadIdx.x == 0) {
-            p.ginfo[0] = p.topk;
-            p.ginfo[1u + p.topk] = p.topk;
+            gi[0] = p.topk;
+            gi[1u + p.topk] = p.topk;
+            if (publish) {
+                p.ginfo[0] = p.topk;
+                p.ginfo[1u + p.topk] = p.topk;
+            }
         }
         return;
     }
@@ -277,7 +297,8 @@ __device__ void select_and_group(const dec_params &p) {
             const uint32_t f = s_e[q];
             pos += (uint32_t)(f < e) + ((uint32_t)(f == e) & (uint32_t)(q < i));
         }
-        p.sorted[pos] = i;
+        so[pos] = i;
+        if (publish) p.sorted[pos] = i;
         s_se[pos] = e;
     }
     __syncthreads();
@@ -294,31 +315,32 @@ __device__ void select_and_group(const dec_params &p) {
     uint32_t base = 0;
     for (uint32_t w = 0; w < wave; w++) base += s_wcnt[w];
     if (start) {
-        p.ginfo[1u + base + below] = i;
-        p.ginfo[2u + p.G + base + below] = e;
+        gi[1u + base + below] = i;
+        gi[2u + p.G + base + below] = e;
+        if (publish) {
+            p.ginfo[1u + base + below] = i;
+            p.ginfo[2u + p.G + base + below] = e;
+        }
     }
     if (i == P - 1u) {
         const uint32_t ng = base + below + (start ? 1u : 0u);
-        p.ginfo[0] = ng;
-        p.ginfo[1u + ng] = P;
+        gi[0] = ng;
+        gi[1u + ng] = P;
+        if (publish) {
+            p.ginfo[0] = ng;
+            p.ginfo[1u + ng] = P;
+        }
     }
 }
 
-// Workgroup 0: select_and_group.  Workgroups 1.. (with the shared expert):
-// SH_RS shared gate/up rows each - the weight tiles copied to LDS while the
-// x blocks of the first 8 tokens load, the terms in LDS, then the
+// Shared gate/up workgroup wg (the leading workgroups of the up launch):
+// SH_RS shared gate/up rows - the weight tiles copied to LDS while the x
+// blocks of the first 8 tokens load, the terms in LDS, then the
 // reference's sequential block sum per (matrix, token, row)
 // (sf37_ops.c:92-108) into sh_gu.
-__global__ void __launch_bounds__(256) dec_select_kernel(dec_params p) {
-    if (blockIdx.x == 0) {
-        if (threadIdx.x < UP_QUEUES) *up_queue(p, threadIdx.x) = 0u;
-        if (threadIdx.x < DN_QUEUES) *dn_queue(p, threadIdx.x) = 0u;
-        select_and_group(p);
-        return;
-    }
-    extern __shared__ __align__(16) unsigned char smem[];
+__device__ void shared_gate_up(const dec_params &p, uint32_t wg, unsigned char *smem) {
     const uint32_t nb8 = p.K / 32u;
-    const uint32_t row0 = (blockIdx.x - 1u) * SH_RS;
+    const uint32_t row0 = wg * SH_RS;
     const uint32_t tbytes = up_shared_tile(p.K), wbuf = tile_buf(tbytes);
     const uint64_t row_bytes = (uint64_t)nb8 * SF37_Q8_0_BYTES;
     uint8_t *wl = smem;                                             // gate tile | up tile
@@ -589,19 +611,27 @@ __device__ void shared_down_pass(const dec_params &p, const int8_t *xq, const fl
 // take more of them and all finish together.  A wave asks for its first
 // dynamic item while computing its last static one; the next item's blocks
 // are always loaded while the current one is computed.
-__global__ void __launch_bounds__(256) dec_up_kernel(dec_params p) {
+// Workgroups [0, n_sh): shared gate/up rows.  The rest: the routed items,
+// after each has formed the top-k and the grouping itself (the first one
+// publishing them).
+__global__ void __launch_bounds__(256) dec_up_kernel(dec_params p, uint32_t n_sh) {
     extern __shared__ __align__(16) unsigned char smem[];
+    if (blockIdx.x < n_sh) {
+        shared_gate_up(p, blockIdx.x, smem);
+        return;
+    }
+    const uint32_t wg = blockIdx.x - n_sh, n_wg = gridDim.x - n_sh;
     const uint32_t nbK = p.K / SF37_QK, P = p.T * p.topk;
     act_lds_t *xs = (act_lds_t *)smem;
     uint32_t *gi = (uint32_t *)(xs + p.T * nbK);
     uint32_t *so = gi + 3u + 2u * p.G;
     uint32_t *xo = so + P;                                        // first x block of each sorted pair's token
-    for (uint32_t i = threadIdx.x; i < 3u + 2u * p.G; i += blockDim.x) gi[i] = p.ginfo[i];
+    select_and_group(p, gi, so, wg == 0u);
     __syncthreads();
 
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const uint32_t nw = gridDim.x * (blockDim.x >> 6), gw = blockIdx.x * (blockDim.x >> 6) + wave;
+    const uint32_t nw = n_wg * (blockDim.x >> 6), gw = wg * (blockDim.x >> 6) + wave;
     const uint32_t m = lane >> 5, rr = (lane >> 4) & 1u, b = lane & 15u;
     const uint32_t bl = b < nbK ? b : nbK - 1u;                    // lanes past the row repeat its last block
     const bool out_lane = b == nbK - 1u;
@@ -647,11 +677,7 @@ __global__ void __launch_bounds__(256) dec_up_kernel(dec_params p) {
         const uint32_t blk = i / A16, c = i - blk * A16;
         ((u32x4 *)xs)[blk * L16 + c] = ((const u32x4 *)p.xq)[i];
     }
-    for (uint32_t i = threadIdx.x; i < P; i += blockDim.x) {
-        const uint32_t pr = p.sorted[i];
-        so[i] = pr;
-        xo[i] = (pr / p.topk) * nbK;
-    }
+    for (uint32_t i = threadIdx.x; i < P; i += blockDim.x) xo[i] = (so[i] / p.topk) * nbK;
     __syncthreads();
     if (cur >= q1) return;
     for (;;) {
@@ -1047,9 +1073,10 @@ dec_shape dec_plan(const dec_params &p) {
     d.n_xq = (p.T * nb + 3u) / 4u;
     d.lds_up = lds_up_routed(p.K, p.T, p.G, p.T * p.topk);
     d.lds_shup = lds_up_shared(p.K, p.T);
-    d.n_shup = 1u + (sh ? p.F / SH_RS : 0u);           // select workgroup + shared rows
+    d.n_shup = sh ? p.F / SH_RS : 0u;                  // shared gate/up workgroups of the up launch
     // persistent kernels: exactly as many workgroups as can be resident
-    const uint32_t up_res = resident_wgs((const void *)dec_up_kernel, 256, d.lds_up);
+    const size_t up_lds = d.lds_up > d.lds_shup || !d.n_shup ? d.lds_up : d.lds_shup;
+    const uint32_t up_res = resident_wgs((const void *)dec_up_kernel, 256, up_lds);
     d.n_up = (p.up_wgs && p.up_wgs < up_res ? p.up_wgs : up_res) * cus;
     d.n_mid = (p.T * p.topk * (p.F / SF37_QK) + (sh ? (p.T * (p.F / 32u) + 1u) / 2u : 0u) + 3u) / 4u;
     d.lds_dn = sh ? (size_t)p.T * p.F + (size_t)p.T * (p.F / 32u) * 4u : 0u;
@@ -1095,22 +1122,13 @@ extern "C" int sf37k_decode_route(const sf37_dec_params *pp, sf37_stream_t s) {
     return (int)hipGetLastError();
 }
 
-extern "C" int sf37k_decode_select(const sf37_dec_params *pp, sf37_stream_t s) {
-    const dec_shape d = dec_plan(*pp);
-    const size_t lds = (pp->flags & SF37_DEC_SHARED) ? d.lds_shup : 0u;
-    static size_t opted = 65536;
-    const int err = set_lds((const void *)dec_select_kernel, lds, &opted);
-    if (err) return err;
-    hipLaunchKernelGGL(dec_select_kernel, dim3(d.n_shup), dim3(256), lds, (hipStream_t)s, *pp);
-    return (int)hipGetLastError();
-}
-
 extern "C" int sf37k_decode_up(const sf37_dec_params *pp, sf37_stream_t s) {
     const dec_shape d = dec_plan(*pp);
+    const size_t lds = d.lds_up > d.lds_shup || !d.n_shup ? d.lds_up : d.lds_shup;
     static size_t opted = 65536;
-    const int err = set_lds((const void *)dec_up_kernel, d.lds_up, &opted);
+    const int err = set_lds((const void *)dec_up_kernel, lds, &opted);
     if (err) return err;
-    hipLaunchKernelGGL(dec_up_kernel, dim3(d.n_up), dim3(256), d.lds_up, (hipStream_t)s, *pp);
+    hipLaunchKernelGGL(dec_up_kernel, dim3(d.n_shup + d.n_up), dim3(256), lds, (hipStream_t)s, *pp, d.n_shup);
     return (int)hipGetLastError();
 }
 

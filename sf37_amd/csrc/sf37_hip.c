@@ -1145,7 +1145,6 @@ static int decode_run(const routed_args *a, const dec_extra *ex, float *out, flo
     p.cnt = cnt;
     const sf37_stream_t st = (sf37_stream_t)g_stream;
     return LAUNCH(SF37_HIP_STAGE_DEC_ROUTE, sf37k_decode_route(&p, st), "decode route launch") &&
-           LAUNCH(SF37_HIP_STAGE_DEC_SELECT, sf37k_decode_select(&p, st), "decode select launch") &&
            LAUNCH(SF37_HIP_STAGE_DEC_UP, sf37k_decode_up(&p, st), "decode up launch") &&
            LAUNCH(SF37_HIP_STAGE_DEC_MID, sf37k_decode_mid(&p, st), "decode mid launch") &&
            LAUNCH(SF37_HIP_STAGE_DEC_DOWN, sf37k_decode_down(&p, st), "decode down launch") &&

@@ -184,7 +184,6 @@ int sf37k_decode_counters(uint32_t T, uint32_t topk, uint32_t E, uint32_t K, uin
 int sf37k_decode_supported(uint32_t T, uint32_t topk, uint32_t E, uint32_t K, uint32_t F, int shared);
 /* The launches, in this order on one stream. */
 int sf37k_decode_route(const sf37_dec_params *p, sf37_stream_t s);
-int sf37k_decode_select(const sf37_dec_params *p, sf37_stream_t s);
 int sf37k_decode_up(const sf37_dec_params *p, sf37_stream_t s);
 int sf37k_decode_mid(const sf37_dec_params *p, sf37_stream_t s);
 int sf37k_decode_down(const sf37_dec_params *p, sf37_stream_t s);
