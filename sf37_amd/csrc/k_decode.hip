@@ -611,9 +611,22 @@ __device__ void shared_down_pass(const dec_params &p, const int8_t *xq, const fl
 // take more of them and all finish together.  A wave asks for its first
 // dynamic item while computing its last static one; the next item's blocks
 // are always loaded while the current one is computed.
-// Workgroups [0, n_sh): shared gate/up rows.  The rest: the routed items,
-// after each has formed the top-k and the grouping itself (the first one
-// publishing them).
+// Select launch (batches of more tokens): workgroup 0 forms the top-k and
+// the grouping; workgroups 1.. the shared gate/up rows.
+__global__ void __launch_bounds__(256) dec_select_kernel(dec_params p) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    if (blockIdx.x == 0) {
+        __shared__ uint32_t s_gi[3u + 2u * DEC_MAX_TOK * 16u], s_so[DEC_MAX_TOK * 16u];
+        select_and_group(p, s_gi, s_so, true);
+        return;
+    }
+    shared_gate_up(p, blockIdx.x - 1u, smem);
+}
+
+// With UPSEL (few tokens, no select launch): workgroups [0, n_sh) run the
+// shared gate/up rows, the rest the routed items after each has formed the
+// top-k and the grouping itself (the first one publishing them).  Without:
+// the routed items, the grouping read from the select launch.
 __global__ void __launch_bounds__(256) dec_up_kernel(dec_params p, uint32_t n_sh) {
     extern __shared__ __align__(16) unsigned char smem[];
     if (blockIdx.x < n_sh) {
@@ -626,7 +639,12 @@ __global__ void __launch_bounds__(256) dec_up_kernel(dec_params p, uint32_t n_sh
     uint32_t *gi = (uint32_t *)(xs + p.T * nbK);
     uint32_t *so = gi + 3u + 2u * p.G;
     uint32_t *xo = so + P;                                        // first x block of each sorted pair's token
-    select_and_group(p, gi, so, wg == 0u);
+    if (p.flags & SF37_DEC_UPSEL) {
+        select_and_group(p, gi, so, wg == 0u);
+    } else {
+        for (uint32_t i = threadIdx.x; i < 3u + 2u * p.G; i += blockDim.x) gi[i] = p.ginfo[i];
+        for (uint32_t i = threadIdx.x; i < P; i += blockDim.x) so[i] = p.sorted[i];
+    }
     __syncthreads();
 
     const uint32_t lane = threadIdx.x & 63u;
@@ -1073,9 +1091,9 @@ dec_shape dec_plan(const dec_params &p) {
     d.n_xq = (p.T * nb + 3u) / 4u;
     d.lds_up = lds_up_routed(p.K, p.T, p.G, p.T * p.topk);
     d.lds_shup = lds_up_shared(p.K, p.T);
-    d.n_shup = sh ? p.F / SH_RS : 0u;                  // shared gate/up workgroups of the up launch
+    d.n_shup = sh ? p.F / SH_RS : 0u;                  // shared gate/up workgroups (select or up launch)
     // persistent kernels: exactly as many workgroups as can be resident
-    const size_t up_lds = d.lds_up > d.lds_shup || !d.n_shup ? d.lds_up : d.lds_shup;
+    const size_t up_lds = d.lds_up > d.lds_shup || !d.n_shup || !(p.flags & SF37_DEC_UPSEL) ? d.lds_up : d.lds_shup;
     const uint32_t up_res = resident_wgs((const void *)dec_up_kernel, 256, up_lds);
     d.n_up = (p.up_wgs && p.up_wgs < up_res ? p.up_wgs : up_res) * cus;
     d.n_mid = (p.T * p.topk * (p.F / SF37_QK) + (sh ? (p.T * (p.F / 32u) + 1u) / 2u : 0u) + 3u) / 4u;
@@ -1122,13 +1140,25 @@ extern "C" int sf37k_decode_route(const sf37_dec_params *pp, sf37_stream_t s) {
     return (int)hipGetLastError();
 }
 
+extern "C" int sf37k_decode_select(const sf37_dec_params *pp, sf37_stream_t s) {
+    const dec_shape d = dec_plan(*pp);
+    static size_t opted = 65536;
+    const int err = set_lds((const void *)dec_select_kernel, d.n_shup ? d.lds_shup : 0u, &opted);
+    if (err) return err;
+    hipLaunchKernelGGL(dec_select_kernel, dim3(1u + d.n_shup), dim3(256), d.n_shup ? d.lds_shup : 0u, (hipStream_t)s,
+                       *pp);
+    return (int)hipGetLastError();
+}
+
 extern "C" int sf37k_decode_up(const sf37_dec_params *pp, sf37_stream_t s) {
     const dec_shape d = dec_plan(*pp);
-    const size_t lds = d.lds_up > d.lds_shup || !d.n_shup ? d.lds_up : d.lds_shup;
+    const bool upsel = (pp->flags & SF37_DEC_UPSEL) != 0u;
+    const uint32_t n_sh = upsel ? d.n_shup : 0u;
+    const size_t lds = d.lds_up > d.lds_shup || !n_sh ? d.lds_up : d.lds_shup;
     static size_t opted = 65536;
     const int err = set_lds((const void *)dec_up_kernel, lds, &opted);
     if (err) return err;
-    hipLaunchKernelGGL(dec_up_kernel, dim3(d.n_shup + d.n_up), dim3(256), lds, (hipStream_t)s, *pp, d.n_shup);
+    hipLaunchKernelGGL(dec_up_kernel, dim3(n_sh + d.n_up), dim3(256), lds, (hipStream_t)s, *pp, n_sh);
     return (int)hipGetLastError();
 }
 

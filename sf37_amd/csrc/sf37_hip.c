@@ -50,7 +50,7 @@ static int64_t g_opt_q8k_min_rows = 512;
 static int64_t g_opt_write_gate_up = 0;
 static int64_t g_opt_decode = 1;
 static int64_t g_opt_router_always = 0;
-static int64_t g_opt_up_dyn_pct = 25, g_opt_up_wgs = 0, g_opt_dn_wgs = 0;
+static int64_t g_opt_up_dyn_pct = 25, g_opt_up_wgs = 0, g_opt_dn_wgs = 0, g_opt_upsel_max_tok = 1;
 static int64_t g_opt_prefill = 1;
 static int64_t g_opt_prefill_min_pairs = 256;
 static int64_t g_opt_shared_min_tok = 64;
@@ -308,6 +308,7 @@ int sf37_hip_set_option(const char *name, int64_t value) {
     else if (!strcmp(name, "decode_up_dyn_pct")) g_opt_up_dyn_pct = value < 0 ? 0 : (value > 100 ? 100 : value);
     else if (!strcmp(name, "decode_up_wgs")) g_opt_up_wgs = value < 0 ? 0 : value;
     else if (!strcmp(name, "decode_down_wgs")) g_opt_dn_wgs = value < 0 ? 0 : value;
+    else if (!strcmp(name, "decode_select_in_up_max_tokens")) g_opt_upsel_max_tok = value < 0 ? 0 : value;
     else if (!strcmp(name, "prefill_mfma")) g_opt_prefill = value ? 1 : 0;
     else if (!strcmp(name, "prefill_min_pairs")) g_opt_prefill_min_pairs = value < 0 ? 0 : value;
     else if (!strcmp(name, "shared_min_tokens")) g_opt_shared_min_tok = value < 0 ? 0 : value;
@@ -325,6 +326,7 @@ int64_t sf37_hip_get_option(const char *name) {
     if (!strcmp(name, "decode_up_dyn_pct")) return g_opt_up_dyn_pct;
     if (!strcmp(name, "decode_up_wgs")) return g_opt_up_wgs;
     if (!strcmp(name, "decode_down_wgs")) return g_opt_dn_wgs;
+    if (!strcmp(name, "decode_select_in_up_max_tokens")) return g_opt_upsel_max_tok;
     if (!strcmp(name, "prefill_mfma")) return g_opt_prefill;
     if (!strcmp(name, "prefill_min_pairs")) return g_opt_prefill_min_pairs;
     if (!strcmp(name, "shared_min_tokens")) return g_opt_shared_min_tok;
@@ -1058,7 +1060,7 @@ static int decode_run(const routed_args *a, const dec_extra *ex, float *out, flo
     p.scale = ex->scale;
     p.clamp_routed = a->clamp;
     p.clamp_shared = ex->clamp_shared;
-    p.flags = ex->flags;
+    p.flags = ex->flags | ((uint64_t)T <= (uint64_t)g_opt_upsel_max_tok ? SF37_DEC_UPSEL : 0u);
     p.x = a->x;
     p.router_w = ex->router_w;
     p.router_bias = ex->router_bias;
@@ -1145,6 +1147,8 @@ static int decode_run(const routed_args *a, const dec_extra *ex, float *out, flo
     p.cnt = cnt;
     const sf37_stream_t st = (sf37_stream_t)g_stream;
     return LAUNCH(SF37_HIP_STAGE_DEC_ROUTE, sf37k_decode_route(&p, st), "decode route launch") &&
+           ((p.flags & SF37_DEC_UPSEL) ||
+            LAUNCH(SF37_HIP_STAGE_DEC_SELECT, sf37k_decode_select(&p, st), "decode select launch")) &&
            LAUNCH(SF37_HIP_STAGE_DEC_UP, sf37k_decode_up(&p, st), "decode up launch") &&
            LAUNCH(SF37_HIP_STAGE_DEC_MID, sf37k_decode_mid(&p, st), "decode mid launch") &&
            LAUNCH(SF37_HIP_STAGE_DEC_DOWN, sf37k_decode_down(&p, st), "decode down launch") &&

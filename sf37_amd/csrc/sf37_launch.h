@@ -146,6 +146,7 @@ int sf37k_sh_down(float *out, const void *d16, const float *ds, const void *a16,
 #define SF37_DEC_SLOTS 8u    /* one group per slot of a single token */
 #define SF37_DEC_NORM 16u    /* x is the hidden state: RMSNorm(w + 1) by the route kernel */
 #define SF37_DEC_RESID 32u   /* out += layer output (out is the hidden state) */
+#define SF37_DEC_UPSEL 64u   /* no select launch: the up launch forms the top-k and runs the shared gate/up */
 #define SF37_DEC_ACT_BYTES 288u  /* activation block: 256 codes, d, 4 sums, pad */
 typedef struct sf37_dec_params {
     uint32_t T, E, K, F, topk, G;
@@ -184,6 +185,7 @@ int sf37k_decode_counters(uint32_t T, uint32_t topk, uint32_t E, uint32_t K, uin
 int sf37k_decode_supported(uint32_t T, uint32_t topk, uint32_t E, uint32_t K, uint32_t F, int shared);
 /* The launches, in this order on one stream. */
 int sf37k_decode_route(const sf37_dec_params *p, sf37_stream_t s);
+int sf37k_decode_select(const sf37_dec_params *p, sf37_stream_t s);   /* skipped with UPSEL */
 int sf37k_decode_up(const sf37_dec_params *p, sf37_stream_t s);
 int sf37k_decode_mid(const sf37_dec_params *p, sf37_stream_t s);
 int sf37k_decode_down(const sf37_dec_params *p, sf37_stream_t s);
