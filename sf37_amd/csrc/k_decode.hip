@@ -1,9 +1,11 @@
 // k_decode.hip - the MoE layer for decode batches (up to 16 tokens) on
-// gfx950, in six launches on one stream:
+// gfx950, in six launches on one stream (five for a single token, where
+// the up launch takes the select work):
 //
 //   route   : router GEMV (binary64 accumulation) and each expert's
 //             selection candidate (sigmoid, key), the Q8_K / Q8_0
-//             quantisation of x.
+//             quantisation of x (optionally RMSNorm of x first); zeroes the
+//             item queues.
 //   select  : one workgroup runs top-k for every token and groups the
 //             (token, slot) pairs by expert; the others compute the shared
 //             expert's Q8_0 gate/up rows (LDS tiles).
@@ -15,7 +17,8 @@
 //   down    : routed Q2 down, one row per pair and output row, then the
 //             shared expert's down rows from atomic queues (they fill the
 //             routed part's tail).
-//   combine : out = shared + sum over slots in slot order.
+//   combine : out = shared + sum over slots in slot order (optionally added
+//             to the hidden state).
 //
 // Nothing waits on another wave, so every wave always runs to completion;
 // the up and down kernels' queues hand out each item once and every wave
