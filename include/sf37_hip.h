@@ -297,6 +297,30 @@ int sf37_hip_moe_stack(sf37_hip_tensor *hidden, uint32_t n_layers,
                        const sf37_hip_tensor *const *logits,
                        sf37_hip_tensor *const *selected, uint32_t n_tok);
 
+/* GGUF weight residency (the engine's reader, sf37.c:506-604, and MoE
+ * tensor contract, sf37.c:1760-1782).  sf37_hip_gguf_open maps a GGUF v3
+ * file read-only; sf37_hip_gguf_from_map parses a mapping the engine already
+ * holds (the map pointer is then the model map of the _mapped calls).  Both
+ * return NULL (with a stderr line) for a file that is not GGUF v3, a
+ * truncated or malformed header, or a tensor outside the file.  Parsing
+ * needs no GPU.  sf37_hip_gguf_tensor gives a tensor's absolute map offset,
+ * bytes (0 for types the MoE path does not read), GGUF type id and up to 4
+ * dims (unused dims 1).  sf37_hip_gguf_bind_moe_layer makes layer il's MoE
+ * tensors device-resident and fills w for sf37_hip_moe_layer /
+ * sf37_hip_moe_block (shapes read from the file and cross-checked; top-k 8,
+ * scale 3.0, the layer's SwiGLU clamps) and the offset of its
+ * post_attention_layernorm weights; the handles in w stay valid until
+ * sf37_hip_gguf_close. */
+typedef struct sf37_hip_gguf sf37_hip_gguf;
+sf37_hip_gguf *sf37_hip_gguf_open(const char *path);
+sf37_hip_gguf *sf37_hip_gguf_from_map(const void *map, uint64_t size);
+void sf37_hip_gguf_close(sf37_hip_gguf *gguf);
+const void *sf37_hip_gguf_map(const sf37_hip_gguf *gguf, uint64_t *size);
+int sf37_hip_gguf_tensor(const sf37_hip_gguf *gguf, const char *name, uint64_t *offset,
+                         uint64_t *bytes, uint32_t *type, uint32_t *ndim, uint64_t *dims);
+int sf37_hip_gguf_bind_moe_layer(sf37_hip_gguf *gguf, uint32_t il,
+                                 sf37_hip_moe_layer_weights *w, uint64_t *post_norm_offset);
+
 /* Stage timing with HIP events, the counterpart of the reference's
  * SF37_CUDA_MOE_PROFILE (sf37_cuda.cu:345-449).  While enabled, every kernel
  * the library launches is bracketed by events on the launch stream;

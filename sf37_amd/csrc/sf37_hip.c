@@ -464,6 +464,15 @@ static const void *model_ptr(const void *model_map, uint64_t offset, uint64_t by
     return g_ranges[g_nranges - 1].dev;
 }
 
+/* A non-owning tensor over the device copy of map[offset, offset+bytes)
+ * (registered or cached now), for the GGUF layer binder (sf37_gguf.c). */
+sf37_hip_tensor *sf37i_map_tensor(const void *model_map, uint64_t model_size, uint64_t offset, uint64_t bytes,
+                                  const char *label) {
+    if (!model_map || !bytes || !mapped_range_ok(model_size, offset, bytes) || !ensure_init()) return NULL;
+    void *dev = (void *)model_ptr(model_map, offset, bytes, label);
+    return dev ? tensor_new(dev, bytes, 0) : NULL;
+}
+
 int sf37_hip_set_model_fd(int fd) {
     g_model_fd = fd;   /* weights are uploaded from the map; the fd is not needed */
     return 1;

@@ -95,6 +95,13 @@ _SIGS = {
     "sf37_hip_q8k_quantize": (C.c_int, [T, T, u32, u32]),
     "sf37_hip_moe_dispatch": (C.c_int, [T, T, T, T, u32, u32]),
     "sf37_hip_moe_layer": (C.c_int, [T, T, T, C.POINTER(LayerWeights), T, T, u32]),
+    "sf37_hip_gguf_open": (vp, [C.c_char_p]),
+    "sf37_hip_gguf_from_map": (vp, [vp, u64]),
+    "sf37_hip_gguf_close": (None, [vp]),
+    "sf37_hip_gguf_map": (vp, [vp, C.POINTER(u64)]),
+    "sf37_hip_gguf_tensor": (C.c_int, [vp, C.c_char_p, C.POINTER(u64), C.POINTER(u64), C.POINTER(u32),
+                                       C.POINTER(u32), C.POINTER(u64)]),
+    "sf37_hip_gguf_bind_moe_layer": (C.c_int, [vp, u32, C.POINTER(LayerWeights), C.POINTER(u64)]),
     "sf37_hip_moe_block": (C.c_int, [T, T, T, T, C.POINTER(LayerWeights), vp, u64, u64, f32, T, u32]),
     "sf37_hip_moe_stack": (C.c_int, [T, u32, C.POINTER(LayerWeights), vp, u64, C.POINTER(u64), f32, C.POINTER(T),
                                      C.POINTER(T), u32]),
