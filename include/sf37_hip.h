@@ -310,7 +310,8 @@ int sf37_hip_moe_stack(sf37_hip_tensor *hidden, uint32_t n_layers,
  * sf37_hip_moe_block (shapes read from the file and cross-checked; top-k 8,
  * scale 3.0, the layer's SwiGLU clamps) and the offset of its
  * post_attention_layernorm weights; the handles in w stay valid until
- * sf37_hip_gguf_close. */
+ * sf37_hip_gguf_close, which (for a handle from sf37_hip_gguf_open) also
+ * drops the device copies of that mapping before unmapping it. */
 typedef struct sf37_hip_gguf sf37_hip_gguf;
 sf37_hip_gguf *sf37_hip_gguf_open(const char *path);
 sf37_hip_gguf *sf37_hip_gguf_from_map(const void *map, uint64_t size);

@@ -9,7 +9,8 @@
  * (Q8_0) and `post_attention_layernorm.weight` (BF16).  The weights become
  * device-resident copies of their map ranges (the same registry the _mapped
  * calls resolve against), so a bound layer runs through sf37_hip_moe_layer /
- * sf37_hip_moe_block with the map as its model map.
+ * sf37_hip_moe_block with the map as its model map.  Closing a handle that
+ * mapped the file itself also drops the device copies of that mapping.
  */
 #include <errno.h>
 #include <fcntl.h>
@@ -25,6 +26,7 @@
 
 sf37_hip_tensor *sf37i_map_tensor(const void *model_map, uint64_t model_size, uint64_t offset, uint64_t bytes,
                                   const char *label);
+void sf37i_drop_map(const void *model_map);
 
 enum { GG_F32 = 0, GG_F16 = 1, GG_Q8_0 = 8, GG_Q2D = 10, GG_Q3GU = 11, GG_BF16 = 30 };
 enum { GV_U8, GV_I8, GV_U16, GV_I16, GV_U32, GV_I32, GV_F32, GV_BOOL, GV_STR, GV_ARR, GV_U64, GV_I64, GV_F64 };
@@ -125,6 +127,9 @@ static void gg_free(sf37_hip_gguf *g) {
     for (uint64_t i = 0; g->t && i < g->n_tensors; i++) free(g->t[i].name);
     free(g->t);
     if (g->fd >= 0) {
+        /* the device copies are keyed by the map address, which a later
+         * mapping may reuse: drop them with the mapping */
+        sf37i_drop_map(g->map);
         munmap((void *)g->map, (size_t)g->size);
         close(g->fd);
     }

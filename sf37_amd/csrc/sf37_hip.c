@@ -464,6 +464,23 @@ static const void *model_ptr(const void *model_map, uint64_t offset, uint64_t by
     return g_ranges[g_nranges - 1].dev;
 }
 
+/* Forget every range of one host map (registered or cached), freeing the
+ * device copies the library made: a map about to be unmapped, whose address
+ * a later mapping may reuse. */
+void sf37i_drop_map(const void *model_map) {
+    if (!g_init || !model_map) return;
+    (void)hipStreamSynchronize(g_stream);
+    size_t w = 0;
+    for (size_t i = 0; i < g_nranges; i++) {
+        if (g_ranges[i].map == (const uint8_t *)model_map) {
+            if (g_ranges[i].owned && g_ranges[i].dev) (void)hipFree(g_ranges[i].dev);
+        } else {
+            g_ranges[w++] = g_ranges[i];
+        }
+    }
+    g_nranges = w;
+}
+
 /* A non-owning tensor over the device copy of map[offset, offset+bytes)
  * (registered or cached now), for the GGUF layer binder (sf37_gguf.c). */
 sf37_hip_tensor *sf37i_map_tensor(const void *model_map, uint64_t model_size, uint64_t offset, uint64_t bytes,
