@@ -309,6 +309,34 @@ __global__ void __launch_bounds__(256) combine_kernel(float *__restrict__ out,
     out[i] = acc;
 }
 
+// The same slot-order sum, four outputs per thread (out_dim % 4 == 0,
+// topk <= 16): every slot's float4 is loaded before the first add.
+__global__ void __launch_bounds__(256) combine4_kernel(float *__restrict__ out,
+                                                       const float *__restrict__ down_pair,
+                                                       uint32_t topk, uint32_t out_dim,
+                                                       uint32_t n_tok) {
+    const uint64_t i = ((uint64_t)blockIdx.x * 256u + threadIdx.x) * 4u;
+    if (i >= (uint64_t)out_dim * n_tok) return;
+    const uint64_t t = i / out_dim, r = i - t * out_dim;
+    float4 v[16];
+#pragma unroll
+    for (uint32_t s = 0; s < 16u; s++) {
+        const uint32_t sc = s < topk ? s : 0u;   // every load in bounds
+        v[s] = *(const float4 *)(down_pair + (t * topk + sc) * out_dim + r);
+    }
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+    for (uint32_t s = 0; s < 16u; s++) {
+        if (s < topk) {
+            acc.x = acc.x + v[s].x;
+            acc.y = acc.y + v[s].y;
+            acc.z = acc.z + v[s].z;
+            acc.w = acc.w + v[s].w;
+        }
+    }
+    *(float4 *)(out + i) = acc;
+}
+
 // ---------------------------------------------------------------------------
 // fp32-activation path (sf37_cuda.cu:5089-5267): one workgroup per
 // (row, slot); lanes stride over the elements, tree reduction in LDS.
@@ -454,8 +482,14 @@ extern "C" int sf37k_moe_combine(float *out, const float *down_pair, uint32_t to
                                  uint32_t n_tok, sf37_stream_t s) {
     const uint64_t n = (uint64_t)out_dim * n_tok;
     if (n == 0) return 0;
-    hipLaunchKernelGGL(combine_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)s,
-                       out, down_pair, topk, out_dim, n_tok);
+    if (out_dim % 4u == 0 && topk >= 1u && topk <= 16u && ((uintptr_t)out & 15u) == 0 && ((uintptr_t)down_pair & 15u) == 0) {
+        const uint64_t n4 = n / 4u;
+        hipLaunchKernelGGL(combine4_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, (hipStream_t)s,
+                           out, down_pair, topk, out_dim, n_tok);
+    } else {
+        hipLaunchKernelGGL(combine_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)s,
+                           out, down_pair, topk, out_dim, n_tok);
+    }
     return (int)hipGetLastError();
 }
 
