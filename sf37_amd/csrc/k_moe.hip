@@ -297,24 +297,33 @@ __global__ void __launch_bounds__(256) down_kernel(float *__restrict__ down_pair
     }
 }
 
-__global__ void __launch_bounds__(256) combine_kernel(float *__restrict__ out,
-                                                      const float *__restrict__ down_pair,
-                                                      uint32_t topk, uint32_t out_dim,
-                                                      uint32_t n_tok) {
+// out = [base +] sum over slots in slot order; with resid (MODE 2):
+// resid = resid + (base + sum).  MODE 0: plain sum, 1: base +, 2: resid.
+template <int MODE>
+__device__ __forceinline__ void combine_store(float *out, const float *base, float *resid, uint64_t i, float v) {
+    if constexpr (MODE == 0) out[i] = v;
+    else if constexpr (MODE == 1) out[i] = base[i] + v;
+    else resid[i] = resid[i] + (base[i] + v);
+}
+
+template <int MODE>
+__global__ void __launch_bounds__(256) combine_kernel(float *out, const float *__restrict__ down_pair,
+                                                      const float *base, float *resid, uint32_t topk,
+                                                      uint32_t out_dim, uint32_t n_tok) {
     const uint64_t i = (uint64_t)blockIdx.x * 256u + threadIdx.x;
     if (i >= (uint64_t)out_dim * n_tok) return;
     const uint64_t t = i / out_dim, r = i - t * out_dim;
     float acc = 0.0f;
     for (uint32_t s = 0; s < topk; s++) acc = acc + down_pair[(t * topk + s) * out_dim + r];
-    out[i] = acc;
+    combine_store<MODE>(out, base, resid, i, acc);
 }
 
-// The same slot-order sum, four outputs per thread (out_dim % 4 == 0,
-// topk <= 16): every slot's float4 is loaded before the first add.
-__global__ void __launch_bounds__(256) combine4_kernel(float *__restrict__ out,
-                                                       const float *__restrict__ down_pair,
-                                                       uint32_t topk, uint32_t out_dim,
-                                                       uint32_t n_tok) {
+// The same, four outputs per thread (out_dim % 4 == 0, 1 <= topk <= 16):
+// every slot's float4 is loaded before the first add.
+template <int MODE>
+__global__ void __launch_bounds__(256) combine4_kernel(float *out, const float *__restrict__ down_pair,
+                                                       const float *base, float *resid, uint32_t topk,
+                                                       uint32_t out_dim, uint32_t n_tok) {
     const uint64_t i = ((uint64_t)blockIdx.x * 256u + threadIdx.x) * 4u;
     if (i >= (uint64_t)out_dim * n_tok) return;
     const uint64_t t = i / out_dim, r = i - t * out_dim;
@@ -334,7 +343,10 @@ __global__ void __launch_bounds__(256) combine4_kernel(float *__restrict__ out,
             acc.w = acc.w + v[s].w;
         }
     }
-    *(float4 *)(out + i) = acc;
+    combine_store<MODE>(out, base, resid, i, acc.x);
+    combine_store<MODE>(out, base, resid, i + 1u, acc.y);
+    combine_store<MODE>(out, base, resid, i + 2u, acc.z);
+    combine_store<MODE>(out, base, resid, i + 3u, acc.w);
 }
 
 // ---------------------------------------------------------------------------
@@ -478,17 +490,22 @@ extern "C" int sf37k_moe_down(float *down_pair, const uint8_t *down_w, const voi
     return (int)hipGetLastError();
 }
 
-extern "C" int sf37k_moe_combine(float *out, const float *down_pair, uint32_t topk, uint32_t out_dim,
-                                 uint32_t n_tok, sf37_stream_t s) {
+extern "C" int sf37k_moe_combine(float *out, const float *down_pair, const float *base, float *resid,
+                                 uint32_t topk, uint32_t out_dim, uint32_t n_tok, sf37_stream_t s) {
     const uint64_t n = (uint64_t)out_dim * n_tok;
     if (n == 0) return 0;
-    if (out_dim % 4u == 0 && topk >= 1u && topk <= 16u && ((uintptr_t)out & 15u) == 0 && ((uintptr_t)down_pair & 15u) == 0) {
-        const uint64_t n4 = n / 4u;
-        hipLaunchKernelGGL(combine4_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, (hipStream_t)s,
-                           out, down_pair, topk, out_dim, n_tok);
+    const int mode = resid ? 2 : (base ? 1 : 0);
+    if ((resid || base) && !base) return (int)hipErrorInvalidValue;
+    const bool vec = out_dim % 4u == 0 && topk >= 1u && topk <= 16u && ((uintptr_t)down_pair & 15u) == 0;
+    const dim3 grid((unsigned)(((vec ? n / 4u : n) + 255) / 256));
+    if (vec) {
+        if (mode == 0) hipLaunchKernelGGL(combine4_kernel<0>, grid, dim3(256), 0, (hipStream_t)s, out, down_pair, base, resid, topk, out_dim, n_tok);
+        else if (mode == 1) hipLaunchKernelGGL(combine4_kernel<1>, grid, dim3(256), 0, (hipStream_t)s, out, down_pair, base, resid, topk, out_dim, n_tok);
+        else hipLaunchKernelGGL(combine4_kernel<2>, grid, dim3(256), 0, (hipStream_t)s, out, down_pair, base, resid, topk, out_dim, n_tok);
     } else {
-        hipLaunchKernelGGL(combine_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)s,
-                           out, down_pair, topk, out_dim, n_tok);
+        if (mode == 0) hipLaunchKernelGGL(combine_kernel<0>, grid, dim3(256), 0, (hipStream_t)s, out, down_pair, base, resid, topk, out_dim, n_tok);
+        else if (mode == 1) hipLaunchKernelGGL(combine_kernel<1>, grid, dim3(256), 0, (hipStream_t)s, out, down_pair, base, resid, topk, out_dim, n_tok);
+        else hipLaunchKernelGGL(combine_kernel<2>, grid, dim3(256), 0, (hipStream_t)s, out, down_pair, base, resid, topk, out_dim, n_tok);
     }
     return (int)hipGetLastError();
 }

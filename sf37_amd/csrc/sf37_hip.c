@@ -840,6 +840,8 @@ typedef struct {
     float clamp;
     const float *x;
     uint32_t n_tok;
+    const float *comb_base;   /* combine: out = comb_base + sum (may be out) */
+    float *comb_resid;        /* combine: comb_resid += comb_base + sum instead */
 } routed_args;
 
 /* Scratch of the Q8_K routed pipeline; mid/down_pair/gate/up may point
@@ -964,7 +966,7 @@ static int routed_pf(const routed_args *a, const routed_scratch *s, float *out, 
            LAUNCH(SF37_HIP_STAGE_PF_DOWN, sf37k_pf_down(down_pair, a->down_w, s->m16, s->mtabs, s->tiles, s->sorted,
                                                        max_tiles, tstride, a->mid_dim, a->out_dim, st),
                   "routed_moe mfma down launch") &&
-           LAUNCH(SF37_HIP_STAGE_COMBINE, sf37k_moe_combine(out, down_pair, a->topk, a->out_dim, a->n_tok, st),
+           LAUNCH(SF37_HIP_STAGE_COMBINE, sf37k_moe_combine(out, down_pair, a->comb_base, a->comb_resid, a->topk, a->out_dim, a->n_tok, st),
                   "routed_moe combine launch");
 }
 
@@ -1009,7 +1011,7 @@ static int routed_q8k(const routed_args *a, float *out, float *mid, float *down_
                                   a->out_dim, st),
                    "routed_moe q8k down launch"))
         return 0;
-    return LAUNCH(SF37_HIP_STAGE_COMBINE, sf37k_moe_combine(out, down_pair, a->topk, a->out_dim, a->n_tok, st),
+    return LAUNCH(SF37_HIP_STAGE_COMBINE, sf37k_moe_combine(out, down_pair, a->comb_base, a->comb_resid, a->topk, a->out_dim, a->n_tok, st),
                      "routed_moe combine launch");
 }
 
@@ -1193,7 +1195,7 @@ static int routed_f32(const routed_args *a, float *out, float *mid, float *down_
                                       a->n_expert, st),
                    "routed_moe down launch"))
         return 0;
-    return LAUNCH(SF37_HIP_STAGE_COMBINE, sf37k_moe_combine(out, down_slot, a->topk, a->out_dim, 1, st), "routed_moe sum launch");
+    return LAUNCH(SF37_HIP_STAGE_COMBINE, sf37k_moe_combine(out, down_slot, NULL, NULL, a->topk, a->out_dim, 1, st), "routed_moe sum launch");
 }
 
 static int routed_one_impl(sf37_hip_tensor *out, sf37_hip_tensor *gate, sf37_hip_tensor *up,
@@ -1485,8 +1487,11 @@ static int moe_layer_impl(sf37_hip_tensor *out, sf37_hip_tensor *selected, sf37_
         if (n_tok != 1u) return 0;
         if (!routed_f32(&a, routed, (float *)ls[5]->ptr, (float *)ls[5]->ptr + (uint64_t)K * F, NULL, NULL))
             return 0;
-    } else if (!routed_q8k(&a, routed, NULL, NULL, NULL, NULL, slots)) {
-        return 0;
+    } else {
+        /* the routed combine adds the shared rows (and the residual) itself */
+        a.comb_base = (const float *)out->ptr;
+        a.comb_resid = resid;
+        return routed_q8k(&a, (float *)out->ptr, NULL, NULL, NULL, NULL, slots);
     }
     if (resid)
         return LAUNCH(SF37_HIP_STAGE_ADD, sf37k_add2_inplace(resid, (const float *)out->ptr, routed, (uint64_t)n_tok * D, st),

@@ -65,8 +65,10 @@ int sf37k_moe_down(float *down_pair, const uint8_t *down_w, const void *midq,
                    const uint32_t *group_info, const uint32_t *sorted_pairs,
                    uint32_t max_groups, uint32_t max_group_pairs, uint32_t mid_dim,
                    uint32_t out_dim, sf37_stream_t s);
-int sf37k_moe_combine(float *out, const float *down_pair, uint32_t topk, uint32_t out_dim,
-                      uint32_t n_tok, sf37_stream_t s);
+/* Slot-order sum of the per-pair rows: out = [base +] sum (base may be out);
+ * with resid, resid = resid + (base + sum) instead and out is not written. */
+int sf37k_moe_combine(float *out, const float *down_pair, const float *base, float *resid, uint32_t topk,
+                      uint32_t out_dim, uint32_t n_tok, sf37_stream_t s);
 /* Build the groups from selected experts: stable counting sort of pairs by
  * expert.  group_info layout: [0] = n_groups, [1 .. 1+E] = group pair
  * offsets, [2+E .. 2+2E) = group experts; counts/offsets per expert also. */
