@@ -90,11 +90,11 @@ def small_stack(H):
     S.free()
 
 
-@pytest.mark.parametrize("n_tok", [3, 40])
+@pytest.mark.parametrize("n_tok", [1, 3, 16, 17, 40])
 def test_small_stack_vs_oracle(H, O, small_stack, n_tok):
-    """sf37_hip_moe_stack (fused norm + residual at 3 tokens, rms_norm +
-    layer + add at 40) and the per-layer entry points, both against the
-    oracle."""
+    """sf37_hip_moe_stack (fused norm + residual up to 16 tokens, the
+    single-token variant at 1, rms_norm + layer + one residual add above) and
+    the per-layer entry points, both against the oracle."""
     from sf37_amd import configs
     S = small_stack
     for k in ("q8k_min_rows", "prefill_min_pairs", "shared_min_tokens"):
@@ -113,6 +113,8 @@ def test_small_stack_vs_oracle(H, O, small_stack, n_tok):
             H.lib().sf37_hip_profile_enable(0)
         if n_tok > 16:
             assert prof["pf_gate_up"][1] == S.n_layers and prof["sh_gate_up"][1] == S.n_layers
+            # the routed combine adds the shared rows (and, in the stack call, the residual)
+            assert prof["add"][1] == (0 if native else S.n_layers), prof["add"]
         else:
             assert prof["dec_up"][1] == S.n_layers
             # the stack call's decode launches take the norm and the residual
