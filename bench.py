@@ -116,7 +116,7 @@ def main():
         return
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only; --gpus {args.gpus} is not supported "
-              "(expert parallelism across GPUs is described in DESIGN.md, not built)", file=sys.stderr)
+              "(expert parallelism across GPUs is a design, not built)", file=sys.stderr)
         sys.exit(2)
 
     from sf37_amd import configs, hip, moe
