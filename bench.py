@@ -230,6 +230,13 @@ def main():
         cpu_layer = moe.SynthLayer(seed=moe.layer_seed(args.seed, 0))
         cpu = cpu_baseline(cpu_layer, xs[0], sels[0], step_bytes[0], n_tok, args.cpu_seconds)
         cpu_layer.free()
+        if cpu and prefill:
+            # the CPU engine has no batch path (sf37.c:7786-7797): a prefill chunk
+            # runs the same per-token layer, so its tokens/s/layer is 1 / (time per token)
+            for pf in prefill:
+                pf["cpu_baseline"] = {"value": round(1e3 / cpu["ms_per_token"], 2), "unit": "tokens/s/layer",
+                                      "cores": 1, "kind": cpu["kind"],
+                                      "sample": "the per-token time of the decode cpu_baseline (same path)"}
 
     stages = {k: {"ms_per_launch": round(v[0] / max(v[1], 1), 5), "launches": v[1]} for k, v in prof.items() if v[1]}
     line = {
@@ -450,6 +457,7 @@ def cpu_baseline(layer, x_dev, sel, step_bytes, n_tok, budget_s):
     except OSError:
         pass
     return {"value": round(step_bytes / dt / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": kind,
+            "ms_per_token": round(dt * 1e3 / n_tok, 3),
             "sample": f"{reps} x one 8-token decode step of layer 0 through the reference CPU MoE path "
                       f"(layer_moe_ffn composition, sf37.c:2127-2194), {dt * 1e3:.1f} ms/step on {cpu_model}"}
 
