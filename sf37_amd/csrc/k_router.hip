@@ -127,19 +127,27 @@ __global__ void __launch_bounds__(256) f64mm_router_kernel(float *__restrict__ o
 }
 
 // The same product with both operands staged in LDS: a workgroup owns 32
-// tokens x 64 experts and walks K in 64-wide chunks (x and W rows copied
-// with float4 loads, the next chunk held in registers while the current one
-// is consumed); wave w takes tokens 16(w & 1).. and experts 32(w >> 1)..,
-// two MFMA tiles sharing the token operand.  Rows are padded by four floats
-// so a step's 16 rows x 4 columns fall in distinct banks.  K % 128 == 0.
-constexpr uint32_t RL_T = 32, RL_E = 64, RL_K = 64, RL_P = RL_K + 4;
+// tokens x RL_E experts (64, or 96: 288 = 3 x 96 has no padded expert
+// columns and needs fewer workgroups) and walks K in 64-wide chunks (x and W
+// rows copied with float4 loads, the next chunk held in registers while the
+// current one is consumed); wave w takes tokens 16(w & 1).. and experts
+// RL_E/2 (w >> 1).., RL_E/32 MFMA tiles sharing the token operand.  Rows are
+// padded by four floats so a step's 16 rows x 4 columns fall in distinct
+// banks.  K % 128 == 0.  The expert tile is chosen per call by the number of
+// rounds of one workgroup per CU each shape needs (a CU running two of these
+// workgroups takes twice as long; a 96-expert workgroup takes 1.5x a 64-expert
+// one).
+constexpr uint32_t RL_T = 32, RL_K = 64, RL_P = RL_K + 4;
 #ifndef RL_MIN_TOK
 #define RL_MIN_TOK 1024u   // smaller batches keep the register kernel (more workgroups)
 #endif
 
+template <uint32_t RL_E>
 __global__ void __launch_bounds__(256) f64mm_router_lds_kernel(float *__restrict__ out, const float *__restrict__ w,
                                                                const float *__restrict__ x, uint32_t K, uint32_t E,
                                                                uint32_t T) {
+    static_assert(RL_T == 32 && RL_E % 32 == 0 && RL_K % 32 == 0, "copy: 32 rows x 8 float4 lanes per pass");
+    constexpr uint32_t RL_WT = RL_E / 32u;     // W rows per copying thread
     __shared__ float xs[2][RL_T * RL_P];
     __shared__ float ws[2][RL_E * RL_P];
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
@@ -149,20 +157,24 @@ __global__ void __launch_bounds__(256) f64mm_router_lds_kernel(float *__restrict
     if (q >= ct * ne) return;
     const uint32_t et = q / ct, tt = xcd + 8u * (q - et * ct);
     const uint32_t t0 = tt * RL_T, e0 = et * RL_E;
-    // copy assignments: x row tid/8 (float4 tid%8); W rows tid/8 and 32 + tid/8
+    // copy assignments: x row tid/8 (float4 tid%8); W rows 32m + tid/8
     const uint32_t cr = tid >> 3, cc = (tid & 7u) * 4u;
     const uint32_t xr = t0 + cr < T ? t0 + cr : T - 1u;               // loads stay in bounds
-    const uint32_t wr0 = e0 + cr < E ? e0 + cr : E - 1u, wr1 = e0 + 32u + cr < E ? e0 + 32u + cr : E - 1u;
     const float *xp = x + (uint64_t)xr * K + cc;
-    const float *wp0 = w + (uint64_t)wr0 * K + cc, *wp1 = w + (uint64_t)wr1 * K + cc;
+    const float *wp[RL_WT];
+#pragma unroll
+    for (uint32_t m = 0; m < RL_WT; m++) {
+        const uint32_t wr = e0 + 32u * m + cr < E ? e0 + 32u * m + cr : E - 1u;
+        wp[m] = w + (uint64_t)wr * K + cc;
+    }
     constexpr uint32_t NC = RL_K / 32u;    // float4 columns per thread and row
-    sf37_f32x4 rx[NC], rw0[NC], rw1[NC];
+    sf37_f32x4 rx[NC], rw[RL_WT][NC];
     auto fetch = [&](uint32_t ko) {
 #pragma unroll
         for (uint32_t c = 0; c < NC; c++) {
             rx[c] = *(const sf37_f32x4 *)(xp + ko + 32u * c);
-            rw0[c] = *(const sf37_f32x4 *)(wp0 + ko + 32u * c);
-            rw1[c] = *(const sf37_f32x4 *)(wp1 + ko + 32u * c);
+#pragma unroll
+            for (uint32_t m = 0; m < RL_WT; m++) rw[m][c] = *(const sf37_f32x4 *)(wp[m] + ko + 32u * c);
         }
     };
     auto stage = [&](uint32_t buf) {
@@ -171,27 +183,31 @@ __global__ void __launch_bounds__(256) f64mm_router_lds_kernel(float *__restrict
 #pragma unroll
             for (int j = 0; j < 4; j++) {
                 xs[buf][cr * RL_P + 32u * c + cc + j] = rx[c][j];
-                ws[buf][cr * RL_P + 32u * c + cc + j] = rw0[c][j];
-                ws[buf][(32u + cr) * RL_P + 32u * c + cc + j] = rw1[c][j];
+#pragma unroll
+                for (uint32_t m = 0; m < RL_WT; m++) ws[buf][(32u * m + cr) * RL_P + 32u * c + cc + j] = rw[m][c][j];
             }
     };
     fetch(0);
     stage(0);
     __syncthreads();
     const uint32_t i = lane & 15u, g = lane >> 4;
-    const uint32_t ta = (wave & 1u) * 16u + i, eb = (wave >> 1) * 32u + i;
-    rt_f64x4 acc[2] = {{0.0, 0.0, 0.0, 0.0}, {0.0, 0.0, 0.0, 0.0}};
+    constexpr uint32_t NT = RL_E / 32u;    // 16-expert MFMA tiles per wave
+    const uint32_t ta = (wave & 1u) * 16u + i, eb = (wave >> 1) * (RL_E / 2u) + i;
+    rt_f64x4 acc[NT];
+#pragma unroll
+    for (uint32_t h = 0; h < NT; h++) acc[h] = rt_f64x4{0.0, 0.0, 0.0, 0.0};
     const uint32_t nk = K / RL_K;
     for (uint32_t kc = 0; kc < nk; kc++) {
         const uint32_t buf = kc & 1u;
         if (kc + 1u < nk) fetch((kc + 1u) * RL_K);
         const float *xa = &xs[buf][ta * RL_P + g];
-        const float *wa = &ws[buf][eb * RL_P + g], *wb = &ws[buf][(eb + 16u) * RL_P + g];
+        const float *wa = &ws[buf][eb * RL_P + g];
 #pragma unroll
         for (uint32_t s4 = 0; s4 < RL_K; s4 += 4u) {
             const double a = (double)xa[s4];
-            acc[0] = __builtin_amdgcn_mfma_f64_16x16x4f64(a, (double)wa[s4], acc[0], 0, 0, 0);
-            acc[1] = __builtin_amdgcn_mfma_f64_16x16x4f64(a, (double)wb[s4], acc[1], 0, 0, 0);
+#pragma unroll
+            for (uint32_t h = 0; h < NT; h++)
+                acc[h] = __builtin_amdgcn_mfma_f64_16x16x4f64(a, (double)wa[16u * h * RL_P + s4], acc[h], 0, 0, 0);
         }
         if (kc + 1u < nk) {
             stage(buf ^ 1u);
@@ -200,8 +216,8 @@ __global__ void __launch_bounds__(256) f64mm_router_lds_kernel(float *__restrict
     }
     // D: lane l holds rows l/16 + 4r (tokens), column l%16 (expert)
 #pragma unroll
-    for (uint32_t h = 0; h < 2u; h++) {
-        const uint32_t e = e0 + (wave >> 1) * 32u + 16u * h + i;
+    for (uint32_t h = 0; h < NT; h++) {
+        const uint32_t e = e0 + (wave >> 1) * (RL_E / 2u) + 16u * h + i;
 #pragma unroll
         for (uint32_t r = 0; r < 4; r++) {
             const uint32_t t = t0 + (wave & 1u) * 16u + g + 4u * r;
@@ -272,6 +288,17 @@ __global__ void __launch_bounds__(256) router_select_kernel(int32_t *__restrict_
     sf37_wave_topk<1>([lg](uint32_t, uint32_t e) { return lg[e]; }, bias, n_experts, topk, scale, tab, so, wo, po);
 }
 
+uint32_t router_cus() {
+    static int cus = 0;
+    if (!cus) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+            cus = 256;
+    }
+    return (uint32_t)cus;
+}
+
 }  // namespace
 
 extern "C" int sf37k_f32_matmul(float *out, const float *w, const float *x, uint64_t in_dim,
@@ -282,9 +309,15 @@ extern "C" int sf37k_f32_matmul(float *out, const float *w, const float *x, uint
                            dim3(256), 0, (hipStream_t)s, out, w, x, in_dim, out_dim, (uint32_t)n_tok);
     } else if (in_dim % 128u == 0 && in_dim <= 0xffffffffu && out_dim <= 0xffffffffu && n_tok <= 0xffffffffu &&
                n_tok >= RL_MIN_TOK) {
-        const uint64_t nt = (n_tok + RL_T - 1) / RL_T, ne = (out_dim + RL_E - 1) / RL_E;
-        hipLaunchKernelGGL(f64mm_router_lds_kernel, dim3((unsigned)(8u * ((nt + 7) / 8) * ne)), dim3(256), 0,
-                           (hipStream_t)s, out, w, x, (uint32_t)in_dim, (uint32_t)out_dim, (uint32_t)n_tok);
+        const uint64_t nt = (n_tok + RL_T - 1) / RL_T, cus = router_cus();
+        const uint64_t ne64 = (out_dim + 63) / 64, ne96 = (out_dim + 95) / 96;
+        const uint64_t r64 = (nt * ne64 + cus - 1) / cus, r96 = (nt * ne96 + cus - 1) / cus;
+        if (3u * r96 < 2u * r64)
+            hipLaunchKernelGGL(f64mm_router_lds_kernel<96>, dim3((unsigned)(8u * ((nt + 7) / 8) * ne96)), dim3(256),
+                               0, (hipStream_t)s, out, w, x, (uint32_t)in_dim, (uint32_t)out_dim, (uint32_t)n_tok);
+        else
+            hipLaunchKernelGGL(f64mm_router_lds_kernel<64>, dim3((unsigned)(8u * ((nt + 7) / 8) * ne64)), dim3(256),
+                               0, (hipStream_t)s, out, w, x, (uint32_t)in_dim, (uint32_t)out_dim, (uint32_t)n_tok);
     } else if (in_dim % 128u == 0 && in_dim <= 0xffffffffu && out_dim <= 0xffffffffu && n_tok <= 0xffffffffu) {
         const uint64_t nt = (n_tok + 15) / 16, ne = (out_dim + 63) / 64;
         hipLaunchKernelGGL(f64mm_router_kernel, dim3((unsigned)(8u * ((nt + 7) / 8) * ne)), dim3(256), 0,

@@ -175,10 +175,11 @@ def test_qlow_small_shapes_fp32_and_q8k_paths(H, O):
 def test_f32_router_gemv_and_gemm(H, O, layer):
     """Router logits accumulate in binary64 like the CPU engine
     (sf37.c:1970-1976); the summation order differs, so <= 1 ulp.  1 and 3
-    tokens: the GEMV kernel; 40: the register fp64-MFMA kernel; 1100: the
-    LDS-staged one (a partial 32-token tile)."""
+    tokens: the GEMV kernel; 40: the register fp64-MFMA kernel; 1100 and
+    2000: the LDS-staged one with 64- and 96-expert workgroups (partial
+    32-token tiles)."""
     wr = layer.router.read(np.float32)
-    for n_tok in (1, 3, 40, 1100):
+    for n_tok in (1, 3, 40, 1100, 2000):
         x = np.random.default_rng(n_tok).standard_normal((n_tok, K)).astype(np.float32)
         out = H.Tensor.alloc(n_tok * E * 4)
         if n_tok == 1:
