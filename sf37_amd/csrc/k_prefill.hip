@@ -732,19 +732,25 @@ __device__ __forceinline__ void sh_chunk(const sh_raw &r, const uint8_t *act_lds
         typedef uint32_t u4 __attribute__((ext_vector_type(4)));
         const u4 t0 = {r.w[j][0], r.w[j][1], r.w[j][2], r.w[j][3]};
         const u4 t1 = {r.w[j][4], r.w[j][5], r.w[j][6], r.w[j][7]};
+        // the MFMAs of every token block first, so the epilogue of one block
+        // runs while the matrix cores still work on the next
+        f16v D[SH_TB];
 #pragma unroll
         for (uint32_t i = 0; i < SH_TB; i++) {
             const uint8_t *ap = a_lane + i * 32u * SH_RS + j * 64u;
-            f16v D = {};
-            D = __builtin_amdgcn_mfma_f32_32x32x16_f16(*(const h8 *)ap, __builtin_bit_cast(h8, t0), D, 0, 0, 0);
-            D = __builtin_amdgcn_mfma_f32_32x32x16_f16(*(const h8 *)(ap + 16), __builtin_bit_cast(h8, t1), D, 0, 0, 0);
+            D[i] = f16v{};
+            D[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(*(const h8 *)ap, __builtin_bit_cast(h8, t0), D[i], 0, 0, 0);
+            D[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(*(const h8 *)(ap + 16), __builtin_bit_cast(h8, t1), D[i], 0, 0, 0);
+        }
+#pragma unroll
+        for (uint32_t i = 0; i < SH_TB; i++) {
 #pragma unroll
             for (int jj = 0; jj < 4; jj++) {
                 const float4 xv = *(const float4 *)(x_lane + j * SH_T + 32u * i + 8u * jj);
                 const float xa[4] = {xv.x, xv.y, xv.z, xv.w};
 #pragma unroll
                 for (int q = 0; q < 4; q++) {
-                    const float t = D[4 * jj + q] * r.s[j] * xa[q];
+                    const float t = D[i][4 * jj + q] * r.s[j] * xa[q];
                     acc[i][4 * jj + q] = acc[i][4 * jj + q] + t;
                 }
             }
