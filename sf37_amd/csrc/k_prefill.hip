@@ -206,7 +206,11 @@ __global__ void __launch_bounds__(256) pf_tab_sort_kernel(float *__restrict__ ta
 // so the compiler does not wait for them before unrelated LDS reads; the
 // kernel waits with s_waitcnt vmcnt(0) + barrier before reading the buffer.
 // Lane i of a dwordx4 load writes LDS bytes [m0 + 16 i, m0 + 16 i + 16);
-// one wait state separates the M0 write from the load.
+// one wait state separates the M0 write from the load.  The compiler ignores
+// the "m0" clobber (it warns that m0 is reserved), so these sequences rely on
+// no compiler-generated code of these kernels reading m0: in the gfx950
+// assembly of this file every m0 access is one of these s_mov_b32 writes (no
+// movrel, gpr-index or sendmsg use).
 // ---------------------------------------------------------------------------
 // sbase must be wave-uniform; it is moved to SGPRs with readfirstlane.
 __device__ __forceinline__ uint64_t sgpr_ptr(const void *p) {

@@ -1246,7 +1246,7 @@ int sf37_hip_routed_moe_one(sf37_hip_tensor *out, sf37_hip_tensor *gate, sf37_hi
     if (moe_gate->bytes < gb || moe_up->bytes < gb || moe_down->bytes < db) return 0;
     routed_args a = {(const uint8_t *)moe_gate->ptr, (const uint8_t *)moe_up->ptr, (const uint8_t *)moe_down->ptr,
                      (const int32_t *)selected->ptr, (const float *)weights->ptr, n_total_expert, topk, in_dim,
-                     expert_mid_dim, out_dim, clamp, (const float *)x->ptr, 1};
+                     expert_mid_dim, out_dim, clamp, (const float *)x->ptr, 1, NULL, NULL};
     return routed_one_impl(out, gate, up, mid, down, &a);
 }
 
@@ -1276,7 +1276,7 @@ int sf37_hip_routed_moe_one_mapped(sf37_hip_tensor *out, sf37_hip_tensor *gate, 
                               expert_mid_dim, out_dim, x, 1))
         return 0;
     routed_args a = {NULL, NULL, NULL, (const int32_t *)selected->ptr, (const float *)weights->ptr, n_total_expert,
-                     topk, in_dim, expert_mid_dim, out_dim, clamp, (const float *)x->ptr, 1};
+                     topk, in_dim, expert_mid_dim, out_dim, clamp, (const float *)x->ptr, 1, NULL, NULL};
     if (!resolve_experts(model_map, model_size, gate_offset, up_offset, down_offset, n_total_expert, in_dim,
                          expert_mid_dim, out_dim, &a.gate_w, &a.up_w, &a.down_w))
         return 0;
@@ -1295,7 +1295,7 @@ int sf37_hip_routed_moe_batch_mapped(sf37_hip_tensor *out, sf37_hip_tensor *gate
                               expert_mid_dim, out_dim, x, n_tok))
         return 0;
     routed_args a = {NULL, NULL, NULL, (const int32_t *)selected->ptr, (const float *)weights->ptr, n_total_expert,
-                     topk, in_dim, expert_mid_dim, out_dim, clamp, (const float *)x->ptr, n_tok};
+                     topk, in_dim, expert_mid_dim, out_dim, clamp, (const float *)x->ptr, n_tok, NULL, NULL};
     if (!resolve_experts(model_map, model_size, gate_offset, up_offset, down_offset, n_total_expert, in_dim,
                          expert_mid_dim, out_dim, &a.gate_w, &a.up_w, &a.down_w))
         return 0;
@@ -1413,7 +1413,7 @@ static int moe_layer_impl(sf37_hip_tensor *out, sf37_hip_tensor *selected, sf37_
     const sf37_stream_t st = (sf37_stream_t)g_stream;
     const int run_router = !logits_in || (g_opt_router_always && w->router);
     routed_args a = {(const uint8_t *)w->gate->ptr, (const uint8_t *)w->up->ptr, (const uint8_t *)w->down->ptr, NULL,
-                     NULL, E, K, D, F, D, w->clamp_routed, (const float *)x->ptr, n_tok};
+                     NULL, E, K, D, F, D, w->clamp_routed, (const float *)x->ptr, n_tok, NULL, NULL};
     const int fused = decode_eligible(&a, SF37_DEC_SELECT | SF37_DEC_SHARED);
     if (bn && !fused) {
         const uint64_t bytes = (uint64_t)n_tok * D * 4u;
