@@ -206,11 +206,11 @@ __global__ void __launch_bounds__(256) pf_tab_sort_kernel(float *__restrict__ ta
 // so the compiler does not wait for them before unrelated LDS reads; the
 // kernel waits with s_waitcnt vmcnt(0) + barrier before reading the buffer.
 // Lane i of a dwordx4 load writes LDS bytes [m0 + 16 i, m0 + 16 i + 16);
-// one wait state separates the M0 write from the load.  The compiler ignores
-// the "m0" clobber (it warns that m0 is reserved), so these sequences rely on
-// no compiler-generated code of these kernels reading m0: in the gfx950
-// assembly of this file every m0 access is one of these s_mov_b32 writes (no
-// movrel, gpr-index or sendmsg use).
+// one wait state separates the M0 write from the load.  m0 cannot be named
+// as a clobber (the compiler reserves it and drops such a clobber), so these
+// sequences rely on no compiler-generated code of these kernels reading m0:
+// in the gfx950 assembly of this file every m0 access is one of these
+// s_mov_b32 writes (no movrel, gpr-index or sendmsg use).
 // ---------------------------------------------------------------------------
 // sbase must be wave-uniform; it is moved to SGPRs with readfirstlane.
 __device__ __forceinline__ uint64_t sgpr_ptr(const void *p) {
@@ -222,12 +222,12 @@ __device__ __forceinline__ uint64_t sgpr_ptr(const void *p) {
 __device__ __forceinline__ void lds_dma16(uint32_t lds, uint32_t voff, const void *sbase) {
     asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(__builtin_amdgcn_readfirstlane(lds)),
                  "v"(voff), "s"(sgpr_ptr(sbase))
-                 : "memory", "m0");
+                 : "memory");
 }
 __device__ __forceinline__ void lds_dma4(uint32_t lds, uint32_t voff, const void *sbase) {
     asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, %2" ::"s"(__builtin_amdgcn_readfirstlane(lds)),
                  "v"(voff), "s"(sgpr_ptr(sbase))
-                 : "memory", "m0");
+                 : "memory");
 }
 __device__ __forceinline__ void wait_vm0() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 // All but the newest PF_DMA_PER_BLOCK vector-memory operations of the wave
