@@ -20,6 +20,7 @@ namespace {
 constexpr uint32_t MOE_TPC = 4;          // pairs per workgroup pass
 constexpr uint32_t DISP_WAVES = 16;
 constexpr uint32_t DISP_MAX_E = 512;
+constexpr uint32_t DISP_UNROLL = 8;     // 64-pair chunks whose expert ids are loaded together
 
 __device__ __forceinline__ uint32_t clamp_expert(int32_t e, uint32_t n) {
     return (e < 0 || (uint32_t)e >= n) ? 0u : (uint32_t)e;   // sf37_cuda.cu:4428-4429
@@ -45,8 +46,18 @@ __global__ void __launch_bounds__(1024) dispatch_kernel(uint32_t *__restrict__ g
     span = (span + 63u) & ~63u;
     const uint32_t beg = wave * span;
     const uint32_t end = beg + span < n_pairs ? beg + span : n_pairs;
-    for (uint32_t p = beg + lane; p < end; p += 64u)
-        atomicAdd(&cnt[wave][clamp_expert(selected[p], n_expert)], 1u);
+    // DISP_UNROLL loads in flight per lane before their counts are added
+    for (uint32_t p0 = beg + lane; p0 < end; p0 += 64u * DISP_UNROLL) {
+        uint32_t ev[DISP_UNROLL];
+#pragma unroll
+        for (uint32_t u = 0; u < DISP_UNROLL; u++) {
+            const uint32_t p = p0 + 64u * u;
+            ev[u] = p < end ? clamp_expert(selected[p], n_expert) : 0u;
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < DISP_UNROLL; u++)
+            if (p0 + 64u * u < end) atomicAdd(&cnt[wave][ev[u]], 1u);
+    }
     __syncthreads();
     // per expert: totals and exclusive offsets of each wave's share
     uint32_t tot = 0u, nz = 0u;
@@ -101,20 +112,33 @@ __global__ void __launch_bounds__(1024) dispatch_kernel(uint32_t *__restrict__ g
     // ordered scatter: each wave walks its own range in pair order
     uint32_t nbits = 1;
     while ((1u << nbits) < n_expert) nbits++;
-    for (uint32_t base = beg; base < end; base += 64u) {
-        const uint32_t p = base + lane;
-        const bool act = p < end;
-        const uint32_t e = act ? clamp_expert(selected[p], n_expert) : 0u;
-        uint64_t peers = __ballot(act);
-        for (uint32_t b = 0; b < nbits; b++) {
-            const uint64_t m = __ballot(act && ((e >> b) & 1u));
-            peers &= ((e >> b) & 1u) ? m : ~m;
+    // chunks of 64 pairs in order; the experts of DISP_UNROLL chunks are
+    // loaded before the first of them is ranked
+    for (uint32_t base0 = beg; base0 < end; base0 += 64u * DISP_UNROLL) {
+        uint32_t ev[DISP_UNROLL];
+#pragma unroll
+        for (uint32_t u = 0; u < DISP_UNROLL; u++) {
+            const uint32_t p = base0 + 64u * u + lane;
+            ev[u] = p < end ? clamp_expert(selected[p], n_expert) : 0u;
         }
-        if (act) {
-            const uint64_t lt = lane ? (~0ull >> (64u - lane)) : 0ull;
-            const uint32_t rank = (uint32_t)__popcll(peers & lt);
-            sorted[off[e] + cnt[wave][e] + rank] = p;
-            if ((peers & lt) == 0ull) cnt[wave][e] += (uint32_t)__popcll(peers);
+#pragma unroll
+        for (uint32_t u = 0; u < DISP_UNROLL; u++) {
+            const uint32_t base = base0 + 64u * u;
+            if (base >= end) break;                       // wave-uniform
+            const uint32_t p = base + lane;
+            const bool act = p < end;
+            const uint32_t e = ev[u];
+            uint64_t peers = __ballot(act);
+            for (uint32_t b = 0; b < nbits; b++) {
+                const uint64_t m = __ballot(act && ((e >> b) & 1u));
+                peers &= ((e >> b) & 1u) ? m : ~m;
+            }
+            if (act) {
+                const uint64_t lt = lane ? (~0ull >> (64u - lane)) : 0ull;
+                const uint32_t rank = (uint32_t)__popcll(peers & lt);
+                sorted[off[e] + cnt[wave][e] + rank] = p;
+                if ((peers & lt) == 0ull) cnt[wave][e] += (uint32_t)__popcll(peers);
+            }
         }
     }
 }
