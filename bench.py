@@ -51,6 +51,8 @@ def parse():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--layers", type=int, default=8, help="distinct layers rotated per step")
+    ap.add_argument("--decode-tokens", type=int, default=8,
+                    help="tokens per decode step (8 = BASELINE configs[1]; 1..16 take the fused decode path)")
     ap.add_argument("--seed", type=int, default=1234)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
@@ -123,7 +125,10 @@ def main():
 
     hip.init()
     H = Hip()
-    n_tok, E, K, F, TOPK = 8, moe.EXPERTS, moe.EMBD, moe.EXPERT_FF, moe.EXPERT_USED
+    n_tok, E, K, F, TOPK = args.decode_tokens, moe.EXPERTS, moe.EMBD, moe.EXPERT_FF, moe.EXPERT_USED
+    if not 1 <= n_tok <= 16:
+        print(f"bench.py: --decode-tokens {n_tok}: the decode step takes 1..16 tokens", file=sys.stderr)
+        sys.exit(2)
     # the router GEMV/GEMM runs inside the layer although injected logits select
     hip.set_option("router_with_logits", 1)
     if args.prefill_only:
@@ -253,7 +258,8 @@ def main():
         "dtype": "int8",
         "data": "synthetic (seeded N(0,0.02) weights quantized by the reference quantizer; x ~ N(0,1); "
                 "injected N(0,1) router logits)",
-        "config": {"workload": "BASELINE configs[1]: one MoE layer decode step, 8 tokens, uniform routing",
+        "config": {"workload": ("BASELINE configs[1]: " if n_tok == 8 else "")
+                               + f"one MoE layer decode step, {n_tok} tokens, uniform routing",
                    "experts": E, "hidden": K, "expert_ff": F, "top_k": TOPK,
                    "formats": "Q3GU gate/up, Q2D down, Q8_0 shared, fp32 router",
                    "layers_rotated": args.layers, "hbm_bytes_per_step": int(mean_bytes),
@@ -458,7 +464,7 @@ def cpu_baseline(layer, x_dev, sel, step_bytes, n_tok, budget_s):
         pass
     return {"value": round(step_bytes / dt / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": kind,
             "ms_per_token": round(dt * 1e3 / n_tok, 3),
-            "sample": f"{reps} x one 8-token decode step of layer 0 through the reference CPU MoE path "
+            "sample": f"{reps} x one {n_tok}-token decode step of layer 0 through the reference CPU MoE path "
                       f"(layer_moe_ffn composition, sf37.c:2127-2194), {dt * 1e3:.1f} ms/step on {cpu_model}"}
 
 
