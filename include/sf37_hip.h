@@ -111,6 +111,10 @@ int sf37_hip_matvec_q8_0_pair(sf37_hip_tensor *out0, sf37_hip_tensor *out1,
 int sf37_hip_matvec_f32(sf37_hip_tensor *out, const sf37_hip_tensor *weights,
                         uint64_t in_dim, uint64_t out_dim,
                         const sf37_hip_tensor *x);                 /* sf37_cuda.h:152-155 */
+/* bf16 weights, binary64 accumulation as the CPU engine (sf37_ops.c:143-151) */
+int sf37_hip_matvec_bf16(sf37_hip_tensor *out, const sf37_hip_tensor *weights,
+                         uint64_t in_dim, uint64_t out_dim,
+                         const sf37_hip_tensor *x);                /* sf37_cuda.h:144-147 */
 int sf37_hip_matvec_q3_asym(sf37_hip_tensor *out, const sf37_hip_tensor *weights,
                             uint64_t in_dim, uint64_t out_dim,
                             const sf37_hip_tensor *x);             /* sf37_cuda.h:156-159 */
@@ -160,6 +164,14 @@ int sf37_hip_matvec_q8_0_pair_mapped(sf37_hip_tensor *out0, sf37_hip_tensor *out
                                      uint64_t weight0_offset, uint64_t weight1_offset,
                                      uint64_t in_dim, uint64_t out_dim,
                                      const sf37_hip_tensor *x);    /* sf37_cuda.h:316-323 */
+int sf37_hip_matvec_bf16_mapped(sf37_hip_tensor *out, const void *model_map,
+                                uint64_t model_size, uint64_t weight_offset,
+                                uint64_t in_dim, uint64_t out_dim,
+                                const sf37_hip_tensor *x);         /* sf37_cuda.h:324-329 */
+int sf37_hip_matmul_bf16_mapped(sf37_hip_tensor *out, const void *model_map,
+                                uint64_t model_size, uint64_t weight_offset,
+                                uint64_t in_dim, uint64_t out_dim,
+                                const sf37_hip_tensor *x, uint64_t n_tok); /* :338-345 */
 int sf37_hip_matvec_f32_mapped(sf37_hip_tensor *out, const void *model_map,
                                uint64_t model_size, uint64_t weight_offset,
                                uint64_t in_dim, uint64_t out_dim,
@@ -258,16 +270,31 @@ int sf37_hip_moe_dispatch(sf37_hip_tensor *counts, sf37_hip_tensor *offsets,
 
 /* Whole MoE layer for n_tok tokens, composed as the engine does
  * (sf37.c:3392-3430 decode, 5959-6071 prefill): router logits, top-k,
- * Q8_0 shared expert, routed experts, out = shared + routed.  Weight
- * pointers are device tensors.  selected/weights may be NULL. */
+ * shared expert, routed experts, out = shared + routed.  Weight pointers
+ * are device tensors whose contents stay fixed while they are in use.
+ * selected/weights may be NULL.
+ *
+ * router_type (GGUF type id of the router weights, any of the engine's
+ * dense types, sf37.c:1775, 1960-1978): 0 F32 (binary64 sums), 30 BF16
+ * (widened exactly, binary64 sums), 8 Q8_0 (the Q8_0 GEMV with Q8_0
+ * activations, sf37_ops.c:110-141).
+ * shared_type: 0 = Q8_0 gate/up/down (the engine's format, sf37.c:1780-1782);
+ * 11 = Q3GU gate/up + Q2D down (the benchmark configurations' "same formats"
+ * option), run on the Q8_K path as one more expert with routing weight 1.0
+ * and the shared clamp. */
+#define SF37_HIP_TYPE_F32 0u
+#define SF37_HIP_TYPE_Q8_0 8u
+#define SF37_HIP_TYPE_Q3GU 11u
+#define SF37_HIP_TYPE_BF16 30u
 typedef struct {
-    const sf37_hip_tensor *router;        /* f32 [n_expert][in_dim] */
+    const sf37_hip_tensor *router;        /* [n_expert][in_dim] of router_type */
     const sf37_hip_tensor *router_bias;   /* f32 [n_expert] */
     const sf37_hip_tensor *gate, *up;     /* Q3 [n_expert][mid][in/256 blocks] */
     const sf37_hip_tensor *down;          /* Q2 [n_expert][in][mid/256 blocks] */
-    const sf37_hip_tensor *sh_gate, *sh_up, *sh_down;  /* Q8_0 shared expert */
+    const sf37_hip_tensor *sh_gate, *sh_up, *sh_down;  /* shared expert of shared_type */
     uint32_t n_expert, topk, in_dim, mid_dim;
     float scale, clamp_routed, clamp_shared;
+    uint32_t router_type, shared_type;
 } sf37_hip_moe_layer_weights;
 int sf37_hip_moe_layer(sf37_hip_tensor *out, sf37_hip_tensor *selected,
                        sf37_hip_tensor *weights, const sf37_hip_moe_layer_weights *w,

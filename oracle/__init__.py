@@ -291,8 +291,16 @@ def shared_expert_q8_0(gate_w, up_w, down_w, in_dim, mid_dim, out_dim, clamp, x)
 
 
 def moe_layer_q8k(weights: dict, x, logits=None, topk=8, scale=3.0, clamp_routed=0.0,
-                  clamp_shared=0.0):
-    """Whole MoE layer (router, shared, routed, add) for rows of x."""
+                  clamp_shared=0.0, shared_format="q8_0"):
+    """Whole MoE layer (router, shared, routed, add) for rows of x.
+
+    shared_format "q8_0": the engine's Q8_0 shared expert (sf37.c:2159-2167).
+    "q3q2": the benchmark configurations' shared expert in the routed formats
+    (Q3GU gate/up, Q2D down), computed as one more routed expert on the Q8_K
+    path with routing weight 1.0 and the shared clamp; out = shared + routed
+    (sf37.c:3428)."""
+    if shared_format == "q3q2":
+        return _moe_layer_shared_q3q2(weights, x, logits, topk, scale, clamp_routed, clamp_shared)
     x = f32(np.atleast_2d(x))
     n_tok, in_dim = x.shape
     n_exp = weights["n_expert"]
@@ -308,6 +316,24 @@ def moe_layer_q8k(weights: dict, x, logits=None, topk=8, scale=3.0, clamp_routed
                             _p(weights["sh_down"], _u8), n_exp, topk, in_dim, mid_dim,
                             clamp_routed, clamp_shared, scale, _p(x, _f), n_tok)
     return out, sel, w
+
+
+def _moe_layer_shared_q3q2(weights, x, logits, topk, scale, clamp_routed, clamp_shared):
+    x = f32(np.atleast_2d(x))
+    n_tok, in_dim = x.shape
+    n_exp, mid_dim = weights["n_expert"], weights["mid_dim"]
+    if logits is None:
+        logits = np.zeros((n_tok, n_exp), np.float32)
+        for t in range(n_tok):
+            lib().orc_f32_matvec_double(_p(logits[t], _f), _p(f32(weights["router"]), _f), in_dim, n_exp,
+                                        _p(np.ascontiguousarray(x[t]), _f))
+    sel, w, _ = router_select(logits, weights["router_bias"], topk, scale)
+    shared, _ = routed_moe_batch_q8k(weights["sh_gate"], weights["sh_up"], weights["sh_down"],
+                                     np.zeros((n_tok, 1), np.int32), np.ones((n_tok, 1), np.float32), 1,
+                                     in_dim, mid_dim, in_dim, clamp_shared, x)
+    routed, _ = routed_moe_batch_q8k(weights["gate"], weights["up"], weights["down"], sel, w, n_exp, in_dim,
+                                     mid_dim, in_dim, clamp_routed, x)
+    return (shared + routed).astype(np.float32), sel, w
 
 
 def max_abs_rel(got, want) -> float:

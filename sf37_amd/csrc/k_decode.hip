@@ -1024,7 +1024,7 @@ __global__ void __launch_bounds__(256) dec_combine_kernel(dec_params p) {
 #pragma unroll
     for (int s = 0; s < 16; s++)
         if ((uint32_t)s < p.topk) acc = acc + v[s];
-    const float y = (p.flags & SF37_DEC_SHARED) ? p.sh_out[i] + acc : acc;
+    const float y = (p.flags & (SF37_DEC_SHARED | SF37_DEC_SHBASE)) ? p.sh_out[i] + acc : acc;
     p.out[i] = (p.flags & SF37_DEC_RESID) ? p.out[i] + y : y;
 }
 

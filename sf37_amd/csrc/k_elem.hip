@@ -1,6 +1,8 @@
 // k_elem.hip - elementwise ops for gfx950: SwiGLU with clamp (sf37_ops.c:30-42),
-// in-place add (sf37_cuda.cu:2137-2151) and RMSNorm with (w + 1) weights
-// (sf37_ops.c:22-28, computed by sf37_norm.h).
+// in-place add (sf37_cuda.cu:2137-2151), RMSNorm with (w + 1) weights
+// (sf37_ops.c:22-28, computed by sf37_norm.h) and the exact bf16 -> f32
+// widening of dense weights (sf37_quant.h bf16 decode: the 16 bits become the
+// high half of the float).
 #include "sf37_dev.h"
 #include "sf37_norm.h"
 #include "sf37_launch.h"
@@ -75,7 +77,31 @@ __global__ void __launch_bounds__(256) rms_norm_kernel(float *__restrict__ out,
     }
 }
 
+// Four bf16 values per thread (one 8-byte load, one 16-byte store).
+__global__ void __launch_bounds__(256) bf16_widen_kernel(float *__restrict__ out, const uint16_t *__restrict__ in,
+                                                         uint64_t n) {
+    const uint64_t i = ((uint64_t)blockIdx.x * 256u + threadIdx.x) * 4u;
+    if (i + 4u <= n && ((uintptr_t)(in + i) & 7u) == 0) {
+        const uint2 v = *(const uint2 *)(in + i);
+        float4 o;
+        o.x = __builtin_bit_cast(float, v.x << 16);
+        o.y = __builtin_bit_cast(float, v.x & 0xffff0000u);
+        o.z = __builtin_bit_cast(float, v.y << 16);
+        o.w = __builtin_bit_cast(float, v.y & 0xffff0000u);
+        *(float4 *)(out + i) = o;
+        return;
+    }
+    for (uint64_t k = i; k < i + 4u && k < n; k++) out[k] = __builtin_bit_cast(float, (uint32_t)in[k] << 16);
+}
+
 }  // namespace
+
+extern "C" int sf37k_bf16_widen(float *out, const uint16_t *in, uint64_t n, sf37_stream_t s) {
+    if (n == 0) return 0;
+    hipLaunchKernelGGL(bf16_widen_kernel, dim3((unsigned)((n + 1023u) / 1024u)), dim3(256), 0, (hipStream_t)s, out,
+                       in, n);
+    return (int)hipGetLastError();
+}
 
 extern "C" int sf37k_swiglu(float *out, const float *gate, const float *up, uint64_t n, float clamp,
                             sf37_stream_t s) {

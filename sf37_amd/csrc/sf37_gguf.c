@@ -3,10 +3,11 @@
  * Reads the GGUF v3 container the engine maps (header, key/value section,
  * tensor table, aligned data section; the reader of sf37.c:506-604) and
  * binds one MoE layer's tensors by the engine's tensor contract
- * (sf37.c:1760-1782): router `moe.gate.weight` (F32, or BF16/F16 widened
- * exactly to F32), `moe.router_bias` (F32), `moe.gate_proj` / `moe.up_proj`
- * (Q3GU, type 11), `moe.down_proj` (Q2D, type 10), `share_expert.*_proj`
- * (Q8_0) and `post_attention_layernorm.weight` (BF16).  The weights become
+ * (sf37.c:1760-1782): router `moe.gate.weight` (F32, BF16 or Q8_0 as stored,
+ * F16 widened exactly to F32), `moe.router_bias` (F32), `moe.gate_proj` /
+ * `moe.up_proj` (Q3GU, type 11), `moe.down_proj` (Q2D, type 10),
+ * `share_expert.*_proj` (Q8_0; or Q3GU gate/up and Q2D down) and
+ * `post_attention_layernorm.weight` (BF16).  The weights become
  * device-resident copies of their map ranges (the same registry the _mapped
  * calls resolve against), so a bound layer runs through sf37_hip_moe_layer /
  * sf37_hip_moe_block with the map as its model map.  Closing a handle that
@@ -25,13 +26,13 @@
 #include "../../include/sf37_hip.h"
 
 sf37_hip_tensor *sf37i_map_tensor(const void *model_map, uint64_t model_size, uint64_t offset, uint64_t bytes,
-                                  const char *label);
+                                  const char *label, int *created);
+void sf37i_drop_range(const void *model_map, uint64_t offset, uint64_t bytes);
 void sf37i_drop_map(const void *model_map);
 
 enum { GG_F32 = 0, GG_F16 = 1, GG_Q8_0 = 8, GG_Q2D = 10, GG_Q3GU = 11, GG_BF16 = 30 };
 enum { GV_U8, GV_I8, GV_U16, GV_I16, GV_U32, GV_I32, GV_F32, GV_BOOL, GV_STR, GV_ARR, GV_U64, GV_I64, GV_F64 };
 #define GG_MAX_DIMS 4
-#define GG_MAX_OWNED 64
 
 typedef struct {
     char *name;
@@ -47,8 +48,10 @@ struct sf37_hip_gguf {
     uint32_t version, alignment;
     uint64_t n_tensors;
     gg_tensor *t;
-    sf37_hip_tensor *owned[GG_MAX_OWNED];   /* handles given out by the binder */
-    uint32_t n_owned;
+    sf37_hip_tensor **owned;   /* handles given out by the binder (8 per bound layer) */
+    uint32_t n_owned, cap_owned;
+    uint64_t (*made)[2];       /* registered ranges the binder created: offset, bytes */
+    uint32_t n_made, cap_made;
 };
 
 typedef struct {
@@ -124,6 +127,11 @@ static uint64_t gg_nbytes(uint32_t type, const uint64_t *dim, uint32_t ndim) {
 static void gg_free(sf37_hip_gguf *g) {
     if (!g) return;
     for (uint32_t i = 0; i < g->n_owned; i++) sf37_hip_tensor_free(g->owned[i]);
+    free(g->owned);
+    /* a caller's map outlives the handle: drop only the ranges bound here */
+    if (g->fd < 0)
+        for (uint32_t i = 0; i < g->n_made; i++) sf37i_drop_range(g->map, g->made[i][0], g->made[i][1]);
+    free(g->made);
     for (uint64_t i = 0; g->t && i < g->n_tensors; i++) free(g->t[i].name);
     free(g->t);
     if (g->fd >= 0) {
@@ -272,44 +280,68 @@ static const gg_tensor *gg_req(const sf37_hip_gguf *g, uint32_t il, const char *
 
 static sf37_hip_tensor *gg_keep(sf37_hip_gguf *g, sf37_hip_tensor *t) {
     if (!t) return NULL;
-    if (g->n_owned == GG_MAX_OWNED) {
-        sf37_hip_tensor_free(t);
-        fprintf(stderr, "sf37_hip gguf: too many bound tensors on one handle\n");
-        return NULL;
+    if (g->n_owned == g->cap_owned) {
+        const uint32_t cap = g->cap_owned ? 2u * g->cap_owned : 64u;
+        sf37_hip_tensor **n = (sf37_hip_tensor **)realloc(g->owned, cap * sizeof(*n));
+        if (!n) {
+            sf37_hip_tensor_free(t);
+            fprintf(stderr, "sf37_hip gguf: out of memory for bound tensors\n");
+            return NULL;
+        }
+        g->owned = n;
+        g->cap_owned = cap;
     }
     g->owned[g->n_owned++] = t;
     return t;
 }
 
+/* Device-resident tensor over a registered range: sf37_hip_evict_model_cache
+ * leaves it alone; the range lives until the handle closes. */
 static sf37_hip_tensor *gg_resident(sf37_hip_gguf *g, const gg_tensor *t) {
-    return gg_keep(g, sf37i_map_tensor(g->map, g->size, t->offset, t->bytes, t->name));
+    int created = 0;
+    sf37_hip_tensor *d = sf37i_map_tensor(g->map, g->size, t->offset, t->bytes, t->name, &created);
+    if (d && created) {
+        if (g->n_made == g->cap_made) {
+            const uint32_t cap = g->cap_made ? 2u * g->cap_made : 64u;
+            uint64_t(*n)[2] = (uint64_t(*)[2])realloc(g->made, cap * sizeof(*n));
+            if (!n) {
+                sf37_hip_tensor_free(d);
+                sf37i_drop_range(g->map, t->offset, t->bytes);
+                return NULL;
+            }
+            g->made = n;
+            g->cap_made = cap;
+        }
+        g->made[g->n_made][0] = t->offset;
+        g->made[g->n_made][1] = t->bytes;
+        g->n_made++;
+    }
+    return gg_keep(g, d);
 }
 
-/* Router rows widened to F32 on the host (BF16 / F16 values are exact in F32). */
-static sf37_hip_tensor *gg_router_f32(sf37_hip_gguf *g, const gg_tensor *t) {
-    if (t->type == GG_F32) return gg_resident(g, t);
-    if (t->type != GG_BF16 && t->type != GG_F16) {
-        fprintf(stderr, "sf37_hip gguf: router type %u (F32, BF16 or F16 are read)\n", t->type);
+/* Router rows: F32, BF16 and Q8_0 stay resident as stored (the layer reads
+ * each type, *type set to it); F16 is widened to F32 on the host (exact). */
+static sf37_hip_tensor *gg_router(sf37_hip_gguf *g, const gg_tensor *t, uint32_t *type) {
+    *type = t->type == GG_F16 ? (uint32_t)GG_F32 : t->type;
+    if (t->type == GG_F32 || t->type == GG_BF16 || t->type == GG_Q8_0) return gg_resident(g, t);
+    if (t->type != GG_F16) {
+        fprintf(stderr, "sf37_hip gguf: router type %u (F32, BF16, F16 or Q8_0 are read)\n", t->type);
         return NULL;
     }
     const uint64_t n = t->bytes / 2;
     float *f = (float *)malloc(n * 4);
     if (!f) return NULL;
     const uint16_t *h = (const uint16_t *)(g->map + t->offset);
-    for (uint64_t i = 0; i < n; i++) {
+    for (uint64_t i = 0; i < n; i++) {   /* IEEE half -> single */
         uint32_t bits;
-        if (t->type == GG_BF16) {
-            bits = (uint32_t)h[i] << 16;
-        } else {   /* IEEE half -> single */
-            const uint32_t s = (uint32_t)(h[i] & 0x8000u) << 16, e = (h[i] >> 10) & 0x1fu, m = h[i] & 0x3ffu;
-            if (e == 0x1fu) bits = s | 0x7f800000u | (m << 13);
-            else if (e) bits = s | ((e + 112u) << 23) | (m << 13);
-            else if (!m) bits = s;
-            else {
-                uint32_t ee = 113u, mm = m;
-                while (!(mm & 0x400u)) { mm <<= 1; ee--; }
-                bits = s | (ee << 23) | ((mm & 0x3ffu) << 13);
-            }
+        const uint32_t s = (uint32_t)(h[i] & 0x8000u) << 16, e = (h[i] >> 10) & 0x1fu, m = h[i] & 0x3ffu;
+        if (e == 0x1fu) bits = s | 0x7f800000u | (m << 13);
+        else if (e) bits = s | ((e + 112u) << 23) | (m << 13);
+        else if (!m) bits = s;
+        else {
+            uint32_t ee = 113u, mm = m;
+            while (!(mm & 0x400u)) { mm <<= 1; ee--; }
+            bits = s | (ee << 23) | ((mm & 0x3ffu) << 13);
         }
         memcpy(&f[i], &bits, 4);
     }
@@ -331,11 +363,20 @@ int sf37_hip_gguf_bind_moe_layer(sf37_hip_gguf *g, uint32_t il, sf37_hip_moe_lay
     const gg_tensor *ga = gg_req(g, il, "moe.gate_proj.weight", GG_Q3GU, 3);
     const gg_tensor *up = gg_req(g, il, "moe.up_proj.weight", GG_Q3GU, 3);
     const gg_tensor *dn = gg_req(g, il, "moe.down_proj.weight", GG_Q2D, 3);
-    const gg_tensor *sg = gg_req(g, il, "share_expert.gate_proj.weight", GG_Q8_0, 2);
-    const gg_tensor *su = gg_req(g, il, "share_expert.up_proj.weight", GG_Q8_0, 2);
-    const gg_tensor *sd = gg_req(g, il, "share_expert.down_proj.weight", GG_Q8_0, 2);
+    /* the shared expert: Q8_0 (the engine's contract), or Q3GU gate/up with a
+     * Q2D down (the benchmark configurations' "same formats" option) */
+    const gg_tensor *sg = gg_req(g, il, "share_expert.gate_proj.weight", -1, 2);
+    const gg_tensor *su = gg_req(g, il, "share_expert.up_proj.weight", -1, 2);
+    const gg_tensor *sd = gg_req(g, il, "share_expert.down_proj.weight", -1, 2);
     const gg_tensor *pn = gg_req(g, il, "post_attention_layernorm.weight", GG_BF16, 1);
     if (!rt || !rb || !ga || !up || !dn || !sg || !su || !sd || !pn) return 0;
+    const int sh_q8 = sg->type == GG_Q8_0 && su->type == GG_Q8_0 && sd->type == GG_Q8_0;
+    const int sh_q3 = sg->type == GG_Q3GU && su->type == GG_Q3GU && sd->type == GG_Q2D;
+    if (!sh_q8 && !sh_q3) {
+        fprintf(stderr, "sf37_hip gguf: layer %u shared expert types %u/%u/%u (Q8_0, or Q3GU with a Q2D down)\n", il,
+                sg->type, su->type, sd->type);
+        return 0;
+    }
     /* GGUF dims are (columns, rows[, experts]): gate/up (D, F, E), down (F, D, E) */
     const uint64_t D = ga->dim[0], F = ga->dim[1], E = ga->dim[2];
     if (up->dim[0] != D || up->dim[1] != F || up->dim[2] != E || dn->dim[0] != F || dn->dim[1] != D ||
@@ -346,7 +387,8 @@ int sf37_hip_gguf_bind_moe_layer(sf37_hip_gguf *g, uint32_t il, sf37_hip_moe_lay
         return 0;
     }
     memset(w, 0, sizeof(*w));
-    w->router = gg_router_f32(g, rt);
+    w->router = gg_router(g, rt, &w->router_type);
+    w->shared_type = sh_q3 ? (uint32_t)GG_Q3GU : 0u;
     w->router_bias = gg_resident(g, rb);
     w->gate = gg_resident(g, ga);
     w->up = gg_resident(g, up);

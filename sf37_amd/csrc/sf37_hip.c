@@ -42,8 +42,8 @@ static void *g_scratch;
 static uint64_t g_scratch_bytes;
 static int g_model_fd = -1;
 
-static sf37_hip_tensor *g_layer_bufs[6];
-static uint64_t g_layer_buf_bytes[6];
+static sf37_hip_tensor *g_layer_bufs[8];
+static uint64_t g_layer_buf_bytes[8];
 
 static int64_t g_opt_q8k = 1;
 static int64_t g_opt_q8k_min_rows = 512;
@@ -70,6 +70,27 @@ typedef struct {
 
 static map_range *g_ranges;
 static size_t g_nranges, g_cap_ranges;
+
+/* f32 copies of resident bf16 weights (dense matvec / router), made once per
+ * weight range and dropped with the range they were read from. */
+typedef struct {
+    const void *src;
+    uint64_t n;
+    float *f32;
+} widened;
+
+static widened *g_wide;
+static size_t g_nwide, g_cap_wide;
+
+static void widen_forget(const void *dev, uint64_t bytes) {
+    size_t w = 0;
+    for (size_t i = 0; i < g_nwide; i++) {
+        const uintptr_t a = (uintptr_t)g_wide[i].src, lo = (uintptr_t)dev;
+        if (a >= lo && a - lo < bytes) (void)hipFree(g_wide[i].f32);
+        else g_wide[w++] = g_wide[i];
+    }
+    g_nwide = w;
+}
 
 static int hip_ok(hipError_t err, const char *what) {
     if (err == hipSuccess) return 1;
@@ -235,6 +256,7 @@ static void free_ranges(int cache_only) {
     size_t w = 0;
     for (size_t i = 0; i < g_nranges; i++) {
         if (!cache_only || g_ranges[i].cache) {
+            widen_forget(g_ranges[i].dev, g_ranges[i].bytes);
             if (g_ranges[i].owned && g_ranges[i].dev) (void)hipFree(g_ranges[i].dev);
         } else {
             g_ranges[w++] = g_ranges[i];
@@ -250,13 +272,17 @@ void sf37_hip_cleanup(void) {
     free(g_ranges);
     g_ranges = NULL;
     g_cap_ranges = 0;
+    widen_forget(NULL, UINT64_MAX);
+    free(g_wide);
+    g_wide = NULL;
+    g_cap_wide = 0;
     if (g_scratch) (void)hipFree(g_scratch);
     g_scratch = NULL;
     g_scratch_bytes = 0;
     if (g_dec_cnt) (void)hipFree(g_dec_cnt);
     g_dec_cnt = NULL;
     g_dec_cnt_words = 0;
-    for (int i = 0; i < 6; i++) {
+    for (int i = 0; i < 8; i++) {
         if (g_layer_bufs[i]) {
             (void)hipFree(g_layer_bufs[i]->ptr);
             free(g_layer_bufs[i]);
@@ -473,6 +499,7 @@ void sf37i_drop_map(const void *model_map) {
     size_t w = 0;
     for (size_t i = 0; i < g_nranges; i++) {
         if (g_ranges[i].map == (const uint8_t *)model_map) {
+            widen_forget(g_ranges[i].dev, g_ranges[i].bytes);
             if (g_ranges[i].owned && g_ranges[i].dev) (void)hipFree(g_ranges[i].dev);
         } else {
             g_ranges[w++] = g_ranges[i];
@@ -481,13 +508,41 @@ void sf37i_drop_map(const void *model_map) {
     g_nranges = w;
 }
 
-/* A non-owning tensor over the device copy of map[offset, offset+bytes)
- * (registered or cached now), for the GGUF layer binder (sf37_gguf.c). */
+/* A non-owning tensor over a device copy of map[offset, offset+bytes) that
+ * sf37_hip_evict_model_cache does not free, for the GGUF layer binder
+ * (sf37_gguf.c): a registered (non-cache) range that covers it, else a new
+ * registered range made here (*created = 1), which the binder drops with
+ * sf37i_drop_range when its handle closes. */
 sf37_hip_tensor *sf37i_map_tensor(const void *model_map, uint64_t model_size, uint64_t offset, uint64_t bytes,
-                                  const char *label) {
+                                  const char *label, int *created) {
+    *created = 0;
     if (!model_map || !bytes || !mapped_range_ok(model_size, offset, bytes) || !ensure_init()) return NULL;
-    void *dev = (void *)model_ptr(model_map, offset, bytes, label);
-    return dev ? tensor_new(dev, bytes, 0) : NULL;
+    const uint8_t *map = (const uint8_t *)model_map;
+    for (size_t i = g_nranges; i-- > 0;) {
+        const map_range *r = &g_ranges[i];
+        if (!r->cache && r->map == map && offset >= r->off && bytes <= r->bytes && offset - r->off <= r->bytes - bytes)
+            return tensor_new((char *)r->dev + (offset - r->off), bytes, 0);
+    }
+    if (!upload_range(map, offset, bytes, 0, label)) return NULL;
+    *created = 1;
+    return tensor_new(g_ranges[g_nranges - 1].dev, bytes, 0);
+}
+
+/* Drop the registered range made for map[offset, offset+bytes) by
+ * sf37i_map_tensor (the newest one of exactly that extent). */
+void sf37i_drop_range(const void *model_map, uint64_t offset, uint64_t bytes) {
+    if (!g_init || !model_map) return;
+    for (size_t i = g_nranges; i-- > 0;) {
+        map_range *r = &g_ranges[i];
+        if (!r->cache && r->map == (const uint8_t *)model_map && r->off == offset && r->bytes == bytes) {
+            (void)hipStreamSynchronize(g_stream);
+            widen_forget(r->dev, r->bytes);
+            if (r->owned && r->dev) (void)hipFree(r->dev);
+            memmove(r, r + 1, (g_nranges - i - 1) * sizeof(map_range));
+            g_nranges--;
+            return;
+        }
+    }
 }
 
 int sf37_hip_set_model_fd(int fd) {
@@ -706,6 +761,70 @@ int sf37_hip_matmul_f32_mapped(sf37_hip_tensor *out, const void *model_map, uint
     return LAUNCH(SF37_HIP_STAGE_ROUTER, sf37k_f32_matmul((float *)out->ptr, w, (const float *)x->ptr, in_dim, out_dim, n_tok,
                                       (sf37_stream_t)g_stream),
                      "f32 matmul launch");
+}
+
+/* ---- bf16 dense weights (sf37_cuda.h:144-147, 324-345) -------------------- */
+/* The CPU engine widens every bf16 weight exactly and accumulates in binary64
+ * (sf37_bf16_matvec, sf37_ops.c:143-151), the arithmetic of the f32 kernels
+ * above: resident bf16 weights are widened once per range into an f32 copy
+ * those kernels read; a tensor's weights (which may change between calls)
+ * are widened into scratch on every call. */
+static const float *bf16_resident_f32(const void *w, uint64_t n) {
+    for (size_t i = 0; i < g_nwide; i++)
+        if (g_wide[i].src == w && g_wide[i].n == n) return g_wide[i].f32;
+    if (g_nwide == g_cap_wide) {
+        const size_t cap = g_cap_wide ? 2 * g_cap_wide : 16;
+        widened *nw = (widened *)realloc(g_wide, cap * sizeof(widened));
+        if (!nw) return NULL;
+        g_wide = nw;
+        g_cap_wide = cap;
+    }
+    void *f = NULL;
+    if (!hip_ok(hipMalloc(&f, n * 4u + SF37_PAD), "bf16 weight widening alloc")) return NULL;
+    if (!LAUNCH(SF37_HIP_STAGE_OTHER, sf37k_bf16_widen((float *)f, (const uint16_t *)w, n, (sf37_stream_t)g_stream),
+                "bf16 widen launch")) {
+        (void)hipFree(f);
+        return NULL;
+    }
+    widened e = {w, n, (float *)f};
+    g_wide[g_nwide++] = e;
+    return (const float *)f;
+}
+
+int sf37_hip_matvec_bf16(sf37_hip_tensor *out, const sf37_hip_tensor *weights, uint64_t in_dim, uint64_t out_dim,
+                         const sf37_hip_tensor *x) {
+    if (!out || !weights || !x || !ensure_init()) return 0;
+    const uint64_t n = in_dim * out_dim;
+    if (out->bytes < out_dim * 4u || x->bytes < in_dim * 4u || weights->bytes < n * 2u) return 0;
+    float *f = (float *)scratch_get(n * 4u, "bf16 weights");
+    if (!f) return 0;
+    return LAUNCH(SF37_HIP_STAGE_OTHER, sf37k_bf16_widen(f, (const uint16_t *)weights->ptr, n, (sf37_stream_t)g_stream),
+                  "bf16 widen launch") &&
+           LAUNCH(SF37_HIP_STAGE_ROUTER, sf37k_f32_matmul((float *)out->ptr, f, (const float *)x->ptr, in_dim, out_dim,
+                                                          1, (sf37_stream_t)g_stream),
+                  "bf16 matvec launch");
+}
+
+int sf37_hip_matvec_bf16_mapped(sf37_hip_tensor *out, const void *model_map, uint64_t model_size,
+                                uint64_t weight_offset, uint64_t in_dim, uint64_t out_dim,
+                                const sf37_hip_tensor *x) {
+    return sf37_hip_matmul_bf16_mapped(out, model_map, model_size, weight_offset, in_dim, out_dim, x, 1);
+}
+
+int sf37_hip_matmul_bf16_mapped(sf37_hip_tensor *out, const void *model_map, uint64_t model_size,
+                                uint64_t weight_offset, uint64_t in_dim, uint64_t out_dim,
+                                const sf37_hip_tensor *x, uint64_t n_tok) {
+    if (!out || !model_map || !x || n_tok == 0 || !ensure_init()) return 0;
+    const uint64_t wb = out_dim * in_dim * 2u;
+    if (!mapped_range_ok(model_size, weight_offset, wb) || out->bytes < n_tok * out_dim * 4u ||
+        x->bytes < n_tok * in_dim * 4u)
+        return 0;
+    const void *w = model_ptr(model_map, weight_offset, wb, "bf16 weights");
+    const float *f = w ? bf16_resident_f32(w, out_dim * in_dim) : NULL;
+    if (!f) return 0;
+    return LAUNCH(SF37_HIP_STAGE_ROUTER, sf37k_f32_matmul((float *)out->ptr, f, (const float *)x->ptr, in_dim, out_dim,
+                                                          n_tok, (sf37_stream_t)g_stream),
+                  "bf16 matmul launch");
 }
 
 /* ------------------------------------------------------------------------ */
@@ -1028,6 +1147,7 @@ typedef struct {
     const uint16_t *norm_w;  /* NORM: bf16 norm weights, epsilon, normalised rows (or NULL) */
     float eps;
     float *xn;
+    float *sh_out;           /* SHBASE: the shared expert's rows, added by the combine */
 } dec_extra;
 
 static uint32_t *dec_counters(uint64_t words) {
@@ -1165,6 +1285,10 @@ static int decode_run(const routed_args *a, const dec_extra *ex, float *out, flo
     }
     if ((ex->flags & SF37_DEC_ROUTER) && !p.router_w) return 0;
     if (sh && (!p.sh_gate || !p.sh_up || !p.sh_down)) return 0;
+    if (ex->flags & SF37_DEC_SHBASE) {
+        if (sh || !ex->sh_out) return 0;
+        p.sh_out = ex->sh_out;
+    }
     if ((ex->flags & SF37_DEC_NORM) && !ex->norm_w) return 0;
     /* automatic share (-1): half the up items dynamic up to 8 tokens, a
      * quarter above (measured best at 1..16 tokens, 288 experts, top-8) */
@@ -1355,9 +1479,9 @@ int sf37_hip_moe_dispatch(sf37_hip_tensor *counts, sf37_hip_tensor *offsets, sf3
                      "dispatch launch");
 }
 
-/* Whole layer: scratch holds logits, selection, the shared expert's
- * activations and the routed output; the routed pipeline then takes the
- * scratch area, so everything it needs from here lives in ls[]. */
+/* Whole layer: the layer buffers (layer_buf) hold logits, selection, the
+ * shared expert's activations and, on the fp32 path, the routed output; the
+ * routed pipeline then takes the scratch area. */
 /* The RMSNorm and residual of an FFN block around the layer (sf37_hip_moe_block). */
 typedef struct {
     const uint16_t *norm_w;
@@ -1378,6 +1502,99 @@ int sf37_hip_moe_layer(sf37_hip_tensor *out, sf37_hip_tensor *selected, sf37_hip
 static sf37_hip_tensor *g_block_buf[2];
 static uint64_t g_block_buf_bytes[2];
 
+/* Layer buffer i of at least bytes (kept and grown across calls). */
+static void *layer_buf(int i, uint64_t bytes) {
+    if (!g_layer_bufs[i] || g_layer_buf_bytes[i] < bytes) {
+        if (g_layer_bufs[i]) sf37_hip_tensor_free(g_layer_bufs[i]);
+        g_layer_bufs[i] = sf37_hip_tensor_alloc(bytes);
+        g_layer_buf_bytes[i] = g_layer_bufs[i] ? bytes : 0;
+        if (!g_layer_bufs[i]) return NULL;
+    }
+    return g_layer_bufs[i]->ptr;
+}
+
+static int tensor_holds(const sf37_hip_tensor *t, uint64_t bytes, const char *what) {
+    if (t && t->bytes >= bytes) return 1;
+    fprintf(stderr, "sf37: HIP moe layer: %s tensor holds %llu bytes, %llu needed\n", what,
+            (unsigned long long)(t ? t->bytes : 0), (unsigned long long)bytes);
+    return 0;
+}
+
+/* Every weight tensor of a layer is at least as large as its shape, in the
+ * formats the layer names. */
+static int layer_weights_ok(const sf37_hip_moe_layer_weights *w, int run_router) {
+    const uint64_t E = w->n_expert, D = w->in_dim, F = w->mid_dim;
+    const uint64_t q3 = E * F * (D / QK) * Q3B, q2 = E * D * (F / QK) * Q2B;
+    const uint32_t rt = w->router_type, st = w->shared_type;
+    if ((rt != SF37_HIP_TYPE_F32 && rt != SF37_HIP_TYPE_BF16 && rt != SF37_HIP_TYPE_Q8_0) ||
+        (st != 0u && st != SF37_HIP_TYPE_Q8_0 && st != SF37_HIP_TYPE_Q3GU)) {
+        fprintf(stderr, "sf37: HIP moe layer: router type %u / shared type %u not supported\n", rt, st);
+        return 0;
+    }
+    const uint64_t rb = rt == SF37_HIP_TYPE_F32 ? E * D * 4u
+                        : rt == SF37_HIP_TYPE_BF16 ? E * D * 2u : E * ((D + 31u) / 32u) * Q8B;
+    const int sq3 = st == SF37_HIP_TYPE_Q3GU;
+    const uint64_t s_gu = sq3 ? F * (D / QK) * Q3B : F * ((D + 31u) / 32u) * Q8B;
+    const uint64_t s_d = sq3 ? D * (F / QK) * Q2B : D * ((F + 31u) / 32u) * Q8B;
+    return (!run_router || tensor_holds(w->router, rb, "router")) &&
+           tensor_holds(w->router_bias, E * 4u, "router bias") && tensor_holds(w->gate, q3, "gate") &&
+           tensor_holds(w->up, q3, "up") && tensor_holds(w->down, q2, "down") &&
+           tensor_holds(w->sh_gate, s_gu, "shared gate") && tensor_holds(w->sh_up, s_gu, "shared up") &&
+           tensor_holds(w->sh_down, s_d, "shared down");
+}
+
+/* Is [p, p + bytes) inside a registered (non-cache) map range?  Weights there
+ * stay put until the range is dropped, so derived copies may be kept. */
+static int dev_registered(const void *p, uint64_t bytes) {
+    for (size_t i = 0; i < g_nranges; i++) {
+        const uintptr_t a = (uintptr_t)p, lo = (uintptr_t)g_ranges[i].dev;
+        if (!g_ranges[i].cache && a >= lo && bytes <= g_ranges[i].bytes && a - lo <= g_ranges[i].bytes - bytes)
+            return 1;
+    }
+    return 0;
+}
+
+/* Router logits of a BF16 or Q8_0 router (the F32 router runs inside the
+ * decode launches or through sf37k_f32_matmul below). */
+static int layer_router_typed(float *logits, const sf37_hip_moe_layer_weights *w, const float *x, uint32_t n_tok) {
+    const uint64_t E = w->n_expert, D = w->in_dim;
+    if (w->router_type == SF37_HIP_TYPE_Q8_0)
+        return q8_0_run(logits, NULL, (const uint8_t *)w->router->ptr, NULL, D, E, x, n_tok);
+    const float *f;
+    if (dev_registered(w->router->ptr, E * D * 2u)) {
+        f = bf16_resident_f32(w->router->ptr, E * D);
+    } else {
+        f = (const float *)layer_buf(7, E * D * 4u);
+        if (f && !LAUNCH(SF37_HIP_STAGE_OTHER, sf37k_bf16_widen((float *)f, (const uint16_t *)w->router->ptr, E * D,
+                                                                 (sf37_stream_t)g_stream),
+                         "router bf16 widen launch"))
+            return 0;
+    }
+    return f && LAUNCH(SF37_HIP_STAGE_ROUTER, sf37k_f32_matmul(logits, f, x, D, E, n_tok, (sf37_stream_t)g_stream),
+                       "moe_layer bf16 router launch");
+}
+
+/* The Q3GU/Q2D shared expert of n_tok rows: one expert, every token selects
+ * it with weight 1.0, the shared clamp (the Q8_K routed pipeline). */
+static int layer_shared_q3q2(float *out, const sf37_hip_moe_layer_weights *w, const float *x, uint32_t n_tok) {
+    const uint32_t D = w->in_dim, F = w->mid_dim;
+    char *sw = (char *)layer_buf(6, align256((uint64_t)n_tok * 4u) + (uint64_t)n_tok * 4u);
+    if (!sw) return 0;
+    int32_t *sel = (int32_t *)sw;
+    float *wts = (float *)(sw + align256((uint64_t)n_tok * 4u));
+    if (!hip_ok(hipMemsetAsync(sel, 0, (uint64_t)n_tok * 4u, g_stream), "shared selection fill") ||
+        !hip_ok(hipMemsetD32Async((hipDeviceptr_t)wts, 0x3f800000, n_tok, g_stream), "shared weight fill"))
+        return 0;
+    routed_args a = {(const uint8_t *)w->sh_gate->ptr, (const uint8_t *)w->sh_up->ptr,
+                     (const uint8_t *)w->sh_down->ptr, sel, wts, 1u, 1u, D, F, D, w->clamp_shared, x, n_tok, NULL, NULL};
+    if (decode_eligible(&a, 0)) {
+        dec_extra ex;
+        memset(&ex, 0, sizeof(ex));
+        return decode_run(&a, &ex, out, NULL, NULL, NULL, NULL);
+    }
+    return routed_q8k(&a, out, NULL, NULL, NULL, NULL, 0);
+}
+
 /* With bn, out is the hidden state (and x the same tensor): out += layer(
  * RMSNorm(out)).  The fused decode launches take the norm and residual
  * themselves; otherwise rms_norm into a block buffer and the layer into
@@ -1396,25 +1613,20 @@ static int moe_layer_impl(sf37_hip_tensor *out, sf37_hip_tensor *selected, sf37_
         (selected && selected->bytes < (uint64_t)n_tok * K * 4u) ||
         (weights && weights->bytes < (uint64_t)n_tok * K * 4u))
         return 0;
-    /* layer-owned buffers (separate from the routed scratch) */
-    sf37_hip_tensor **ls = g_layer_bufs;
-    uint64_t *ls_bytes = g_layer_buf_bytes;
-    const uint64_t need[6] = {(uint64_t)n_tok * E * 4u, (uint64_t)n_tok * K * 4u, (uint64_t)n_tok * K * 4u,
-                              (uint64_t)n_tok * F * 4u * 3u, (uint64_t)n_tok * D * 4u,
-                              (uint64_t)n_tok * K * ((uint64_t)F + D) * 4u};
-    for (int i = 0; i < 6; i++) {
-        if (!ls[i] || ls_bytes[i] < need[i]) {
-            if (ls[i]) sf37_hip_tensor_free(ls[i]);
-            ls[i] = sf37_hip_tensor_alloc(need[i]);
-            ls_bytes[i] = need[i];
-            if (!ls[i]) return 0;
-        }
+    const int run_router = !logits_in || (g_opt_router_always && w->router);
+    /* weight tensors hold the shapes they are read at (the kernels do not
+     * bound their reads by the tensors' sizes) */
+    if (!layer_weights_ok(w, run_router)) return 0;
+    const int router_f32 = w->router_type == SF37_HIP_TYPE_F32;
+    const int shared_q3 = w->shared_type == SF37_HIP_TYPE_Q3GU;
+    if (shared_q3 && (!q8k_use_for(F) || !q8k_use_for(D))) {
+        fprintf(stderr, "sf37: HIP moe layer: the Q3GU/Q2D shared expert takes the Q8_K path (rows >= q8k_min_rows)\n");
+        return 0;
     }
     const sf37_stream_t st = (sf37_stream_t)g_stream;
-    const int run_router = !logits_in || (g_opt_router_always && w->router);
     routed_args a = {(const uint8_t *)w->gate->ptr, (const uint8_t *)w->up->ptr, (const uint8_t *)w->down->ptr, NULL,
                      NULL, E, K, D, F, D, w->clamp_routed, (const float *)x->ptr, n_tok, NULL, NULL};
-    const int fused = decode_eligible(&a, SF37_DEC_SELECT | SF37_DEC_SHARED);
+    const int fused = decode_eligible(&a, SF37_DEC_SELECT | (shared_q3 ? 0u : SF37_DEC_SHARED));
     if (bn && !fused) {
         const uint64_t bytes = (uint64_t)n_tok * D * 4u;
         for (int i = 0; i < 2; i++) {
@@ -1431,63 +1643,104 @@ static int moe_layer_impl(sf37_hip_tensor *out, sf37_hip_tensor *selected, sf37_
                       "moe block rms_norm launch") &&
                moe_layer_impl(y, selected, weights, w, logits_in, &xnt, n_tok, NULL, (float *)out->ptr);
     }
+    /* the rows the router and shared expert read: x, or with a block's norm
+     * on the fused path (whose launches normalise x themselves), the rows
+     * normalised here for the steps that run before those launches */
+    const float *xl = (const float *)x->ptr;
+    if (bn && ((run_router && !router_f32) || shared_q3)) {
+        float *xn = bn->xn ? bn->xn : (float *)layer_buf(5, (uint64_t)n_tok * D * 4u);
+        if (!xn || !LAUNCH(SF37_HIP_STAGE_OTHER, sf37k_rms_norm(xn, (const float *)x->ptr, bn->norm_w, 1, D, n_tok,
+                                                                bn->eps, st),
+                           "moe block rms_norm launch"))
+            return 0;
+        xl = xn;
+    }
+    /* logits: injected, or a BF16 / Q8_0 router computed here; the F32
+     * router runs in the decode route launch or below */
+    float *lg_buf = (float *)layer_buf(0, (uint64_t)n_tok * E * 4u);
+    if (!lg_buf) return 0;
+    const float *logits = logits_in ? (const float *)logits_in->ptr : NULL;
+    if (run_router && !router_f32) {
+        if (!layer_router_typed(lg_buf, w, xl, n_tok)) return 0;
+        if (!logits) logits = lg_buf;
+    }
     if (fused) {
+        /* a Q3GU/Q2D shared expert first, then the routed launches add it */
+        float *sh_out = NULL;
+        if (shared_q3) {
+            sh_out = (float *)layer_buf(4, (uint64_t)n_tok * D * 4u);
+            if (!sh_out || !layer_shared_q3q2(sh_out, w, xl, n_tok)) return 0;
+        }
         dec_extra ex;
         memset(&ex, 0, sizeof(ex));
-        ex.flags = SF37_DEC_SELECT | SF37_DEC_SHARED | (run_router ? SF37_DEC_ROUTER : 0u);
+        ex.flags = SF37_DEC_SELECT | (shared_q3 ? SF37_DEC_SHBASE : SF37_DEC_SHARED) |
+                   (run_router && router_f32 ? SF37_DEC_ROUTER : 0u);
         if (bn) {
             ex.flags |= SF37_DEC_NORM | SF37_DEC_RESID;
             ex.norm_w = bn->norm_w;
             ex.eps = bn->eps;
             ex.xn = bn->xn;
         }
-        ex.router_w = w->router ? (const float *)w->router->ptr : NULL;
+        ex.router_w = w->router && router_f32 ? (const float *)w->router->ptr : NULL;
         ex.router_bias = (const float *)w->router_bias->ptr;
-        ex.logits_sel = logits_in ? (const float *)logits_in->ptr : NULL;
+        ex.logits_sel = logits;
         ex.sh_gate = (const uint8_t *)w->sh_gate->ptr;
         ex.sh_up = (const uint8_t *)w->sh_up->ptr;
         ex.sh_down = (const uint8_t *)w->sh_down->ptr;
+        ex.sh_out = sh_out;
         ex.scale = w->scale;
         ex.clamp_shared = w->clamp_shared;
         ex.sel = selected ? (int32_t *)selected->ptr : NULL;
         ex.wts = weights ? (float *)weights->ptr : NULL;
         return decode_run(&a, &ex, (float *)out->ptr, NULL, NULL, NULL, NULL);
     }
-    float *logits = logits_in ? (float *)logits_in->ptr : (float *)ls[0]->ptr;
-    int32_t *sel = selected ? (int32_t *)selected->ptr : (int32_t *)ls[1]->ptr;
-    float *wts = weights ? (float *)weights->ptr : (float *)ls[2]->ptr;
-    float *sh = (float *)ls[3]->ptr;   /* gate | up | mid for the shared expert */
-    float *routed = (float *)ls[4]->ptr;
-    if (run_router && !LAUNCH(SF37_HIP_STAGE_ROUTER, sf37k_f32_matmul((float *)ls[0]->ptr, (const float *)w->router->ptr,
-                                                      (const float *)x->ptr, D, E, n_tok, st),
-                              "moe_layer router launch"))
+    /* layer-owned buffers (separate from the routed scratch): selection,
+     * routing weights, the Q8_0 shared expert's gate | up | mid */
+    int32_t *sel = selected ? (int32_t *)selected->ptr : (int32_t *)layer_buf(1, (uint64_t)n_tok * K * 4u);
+    float *wts = weights ? (float *)weights->ptr : (float *)layer_buf(2, (uint64_t)n_tok * K * 4u);
+    if (!sel || !wts) return 0;
+    if (run_router && router_f32 &&
+        !LAUNCH(SF37_HIP_STAGE_ROUTER, sf37k_f32_matmul(lg_buf, (const float *)w->router->ptr, xl, D, E, n_tok, st),
+                "moe_layer router launch"))
         return 0;
+    if (!logits) logits = lg_buf;
     if (E > ROUTER_MAX_EXPERTS ||
         !LAUNCH(SF37_HIP_STAGE_SELECT, sf37k_router_select(sel, wts, NULL, logits, (const float *)w->router_bias->ptr, E, K, w->scale,
                                        n_tok, st),
                    "moe_layer router_select launch"))
         return 0;
-    /* shared expert: Q8_0 gate/up pair -> SwiGLU -> Q8_0 down into out */
-    if (shared_mfma_eligible(n_tok, D, F)) {
-        if (!shared_mfma((float *)out->ptr, sh + 2u * (uint64_t)n_tok * F, (const uint8_t *)w->sh_gate->ptr,
-                         (const uint8_t *)w->sh_up->ptr, (const uint8_t *)w->sh_down->ptr, D, F, (const float *)x->ptr,
-                         n_tok, w->clamp_shared))
+    /* shared expert into out: Q3GU/Q2D on the Q8_K path, or Q8_0 gate/up
+     * pair -> SwiGLU -> Q8_0 down */
+    if (shared_q3) {
+        if (!layer_shared_q3q2((float *)out->ptr, w, xl, n_tok)) return 0;
+    } else if (shared_mfma_eligible(n_tok, D, F)) {
+        float *sh = (float *)layer_buf(3, (uint64_t)n_tok * F * 4u);
+        if (!sh || !shared_mfma((float *)out->ptr, sh, (const uint8_t *)w->sh_gate->ptr, (const uint8_t *)w->sh_up->ptr,
+                                (const uint8_t *)w->sh_down->ptr, D, F, xl, n_tok, w->clamp_shared))
             return 0;
-    } else if (!q8_0_run(sh, sh + (uint64_t)n_tok * F, (const uint8_t *)w->sh_gate->ptr, (const uint8_t *)w->sh_up->ptr, D,
-                  F, (const float *)x->ptr, n_tok) ||
-        !LAUNCH(SF37_HIP_STAGE_SWIGLU, sf37k_swiglu(sh + 2u * (uint64_t)n_tok * F, sh, sh + (uint64_t)n_tok * F, (uint64_t)n_tok * F,
-                                w->clamp_shared, st),
-                   "moe_layer shared swiglu launch") ||
-        !q8_0_run((float *)out->ptr, NULL, (const uint8_t *)w->sh_down->ptr, NULL, F, D,
-                  sh + 2u * (uint64_t)n_tok * F, n_tok))
-        return 0;
+    } else {
+        float *sh = (float *)layer_buf(3, (uint64_t)n_tok * F * 4u * 3u);   /* gate | up | mid */
+        if (!sh ||
+            !q8_0_run(sh, sh + (uint64_t)n_tok * F, (const uint8_t *)w->sh_gate->ptr, (const uint8_t *)w->sh_up->ptr, D,
+                      F, xl, n_tok) ||
+            !LAUNCH(SF37_HIP_STAGE_SWIGLU, sf37k_swiglu(sh + 2u * (uint64_t)n_tok * F, sh, sh + (uint64_t)n_tok * F,
+                                                        (uint64_t)n_tok * F, w->clamp_shared, st),
+                    "moe_layer shared swiglu launch") ||
+            !q8_0_run((float *)out->ptr, NULL, (const uint8_t *)w->sh_down->ptr, NULL, F, D,
+                      sh + 2u * (uint64_t)n_tok * F, n_tok))
+            return 0;
+    }
     a.selected = sel;
     a.weights = wts;
     const int slots = n_tok == 1u;
     if (!slots && E > DISPATCH_MAX_EXPERTS) return 0;
+    /* the fp32-activation path (one token, small shapes) */
+    float *routed = NULL;
     if (!q8k_use_for(F) || !q8k_use_for(D)) {
         if (n_tok != 1u) return 0;
-        if (!routed_f32(&a, routed, (float *)ls[5]->ptr, (float *)ls[5]->ptr + (uint64_t)K * F, NULL, NULL))
+        routed = (float *)layer_buf(4, (uint64_t)D * 4u);
+        float *mid_down = (float *)layer_buf(5, (uint64_t)K * ((uint64_t)F + D) * 4u);
+        if (!routed || !mid_down || !routed_f32(&a, routed, mid_down, mid_down + (uint64_t)K * F, NULL, NULL))
             return 0;
     } else {
         /* the routed combine adds the shared rows (and the residual) itself */

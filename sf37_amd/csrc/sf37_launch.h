@@ -52,6 +52,8 @@ int sf37k_add_inplace(float *dst, const float *src, uint64_t n, sf37_stream_t s)
 int sf37k_add2_inplace(float *dst, const float *a, const float *b, uint64_t n, sf37_stream_t s);
 int sf37k_rms_norm(float *out, const float *x, const void *w, int w_is_bf16, uint32_t n,
                    uint32_t n_tok, float eps, sf37_stream_t s);
+/* out[i] = bf16 in[i] as float (exact), out 16-byte aligned. */
+int sf37k_bf16_widen(float *out, const uint16_t *in, uint64_t n, sf37_stream_t s);
 
 /* Routed experts, Q8_K path.  Work is organised in groups: group g covers
  * pairs sorted[pair_off[g] .. pair_off[g+1]) that all use expert
@@ -149,6 +151,7 @@ int sf37k_sh_down(float *out, const void *d16, const float *ds, const void *a16,
 #define SF37_DEC_NORM 16u    /* x is the hidden state: RMSNorm(w + 1) by the route kernel */
 #define SF37_DEC_RESID 32u   /* out += layer output (out is the hidden state) */
 #define SF37_DEC_UPSEL 64u   /* no select launch: the up launch forms the top-k and runs the shared gate/up */
+#define SF37_DEC_SHBASE 128u /* out = sh_out (computed before) + routed; no shared expert here */
 #define SF37_DEC_ACT_BYTES 288u  /* activation block: 256 codes, d, 4 sums, pad */
 typedef struct sf37_dec_params {
     uint32_t T, E, K, F, topk, G;

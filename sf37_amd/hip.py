@@ -33,7 +33,10 @@ class LayerWeights(C.Structure):
     _fields_ = [("router", T), ("router_bias", T), ("gate", T), ("up", T), ("down", T),
                 ("sh_gate", T), ("sh_up", T), ("sh_down", T),
                 ("n_expert", u32), ("topk", u32), ("in_dim", u32), ("mid_dim", u32),
-                ("scale", f32), ("clamp_routed", f32), ("clamp_shared", f32)]
+                ("scale", f32), ("clamp_routed", f32), ("clamp_shared", f32),
+                ("router_type", u32), ("shared_type", u32)]
+
+TYPE_F32, TYPE_Q8_0, TYPE_Q3GU, TYPE_BF16 = 0, 8, 11, 30
 
 
 _SIGS = {
@@ -65,6 +68,9 @@ _SIGS = {
     "sf37_hip_matvec_q8_0": (C.c_int, [T, T, u64, u64, T]),
     "sf37_hip_matvec_q8_0_pair": (C.c_int, [T, T, T, T, u64, u64, T]),
     "sf37_hip_matvec_f32": (C.c_int, [T, T, u64, u64, T]),
+    "sf37_hip_matvec_bf16": (C.c_int, [T, T, u64, u64, T]),
+    "sf37_hip_matvec_bf16_mapped": (C.c_int, [T, vp, u64, u64, u64, u64, T]),
+    "sf37_hip_matmul_bf16_mapped": (C.c_int, [T, vp, u64, u64, u64, u64, T, u64]),
     "sf37_hip_matvec_q3_asym": (C.c_int, [T, T, u64, u64, T]),
     "sf37_hip_matvec_q2_asym": (C.c_int, [T, T, u64, u64, T]),
     "sf37_hip_router_select": (C.c_int, [T, T, T, T, T, u32, u32, f32]),

@@ -39,9 +39,12 @@ class SynthLayer:
     """One MoE layer's weights on the device."""
 
     def __init__(self, seed: int, n_expert: int = EXPERTS, in_dim: int = EMBD, mid_dim: int = EXPERT_FF,
-                 topk: int = EXPERT_USED, il: int = 3, sigma: float = 0.02):
+                 topk: int = EXPERT_USED, il: int = 3, sigma: float = 0.02, shared: str = "q8_0"):
+        """shared: "q8_0" (the engine's shared expert) or "q3q2" (Q3GU gate/up
+        and Q2D down, the BASELINE configurations' "same formats" option)."""
         self.seed, self.n_expert, self.in_dim, self.mid_dim, self.topk, self.il = \
             seed, n_expert, in_dim, mid_dim, topk, il
+        self.shared = shared
         E, D, F = n_expert, in_dim, mid_dim
         self.g_row = D // 256 * hip.Q3_BLOCK
         self.d_row = F // 256 * hip.Q2_BLOCK
@@ -50,9 +53,10 @@ class SynthLayer:
         self.gate = hip.synth_quant("q3", E * F, D, seed, STREAM["gate"], sigma=sigma)
         self.up = hip.synth_quant("q3", E * F, D, seed, STREAM["up"], sigma=sigma)
         self.down = hip.synth_quant("q2", E * D, F, seed, STREAM["down"], sigma=sigma)
-        self.sh_gate = hip.synth_quant("q8_0", F, D, seed, STREAM["sh_gate"], sigma=sigma)
-        self.sh_up = hip.synth_quant("q8_0", F, D, seed, STREAM["sh_up"], sigma=sigma)
-        self.sh_down = hip.synth_quant("q8_0", D, F, seed, STREAM["sh_down"], sigma=sigma)
+        gu, dn = ("q3", "q2") if shared == "q3q2" else ("q8_0", "q8_0")
+        self.sh_gate = hip.synth_quant(gu, F, D, seed, STREAM["sh_gate"], sigma=sigma)
+        self.sh_up = hip.synth_quant(gu, F, D, seed, STREAM["sh_up"], sigma=sigma)
+        self.sh_down = hip.synth_quant(dn, D, F, seed, STREAM["sh_down"], sigma=sigma)
         self.clamp_routed = swiglu_limit(il, False)
         self.clamp_shared = swiglu_limit(il, True)
 
@@ -69,7 +73,8 @@ class SynthLayer:
     def weights_struct(self, scale: float = 3.0) -> hip.LayerWeights:
         return hip.LayerWeights(self.router.h, self.router_bias.h, self.gate.h, self.up.h, self.down.h,
                                 self.sh_gate.h, self.sh_up.h, self.sh_down.h, self.n_expert, self.topk,
-                                self.in_dim, self.mid_dim, scale, self.clamp_routed, self.clamp_shared)
+                                self.in_dim, self.mid_dim, scale, self.clamp_routed, self.clamp_shared,
+                                hip.TYPE_F32, hip.TYPE_Q3GU if self.shared == "q3q2" else 0)
 
     def host_experts(self, experts) -> dict:
         """Host copies of the given experts' packed rows (for the CPU oracle),

@@ -47,21 +47,26 @@ def gguf_bytes(kvs, tensors, alignment=32, version=3):
 
 
 def moe_layer_tensors(il, router, router_type, router_bias, gate, up, down, sh_gate, sh_up, sh_down, norm_bits,
-                      E, D, F):
-    """The MoE tensors of layer il by the engine's contract (sf37.c:1760-1782)."""
+                      E, D, F, shared_q3q2=False):
+    """The MoE tensors of layer il by the engine's contract (sf37.c:1760-1782);
+    router is F32 / BF16 values or Q8_0 bytes; shared_q3q2: the shared expert
+    in Q3GU (gate/up) and Q2D (down) instead of Q8_0."""
     p = f"model.layers.{il}."
-    if router_type == T_BF16:
+    if router_type in (T_BF16, T_F16):
         rb = np.asarray(router, np.uint16).tobytes()
+    elif router_type == T_Q8_0:
+        rb = bytes(router)
     else:
         rb = np.asarray(router, np.float32).tobytes()
+    sg, sd = (T_Q3GU, T_Q2D) if shared_q3q2 else (T_Q8_0, T_Q8_0)
     return [
         (p + "moe.gate.weight", (D, E), router_type, rb),
         (p + "moe.router_bias", (E,), T_F32, np.asarray(router_bias, np.float32).tobytes()),
         (p + "moe.gate_proj.weight", (D, F, E), T_Q3GU, gate),
         (p + "moe.up_proj.weight", (D, F, E), T_Q3GU, up),
         (p + "moe.down_proj.weight", (F, D, E), T_Q2D, down),
-        (p + "share_expert.gate_proj.weight", (D, F), T_Q8_0, sh_gate),
-        (p + "share_expert.up_proj.weight", (D, F), T_Q8_0, sh_up),
-        (p + "share_expert.down_proj.weight", (F, D), T_Q8_0, sh_down),
+        (p + "share_expert.gate_proj.weight", (D, F), sg, sh_gate),
+        (p + "share_expert.up_proj.weight", (D, F), sg, sh_up),
+        (p + "share_expert.down_proj.weight", (F, D), sd, sh_down),
         (p + "post_attention_layernorm.weight", (D,), T_BF16, np.asarray(norm_bits, np.uint16).tobytes()),
     ]

@@ -20,6 +20,20 @@ def test_library_exports_every_declared_symbol():
     assert set(syms) <= set(hip._SIGS), sorted(set(syms) - set(hip._SIGS))
 
 
+def test_engine_hook_library_exports_its_header():
+    """libsf37_engine_moe.so (the engine's SF37_USE_HIP MoE block, a C caller
+    of libsf37_hip.so) loads and exports what include/sf37_engine_moe.h
+    declares."""
+    import ctypes as C
+    import re
+    text = open(os.path.join(ROOT, "include", "sf37_engine_moe.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    syms = sorted(set(re.findall(r"\b(sf37_engine_[a-z0-9_]+)\s*\(", text)))
+    assert syms == ["sf37_engine_moe_decode", "sf37_engine_moe_prefill"]
+    L = C.CDLL(os.path.join(ROOT, "sf37_amd", "libsf37_engine_moe.so"))
+    assert all(hasattr(L, s) for s in syms)
+
+
 def test_reference_entry_points_are_mirrored():
     """Each hot-path entry of the reference interface (sf37_cuda.h) has a
     sf37_hip_ twin with the same name suffix."""
@@ -34,7 +48,8 @@ def test_reference_entry_points_are_mirrored():
            "rms_norm_weight1_bf16_batch_mapped", "matvec_q8_0_mapped", "matmul_q8_0_mapped",
            "matmul_q8_0_pair_mapped", "matvec_q8_0_pair_mapped", "matvec_f32_mapped", "matmul_f32_mapped",
            "matvec_q3_asym_mapped", "matvec_q2_asym_mapped", "router_select_mapped",
-           "router_select_batch_mapped", "routed_moe_one_mapped", "routed_moe_batch_mapped"]
+           "router_select_batch_mapped", "routed_moe_one_mapped", "routed_moe_batch_mapped",
+           "matvec_bf16", "matvec_bf16_mapped", "matmul_bf16_mapped"]
     syms = set(hip.header_symbols())
     assert {"sf37_hip_" + h for h in hot} <= syms
 
