@@ -301,6 +301,22 @@ int sf37_hip_moe_layer(sf37_hip_tensor *out, sf37_hip_tensor *selected,
                        const sf37_hip_tensor *logits_in, const sf37_hip_tensor *x,
                        uint32_t n_tok);
 
+/* sf37_hip_moe_layer without any allocation.  No counterpart in the
+ * reference: for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).  It
+ * takes decode batches of 1..16 tokens on the fused decode path (an F32
+ * router or injected logits, the Q8_0 shared expert, in/mid dims multiples of
+ * 256 of at least q8k_min_rows) and keeps all of its scratch in one static
+ * device array of 10 MiB per GPU (held until the process ends); a batch whose
+ * scratch would not fit is refused with a message (288 experts x 4096 x 1280
+ * at top-8 take 5 MiB at 16 tokens).  Results equal sf37_hip_moe_layer's bit
+ * for bit.  Every call on a GPU uses that GPU's one array: calls that overlap
+ * on one GPU (other streams, other threads) race. */
+int sf37_hip_moe_layer_noalloc(sf37_hip_tensor *out, sf37_hip_tensor *selected,
+                               sf37_hip_tensor *weights, const sf37_hip_moe_layer_weights *w,
+                               const sf37_hip_tensor *logits_in, const sf37_hip_tensor *x,
+                               uint32_t n_tok);
+
 /* The FFN block of an MoE decoder layer as the engine runs it
  * (sf37.c:2243-2250): hidden += moe_layer(rms_norm_weight1_bf16(hidden)),
  * the bf16 norm weights (in_dim of them) at norm_offset of a registered

@@ -1115,6 +1115,38 @@ extern "C" int sf37k_decode_counters(uint32_t T, uint32_t topk, uint32_t E, uint
     return (int)(32u * (UP_QUEUES + DN_QUEUES));
 }
 
+// Scratch of the no-alloc decode entry point (sf37_hip_moe_layer_noalloc):
+// device memory that exists from module load to process end, one copy per
+// GPU.  The queues at its start are zeroed by every route launch.  In host
+// code `scratch` names a host-side stand-in: only the address from
+// hipGetSymbolAddress, looked up per device, is handed to kernels.
+static_assert(32u * (UP_QUEUES + DN_QUEUES) * 4u <= SF37_NOALLOC_QUEUE_BYTES, "queues fit their region");
+static __device__ __align__(256) uint8_t scratch[SF37_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int NOALLOC_MAX_DEVICES = 64;
+void *g_noalloc_ptr[NOALLOC_MAX_DEVICES];
+}  // namespace
+
+extern "C" int sf37k_noalloc_scratch_init(void) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return (int)e;
+    if (dev < 0 || dev >= NOALLOC_MAX_DEVICES) return (int)hipErrorInvalidDevice;
+    if (g_noalloc_ptr[dev]) return 0;
+    void *ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return (int)e;
+    g_noalloc_ptr[dev] = ptr;
+    return 0;
+}
+
+extern "C" void *sf37k_noalloc_scratch(void) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= NOALLOC_MAX_DEVICES) return nullptr;
+    return g_noalloc_ptr[dev];
+}
+
 extern "C" int sf37k_decode_supported(uint32_t T, uint32_t topk, uint32_t E, uint32_t K, uint32_t F, int shared) {
     if (T == 0 || T > DEC_MAX_TOK || topk == 0 || K % SF37_QK || F % SF37_QK || K / SF37_QK > 16u ||
         F / SF37_QK > DN_MAX_NB)

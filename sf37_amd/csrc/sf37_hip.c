@@ -248,6 +248,8 @@ int sf37_hip_init(void) {
     if (g_init) return 1;
     if (!hip_ok(hipSetDevice(0), "set device")) return 0;
     g_stream = NULL;
+    /* the no-alloc entry point's static scratch on this device */
+    if (!hip_ok((hipError_t)sf37k_noalloc_scratch_init(), "no-alloc scratch address")) (void)0;
     g_init = 1;
     return 1;
 }
@@ -1187,8 +1189,11 @@ static int decode_eligible(const routed_args *a, uint32_t flags) {
 /* out = [shared +] sum over slots of the routed experts; mid / down_pair /
  * gate_out / up_out receive per-pair results when given (pairs x F, pairs x
  * D), else scratch is used. */
-static int decode_run(const routed_args *a, const dec_extra *ex, float *out, float *mid, float *down_pair,
-                      float *gate_out, float *up_out) {
+/* fixed_base != NULL: lay the scratch out in [fixed_base, + fixed_bytes) and
+ * use fixed_cnt as the item queues instead of the library's allocations. */
+static int decode_run_in(const routed_args *a, const dec_extra *ex, float *out, float *mid, float *down_pair,
+                         float *gate_out, float *up_out, char *fixed_base, uint64_t fixed_bytes,
+                         uint32_t *fixed_cnt) {
     if (!aligned4(a->gate_w) || !aligned4(a->up_w) || !aligned4(a->down_w) || !aligned4(a->x) ||
         !aligned4(out) || (mid && !aligned4(mid)) || (down_pair && !aligned4(down_pair)) ||
         (gate_out && !aligned4(gate_out)) || (up_out && !aligned4(up_out)))
@@ -1252,8 +1257,20 @@ static int decode_run(const routed_args *a, const dec_extra *ex, float *out, flo
     if ((ex->flags & SF37_DEC_SELECT) && !ex->sel) TAKE(o_sel, P * 4u);
     if ((ex->flags & SF37_DEC_SELECT) && !ex->wts) TAKE(o_wts, P * 4u);
 #undef TAKE
-    char *base = scratch_get(off, "decode scratch");
-    uint32_t *cnt = dec_counters((uint64_t)sf37k_decode_counters(T, TK, E, K, F));
+    char *base;
+    uint32_t *cnt;
+    if (fixed_base) {
+        if (off > fixed_bytes) {
+            fprintf(stderr, "sf37: HIP moe_layer_noalloc: this batch needs %llu bytes of scratch, the static "
+                            "scratch holds %llu\n", (unsigned long long)off, (unsigned long long)fixed_bytes);
+            return 0;
+        }
+        base = fixed_base;
+        cnt = fixed_cnt;
+    } else {
+        base = scratch_get(off, "decode scratch");
+        cnt = dec_counters((uint64_t)sf37k_decode_counters(T, TK, E, K, F));
+    }
     if (!base || !cnt) return 0;
     p.xq = base + o_xq;
     p.xq8 = (int8_t *)(base + o_xq8);
@@ -1307,6 +1324,11 @@ static int decode_run(const routed_args *a, const dec_extra *ex, float *out, flo
            LAUNCH(SF37_HIP_STAGE_DEC_MID, sf37k_decode_mid(&p, st), "decode mid launch") &&
            LAUNCH(SF37_HIP_STAGE_DEC_DOWN, sf37k_decode_down(&p, st), "decode down launch") &&
            LAUNCH(SF37_HIP_STAGE_DEC_COMBINE, sf37k_decode_combine(&p, st), "decode combine launch");
+}
+
+static int decode_run(const routed_args *a, const dec_extra *ex, float *out, float *mid, float *down_pair,
+                      float *gate_out, float *up_out) {
+    return decode_run_in(a, ex, out, mid, down_pair, gate_out, up_out, NULL, 0, NULL);
 }
 
 /* fp32-activation path for one token (sf37_cuda.cu:5382-5446). */
@@ -1595,6 +1617,34 @@ static int layer_shared_q3q2(float *out, const sf37_hip_moe_layer_weights *w, co
     return routed_q8k(&a, out, NULL, NULL, NULL, NULL, 0);
 }
 
+/* The fused decode launches' inputs for a whole layer: top-k from the
+ * logits (computed by the route launch with f32_router, else given), the
+ * Q8_0 shared expert (or, with sh_out, a Q3GU/Q2D shared expert's rows
+ * computed before), the block's norm and residual with bn. */
+static void layer_fused_extra(dec_extra *ex, const sf37_hip_moe_layer_weights *w, const float *logits,
+                              sf37_hip_tensor *selected, sf37_hip_tensor *weights, const block_norm *bn,
+                              int f32_router, float *sh_out) {
+    memset(ex, 0, sizeof(*ex));
+    ex->flags = SF37_DEC_SELECT | (sh_out ? SF37_DEC_SHBASE : SF37_DEC_SHARED) | (f32_router ? SF37_DEC_ROUTER : 0u);
+    if (bn) {
+        ex->flags |= SF37_DEC_NORM | SF37_DEC_RESID;
+        ex->norm_w = bn->norm_w;
+        ex->eps = bn->eps;
+        ex->xn = bn->xn;
+    }
+    ex->router_w = f32_router ? (const float *)w->router->ptr : NULL;
+    ex->router_bias = (const float *)w->router_bias->ptr;
+    ex->logits_sel = logits;
+    ex->sh_gate = (const uint8_t *)w->sh_gate->ptr;
+    ex->sh_up = (const uint8_t *)w->sh_up->ptr;
+    ex->sh_down = (const uint8_t *)w->sh_down->ptr;
+    ex->sh_out = sh_out;
+    ex->scale = w->scale;
+    ex->clamp_shared = w->clamp_shared;
+    ex->sel = selected ? (int32_t *)selected->ptr : NULL;
+    ex->wts = weights ? (float *)weights->ptr : NULL;
+}
+
 /* With bn, out is the hidden state (and x the same tensor): out += layer(
  * RMSNorm(out)).  The fused decode launches take the norm and residual
  * themselves; otherwise rms_norm into a block buffer and the layer into
@@ -1672,26 +1722,7 @@ static int moe_layer_impl(sf37_hip_tensor *out, sf37_hip_tensor *selected, sf37_
             if (!sh_out || !layer_shared_q3q2(sh_out, w, xl, n_tok)) return 0;
         }
         dec_extra ex;
-        memset(&ex, 0, sizeof(ex));
-        ex.flags = SF37_DEC_SELECT | (shared_q3 ? SF37_DEC_SHBASE : SF37_DEC_SHARED) |
-                   (run_router && router_f32 ? SF37_DEC_ROUTER : 0u);
-        if (bn) {
-            ex.flags |= SF37_DEC_NORM | SF37_DEC_RESID;
-            ex.norm_w = bn->norm_w;
-            ex.eps = bn->eps;
-            ex.xn = bn->xn;
-        }
-        ex.router_w = w->router && router_f32 ? (const float *)w->router->ptr : NULL;
-        ex.router_bias = (const float *)w->router_bias->ptr;
-        ex.logits_sel = logits;
-        ex.sh_gate = (const uint8_t *)w->sh_gate->ptr;
-        ex.sh_up = (const uint8_t *)w->sh_up->ptr;
-        ex.sh_down = (const uint8_t *)w->sh_down->ptr;
-        ex.sh_out = sh_out;
-        ex.scale = w->scale;
-        ex.clamp_shared = w->clamp_shared;
-        ex.sel = selected ? (int32_t *)selected->ptr : NULL;
-        ex.wts = weights ? (float *)weights->ptr : NULL;
+        layer_fused_extra(&ex, w, logits, selected, weights, bn, run_router && router_f32, sh_out);
         return decode_run(&a, &ex, (float *)out->ptr, NULL, NULL, NULL, NULL);
     }
     /* layer-owned buffers (separate from the routed scratch): selection,
@@ -1752,6 +1783,45 @@ static int moe_layer_impl(sf37_hip_tensor *out, sf37_hip_tensor *selected, sf37_
         return LAUNCH(SF37_HIP_STAGE_ADD, sf37k_add2_inplace(resid, (const float *)out->ptr, routed, (uint64_t)n_tok * D, st),
                       "moe block residual launch");
     return LAUNCH(SF37_HIP_STAGE_ADD, sf37k_add_inplace((float *)out->ptr, routed, (uint64_t)n_tok * D, st), "moe_layer add launch");
+}
+
+/* sf37_hip_moe_layer for decode batches without any allocation: the fused
+ * decode launches with their scratch (activation blocks, group tables,
+ * per-pair rows, queues) in the library's static device array.  Calls that
+ * overlap on one GPU share that array and race. */
+int sf37_hip_moe_layer_noalloc(sf37_hip_tensor *out, sf37_hip_tensor *selected, sf37_hip_tensor *weights,
+                               const sf37_hip_moe_layer_weights *w, const sf37_hip_tensor *logits_in,
+                               const sf37_hip_tensor *x, uint32_t n_tok) {
+    if (!out || !w || !x || n_tok == 0 || !ensure_init()) return 0;
+    const uint32_t E = w->n_expert, K = w->topk, D = w->in_dim, F = w->mid_dim;
+    if (!w->router_bias || !w->gate || !w->up || !w->down || !w->sh_gate || !w->sh_up || !w->sh_down || E == 0 ||
+        K == 0 || K > 16u || D % QK != 0 || F % QK != 0 || (!logits_in && !w->router))
+        return 0;
+    if (out->bytes < (uint64_t)n_tok * D * 4u || x->bytes < (uint64_t)n_tok * D * 4u ||
+        (logits_in && logits_in->bytes < (uint64_t)n_tok * E * 4u) ||
+        (selected && selected->bytes < (uint64_t)n_tok * K * 4u) ||
+        (weights && weights->bytes < (uint64_t)n_tok * K * 4u))
+        return 0;
+    const int run_router = !logits_in || (g_opt_router_always && w->router);
+    if (!layer_weights_ok(w, run_router)) return 0;
+    routed_args a = {(const uint8_t *)w->gate->ptr, (const uint8_t *)w->up->ptr, (const uint8_t *)w->down->ptr, NULL,
+                     NULL, E, K, D, F, D, w->clamp_routed, (const float *)x->ptr, n_tok, NULL, NULL};
+    if ((run_router && w->router_type != SF37_HIP_TYPE_F32) || w->shared_type == SF37_HIP_TYPE_Q3GU ||
+        !decode_eligible(&a, SF37_DEC_SELECT | SF37_DEC_SHARED)) {
+        fprintf(stderr, "sf37: HIP moe_layer_noalloc takes decode batches of 1..%u tokens on the Q8_K path with an "
+                        "F32 router (or injected logits) and a Q8_0 shared expert\n", SF37_DEC_MAX_TOK);
+        return 0;
+    }
+    char *base = (char *)sf37k_noalloc_scratch();
+    if (!base) {
+        fprintf(stderr, "sf37: HIP moe_layer_noalloc: the static scratch of this device has no address\n");
+        return 0;
+    }
+    dec_extra ex;
+    layer_fused_extra(&ex, w, logits_in ? (const float *)logits_in->ptr : NULL, selected, weights, NULL, run_router,
+                      NULL);
+    return decode_run_in(&a, &ex, (float *)out->ptr, NULL, NULL, NULL, NULL, base + SF37_NOALLOC_QUEUE_BYTES,
+                         SF37_NOALLOC_SCRATCH_BYTES - SF37_NOALLOC_QUEUE_BYTES, (uint32_t *)base);
 }
 
 int sf37_hip_moe_block(sf37_hip_tensor *hidden, sf37_hip_tensor *normed, sf37_hip_tensor *selected,

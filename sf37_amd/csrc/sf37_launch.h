@@ -186,6 +186,15 @@ typedef struct sf37_dec_params {
     uint32_t up_wgs, dn_wgs; /* up / down workgroups per CU (0 = as many as fit) */
 } sf37_dec_params;
 int sf37k_decode_counters(uint32_t T, uint32_t topk, uint32_t E, uint32_t K, uint32_t F);
+/* The no-alloc decode entry point's scratch: a static device array of
+ * SF37_NOALLOC_SCRATCH_BYTES per GPU, the item queues in its first
+ * SF37_NOALLOC_QUEUE_BYTES.  _init (once per device, that device current)
+ * looks its address up; _scratch returns the current device's address
+ * (NULL before _init). */
+#define SF37_NOALLOC_SCRATCH_BYTES (10u << 20)
+#define SF37_NOALLOC_QUEUE_BYTES (16u << 10)
+int sf37k_noalloc_scratch_init(void);
+void *sf37k_noalloc_scratch(void);
 /* 1 if the fused kernels take this shape (token count, dims, LDS). */
 int sf37k_decode_supported(uint32_t T, uint32_t topk, uint32_t E, uint32_t K, uint32_t F, int shared);
 /* The launches, in this order on one stream. */

@@ -101,6 +101,7 @@ _SIGS = {
     "sf37_hip_q8k_quantize": (C.c_int, [T, T, u32, u32]),
     "sf37_hip_moe_dispatch": (C.c_int, [T, T, T, T, u32, u32]),
     "sf37_hip_moe_layer": (C.c_int, [T, T, T, C.POINTER(LayerWeights), T, T, u32]),
+    "sf37_hip_moe_layer_noalloc": (C.c_int, [T, T, T, C.POINTER(LayerWeights), T, T, u32]),
     "sf37_hip_gguf_open": (vp, [C.c_char_p]),
     "sf37_hip_gguf_from_map": (vp, [vp, u64]),
     "sf37_hip_gguf_close": (None, [vp]),
