@@ -89,8 +89,20 @@ struct act_lds_t {
     uint32_t pad[4];
 };
 static_assert(sizeof(act_lds_t) == 304, "act_lds_t is 304 bytes");
-__host__ __device__ constexpr size_t lds_up_routed(uint32_t K, uint32_t T, uint32_t G, uint32_t P) {
+__host__ __device__ constexpr size_t lds_up_meta(uint32_t K, uint32_t T, uint32_t G, uint32_t P) {
     return (size_t)T * (K / SF37_QK) * sizeof(act_lds_t) + (size_t)(3u + 2u * G + 2u * P) * 4u;
+}
+// Rows of 4, 8 or 16 blocks can run on block pairs streamed through LDS.
+__host__ __device__ constexpr bool up_pairs(uint32_t K) {
+    return K / SF37_QK == 4u || K / SF37_QK == 8u || K / SF37_QK == 16u;
+}
+__host__ __device__ constexpr size_t tile_base(uint32_t K, uint32_t T, uint32_t G, uint32_t P) {
+    return (lds_up_meta(K, T, G, P) + 15u) & ~(size_t)15u;
+}
+// LDS of a routed up workgroup on the block-pair path: a 14 KiB tile per
+// wave after the activations and tables.
+__host__ __device__ constexpr size_t lds_up_dma(uint32_t K, uint32_t T, uint32_t G, uint32_t P, uint32_t waves) {
+    return tile_base(K, T, G, P) + (size_t)waves * 14336u;
 }
 __host__ __device__ constexpr size_t lds_up_shared(uint32_t K, uint32_t T) {
     return 2u * (size_t)tile_buf(up_shared_tile(K)) + (size_t)T * 2u * SH_RS * (K / 32u) * 4u;
@@ -604,6 +616,206 @@ __device__ void shared_down_pass(const dec_params &p, const int8_t *xq, const fl
     if (lane_ok && j == ns - 1u && row < p.K) p.sh_out[(uint64_t)t * p.K + row] = acc;
 }
 
+// ---------------------------------------------------------------------------
+// routed gate/up on block pairs
+// ---------------------------------------------------------------------------
+// A lane owns the block pair (2j, 2j+1) of one weight row: 220 bytes that
+// start on a 4-byte boundary (rows are 1760-byte multiples of 220 apart), read
+// as 14 dwordx4 loads.  The even block sits at byte 0 and the odd one at byte
+// 110 of the lane's registers, both compile-time offsets, so no lane
+// realigns its data.  A wave owns 64 / NBP rows (NBP = K / 512 pairs per
+// row) of one matrix of one group's expert; the chain over the row's blocks
+// runs over the NBP lanes of the row, two blocks per step.
+constexpr uint32_t PAIR_DW = 56;      // dwords of a lane's pair in registers (55 used)
+constexpr uint32_t TILE_BYTES = 14080; // an item: 64 pairs of 220 bytes, contiguous in the matrix
+constexpr uint32_t TILE_LOADS = 14;    // 16-byte loads per lane to move a tile (64 x 16 bytes each)
+constexpr uint32_t TILE_LDS = TILE_LOADS * 1024u;   // a wave's LDS tile
+static_assert(TILE_BYTES <= TILE_LDS, "tile fits its LDS slot");
+
+// Byte B / the f16 at even byte B of the dword array w (B folds to a constant).
+__device__ __forceinline__ uint32_t w_byte(const uint32_t *w, int B) { return (w[B >> 2] >> (8 * (B & 3))) & 0xffu; }
+__device__ __forceinline__ float w_f16(const uint32_t *w, int B) { return sf37_f16(w[B >> 2] >> (8 * (B & 3))); }
+
+// bs[t] = sum_g fma(s_g, I_g) (group order) of the Q3 block at byte BB of w
+// against NT activation blocks in LDS (Q3 act layout).
+template <int NT, int BB>
+__device__ __forceinline__ void q3_block_dots_at(const uint32_t *w, const act_t *const *x, float (&bs)[4]) {
+#pragma unroll
+    for (int t = 0; t < NT; t++) bs[t] = 0.0f;
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+        uint32_t c0[8], c1[8];
+        q3_unpack32(w, BB + 12 + 24 * g, c0);
+        q3_unpack32(w, BB + 24 + 24 * g, c1);
+        const int32_t zp = (int32_t)(w_byte(w, BB + 8 + g) & 7u);
+        const float sc = w_f16(w, BB + 2 * g);
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+            const u32x4 *xq = (const u32x4 *)&x[t]->qs[16 * g];
+            int32_t acc = 0;
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const u32x4 v0 = xq[2 * h], v1 = xq[2 * h + 1];
+                const uint32_t *c = h ? c1 : c0;
+                acc = sdot4(c[0], v0.x, acc);
+                acc = sdot4(c[1], v0.y, acc);
+                acc = sdot4(c[2], v0.z, acc);
+                acc = sdot4(c[3], v0.w, acc);
+                acc = sdot4(c[4], v1.x, acc);
+                acc = sdot4(c[5], v1.y, acc);
+                acc = sdot4(c[6], v1.z, acc);
+                acc = sdot4(c[7], v1.w, acc);
+            }
+            bs[t] = __builtin_fmaf(sc, (float)(acc - __mul24(zp, x[t]->gs[g])), bs[t]);
+        }
+    }
+}
+
+// acc = fma(d_b, blk_b, acc) over the row's blocks in order, two per lane:
+// step s takes the previous lane's total (row_shr:1) and adds blocks 2s,
+// 2s+1.  The row's segment of NBP lanes sits inside one 16-lane DPP row;
+// after NBP - 1 steps its last lane holds the exact chain (a value that
+// entered the segment from the previous one cannot reach its last lane).
+template <int NT, int NBP>
+__device__ __forceinline__ void pair_chains(const float (&dE)[4], const float (&bE)[4], const float (&dO)[4],
+                                            const float (&bO)[4], float (&acc)[4]) {
+#pragma unroll
+    for (int t = 0; t < NT; t++) acc[t] = __builtin_fmaf(dO[t], bO[t], __builtin_fmaf(dE[t], bE[t], 0.0f));
+#pragma unroll
+    for (int st = 1; st < NBP; st++) {
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+            const float prev = __builtin_bit_cast(
+                float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, acc[t]), 0x111, 0xf, 0xf, true));
+            acc[t] = __builtin_fmaf(dO[t], bO[t], __builtin_fmaf(dE[t], bE[t], prev));
+        }
+    }
+}
+
+// LDS direct loads (global -> LDS, no registers), issued through inline asm
+// so the compiler neither waits for them before unrelated LDS reads nor
+// tracks them: the loop waits for them itself (s_waitcnt vmcnt).  Lane i of
+// a dwordx4 load writes LDS bytes [m0 + 16 i, m0 + 16 i + 16); one wait
+// state separates the M0 write from the load.  m0 cannot be named as a
+// clobber; in the gfx950 assembly of this kernel every other m0 write sits
+// right before the compiler's own LDS direct loads of the shared gate/up
+// path (lds_copy), which never run in the same wave as these.
+__device__ __forceinline__ void dma16(uint32_t lds, uint32_t voff, const uint8_t *base) {
+    const uint64_t b = (uint64_t)(uintptr_t)base;
+    const uint64_t sb = ((uint64_t)__builtin_amdgcn_readfirstlane((uint32_t)(b >> 32)) << 32) |
+                        (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)b);
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2 nt" ::"s"(
+                     __builtin_amdgcn_readfirstlane(lds)),
+                 "v"(voff), "s"(sb)
+                 : "memory");
+}
+
+// The routed items of the up launch on block pairs (K = 512 * NBP).  An
+// item is RPI = 64 / NBP rows of one matrix (gate or up) of one group's
+// expert: 14080 contiguous bytes, moved by fully coalesced LDS direct loads
+// (load i of lane l = bytes 16 (64 i + l)) into the wave's LDS tile one item
+// ahead of the compute; each lane reads its block pair (220 bytes at 220 *
+// lane) into registers, the tile is refilled with the next item, and the pair
+// is computed while it loads.  xs holds each token's activation blocks with
+// the even blocks first, then the odd ones (bank-conflict-free: the NBP lanes
+// of a row read NBP distinct blocks 304 bytes apart).  Wave w takes items w,
+// w + nw, ... (no atomics: waiting for an atomic's result would also wait
+// for every load issued before it).
+constexpr uint32_t ITEM_NONE = 0xffffffffu;
+template <int NBP>
+__device__ void up_items_pairs(const dec_params &p, const uint32_t *gi, const uint32_t *so, const uint32_t *xo,
+                               const act_lds_t *xs, uint8_t *tile, uint32_t gw, uint32_t nw) {
+    constexpr uint32_t RPI = 64u / (uint32_t)NBP;           // rows per item
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t r = lane / (uint32_t)NBP, j = lane % (uint32_t)NBP;
+    const bool out_lane = j == (uint32_t)NBP - 1u;
+    const uint32_t nbK = 2u * (uint32_t)NBP;
+    const uint32_t ipm = p.F / RPI, ipg = 2u * ipm, n_items = gi[0] * ipg;
+    const uint64_t row_bytes = (uint64_t)nbK * SF37_Q3_BYTES, exp_bytes = (uint64_t)p.F * row_bytes;
+    uint32_t pos = gw;
+    auto next_item = [&]() -> uint32_t {
+        const uint32_t it = pos;
+        pos += nw;
+        return it < n_items ? it : ITEM_NONE;
+    };
+    // an item's RPI rows are one contiguous 14080-byte span of the matrix
+    auto tile_src = [&](uint32_t it) -> const uint8_t * {
+        const uint32_t g = it / ipg, r2 = it - g * ipg;
+        const uint32_t m = r2 >= ipm ? 1u : 0u, k = r2 - m * ipm;
+        const uint8_t *W = m ? p.up_w : p.gate_w;
+        return W + (uint64_t)gi[2u + p.G + g] * exp_bytes + (uint64_t)(k * RPI) * row_bytes;
+    };
+    const uint32_t tile_lds = (uint32_t)(uintptr_t)tile;
+    auto fill = [&](uint32_t it) {
+        const uint8_t *src = tile_src(it);
+        constexpr uint32_t last = TILE_BYTES / 16u - 1u;
+#pragma unroll
+        for (uint32_t i = 0; i < TILE_LOADS; i++) {
+            const uint32_t c = i * 64u + lane;
+            dma16(tile_lds + 1024u * i, 16u * (c < last ? c : last), src);
+        }
+    };
+    auto compute = [&](uint32_t (&w)[PAIR_DW], uint32_t it) {
+        const uint32_t g = it / ipg, r2 = it - g * ipg;
+        const uint32_t m = r2 >= ipm ? 1u : 0u, k = r2 - m * ipm;
+        float *const out_rows = m ? p.up_out : p.gate_out;
+        const uint32_t row = k * RPI + r;
+        const uint32_t p0 = gi[1u + g], p1 = gi[2u + g];
+        for (uint32_t c0 = p0; c0 < p1; c0 += DEC_TPC) {
+            const uint32_t nt = p1 - c0 < DEC_TPC ? p1 - c0 : DEC_TPC;
+            opaque<PAIR_DW>(w);
+            const act_t *xe[DEC_TPC], *xd[DEC_TPC];
+#pragma unroll
+            for (uint32_t t = 0; t < DEC_TPC; t++) {
+                const uint32_t base = xo[c0 + (t < nt ? t : 0u)];
+                xe[t] = &xs[base + j].a;
+                xd[t] = &xs[base + (uint32_t)NBP + j].a;
+            }
+            float bE[4], bO[4], dE[4], dO[4], acc[4];
+#pragma unroll
+            for (uint32_t t = 0; t < DEC_TPC; t++) {
+                dE[t] = xe[t]->d;
+                dO[t] = xd[t]->d;
+            }
+#define SF37_UP_PASS(NTc)                                  \
+    q3_block_dots_at<NTc, 0>(w, xe, bE);                   \
+    q3_block_dots_at<NTc, SF37_Q3_BYTES>(w, xd, bO);       \
+    pair_chains<NTc, NBP>(dE, bE, dO, bO, acc);
+            switch (nt) {
+                case 1: SF37_UP_PASS(1) break;
+                case 2: SF37_UP_PASS(2) break;
+                case 3: SF37_UP_PASS(3) break;
+                default: SF37_UP_PASS(4) break;
+            }
+#undef SF37_UP_PASS
+            if (out_lane) {
+#pragma unroll
+                for (uint32_t t = 0; t < DEC_TPC; t++)
+                    if (t < nt) out_rows[(uint64_t)so[c0 + t] * p.F + row] = acc[t];
+            }
+        }
+    };
+    // one item: wait for its tile (and the stores before it), read the
+    // lane's pair, refill the tile with the next item, compute
+    const uint32_t *pl = (const uint32_t *)tile + lane * 55u;
+    uint32_t it = next_item();
+    if (it != ITEM_NONE) fill(it);
+    while (it != ITEM_NONE) {
+        const uint32_t nx = next_item();
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        uint32_t w[PAIR_DW];
+#pragma unroll
+        for (uint32_t i = 0; i < 55u; i++) w[i] = pl[i];
+        w[55] = 0u;
+        opaque<PAIR_DW>(w);                         // the reads are done before the tile is refilled
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        if (nx != ITEM_NONE) fill(nx);
+        compute(w, it);
+        it = nx;
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");       // no load into LDS outlives the wave
+}
+
 // Routed gate/up.  An item is 2 rows of one group's expert for both
 // matrices: lane = matrix (gate/up) | row | block, so each wave reads two
 // contiguous 2-row spans; the gate lane of each row stores gate and up.
@@ -624,6 +836,44 @@ __global__ void __launch_bounds__(256) dec_select_kernel(dec_params p) {
         return;
     }
     shared_gate_up(p, blockIdx.x - 1u, smem);
+}
+
+// The routed part of the up launch on the block-pair DMA path (rows of 4, 8
+// or 16 blocks): each token's activation blocks staged even blocks first,
+// then odd ones, and a 14 KiB tile per wave after them.
+__device__ void up_routed_dma(const dec_params &p, unsigned char *smem, act_lds_t *xs, const uint32_t *gi,
+                              const uint32_t *so, uint32_t *xo, uint32_t gw, uint32_t nw, uint32_t wave) {
+    const uint32_t nbK = p.K / SF37_QK, P = p.T * p.topk;
+    constexpr uint32_t A16 = sizeof(act_t) / 16u, L16 = sizeof(act_lds_t) / 16u;
+    for (uint32_t i = threadIdx.x; i < p.T * nbK * A16; i += blockDim.x) {
+        const uint32_t blk = i / A16, c = i - blk * A16;
+        const uint32_t t = blk / nbK, b = blk - t * nbK;
+        ((u32x4 *)xs)[(t * nbK + (b & 1u) * (nbK >> 1) + (b >> 1)) * L16 + c] = ((const u32x4 *)p.xq)[i];
+    }
+    for (uint32_t i = threadIdx.x; i < P; i += blockDim.x) xo[i] = (so[i] / p.topk) * nbK;
+    __syncthreads();
+    uint8_t *tile = smem + tile_base(p.K, p.T, p.G, P) + wave * TILE_LDS;
+    switch (nbK) {
+        case 4: up_items_pairs<2>(p, gi, so, xo, xs, tile, gw, nw); break;
+        case 8: up_items_pairs<4>(p, gi, so, xo, xs, tile, gw, nw); break;
+        default: up_items_pairs<8>(p, gi, so, xo, xs, tile, gw, nw); break;
+    }
+}
+
+// Batches with a select launch on the DMA path: 512-thread workgroups (8
+// waves, one LDS tile each, the activations staged once per workgroup).
+__global__ void __launch_bounds__(512) dec_up_dma_kernel(dec_params p) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    const uint32_t nbK = p.K / SF37_QK, P = p.T * p.topk;
+    act_lds_t *xs = (act_lds_t *)smem;
+    uint32_t *gi = (uint32_t *)(xs + p.T * nbK);
+    uint32_t *so = gi + 3u + 2u * p.G;
+    uint32_t *xo = so + P;
+    for (uint32_t i = threadIdx.x; i < 3u + 2u * p.G; i += blockDim.x) gi[i] = p.ginfo[i];
+    for (uint32_t i = threadIdx.x; i < P; i += blockDim.x) so[i] = p.sorted[i];
+    __syncthreads();
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), nwg = blockDim.x >> 6;
+    up_routed_dma(p, smem, xs, gi, so, xo, blockIdx.x * nwg + wave, gridDim.x * nwg, wave);
 }
 
 // With UPSEL (few tokens, no select launch): workgroups [0, n_sh) run the
@@ -1033,6 +1283,7 @@ __global__ void __launch_bounds__(256) dec_combine_kernel(dec_params p) {
 namespace {
 
 struct dec_shape {
+    bool up_wide;
     uint32_t n_rt, n_xq, n_shup, n_up, n_mid, n_dn, n_cb;
     size_t lds_up, lds_shup, lds_dn;
     const void *dn_kernel;
@@ -1092,12 +1343,18 @@ dec_shape dec_plan(const dec_params &p) {
     const uint32_t cus = device_cus();
     d.n_rt = (p.flags & (SF37_DEC_ROUTER | SF37_DEC_SELECT)) ? (p.E + RT_ROWS - 1u) / RT_ROWS : 0u;
     d.n_xq = (p.T * nb + 3u) / 4u;
-    d.lds_up = lds_up_routed(p.K, p.T, p.G, p.T * p.topk);
+    // routed up: 8-wave block-pair DMA workgroups when the batch has a
+    // select launch and they fit, else the row-pair loop
+    const uint32_t P = p.T * p.topk;
+    const bool upsel = (p.flags & SF37_DEC_UPSEL) != 0;
+    d.up_wide = up_pairs(p.K) && !upsel && lds_up_dma(p.K, p.T, p.G, P, 8u) <= device_max_lds();
+    d.lds_up = d.up_wide ? lds_up_dma(p.K, p.T, p.G, P, 8u) : lds_up_meta(p.K, p.T, p.G, P);
     d.lds_shup = lds_up_shared(p.K, p.T);
     d.n_shup = sh ? p.F / SH_RS : 0u;                  // shared gate/up workgroups (select or up launch)
     // persistent kernels: exactly as many workgroups as can be resident
     const size_t up_lds = d.lds_up > d.lds_shup || !d.n_shup || !(p.flags & SF37_DEC_UPSEL) ? d.lds_up : d.lds_shup;
-    const uint32_t up_res = resident_wgs((const void *)dec_up_kernel, 256, up_lds);
+    const uint32_t up_res = d.up_wide ? resident_wgs((const void *)dec_up_dma_kernel, 512, d.lds_up)
+                                      : resident_wgs((const void *)dec_up_kernel, 256, up_lds);
     d.n_up = (p.up_wgs && p.up_wgs < up_res ? p.up_wgs : up_res) * cus;
     d.n_mid = (p.T * p.topk * (p.F / SF37_QK) + (sh ? (p.T * (p.F / 32u) + 1u) / 2u : 0u) + 3u) / 4u;
     d.lds_dn = sh ? (size_t)p.T * p.F + (size_t)p.T * (p.F / 32u) * 4u : 0u;
@@ -1154,7 +1411,7 @@ extern "C" int sf37k_decode_supported(uint32_t T, uint32_t topk, uint32_t E, uin
     // shared down: the shared mid fits in the x area, a lane's slice in registers
     if (shared && shd_bps(F / 32u, shd_slices(T)) > SHD_MAX_BPS) return 0;
     const uint32_t P = T * topk, G = P < E ? P : E;
-    if (lds_up_routed(K, T, G, P) > device_max_lds()) return 0;
+    if (lds_up_meta(K, T, G, P) > device_max_lds()) return 0;
     if (shared && lds_up_shared(K, T) > device_max_lds()) return 0;
     return 1;
 }
@@ -1187,13 +1444,21 @@ extern "C" int sf37k_decode_select(const sf37_dec_params *pp, sf37_stream_t s) {
 
 extern "C" int sf37k_decode_up(const sf37_dec_params *pp, sf37_stream_t s) {
     const dec_shape d = dec_plan(*pp);
+    if (d.up_wide) {
+        static size_t opted_w = 65536;
+        const int err = set_lds((const void *)dec_up_dma_kernel, d.lds_up, &opted_w);
+        if (err) return err;
+        hipLaunchKernelGGL(dec_up_dma_kernel, dim3(d.n_up), dim3(512), d.lds_up, (hipStream_t)s, *pp);
+        return (int)hipGetLastError();
+    }
     const bool upsel = (pp->flags & SF37_DEC_UPSEL) != 0u;
     const uint32_t n_sh = upsel ? d.n_shup : 0u;
     const size_t lds = d.lds_up > d.lds_shup || !n_sh ? d.lds_up : d.lds_shup;
     static size_t opted = 65536;
     const int err = set_lds((const void *)dec_up_kernel, lds, &opted);
     if (err) return err;
-    hipLaunchKernelGGL(dec_up_kernel, dim3(n_sh + d.n_up), dim3(256), lds, (hipStream_t)s, *pp, n_sh);
+    sf37_dec_params p = *pp;
+    hipLaunchKernelGGL(dec_up_kernel, dim3(n_sh + d.n_up), dim3(256), lds, (hipStream_t)s, p, n_sh);
     return (int)hipGetLastError();
 }
 
