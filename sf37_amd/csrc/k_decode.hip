@@ -128,17 +128,34 @@ __device__ __forceinline__ float q8_0_lds(const uint8_t *base, uint32_t L, uint3
 
 // Route workgroups [0, n_rt): RT_ROWS experts each - router logits, then
 // each expert's selection candidate per token (p = sigmoid, key of
-// p + bias).  Then workgroups quantising x (one 256-block of one token per
-// wave) to Q8_K for the routed experts and Q8_0 for the shared expert.
-// With NORM, x is the hidden state and every workgroup first forms the
-// RMSNorm scale of each token (sf37_rms_scale_wave, one wave per token);
-// the x values are normalised as they are loaded.
-__global__ void __launch_bounds__(256) dec_route_kernel(dec_params p, uint32_t n_rt) {
+// p + bias).  Wave w takes chunk group w & 3 of tokens 4 g .. 4 g + 3 for
+// g = w >> 2, w >> 2 + nw / 4, ... (sf37_router_wave); the four chunk
+// groups' sums are joined as (w0 + w1) + (w2 + w3).  Then workgroups
+// quantising x (one 256-block of one token per wave) to Q8_K for the routed
+// experts and Q8_0 for the shared expert.  With NORM, x is the hidden state
+// and every workgroup first forms the RMSNorm scale of each token
+// (sf37_rms_scale_wave, one wave per token); the x values are normalised as
+// they are loaded.  Workgroups of 256 threads up to 4 tokens, else 512.
+__host__ __device__ constexpr uint32_t route_threads(uint32_t T) { return T <= 4u ? 256u : 512u; }
+
+// The exponential table in LDS from immediates (no memory load on the
+// launch's critical path): thread i < 32 writes entry i.
+__device__ __forceinline__ void stage_exp_tab_imm(uint64_t *tab) {
+    if (threadIdx.x < 32u) {
+        uint64_t v = 0;
+#pragma unroll
+        for (uint32_t i = 0; i < 32u; i++) v = threadIdx.x == i ? sf37_exp2_tab(i) : v;
+        tab[threadIdx.x] = v;
+    }
+}
+
+__global__ void __launch_bounds__(512) dec_route_kernel(dec_params p, uint32_t n_rt) {
     __shared__ double part[RT_ROWS][DEC_MAX_TOK][4];
     __shared__ float s_logit[RT_ROWS][DEC_MAX_TOK];
     __shared__ float s_scale[DEC_MAX_TOK];
     __shared__ uint64_t tab[32];
-    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+    __shared__ double scr[8][8 * 64];                  // per wave: the partials' transposition
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u, nw = blockDim.x >> 6;
     const uint32_t nb = p.K / SF37_QK;
     const bool norm = (p.flags & SF37_DEC_NORM) != 0u;
     if (blockIdx.x == 0) {   // the up and down kernels' item queues
@@ -146,14 +163,14 @@ __global__ void __launch_bounds__(256) dec_route_kernel(dec_params p, uint32_t n
         if (threadIdx.x < DN_QUEUES) *dn_queue(p, threadIdx.x) = 0u;
     }
     if (norm) {
-        for (uint32_t t = wave; t < p.T; t += 4u) {
+        for (uint32_t t = wave; t < p.T; t += nw) {
             const float sc = sf37_rms_scale_wave(p.x + (uint64_t)t * p.K, p.K, p.eps);
             if (lane == 0) s_scale[t] = sc;
         }
         __syncthreads();
     }
     if (blockIdx.x >= n_rt) {
-        const uint32_t wq = (blockIdx.x - n_rt) * 4u + wave;
+        const uint32_t wq = (blockIdx.x - n_rt) * nw + wave;
         if (wq >= p.T * nb) return;
         const uint32_t t = wq / nb, b = wq - t * nb;
         const uint32_t k0 = b * SF37_QK + 4u * lane;
@@ -200,19 +217,34 @@ __global__ void __launch_bounds__(256) dec_route_kernel(dec_params p, uint32_t n
         }
         return;
     }
-    sf37_stage_exp_tab(tab);
+    stage_exp_tab_imm(tab);
     const uint32_t e0 = blockIdx.x * RT_ROWS;
     if (p.flags & SF37_DEC_ROUTER) {
         const uint32_t nr = p.E - e0 < RT_ROWS ? p.E - e0 : RT_ROWS;
-        const auto store = [](uint32_t r, uint32_t t, uint32_t w, double v) { part[r][t][w] = v; };
-        if (norm) {
-            const uint16_t *nw = p.norm_w;
-            sf37_router_rows_n<RT_ROWS>(p.router_w + (uint64_t)e0 * p.K, nr, p.x, p.K, p.T, store,
-                                        [nw](uint32_t t, uint32_t k, float v) {
-                                            return sf37_norm_w1_bf16(v, s_scale[t], nw[k]);
-                                        });
-        } else {
-            sf37_router_rows_n<RT_ROWS>(p.router_w + (uint64_t)e0 * p.K, nr, p.x, p.K, p.T, store);
+        const float *wr = p.router_w + (uint64_t)e0 * p.K;
+        const uint32_t cg = wave & 3u;
+        for (uint32_t t0 = 4u * (wave >> 2); t0 < p.T; t0 += nw) {
+            const auto store = [cg, t0](uint32_t r, uint32_t t, double v) { part[r][t0 + t][cg] = v; };
+            const uint32_t nt = p.T - t0 < 4u ? p.T - t0 : 4u;
+            if (norm) {
+                const uint16_t *nw16 = p.norm_w;
+                const auto xf = [nw16](uint32_t t, uint32_t k, float v) {
+                    return sf37_norm_w1_bf16(v, s_scale[t], nw16[k]);
+                };
+                switch (nt) {
+                    case 1: sf37_router_wave<RT_ROWS, 1>(wr, nr, p.x, p.K, cg, t0, scr[wave], store, xf); break;
+                    case 2: sf37_router_wave<RT_ROWS, 2>(wr, nr, p.x, p.K, cg, t0, scr[wave], store, xf); break;
+                    case 3: sf37_router_wave<RT_ROWS, 3>(wr, nr, p.x, p.K, cg, t0, scr[wave], store, xf); break;
+                    default: sf37_router_wave<RT_ROWS, 4>(wr, nr, p.x, p.K, cg, t0, scr[wave], store, xf); break;
+                }
+            } else {
+                switch (nt) {
+                    case 1: sf37_router_wave<RT_ROWS, 1>(wr, nr, p.x, p.K, cg, t0, scr[wave], store); break;
+                    case 2: sf37_router_wave<RT_ROWS, 2>(wr, nr, p.x, p.K, cg, t0, scr[wave], store); break;
+                    case 3: sf37_router_wave<RT_ROWS, 3>(wr, nr, p.x, p.K, cg, t0, scr[wave], store); break;
+                    default: sf37_router_wave<RT_ROWS, 4>(wr, nr, p.x, p.K, cg, t0, scr[wave], store); break;
+                }
+            }
         }
         __syncthreads();
         if (threadIdx.x < RT_ROWS * p.T) {
@@ -1342,7 +1374,7 @@ dec_shape dec_plan(const dec_params &p) {
     const bool sh = (p.flags & SF37_DEC_SHARED) != 0;
     const uint32_t cus = device_cus();
     d.n_rt = (p.flags & (SF37_DEC_ROUTER | SF37_DEC_SELECT)) ? (p.E + RT_ROWS - 1u) / RT_ROWS : 0u;
-    d.n_xq = (p.T * nb + 3u) / 4u;
+    d.n_xq = (p.T * nb + route_threads(p.T) / 64u - 1u) / (route_threads(p.T) / 64u);
     // routed up: 8-wave block-pair DMA workgroups when the batch has a
     // select launch and they fit, else the row-pair loop
     const uint32_t P = p.T * p.topk;
@@ -1428,7 +1460,8 @@ int set_lds(const void *fn, size_t bytes, size_t *opted) {
 
 extern "C" int sf37k_decode_route(const sf37_dec_params *pp, sf37_stream_t s) {
     const dec_shape d = dec_plan(*pp);
-    hipLaunchKernelGGL(dec_route_kernel, dim3(d.n_rt + d.n_xq), dim3(256), 0, (hipStream_t)s, *pp, d.n_rt);
+    hipLaunchKernelGGL(dec_route_kernel, dim3(d.n_rt + d.n_xq), dim3(route_threads(pp->T)), 0, (hipStream_t)s, *pp,
+                       d.n_rt);
     return (int)hipGetLastError();
 }
 

@@ -136,6 +136,96 @@ __device__ __forceinline__ void sf37_router_rows_n(const float *wr, uint32_t nr,
     }
 }
 
+// One wave's share of NR router rows x NT tokens: the partials of chunk
+// group cg (chunks 64 cg .. 64 cg + 63; chunk i owns k in [c i, c (i + 1)),
+// c = K / 256, accumulated in order in binary64 as sf37_router_block does),
+// each summed over the wave's 64 lanes by the balanced pairwise tree in
+// lane order that sf37_wave_sum_f64 forms.  Here the tree is split through
+// LDS: lane l writes its NR * NT partials to scr[v * 64 + l]; lane 8 v + g
+// adds scr[v * 64 + 8 g .. + 7] as a balanced tree, and three DPP levels
+// (lane ^ 1, lane ^ 2, the mirror within eight lanes) join the eight group
+// sums of value v, so every value costs a few instructions instead of a DPP
+// chain of its own.  store(r, t, v) receives value v = r * NT + t (from
+// lane 8 v).  scr holds NR * NT * 64 doubles for this wave; NR * NT <= 8.
+template <int NR, int NT, class STORE, class XF = sf37_x_identity>
+__device__ __forceinline__ void sf37_router_wave(const float *wr, uint32_t nr, const float *x, uint32_t K,
+                                                 uint32_t cg, uint32_t t0, double *scr, STORE store, XF xf = XF()) {
+    static_assert(NR * NT <= 8, "eight values per wave at most");
+    constexpr int NV = NR * NT;
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t c = K >> 8, k0 = (cg * 64u + lane) * c;
+    double acc[NR][NT];
+#pragma unroll
+    for (int r = 0; r < NR; r++)
+#pragma unroll
+        for (int t = 0; t < NT; t++) acc[r][t] = 0.0;
+    if ((c & 3u) == 0) {
+        for (uint32_t kk = 0; kk < c; kk += 16u) {
+            const uint32_t n4 = (c - kk) < 16u ? (c - kk) >> 2 : 4u;
+            sf37_f32x4 wv[NR][4], xv[NT][4];
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const uint32_t jj = (uint32_t)j < n4 ? (uint32_t)j : 0u;
+#pragma unroll
+                for (int r = 0; r < NR; r++) {
+                    const uint32_t rr = (uint32_t)r < nr ? (uint32_t)r : 0u;
+                    wv[r][j] = *(const sf37_f32x4 *)(wr + (uint64_t)rr * K + k0 + kk + 4u * jj);
+                }
+#pragma unroll
+                for (int t = 0; t < NT; t++)
+                    xv[t][j] = *(const sf37_f32x4 *)(x + (uint64_t)(t0 + t) * K + k0 + kk + 4u * jj);
+            }
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                if ((uint32_t)j < n4) {
+#pragma unroll
+                    for (int q = 0; q < 4; q++) {
+                        const uint32_t k = k0 + kk + 4u * (uint32_t)j + (uint32_t)q;
+#pragma unroll
+                        for (int t = 0; t < NT; t++) {
+                            const double xd = (double)xf(t0 + (uint32_t)t, k, xv[t][j][q]);
+#pragma unroll
+                            for (int r = 0; r < NR; r++)
+                                acc[r][t] = __builtin_fma((double)wv[r][j][q], xd, acc[r][t]);
+                        }
+                    }
+                }
+            }
+        }
+    } else {
+        for (uint32_t k = k0; k < k0 + c; k++) {
+#pragma unroll
+            for (int t = 0; t < NT; t++) {
+                const double xd = (double)xf(t0 + (uint32_t)t, k, x[(uint64_t)(t0 + t) * K + k]);
+#pragma unroll
+                for (int r = 0; r < NR; r++)
+                    acc[r][t] = __builtin_fma((double)wr[(uint64_t)((uint32_t)r < nr ? r : 0) * K + k], xd,
+                                              acc[r][t]);
+            }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < NR; r++)
+#pragma unroll
+        for (int t = 0; t < NT; t++) scr[(r * NT + t) * 64 + lane] = acc[r][t];
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const uint32_t v = lane >> 3 < (uint32_t)NV ? lane >> 3 : (uint32_t)NV - 1u;
+    const double *g = scr + v * 64u + (lane & 7u) * 8u;
+    double e[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) e[i] = g[i];
+    double s = ((e[0] + e[1]) + (e[2] + e[3])) + ((e[4] + e[5]) + (e[6] + e[7]));
+    s = s + __builtin_bit_cast(double, sf37_dpp64<0xb1>(__builtin_bit_cast(uint64_t, s)));    // lane ^ 1
+    s = s + __builtin_bit_cast(double, sf37_dpp64<0x4e>(__builtin_bit_cast(uint64_t, s)));    // lane ^ 2
+    s = s + __builtin_bit_cast(double, sf37_dpp64<0x141>(__builtin_bit_cast(uint64_t, s)));   // 7 - lane in eight
+    if ((lane & 7u) == 0 && (lane >> 3) < (uint32_t)NV) {
+        const uint32_t vv = lane >> 3;
+        store(vv / (uint32_t)NT, vv % (uint32_t)NT, s);
+    }
+}
+
 // One row, all T tokens: part[t][wave] receives the wave sums.
 __device__ __forceinline__ void sf37_router_rows(const float *wr, const float *x, uint32_t K, uint32_t T,
                                                  double (*part)[4]) {
