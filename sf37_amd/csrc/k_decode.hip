@@ -37,7 +37,6 @@ namespace {
 constexpr uint32_t DEC_MAX_TOK = 16;
 constexpr uint32_t DEC_TPC = 4;      // pairs per pass in the routed kernels
 constexpr uint32_t SH_RS = 2;        // shared gate/up rows per workgroup
-constexpr uint32_t RT_ROWS = 2;      // router rows (experts) per route workgroup
 constexpr uint32_t DN_MAX_NB = 5;    // down blocks per row held in registers (F <= 1280)
 constexpr uint32_t DN_TPC = 2;       // pairs per pass in the routed down kernel
 constexpr uint32_t DN_STAGE = 4;     // pairs whose activation blocks a down wave keeps in LDS
@@ -66,6 +65,9 @@ __device__ __forceinline__ uint32_t *up_queue(const dec_params &p, uint32_t q) {
 __device__ __forceinline__ uint32_t *dn_queue(const dec_params &p, uint32_t q) {
     return p.cnt + 32u * (UP_QUEUES + q);
 }
+// Arrivals of the select launch's top-k workgroups (the last one groups): a
+// spare word of up queue 0's stripe (the two are used by different launches).
+__device__ __forceinline__ uint32_t *sel_arrivals(const dec_params &p) { return p.cnt + 16u; }
 
 // Shared-down lane layout: the Q8_0 blocks of a row are split into S slices
 // (a power of two <= 16 with S * T <= 64, so one token's slices sit in one
@@ -126,17 +128,19 @@ __device__ __forceinline__ float q8_0_lds(const uint8_t *base, uint32_t L, uint3
 // route
 // ---------------------------------------------------------------------------
 
-// Route workgroups [0, n_rt): RT_ROWS experts each - router logits, then
-// each expert's selection candidate per token (p = sigmoid, key of
-// p + bias).  Wave w takes chunk group w & 3 of tokens 4 g .. 4 g + 3 for
-// g = w >> 2, w >> 2 + nw / 4, ... (sf37_router_wave); the four chunk
-// groups' sums are joined as (w0 + w1) + (w2 + w3).  Then workgroups
-// quantising x (one 256-block of one token per wave) to Q8_K for the routed
-// experts and Q8_0 for the shared expert.  With NORM, x is the hidden state
-// and every workgroup first forms the RMSNorm scale of each token
-// (sf37_rms_scale_wave, one wave per token); the x values are normalised as
-// they are loaded.  Workgroups of 256 threads up to 4 tokens, else 512.
-__host__ __device__ constexpr uint32_t route_threads(uint32_t T) { return T <= 4u ? 256u : 512u; }
+// Route workgroups [0, n_rt): workgroup u takes router rows 2 (u / ntg),
+// +1 and tokens 4 (u % ntg) .. + 3 (ntg = ceil(T / 4)); with ROUTER, wave
+// w forms the partial sums of quarter w (columns 1024 w .. + 1023) of those
+// rows and tokens (sf37_router_wave, the order of the reference's
+// 256-thread binary64 GEMV, sf37.c:1970-1976) and the logits are
+// (q0 + q1) + (q2 + q3).  Then each (row, token)'s selection candidate
+// (SELECT): p = sigmoid of the selecting logit, the key of p + bias.
+// Workgroups [n_rt, ...) quantise x (one 256-block of one token per wave)
+// to Q8_K for the routed experts and Q8_0 for the shared expert.  With
+// NORM, x is the hidden state: the waves first form the RMSNorm scales of
+// the tokens they use (sf37_rms_scale_wave, one wave per token) and
+// normalise x as they load it.
+__host__ __device__ constexpr uint32_t route_wgs(uint32_t T, uint32_t E) { return (E + 1u) / 2u * ((T + 3u) / 4u); }
 
 // The exponential table in LDS from immediates (no memory load on the
 // launch's critical path): thread i < 32 writes entry i.
@@ -149,30 +153,24 @@ __device__ __forceinline__ void stage_exp_tab_imm(uint64_t *tab) {
     }
 }
 
-__global__ void __launch_bounds__(512) dec_route_kernel(dec_params p, uint32_t n_rt) {
-    __shared__ double part[RT_ROWS][DEC_MAX_TOK][4];
-    __shared__ float s_logit[RT_ROWS][DEC_MAX_TOK];
-    __shared__ float s_scale[DEC_MAX_TOK];
+__global__ void __launch_bounds__(256) dec_route_kernel(dec_params p, uint32_t n_rt) {
+    __shared__ double scr[4][8 * 64];                  // per wave: the partials' transposition
+    __shared__ double part[2][4][4];                   // [row][token][quarter]
+    __shared__ float s_scale[4];
     __shared__ uint64_t tab[32];
-    __shared__ double scr[8][8 * 64];                  // per wave: the partials' transposition
-    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u, nw = blockDim.x >> 6;
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
     const uint32_t nb = p.K / SF37_QK;
     const bool norm = (p.flags & SF37_DEC_NORM) != 0u;
-    if (blockIdx.x == 0) {   // the up and down kernels' item queues
+    if (blockIdx.x == 0) {   // the up and down kernels' item queues, the select arrivals
         if (threadIdx.x < UP_QUEUES) *up_queue(p, threadIdx.x) = 0u;
         if (threadIdx.x < DN_QUEUES) *dn_queue(p, threadIdx.x) = 0u;
-    }
-    if (norm) {
-        for (uint32_t t = wave; t < p.T; t += nw) {
-            const float sc = sf37_rms_scale_wave(p.x + (uint64_t)t * p.K, p.K, p.eps);
-            if (lane == 0) s_scale[t] = sc;
-        }
-        __syncthreads();
+        if (threadIdx.x == 0) *sel_arrivals(p) = 0u;
     }
     if (blockIdx.x >= n_rt) {
-        const uint32_t wq = (blockIdx.x - n_rt) * nw + wave;
+        const uint32_t wq = (blockIdx.x - n_rt) * 4u + wave;
         if (wq >= p.T * nb) return;
         const uint32_t t = wq / nb, b = wq - t * nb;
+        const float scale = norm ? sf37_rms_scale_wave(p.x + (uint64_t)t * p.K, p.K, p.eps) : 0.0f;
         const uint32_t k0 = b * SF37_QK + 4u * lane;
         const float *xb = p.x + (uint64_t)t * p.K + k0;
         float v[4];
@@ -180,7 +178,7 @@ __global__ void __launch_bounds__(512) dec_route_kernel(dec_params p, uint32_t n
         for (int k = 0; k < 4; k++) v[k] = xb[k];
         if (norm) {
 #pragma unroll
-            for (int k = 0; k < 4; k++) v[k] = sf37_norm_w1_bf16(v[k], s_scale[t], p.norm_w[k0 + k]);
+            for (int k = 0; k < 4; k++) v[k] = sf37_norm_w1_bf16(v[k], scale, p.norm_w[k0 + k]);
             if (p.xn) {
 #pragma unroll
                 for (int k = 0; k < 4; k++) p.xn[(uint64_t)t * p.K + k0 + k] = v[k];
@@ -217,54 +215,57 @@ __global__ void __launch_bounds__(512) dec_route_kernel(dec_params p, uint32_t n
         }
         return;
     }
-    stage_exp_tab_imm(tab);
-    const uint32_t e0 = blockIdx.x * RT_ROWS;
-    if (p.flags & SF37_DEC_ROUTER) {
-        const uint32_t nr = p.E - e0 < RT_ROWS ? p.E - e0 : RT_ROWS;
-        const float *wr = p.router_w + (uint64_t)e0 * p.K;
-        const uint32_t cg = wave & 3u;
-        for (uint32_t t0 = 4u * (wave >> 2); t0 < p.T; t0 += nw) {
-            const auto store = [cg, t0](uint32_t r, uint32_t t, double v) { part[r][t0 + t][cg] = v; };
-            const uint32_t nt = p.T - t0 < 4u ? p.T - t0 : 4u;
-            if (norm) {
-                const uint16_t *nw16 = p.norm_w;
-                const auto xf = [nw16](uint32_t t, uint32_t k, float v) {
-                    return sf37_norm_w1_bf16(v, s_scale[t], nw16[k]);
-                };
-                switch (nt) {
-                    case 1: sf37_router_wave<RT_ROWS, 1>(wr, nr, p.x, p.K, cg, t0, scr[wave], store, xf); break;
-                    case 2: sf37_router_wave<RT_ROWS, 2>(wr, nr, p.x, p.K, cg, t0, scr[wave], store, xf); break;
-                    case 3: sf37_router_wave<RT_ROWS, 3>(wr, nr, p.x, p.K, cg, t0, scr[wave], store, xf); break;
-                    default: sf37_router_wave<RT_ROWS, 4>(wr, nr, p.x, p.K, cg, t0, scr[wave], store, xf); break;
-                }
-            } else {
-                switch (nt) {
-                    case 1: sf37_router_wave<RT_ROWS, 1>(wr, nr, p.x, p.K, cg, t0, scr[wave], store); break;
-                    case 2: sf37_router_wave<RT_ROWS, 2>(wr, nr, p.x, p.K, cg, t0, scr[wave], store); break;
-                    case 3: sf37_router_wave<RT_ROWS, 3>(wr, nr, p.x, p.K, cg, t0, scr[wave], store); break;
-                    default: sf37_router_wave<RT_ROWS, 4>(wr, nr, p.x, p.K, cg, t0, scr[wave], store); break;
-                }
-            }
+    const uint32_t ntg = (p.T + 3u) / 4u;
+    const uint32_t t0 = 4u * (blockIdx.x % ntg), e0 = 2u * (blockIdx.x / ntg);
+    const uint32_t nt = p.T - t0 < 4u ? p.T - t0 : 4u, nr = p.E - e0 < 2u ? p.E - e0 : 2u;
+    if (norm && (p.flags & SF37_DEC_ROUTER)) {
+        if (wave < nt) {
+            const float sc = sf37_rms_scale_wave(p.x + (uint64_t)(t0 + wave) * p.K, p.K, p.eps);
+            if (lane == 0) s_scale[wave] = sc;
         }
         __syncthreads();
-        if (threadIdx.x < RT_ROWS * p.T) {
-            const uint32_t r = threadIdx.x / p.T, t = threadIdx.x - r * p.T;
-            if (e0 + r < p.E) {
-                const float l = sf37_router_combine(part[r][t]);
-                s_logit[r][t] = l;
-                p.logits[(uint64_t)t * p.E + e0 + r] = l;
+    }
+    stage_exp_tab_imm(tab);
+    if (p.flags & SF37_DEC_ROUTER) {
+        const float *wr = p.router_w + (uint64_t)e0 * p.K;
+        const uint32_t cg = wave;
+        const auto store = [cg](uint32_t r, uint32_t t, double v) { part[r][t][cg] = v; };
+        if (norm) {
+            const uint16_t *nw16 = p.norm_w;
+            const auto xf = [nw16, t0](uint32_t t, uint32_t k, float v) {
+                return sf37_norm_w1_bf16(v, s_scale[t - t0], nw16[k]);
+            };
+            switch (nt) {
+                case 1: sf37_router_wave<2, 1>(wr, nr, p.x, p.K, cg, t0, scr[wave], store, xf); break;
+                case 2: sf37_router_wave<2, 2>(wr, nr, p.x, p.K, cg, t0, scr[wave], store, xf); break;
+                case 3: sf37_router_wave<2, 3>(wr, nr, p.x, p.K, cg, t0, scr[wave], store, xf); break;
+                default: sf37_router_wave<2, 4>(wr, nr, p.x, p.K, cg, t0, scr[wave], store, xf); break;
+            }
+        } else {
+            switch (nt) {
+                case 1: sf37_router_wave<2, 1>(wr, nr, p.x, p.K, cg, t0, scr[wave], store); break;
+                case 2: sf37_router_wave<2, 2>(wr, nr, p.x, p.K, cg, t0, scr[wave], store); break;
+                case 3: sf37_router_wave<2, 3>(wr, nr, p.x, p.K, cg, t0, scr[wave], store); break;
+                default: sf37_router_wave<2, 4>(wr, nr, p.x, p.K, cg, t0, scr[wave], store); break;
             }
         }
     }
     __syncthreads();
-    if ((p.flags & SF37_DEC_SELECT) && threadIdx.x < RT_ROWS * p.T) {
-        const uint32_t r = threadIdx.x / p.T, t = threadIdx.x - r * p.T, e = e0 + r;
-        if (e < p.E) {
-            const bool own = (p.flags & SF37_DEC_ROUTER) && p.logits_sel == p.logits;
-            const float l = own ? s_logit[r][t] : p.logits_sel[(uint64_t)t * p.E + e];
-            float pr;
-            p.cand_key[(uint64_t)t * p.E + e] = sf37_topk_candidate(l, p.router_bias[e], e, tab, pr);
-            p.cand_p[(uint64_t)t * p.E + e] = pr;
+    if (threadIdx.x < 2u * nt) {
+        const uint32_t r = threadIdx.x / nt, t = threadIdx.x - r * nt, e = e0 + r;
+        if (r < nr) {
+            float l = 0.0f;
+            if (p.flags & SF37_DEC_ROUTER) {
+                l = sf37_router_combine(part[r][t]);
+                p.logits[(uint64_t)(t0 + t) * p.E + e] = l;
+            }
+            if (p.flags & SF37_DEC_SELECT) {
+                const bool own = (p.flags & SF37_DEC_ROUTER) && p.logits_sel == p.logits;
+                const float ls = own ? l : p.logits_sel[(uint64_t)(t0 + t) * p.E + e];
+                float pr;
+                p.cand_key[(uint64_t)(t0 + t) * p.E + e] = sf37_topk_candidate(ls, p.router_bias[e], e, tab, pr);
+                p.cand_p[(uint64_t)(t0 + t) * p.E + e] = pr;
+            }
         }
     }
 }
@@ -273,55 +274,61 @@ __global__ void __launch_bounds__(512) dec_route_kernel(dec_params p, uint32_t n
 // select + shared gate/up
 // ---------------------------------------------------------------------------
 
-// Top-k of every token from the candidates (SELECT; else sel and wts are
-// inputs), then the (token, slot) pairs grouped by expert: the group table
-// gi ([0] groups, [1..G+1] pair offsets, [G+2..2G+2) experts) and the
-// sorted pairs so, in the caller's LDS.  Every routed up workgroup runs it;
-// the one with publish also writes sel, wts, ginfo and sorted for the later
-// kernels.  All threads of the workgroup take part.
-__device__ void select_and_group(const dec_params &p, uint32_t *gi, uint32_t *so, bool publish) {
-    __shared__ uint32_t s_sel[DEC_MAX_TOK * 16];    // selected expert ids (raw)
-    __shared__ uint32_t s_e[DEC_MAX_TOK * 16];      // clamped ids, pair order
-    __shared__ uint32_t s_se[DEC_MAX_TOK * 16];     // clamped ids, sorted order
-    __shared__ float s_wts[DEC_MAX_TOK * 16];
-    __shared__ uint32_t s_wcnt[4];
-    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+// Token t's top-k by one wave from the candidates the route launch formed
+// (sf37_wave_topk_cand: k rounds of a wave arg-max, sf37.c:2144-2157);
+// sel_out / w_out receive the k slots.
+__device__ void token_topk(const dec_params &p, uint32_t t, int32_t *sel_out, float *w_out) {
+    const uint64_t *ck = p.cand_key + (uint64_t)t * p.E;
+    const float *cp = p.cand_p + (uint64_t)t * p.E;
+    int32_t *so[1] = {sel_out};
+    float *wo[1] = {w_out};
+    sf37_wave_topk_cand<1>(
+        [ck, cp](uint32_t, uint32_t e, float &pr) {
+            pr = cp[e];
+            return ck[e];
+        },
+        p.E, p.topk, p.scale, so, wo);
+}
+
+// Inclusive sum over the wave's lanes (DPP row shifts, then rows 0-1 into
+// 1-3), broadcast from lane 63 by the caller as needed.
+__device__ __forceinline__ uint32_t wave_incl_sum(uint32_t v) {
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x111, 0xf, 0xf, false);   // row_shr 1
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x112, 0xf, 0xf, false);   // row_shr 2
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x114, 0xf, 0xf, false);   // row_shr 4
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x118, 0xf, 0xf, false);   // row_shr 8
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x142, 0xa, 0xf, false);   // row_bcast 15
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x143, 0xc, 0xf, false);   // row_bcast 31
+    return v;
+}
+
+constexpr uint32_t GROUP_MAX_E = 1024;   // experts the token-mask grouping handles
+
+// The P = T * topk (token, slot) pairs grouped by expert, stably in pair
+// order: gi ([0] groups n, [1 + g] first sorted position of group g,
+// [1 + n] = P, [2 + G + g] its expert) and so (sorted position -> pair), in
+// the caller's LDS; publish also writes ginfo and sorted.  s_sel holds the
+// P selected ids (invalid ids act as expert 0).  When no token holds one
+// expert twice, pair i = t * topk + s of expert e goes to start(e) + the
+// number of earlier tokens holding e (per-expert token masks, one scan over
+// the experts); otherwise every pair counts the pairs ordered before it.
+// All threads of the workgroup take part; ends with a barrier.
+__device__ void group_pairs(const dec_params &p, const uint32_t *s_sel, uint32_t *gi, uint32_t *so, bool publish) {
+    __shared__ uint32_t msk[GROUP_MAX_E], st[GROUP_MAX_E];
+    __shared__ uint32_t s_e[DEC_MAX_TOK * 16], s_se[DEC_MAX_TOK * 16];
+    __shared__ uint32_t s_tot[2], s_wcnt[16];
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u, nthr = blockDim.x;
     const uint32_t P = p.T * p.topk;
-    if (p.flags & SF37_DEC_SELECT) {
-        // wave w: tokens w, w + 4, ... two at a time; selections into LDS
-        for (uint32_t t = wave; t < p.T; t += 8u) {
-            const uint32_t t2 = t + 4u < p.T ? t + 4u : t;
-            const uint64_t *k0 = p.cand_key + (uint64_t)t * p.E, *k1 = p.cand_key + (uint64_t)t2 * p.E;
-            const float *p0 = p.cand_p + (uint64_t)t * p.E, *p1 = p.cand_p + (uint64_t)t2 * p.E;
-            int32_t *sl[2] = {(int32_t *)s_sel + t * p.topk, (int32_t *)s_sel + t2 * p.topk};
-            float *wo[2] = {s_wts + t * p.topk, s_wts + t2 * p.topk};
-            sf37_wave_topk_cand<2>(
-                [k0, k1, p0, p1](uint32_t k, uint32_t e, float &pr) {
-                    pr = (k ? p1 : p0)[e];
-                    return (k ? k1 : k0)[e];
-                },
-                p.E, p.topk, p.scale, sl, wo);
-        }
-        __syncthreads();
-        if (publish && threadIdx.x < P) {
-            p.sel[threadIdx.x] = (int32_t)s_sel[threadIdx.x];
-            p.wts[threadIdx.x] = s_wts[threadIdx.x];
-        }
-    } else if (threadIdx.x < P) {
-        s_sel[threadIdx.x] = (uint32_t)p.sel[threadIdx.x];
-    }
-    if (threadIdx.x < P) s_e[threadIdx.x] = clamp_expert((int32_t)s_sel[threadIdx.x], p.E);
-    __syncthreads();
     if (p.flags & SF37_DEC_SLOTS) {
         if (threadIdx.x < p.topk) {
-            const uint32_t s = threadIdx.x;
+            const uint32_t s = threadIdx.x, e = clamp_expert((int32_t)s_sel[s], p.E);
             so[s] = s;
             gi[1u + s] = s;
-            gi[2u + p.G + s] = s_e[s];
+            gi[2u + p.G + s] = e;
             if (publish) {
                 p.sorted[s] = s;
                 p.ginfo[1u + s] = s;
-                p.ginfo[2u + p.G + s] = s_e[s];
+                p.ginfo[2u + p.G + s] = e;
             }
         }
         if (threadIdx.x == 0) {
@@ -332,10 +339,77 @@ __device__ void select_and_group(const dec_params &p, uint32_t *gi, uint32_t *so
                 p.ginfo[1u + p.topk] = p.topk;
             }
         }
+        __syncthreads();
         return;
     }
-    // stable order by (expert, pair id): position = #pairs with a smaller
-    // expert + #earlier pairs with the same expert
+    const bool masks = p.E <= GROUP_MAX_E;
+    if (masks) {
+        for (uint32_t e = threadIdx.x; e < p.E; e += nthr) msk[e] = 0u;
+        __syncthreads();
+        if (threadIdx.x < P)
+            atomicOr(&msk[clamp_expert((int32_t)s_sel[threadIdx.x], p.E)], 1u << (threadIdx.x / p.topk));
+        __syncthreads();
+        if (wave == 0) {
+            // lane l: experts [c l, c l + c); exclusive scans of the pair
+            // counts and of the non-empty experts
+            const uint32_t c = (p.E + 63u) >> 6, e0 = lane * c;
+            uint32_t n = 0, g = 0;
+            for (uint32_t i = 0; i < c; i++) {
+                const uint32_t e = e0 + i;
+                if (e < p.E) {
+                    const uint32_t m = msk[e];
+                    n += (uint32_t)__builtin_popcount(m);
+                    g += m != 0u;
+                }
+            }
+            const uint32_t ni = wave_incl_sum(n), gin = wave_incl_sum(g);
+            uint32_t ne = ni - n, ge = gin - g;
+            if (lane == 63u) {
+                s_tot[0] = ni;
+                s_tot[1] = gin;
+            }
+            for (uint32_t i = 0; i < c; i++) {
+                const uint32_t e = e0 + i;
+                if (e < p.E) {
+                    const uint32_t m = msk[e];
+                    st[e] = ne;
+                    if (m) {
+                        gi[1u + ge] = ne;
+                        gi[2u + p.G + ge] = e;
+                        if (publish) {
+                            p.ginfo[1u + ge] = ne;
+                            p.ginfo[2u + p.G + ge] = e;
+                        }
+                        ge++;
+                        ne += (uint32_t)__builtin_popcount(m);
+                    }
+                }
+            }
+        }
+        __syncthreads();
+    }
+    if (masks && s_tot[0] == P) {
+        if (threadIdx.x == 0) {
+            const uint32_t ng = s_tot[1];
+            gi[0] = ng;
+            gi[1u + ng] = P;
+            if (publish) {
+                p.ginfo[0] = ng;
+                p.ginfo[1u + ng] = P;
+            }
+        }
+        if (threadIdx.x < P) {
+            const uint32_t i = threadIdx.x, e = clamp_expert((int32_t)s_sel[i], p.E), t = i / p.topk;
+            const uint32_t pos = st[e] + (uint32_t)__builtin_popcount(msk[e] & ((1u << t) - 1u));
+            so[pos] = i;
+            if (publish) p.sorted[pos] = i;
+        }
+        __syncthreads();
+        return;
+    }
+    // a token holds an expert twice: each pair counts the pairs before it
+    if (threadIdx.x < P) s_e[threadIdx.x] = clamp_expert((int32_t)s_sel[threadIdx.x], p.E);
+    __syncthreads();
     if (threadIdx.x < P) {
         const uint32_t i = threadIdx.x, e = s_e[i];
         uint32_t pos = 0;
@@ -378,6 +452,30 @@ __device__ void select_and_group(const dec_params &p, uint32_t *gi, uint32_t *so
             p.ginfo[1u + ng] = P;
         }
     }
+    __syncthreads();
+}
+
+// Top-k of every token inside one workgroup (one wave per token, waves
+// looping) into s_sel / s_wts, or the selections read from sel when they
+// are inputs; then the grouping.  publish: this workgroup also writes sel
+// and wts (SELECT), ginfo and sorted.  Used by the up launch when it runs
+// the select step itself (UPSEL).
+__device__ void select_and_group(const dec_params &p, uint32_t *gi, uint32_t *so, bool publish) {
+    __shared__ int32_t s_sel[DEC_MAX_TOK * 16];
+    __shared__ float s_wts[DEC_MAX_TOK * 16];
+    const uint32_t wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    const uint32_t P = p.T * p.topk;
+    if (p.flags & SF37_DEC_SELECT) {
+        for (uint32_t t = wave; t < p.T; t += nw) token_topk(p, t, s_sel + t * p.topk, s_wts + t * p.topk);
+    } else if (threadIdx.x < P) {
+        s_sel[threadIdx.x] = p.sel[threadIdx.x];
+    }
+    __syncthreads();
+    if (publish && (p.flags & SF37_DEC_SELECT) && threadIdx.x < P) {
+        p.sel[threadIdx.x] = s_sel[threadIdx.x];
+        p.wts[threadIdx.x] = s_wts[threadIdx.x];
+    }
+    group_pairs(p, (const uint32_t *)s_sel, gi, so, publish);
 }
 
 // Shared gate/up workgroup wg (the leading workgroups of the up launch):
@@ -860,14 +958,35 @@ __device__ void up_items_pairs(const dec_params &p, const uint32_t *gi, const ui
 // are always loaded while the current one is computed.
 // Select launch (batches of more tokens): workgroup 0 forms the top-k and
 // the grouping; workgroups 1.. the shared gate/up rows.
-__global__ void __launch_bounds__(256) dec_select_kernel(dec_params p) {
+// Select launch: workgroups [0, n_tk) - wave w of workgroup b takes token
+// 4 b + w (token_topk, writing sel and wts); the last of them to
+// arrive (a counter; each releases its writes before arriving) groups the
+// pairs and publishes ginfo and sorted.  Workgroups [n_tk, ...) compute the
+// shared gate/up rows.
+__global__ void __launch_bounds__(256) dec_select_kernel(dec_params p, uint32_t n_tk) {
     extern __shared__ __align__(16) unsigned char smem[];
-    if (blockIdx.x == 0) {
-        __shared__ uint32_t s_gi[3u + 2u * DEC_MAX_TOK * 16u], s_so[DEC_MAX_TOK * 16u];
-        select_and_group(p, s_gi, s_so, true);
+    if (blockIdx.x >= n_tk) {
+        shared_gate_up(p, blockIdx.x - n_tk, smem);
         return;
     }
-    shared_gate_up(p, blockIdx.x - 1u, smem);
+    __shared__ uint32_t s_sel[DEC_MAX_TOK * 16], s_gi[3u + 2u * DEC_MAX_TOK * 16u], s_so[DEC_MAX_TOK * 16u];
+    __shared__ uint32_t s_last;
+    const uint32_t wave = threadIdx.x >> 6, P = p.T * p.topk;
+    const uint32_t t = blockIdx.x * 4u + wave;
+    if ((p.flags & SF37_DEC_SELECT) && t < p.T) token_topk(p, t, p.sel + t * p.topk, p.wts + t * p.topk);
+    __syncthreads();
+    if (n_tk > 1u) {
+        if (threadIdx.x == 0) {
+            __threadfence();
+            s_last = atomicAdd(sel_arrivals(p), 1u) == n_tk - 1u;
+        }
+        __syncthreads();
+        if (!s_last) return;
+        __threadfence();
+    }
+    if (threadIdx.x < P) s_sel[threadIdx.x] = (uint32_t)p.sel[threadIdx.x];
+    __syncthreads();
+    group_pairs(p, s_sel, s_gi, s_so, true);
 }
 
 // The routed part of the up launch on the block-pair DMA path (rows of 4, 8
@@ -1043,7 +1162,7 @@ __global__ void __launch_bounds__(256) dec_up_kernel(dec_params p, uint32_t n_sh
 // ---------------------------------------------------------------------------
 __global__ void __launch_bounds__(256) dec_mid_kernel(dec_params p) {
     __shared__ uint64_t tab[32];
-    sf37_stage_exp_tab(tab);
+    stage_exp_tab_imm(tab);
     __syncthreads();
     const uint32_t lane = threadIdx.x & 63u, nbm = p.F / SF37_QK;
     const uint32_t w = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6), n_routed = p.T * p.topk * nbm;
@@ -1316,7 +1435,7 @@ namespace {
 
 struct dec_shape {
     bool up_wide;
-    uint32_t n_rt, n_xq, n_shup, n_up, n_mid, n_dn, n_cb;
+    uint32_t n_rt, n_xq, n_tk, n_shup, n_up, n_mid, n_dn, n_cb;
     size_t lds_up, lds_shup, lds_dn;
     const void *dn_kernel;
 };
@@ -1373,8 +1492,9 @@ dec_shape dec_plan(const dec_params &p) {
     const uint32_t nb = p.K / SF37_QK;
     const bool sh = (p.flags & SF37_DEC_SHARED) != 0;
     const uint32_t cus = device_cus();
-    d.n_rt = (p.flags & (SF37_DEC_ROUTER | SF37_DEC_SELECT)) ? (p.E + RT_ROWS - 1u) / RT_ROWS : 0u;
-    d.n_xq = (p.T * nb + route_threads(p.T) / 64u - 1u) / (route_threads(p.T) / 64u);
+    d.n_rt = (p.flags & (SF37_DEC_ROUTER | SF37_DEC_SELECT)) ? route_wgs(p.T, p.E) : 0u;
+    d.n_xq = (p.T * nb + 3u) / 4u;
+    d.n_tk = (p.T + 3u) / 4u;
     // routed up: 8-wave block-pair DMA workgroups when the batch has a
     // select launch and they fit, else the row-pair loop
     const uint32_t P = p.T * p.topk;
@@ -1460,8 +1580,7 @@ int set_lds(const void *fn, size_t bytes, size_t *opted) {
 
 extern "C" int sf37k_decode_route(const sf37_dec_params *pp, sf37_stream_t s) {
     const dec_shape d = dec_plan(*pp);
-    hipLaunchKernelGGL(dec_route_kernel, dim3(d.n_rt + d.n_xq), dim3(route_threads(pp->T)), 0, (hipStream_t)s, *pp,
-                       d.n_rt);
+    hipLaunchKernelGGL(dec_route_kernel, dim3(d.n_rt + d.n_xq), dim3(256), 0, (hipStream_t)s, *pp, d.n_rt);
     return (int)hipGetLastError();
 }
 
@@ -1470,8 +1589,8 @@ extern "C" int sf37k_decode_select(const sf37_dec_params *pp, sf37_stream_t s) {
     static size_t opted = 65536;
     const int err = set_lds((const void *)dec_select_kernel, d.n_shup ? d.lds_shup : 0u, &opted);
     if (err) return err;
-    hipLaunchKernelGGL(dec_select_kernel, dim3(1u + d.n_shup), dim3(256), d.n_shup ? d.lds_shup : 0u, (hipStream_t)s,
-                       *pp);
+    hipLaunchKernelGGL(dec_select_kernel, dim3(d.n_tk + d.n_shup), dim3(256), d.n_shup ? d.lds_shup : 0u,
+                       (hipStream_t)s, *pp, d.n_tk);
     return (int)hipGetLastError();
 }
 
