@@ -36,7 +36,8 @@ namespace {
 
 constexpr uint32_t DEC_MAX_TOK = 16;
 constexpr uint32_t DEC_TPC = 4;      // pairs per pass in the routed kernels
-constexpr uint32_t SH_RS = 2;        // shared gate/up rows per workgroup
+constexpr uint32_t SH_RS_UP = 2;     // shared gate/up rows per workgroup in the up launch (256 threads)
+constexpr uint32_t SH_RS_SEL = 4;    // ... in the select launch (512 threads)
 constexpr uint32_t DN_MAX_NB = 5;    // down blocks per row held in registers (F <= 1280)
 constexpr uint32_t DN_TPC = 2;       // pairs per pass in the routed down kernel
 constexpr uint32_t DN_STAGE = 4;     // pairs whose activation blocks a down wave keeps in LDS
@@ -81,7 +82,7 @@ __host__ __device__ constexpr uint32_t shd_bps(uint32_t nb8, uint32_t S) { retur
 // LDS layout sizes, shared by the kernels and the host-side launch plan.
 // A weight tile buffer holds the tile plus the copy's leading offset.
 __host__ __device__ constexpr uint32_t tile_buf(uint32_t bytes) { return (bytes + 31u + 15u) & ~15u; }
-__host__ __device__ constexpr uint32_t up_shared_tile(uint32_t K) { return SH_RS * (K / 32u) * SF37_Q8_0_BYTES; }
+__host__ __device__ constexpr uint32_t up_shared_tile(uint32_t K, uint32_t rs) { return rs * (K / 32u) * SF37_Q8_0_BYTES; }
 // up workgroup: x of every token, then group info and sorted pairs
 // An activation block in the up kernel's LDS, padded to 304 bytes so the 16
 // blocks a wave reads at once spread over the LDS banks (a 288-byte stride
@@ -106,8 +107,8 @@ __host__ __device__ constexpr size_t tile_base(uint32_t K, uint32_t T, uint32_t 
 __host__ __device__ constexpr size_t lds_up_dma(uint32_t K, uint32_t T, uint32_t G, uint32_t P, uint32_t waves) {
     return tile_base(K, T, G, P) + (size_t)waves * 14336u;
 }
-__host__ __device__ constexpr size_t lds_up_shared(uint32_t K, uint32_t T) {
-    return 2u * (size_t)tile_buf(up_shared_tile(K)) + (size_t)T * 2u * SH_RS * (K / 32u) * 4u;
+__host__ __device__ constexpr size_t lds_up_shared(uint32_t K, uint32_t T, uint32_t rs) {
+    return 2u * (size_t)tile_buf(up_shared_tile(K, rs)) + (size_t)T * 2u * rs * (K / 32u) * 4u;
 }
 
 // Q8_0 block (34 bytes) at LDS byte offset L of base: scale, eight i8x4 words.
@@ -479,14 +480,14 @@ __device__ void select_and_group(const dec_params &p, uint32_t *gi, uint32_t *so
 }
 
 // Shared gate/up workgroup wg (the leading workgroups of the up launch):
-// SH_RS shared gate/up rows - the weight tiles copied to LDS while the x
+// rs shared gate/up rows - the weight tiles copied to LDS while the x
 // blocks of the first 8 tokens load, the terms in LDS, then the
 // reference's sequential block sum per (matrix, token, row)
 // (sf37_ops.c:92-108) into sh_gu.
-__device__ void shared_gate_up(const dec_params &p, uint32_t wg, unsigned char *smem) {
+__device__ void shared_gate_up(const dec_params &p, uint32_t wg, unsigned char *smem, uint32_t rs) {
     const uint32_t nb8 = p.K / 32u;
-    const uint32_t row0 = wg * SH_RS;
-    const uint32_t tbytes = up_shared_tile(p.K), wbuf = tile_buf(tbytes);
+    const uint32_t row0 = wg * rs;
+    const uint32_t tbytes = up_shared_tile(p.K, rs), wbuf = tile_buf(tbytes);
     const uint64_t row_bytes = (uint64_t)nb8 * SF37_Q8_0_BYTES;
     uint8_t *wl = smem;                                             // gate tile | up tile
     float *red = (float *)(smem + 2u * wbuf);                       // [T][2][RS][nb8]
@@ -505,9 +506,9 @@ __device__ void shared_gate_up(const dec_params &p, uint32_t wg, unsigned char *
             xs[j] = p.xs8[(uint64_t)t * nb8 + b];
         }
     };
-    if (threadIdx.x < SH_RS * nb8) load_x(threadIdx.x % nb8, 0);
+    if (threadIdx.x < rs * nb8) load_x(threadIdx.x % nb8, 0);
     lds_copy_wait();
-    for (uint32_t rb = threadIdx.x; rb < SH_RS * nb8; rb += blockDim.x) {
+    for (uint32_t rb = threadIdx.x; rb < rs * nb8; rb += blockDim.x) {
         const uint32_t r = rb / nb8, b = rb - r * nb8;
         uint32_t qg[8], qu[8];
         const float wg = q8_0_lds(wl, og + rb * SF37_Q8_0_BYTES, qg);
@@ -525,16 +526,16 @@ __device__ void shared_gate_up(const dec_params &p, uint32_t wg, unsigned char *
                         ig = sdot4(qg[k], xv[k], ig);
                         iu = sdot4(qu[k], xv[k], iu);
                     }
-                    red[((t * 2u + 0u) * SH_RS + r) * nb8 + b] = (float)ig * wg * xs[j];
-                    red[((t * 2u + 1u) * SH_RS + r) * nb8 + b] = (float)iu * wu * xs[j];
+                    red[((t * 2u + 0u) * rs + r) * nb8 + b] = (float)ig * wg * xs[j];
+                    red[((t * 2u + 1u) * rs + r) * nb8 + b] = (float)iu * wu * xs[j];
                 }
             }
         }
     }
     __syncthreads();
-    for (uint32_t i = threadIdx.x; i < p.T * 2u * SH_RS; i += blockDim.x) {
-        const uint32_t t = i / (2u * SH_RS), mr = i - t * 2u * SH_RS;
-        const uint32_t m = mr / SH_RS, r = mr - m * SH_RS;
+    for (uint32_t i = threadIdx.x; i < p.T * 2u * rs; i += blockDim.x) {
+        const uint32_t t = i / (2u * rs), mr = i - t * 2u * rs;
+        const uint32_t m = mr / rs, r = mr - m * rs;
         const float *rv = red + (uint64_t)i * nb8;
         float acc = 0.0f;
         if ((nb8 & 15u) == 0) {
@@ -958,24 +959,37 @@ __device__ void up_items_pairs(const dec_params &p, const uint32_t *gi, const ui
 // are always loaded while the current one is computed.
 // Select launch (batches of more tokens): workgroup 0 forms the top-k and
 // the grouping; workgroups 1.. the shared gate/up rows.
-// Select launch: workgroups [0, n_tk) - wave w of workgroup b takes token
-// 4 b + w (token_topk, writing sel and wts); the last of them to
-// arrive (a counter; each releases its writes before arriving) groups the
-// pairs and publishes ginfo and sorted.  Workgroups [n_tk, ...) compute the
-// shared gate/up rows.
-__global__ void __launch_bounds__(256) dec_select_kernel(dec_params p, uint32_t n_tk) {
+// Select launch (512 threads): workgroups [0, n_tk) - wave w of workgroup
+// b takes token 8 b + w (token_topk into LDS, then sel and wts); up to 8
+// tokens the one workgroup groups the pairs from LDS, above that the last
+// top-k workgroup to arrive (a counter; each releases its writes before
+// arriving) groups them from sel.  Both publish ginfo and sorted.
+// Workgroups [n_tk, ...) compute the shared gate/up rows.
+__global__ void __launch_bounds__(512) dec_select_kernel(dec_params p, uint32_t n_tk) {
     extern __shared__ __align__(16) unsigned char smem[];
     if (blockIdx.x >= n_tk) {
-        shared_gate_up(p, blockIdx.x - n_tk, smem);
+        shared_gate_up(p, blockIdx.x - n_tk, smem, SH_RS_SEL);
         return;
     }
-    __shared__ uint32_t s_sel[DEC_MAX_TOK * 16], s_gi[3u + 2u * DEC_MAX_TOK * 16u], s_so[DEC_MAX_TOK * 16u];
+    __shared__ int32_t s_sel[DEC_MAX_TOK * 16];
+    __shared__ float s_wts[DEC_MAX_TOK * 16];
+    __shared__ uint32_t s_gi[3u + 2u * DEC_MAX_TOK * 16u], s_so[DEC_MAX_TOK * 16u];
     __shared__ uint32_t s_last;
     const uint32_t wave = threadIdx.x >> 6, P = p.T * p.topk;
-    const uint32_t t = blockIdx.x * 4u + wave;
-    if ((p.flags & SF37_DEC_SELECT) && t < p.T) token_topk(p, t, p.sel + t * p.topk, p.wts + t * p.topk);
-    __syncthreads();
+    const uint32_t t = blockIdx.x * 8u + wave, t0 = blockIdx.x * 8u;
+    const uint32_t p0 = t0 * p.topk, p1 = (p.T < t0 + 8u ? p.T : t0 + 8u) * p.topk;
+    if (p.flags & SF37_DEC_SELECT) {
+        if (t < p.T) token_topk(p, t, s_sel + t * p.topk, s_wts + t * p.topk);
+        __syncthreads();
+        if (threadIdx.x >= p0 && threadIdx.x < p1) {
+            p.sel[threadIdx.x] = s_sel[threadIdx.x];
+            p.wts[threadIdx.x] = s_wts[threadIdx.x];
+        }
+    } else if (threadIdx.x < P) {
+        s_sel[threadIdx.x] = p.sel[threadIdx.x];
+    }
     if (n_tk > 1u) {
+        __syncthreads();
         if (threadIdx.x == 0) {
             __threadfence();
             s_last = atomicAdd(sel_arrivals(p), 1u) == n_tk - 1u;
@@ -983,10 +997,10 @@ __global__ void __launch_bounds__(256) dec_select_kernel(dec_params p, uint32_t 
         __syncthreads();
         if (!s_last) return;
         __threadfence();
+        if (threadIdx.x < P && (threadIdx.x < p0 || threadIdx.x >= p1)) s_sel[threadIdx.x] = p.sel[threadIdx.x];
     }
-    if (threadIdx.x < P) s_sel[threadIdx.x] = (uint32_t)p.sel[threadIdx.x];
     __syncthreads();
-    group_pairs(p, s_sel, s_gi, s_so, true);
+    group_pairs(p, (const uint32_t *)s_sel, s_gi, s_so, true);
 }
 
 // The routed part of the up launch on the block-pair DMA path (rows of 4, 8
@@ -1034,7 +1048,7 @@ __global__ void __launch_bounds__(512) dec_up_dma_kernel(dec_params p) {
 __global__ void __launch_bounds__(256) dec_up_kernel(dec_params p, uint32_t n_sh) {
     extern __shared__ __align__(16) unsigned char smem[];
     if (blockIdx.x < n_sh) {
-        shared_gate_up(p, blockIdx.x, smem);
+        shared_gate_up(p, blockIdx.x, smem, SH_RS_UP);
         return;
     }
     const uint32_t wg = blockIdx.x - n_sh, n_wg = gridDim.x - n_sh;
@@ -1435,7 +1449,7 @@ namespace {
 
 struct dec_shape {
     bool up_wide;
-    uint32_t n_rt, n_xq, n_tk, n_shup, n_up, n_mid, n_dn, n_cb;
+    uint32_t n_rt, n_xq, n_tk, n_shup, sh_rs, n_up, n_mid, n_dn, n_cb;
     size_t lds_up, lds_shup, lds_dn;
     const void *dn_kernel;
 };
@@ -1494,15 +1508,16 @@ dec_shape dec_plan(const dec_params &p) {
     const uint32_t cus = device_cus();
     d.n_rt = (p.flags & (SF37_DEC_ROUTER | SF37_DEC_SELECT)) ? route_wgs(p.T, p.E) : 0u;
     d.n_xq = (p.T * nb + 3u) / 4u;
-    d.n_tk = (p.T + 3u) / 4u;
+    d.n_tk = (p.T + 7u) / 8u;
     // routed up: 8-wave block-pair DMA workgroups when the batch has a
     // select launch and they fit, else the row-pair loop
     const uint32_t P = p.T * p.topk;
     const bool upsel = (p.flags & SF37_DEC_UPSEL) != 0;
     d.up_wide = up_pairs(p.K) && !upsel && lds_up_dma(p.K, p.T, p.G, P, 8u) <= device_max_lds();
     d.lds_up = d.up_wide ? lds_up_dma(p.K, p.T, p.G, P, 8u) : lds_up_meta(p.K, p.T, p.G, P);
-    d.lds_shup = lds_up_shared(p.K, p.T);
-    d.n_shup = sh ? p.F / SH_RS : 0u;                  // shared gate/up workgroups (select or up launch)
+    d.sh_rs = (p.flags & SF37_DEC_UPSEL) ? SH_RS_UP : SH_RS_SEL;
+    d.lds_shup = lds_up_shared(p.K, p.T, d.sh_rs);
+    d.n_shup = sh ? p.F / d.sh_rs : 0u;                // shared gate/up workgroups (select or up launch)
     // persistent kernels: exactly as many workgroups as can be resident
     const size_t up_lds = d.lds_up > d.lds_shup || !d.n_shup || !(p.flags & SF37_DEC_UPSEL) ? d.lds_up : d.lds_shup;
     const uint32_t up_res = d.up_wide ? resident_wgs((const void *)dec_up_dma_kernel, 512, d.lds_up)
@@ -1564,7 +1579,8 @@ extern "C" int sf37k_decode_supported(uint32_t T, uint32_t topk, uint32_t E, uin
     if (shared && shd_bps(F / 32u, shd_slices(T)) > SHD_MAX_BPS) return 0;
     const uint32_t P = T * topk, G = P < E ? P : E;
     if (lds_up_meta(K, T, G, P) > device_max_lds()) return 0;
-    if (shared && lds_up_shared(K, T) > device_max_lds()) return 0;
+    if (shared && (lds_up_shared(K, T, SH_RS_UP) > device_max_lds() || lds_up_shared(K, T, SH_RS_SEL) > device_max_lds()))
+        return 0;
     return 1;
 }
 
@@ -1589,7 +1605,7 @@ extern "C" int sf37k_decode_select(const sf37_dec_params *pp, sf37_stream_t s) {
     static size_t opted = 65536;
     const int err = set_lds((const void *)dec_select_kernel, d.n_shup ? d.lds_shup : 0u, &opted);
     if (err) return err;
-    hipLaunchKernelGGL(dec_select_kernel, dim3(d.n_tk + d.n_shup), dim3(256), d.n_shup ? d.lds_shup : 0u,
+    hipLaunchKernelGGL(dec_select_kernel, dim3(d.n_tk + d.n_shup), dim3(512), d.n_shup ? d.lds_shup : 0u,
                        (hipStream_t)s, *pp, d.n_tk);
     return (int)hipGetLastError();
 }
