@@ -21,6 +21,14 @@ algorithmic bytes per launch over its average launch time from HIP events
 on the launch stream in a second, identical pass with stage events enabled.
 cpu_baseline: the reference CPU MoE path (sf37_ops.c/sf37_quant.c built with
 the reference `make cpu` flags) on one step's tokens, single core.
+
+Also on the line: config0 (the one-token decode step,
+same layers) with its own roofline; parity of the HIP layer against the
+reference CPU layer on the same weights and x (router logits from x):
+indices equal and max |gpu - cpu| / max(|cpu|, 1), for the decode configs
+and 8 sampled tokens of each prefill chunk; prefill (configs 3 and 2) with
+its matrix-core figures and a CPU baseline timed on the leading tokens of
+the config 3 chunk; stack.
 """
 from __future__ import annotations
 
@@ -139,10 +147,89 @@ def main():
         print(json.dumps({"stack": stack_bench(args, H)}), flush=True)
         return
 
-    layers, xs, lgs, sels = [], [], [], []
+    dec = decode_bench(args, H, n_tok)
+    dec1 = decode_bench(args, H, 1, layers=dec["layers"], summary=True) if n_tok != 1 else None
+    prefill = [prefill_bench(args, H, dec["layers"][0], c) for c in (3, 2)] if args.prefill_steps > 0 else None
+
+    cpu, parity = None, None
+    if not args.no_cpu:
+        lay0 = dec["layers"][0]
+        cpu = cpu_baseline(lay0, dec["xs"][0], dec["sels"][0], dec["step_bytes"][0], n_tok, args.cpu_seconds)
+        parity = {f"config{1 if n_tok == 8 else 'x'}_decode_{n_tok}tok":
+                  parity_vs_cpu(lay0, dec["xs"][0].read(np.float32).reshape(n_tok, K))}
+        if dec1 is not None:
+            parity["config0_decode_1tok"] = parity_vs_cpu(lay0, dec["xs"][0].read(np.float32).reshape(n_tok, K)[:1])
+        if prefill:
+            for pf in prefill:
+                c = pf["config"]
+                xs_c = configs.x_device(c, args.seed + 1000 * c, pf["tokens"])
+                parity[f"config{c}_prefill_{pf['tokens']}tok_sample8"] = parity_vs_cpu(
+                    lay0, xs_c.read(np.float32).reshape(pf["tokens"], K), n_check=8)
+                if c == 3 and cpu is not None:
+                    pf["cpu_baseline"] = cpu_prefill_baseline(lay0, xs_c.read(np.float32).reshape(pf["tokens"], K),
+                                                              args.cpu_seconds)
+                xs_c.free()
+            for pf in prefill:
+                if pf["config"] != 3 and cpu is not None:
+                    pf["cpu_baseline"] = dict(prefill[0].get("cpu_baseline") or {}, note=
+                                              "the CPU path is per token (sf37.c:7786-7797); the config 3 sample "
+                                              "time applies to any chunk")
+    for lay in dec["layers"]:
+        lay.free()
+    stack = stack_bench(args, H) if args.stack_layers > 0 else None
+
+    value, ms_per_step, mean_bytes = dec["value"], dec["ms_per_step"], dec["mean_bytes"]
+    line = {
+        "metric": "MoE layer decode HBM GB/s (% of peak); prefill tokens/s/layer, MFMA util",
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic (seeded N(0,0.02) weights quantized by the reference quantizer; x ~ N(0,1); "
+                "injected N(0,1) router logits)",
+        "config": {"workload": ("BASELINE configs[1]: " if n_tok == 8 else "")
+                               + f"one MoE layer decode step, {n_tok} tokens, uniform routing",
+                   "experts": E, "hidden": K, "expert_ff": F, "top_k": TOPK,
+                   "formats": "Q3GU gate/up, Q2D down, Q8_0 shared, fp32 router",
+                   "layers_rotated": args.layers, "hbm_bytes_per_step": int(mean_bytes),
+                   "pct_of_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 2)},
+        "roofline": dec["roofline"],
+        "cpu_baseline": cpu,
+        "stages": dec["stages"],
+        "stage_timing": STAGE_TIMING_NOTE,
+        "config0": dec1,
+        "parity": parity,
+        "prefill": prefill,
+        "stack": stack,
+    }
+    print(json.dumps(line), flush=True)
+
+
+STAGE_TIMING_NOTE = ("stage and roofline kernel times are HIP events recorded around each launch on the launch "
+                     "stream in a second identical pass: they include the dispatch, so short kernels read longer "
+                     "than rocprofv3's kernel durations (profiles/ holds the rocprofv3 traces of the same command)")
+
+
+def decode_bench(args, H, n_tok, layers=None, summary=False):
+    """Timed decode steps of n_tok tokens over --layers rotated layers (made
+    here unless given); the dominant kernel's roofline from a second pass
+    with stage events.  With summary, only the figures are returned (the
+    inputs made here are freed)."""
+    from sf37_amd import configs, hip, moe
+    E, K, F, TOPK = moe.EXPERTS, moe.EMBD, moe.EXPERT_FF, moe.EXPERT_USED
+    own = layers is None
+    layers = [] if own else layers
+    xs, lgs, sels = [], [], []
     for l in range(args.layers):
         seed = moe.layer_seed(args.seed, l)
-        layers.append(moe.SynthLayer(seed=seed))
+        if own:
+            layers.append(moe.SynthLayer(seed=seed))
         xs.append(configs.x_device(1, seed, n_tok))
         lg = configs.logits_for(1, seed, n_tok)
         lgs.append(hip.Tensor.from_array(lg))
@@ -223,56 +310,117 @@ def main():
     k_avg_ms = k_ms / k_n
     k_mean_bytes = float(np.mean([kern_bytes[i % args.layers][kern] for i in range(args.steps)]))
     achieved = k_mean_bytes / (k_avg_ms * 1e-3) / 1e9
-    traffic = measured_traffic(kern)
-
-    prefill = [prefill_bench(args, H, layers[0], c) for c in (3, 2)] if args.prefill_steps > 0 else None
-    for lay in layers:
-        lay.free()
-    stack = stack_bench(args, H) if args.stack_layers > 0 else None
-
-    cpu = None
-    if not args.no_cpu:
-        cpu_layer = moe.SynthLayer(seed=moe.layer_seed(args.seed, 0))
-        cpu = cpu_baseline(cpu_layer, xs[0], sels[0], step_bytes[0], n_tok, args.cpu_seconds)
-        cpu_layer.free()
-        if cpu and prefill:
-            # the CPU engine has no batch path (sf37.c:7786-7797): a prefill chunk
-            # runs the same per-token layer, so its tokens/s/layer is 1 / (time per token)
-            for pf in prefill:
-                pf["cpu_baseline"] = {"value": round(1e3 / cpu["ms_per_token"], 2), "unit": "tokens/s/layer",
-                                      "cores": 1, "kind": cpu["kind"],
-                                      "sample": "the per-token time of the decode cpu_baseline (same path)"}
-
+    traffic = measured_traffic(kern) if n_tok == 8 else None
     stages = {k: {"ms_per_launch": round(v[0] / max(v[1], 1), 5), "launches": v[1]} for k, v in prof.items() if v[1]}
-    line = {
-        "metric": "MoE layer decode HBM GB/s (% of peak); prefill tokens/s/layer, MFMA util",
-        "value": round(value, 2),
-        "unit": "GB/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(ms_per_step, 5),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "int8",
-        "data": "synthetic (seeded N(0,0.02) weights quantized by the reference quantizer; x ~ N(0,1); "
-                "injected N(0,1) router logits)",
-        "config": {"workload": ("BASELINE configs[1]: " if n_tok == 8 else "")
-                               + f"one MoE layer decode step, {n_tok} tokens, uniform routing",
-                   "experts": E, "hidden": K, "expert_ff": F, "top_k": TOPK,
-                   "formats": "Q3GU gate/up, Q2D down, Q8_0 shared, fp32 router",
-                   "layers_rotated": args.layers, "hbm_bytes_per_step": int(mean_bytes),
-                   "pct_of_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 2)},
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "kernel": kern, "bytes_per_launch": int(k_mean_bytes), "ms_per_launch": round(k_avg_ms, 5)},
-        "cpu_baseline": cpu,
-        "stages": stages,
-        "prefill": prefill,
-        "stack": stack,
-    }
-    print(json.dumps(line), flush=True)
+    roof = {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+            "kernel": kern, "bytes_per_launch": int(k_mean_bytes), "ms_per_launch": round(k_avg_ms, 5)}
+    for t in [out, sel, wts] + lgs:
+        t.free()
+    res = {"value": value, "ms_per_step": ms_per_step, "mean_bytes": mean_bytes, "roofline": roof,
+           "stages": stages}
+    if summary:
+        if own:
+            for lay in layers:
+                lay.free()
+        for x in xs:
+            x.free()
+        return {"workload": ("BASELINE configs[0]: " if n_tok == 1 else "")
+                            + f"one MoE layer decode step, {n_tok} token(s), uniform routing",
+                "value": round(value, 2), "unit": "GB/s", "ms_per_step": round(ms_per_step, 5),
+                "hbm_bytes_per_step": int(mean_bytes), "pct_of_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 2),
+                "roofline": roof, "stages": stages}
+    res.update(layers=layers, xs=xs, sels=sels, step_bytes=step_bytes)
+    return res
+
+
+def parity_vs_cpu(layer, x, n_check=None):
+    """The HIP layer (router logits from x) against the reference CPU layer
+    (oracle/_ref/libsf37cpu_ref.so: the reference's sf37_ops.c / sf37_quant.c
+    composed as layer_moe_ffn, sf37.c:2127-2194) on the first n_check rows of
+    x: whether both select the same experts per token, and
+    max |gpu - cpu| / max(|cpu|, 1) over the outputs."""
+    import oracle
+    from sf37_amd import hip
+    lib = oracle.cpu_baseline_lib("reference")
+    kind = "reference"
+    if lib is None:
+        lib, kind = oracle.cpu_baseline_lib("port"), "port"
+    if lib is None:
+        return None
+    n_tok, K = x.shape
+    E, F, TOPK = layer.n_expert, layer.mid_dim, layer.topk
+    xd = hip.Tensor.from_array(np.ascontiguousarray(x, np.float32))
+    out, sel, wts = hip.Tensor.alloc(n_tok * K * 4), hip.Tensor.alloc(n_tok * TOPK * 4), \
+        hip.Tensor.alloc(n_tok * TOPK * 4)
+    hip.check(hip.lib().sf37_hip_moe_layer(out, sel, wts, layer.weights_struct(), None, xd, n_tok), "moe layer (parity)")
+    n = n_tok if n_check is None else min(n_check, n_tok)
+    got = out.read(np.float32).reshape(n_tok, K)[:n]
+    gsel = sel.read(np.int32).reshape(n_tok, TOPK)[:n]
+    for t in (xd, out, sel, wts):
+        t.free()
+    dense = layer.host_dense()
+    fp = lambda a: a.ctypes.data_as(C.POINTER(C.c_float))
+    bp = lambda a: a.ctypes.data_as(C.POINTER(C.c_uint8))
+
+    def cpu_rows(experts):
+        want = np.zeros((n, K), np.float32)
+        csel = np.zeros((n, TOPK), np.int32)
+        for t in range(n):
+            lib.sf37cpu_moe_ffn_token(fp(want[t]), csel[t].ctypes.data_as(C.POINTER(C.c_int32)),
+                                      fp(dense["router"]), fp(dense["router_bias"]), bp(experts["gate"]),
+                                      bp(experts["up"]), bp(experts["down"]), bp(dense["sh_gate"]),
+                                      bp(dense["sh_up"]), bp(dense["sh_down"]), E, TOPK, K, F,
+                                      layer.clamp_routed, layer.clamp_shared, fp(np.ascontiguousarray(x[t], np.float32)))
+        return want, csel
+
+    want, csel = cpu_rows(layer.host_experts(np.unique(gsel)))
+    same = bool(np.array_equal(np.sort(gsel, axis=1), np.sort(csel, axis=1)))
+    if not same:                       # the CPU chose other experts: run it with those present
+        want, csel = cpu_rows(layer.host_experts(np.unique(np.concatenate([gsel.ravel(), csel.ravel()]))))
+    diff = np.abs(got.astype(np.float64) - want)
+    scale = np.maximum(np.abs(want.astype(np.float64)), 1.0)
+    err = diff / scale
+    ok = bool(np.all((diff <= 5e-2) | (diff <= 1e-1 * scale)))
+    return {"reference": f"CPU MoE layer from the reference sources ({kind}), same weights and x, router from x",
+            "tokens_compared": int(n), "indices_equal": same, "max_abs_rel": float(f"{err.max():.4e}"),
+            "max_abs": float(f"{diff.max():.4e}"), "within_reference_tolerance": ok,
+            "tolerance": "an element fails when |diff| > 5e-2 and |diff| > 1e-1 * max(1, |cpu|) (the reference's "
+                         "own Q8_K-GPU-vs-CPU MoE check, tests/test_sf37_cuda_ops.cu:20-30,814); the GPU path "
+                         "quantises activations to Q8_K as the reference CUDA path does, the CPU path keeps fp32"}
+
+
+def cpu_prefill_baseline(layer, x, budget_s):
+    """The reference CPU MoE path over the leading tokens of a prefill chunk
+    (the CPU engine runs a chunk token by token, sf37.c:7786-7797), for about
+    budget_s seconds; tokens/s/layer of that sample."""
+    import oracle
+    lib = oracle.cpu_baseline_lib("reference")
+    kind = "reference"
+    if lib is None:
+        lib, kind = oracle.cpu_baseline_lib("port"), "port"
+    if lib is None:
+        return None
+    K, F, E, TOPK = layer.in_dim, layer.mid_dim, layer.n_expert, layer.topk
+    dense = layer.host_dense()
+    experts = layer.host_experts(np.arange(E))
+    out = np.zeros(K, np.float32)
+    csel = np.zeros(TOPK, np.int32)
+    fp = lambda a: a.ctypes.data_as(C.POINTER(C.c_float))
+    bp = lambda a: a.ctypes.data_as(C.POINTER(C.c_uint8))
+    n, t0 = 0, time.perf_counter()
+    while n < x.shape[0]:
+        lib.sf37cpu_moe_ffn_token(fp(out), csel.ctypes.data_as(C.POINTER(C.c_int32)), fp(dense["router"]),
+                                  fp(dense["router_bias"]), bp(experts["gate"]), bp(experts["up"]),
+                                  bp(experts["down"]), bp(dense["sh_gate"]), bp(dense["sh_up"]),
+                                  bp(dense["sh_down"]), E, TOPK, K, F, 0.0, 0.0, fp(np.ascontiguousarray(x[n])))
+        n += 1
+        if time.perf_counter() - t0 >= budget_s:
+            break
+    dt = time.perf_counter() - t0
+    return {"value": round(n / dt, 2), "unit": "tokens/s/layer", "cores": 1, "kind": kind,
+            "sample": f"the first {n} tokens of the config 3 chunk (its x rows, routing from x) through the "
+                      f"reference CPU MoE path, one token at a time as the CPU engine runs a chunk, {dt:.1f} s"}
 
 
 def prefill_bench(args, H, layer, config):

@@ -313,11 +313,14 @@ constexpr uint32_t GROUP_MAX_E = 1024;   // experts the token-mask grouping hand
 // expert twice, pair i = t * topk + s of expert e goes to start(e) + the
 // number of earlier tokens holding e (per-expert token masks, one scan over
 // the experts); otherwise every pair counts the pairs ordered before it.
-// All threads of the workgroup take part; ends with a barrier.
-__device__ void group_pairs(const dec_params &p, const uint32_t *s_sel, uint32_t *gi, uint32_t *so, bool publish) {
-    __shared__ uint32_t msk[GROUP_MAX_E], st[GROUP_MAX_E];
-    __shared__ uint32_t s_e[DEC_MAX_TOK * 16], s_se[DEC_MAX_TOK * 16];
-    __shared__ uint32_t s_tot[2], s_wcnt[16];
+// scr: GROUP_SCR words of LDS.  All threads of the workgroup take part;
+// ends with a barrier.
+constexpr uint32_t GROUP_SCR = 2u * GROUP_MAX_E + 2u * DEC_MAX_TOK * 16u + 2u + 16u;   // words of scratch
+__device__ void group_pairs(const dec_params &p, const uint32_t *s_sel, uint32_t *gi, uint32_t *so, bool publish,
+                            uint32_t *scr) {
+    uint32_t *msk = scr, *st = msk + GROUP_MAX_E;
+    uint32_t *s_e = st + GROUP_MAX_E, *s_se = s_e + DEC_MAX_TOK * 16u;
+    uint32_t *s_tot = s_se + DEC_MAX_TOK * 16u, *s_wcnt = s_tot + 2u;
     const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u, nthr = blockDim.x;
     const uint32_t P = p.T * p.topk;
     if (p.flags & SF37_DEC_SLOTS) {
@@ -464,6 +467,7 @@ __device__ void group_pairs(const dec_params &p, const uint32_t *s_sel, uint32_t
 __device__ void select_and_group(const dec_params &p, uint32_t *gi, uint32_t *so, bool publish) {
     __shared__ int32_t s_sel[DEC_MAX_TOK * 16];
     __shared__ float s_wts[DEC_MAX_TOK * 16];
+    __shared__ uint32_t scr[GROUP_SCR];
     const uint32_t wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
     const uint32_t P = p.T * p.topk;
     if (p.flags & SF37_DEC_SELECT) {
@@ -476,7 +480,7 @@ __device__ void select_and_group(const dec_params &p, uint32_t *gi, uint32_t *so
         p.sel[threadIdx.x] = s_sel[threadIdx.x];
         p.wts[threadIdx.x] = s_wts[threadIdx.x];
     }
-    group_pairs(p, (const uint32_t *)s_sel, gi, so, publish);
+    group_pairs(p, (const uint32_t *)s_sel, gi, so, publish, scr);
 }
 
 // Shared gate/up workgroup wg (the leading workgroups of the up launch):
@@ -959,25 +963,36 @@ __device__ void up_items_pairs(const dec_params &p, const uint32_t *gi, const ui
 // are always loaded while the current one is computed.
 // Select launch (batches of more tokens): workgroup 0 forms the top-k and
 // the grouping; workgroups 1.. the shared gate/up rows.
-// Select launch (512 threads): workgroups [0, n_tk) - wave w of workgroup
-// b takes token 8 b + w (token_topk into LDS, then sel and wts); up to 8
-// tokens the one workgroup groups the pairs from LDS, above that the last
-// top-k workgroup to arrive (a counter; each releases its writes before
-// arriving) groups them from sel.  Both publish ginfo and sorted.
-// Workgroups [n_tk, ...) compute the shared gate/up rows.
+// LDS of a top-k workgroup of the select launch: selections, weights,
+// group table, sorted pairs, a flag and the grouping scratch.
+__host__ __device__ constexpr size_t lds_select_topk() {
+    return (2u * DEC_MAX_TOK * 16u + 3u + 2u * DEC_MAX_TOK * 16u + DEC_MAX_TOK * 16u + 1u + GROUP_SCR) * 4u;
+}
+
+// Select launch (512 threads up to 8 tokens, 256 above): workgroups
+// [0, n_tk) - wave w of workgroup b takes token nw b + w (token_topk into
+// LDS, then sel and wts); with one top-k workgroup it groups the pairs from
+// LDS, otherwise the last top-k workgroup to arrive (a counter; each
+// releases its writes before arriving) groups them from sel.  Both publish
+// ginfo and sorted.  Workgroups [n_tk, ...) compute the shared gate/up rows
+// (4 per workgroup of 512 threads, 2 of 256).
 __global__ void __launch_bounds__(512) dec_select_kernel(dec_params p, uint32_t n_tk) {
     extern __shared__ __align__(16) unsigned char smem[];
     if (blockIdx.x >= n_tk) {
-        shared_gate_up(p, blockIdx.x - n_tk, smem, SH_RS_SEL);
+        shared_gate_up(p, blockIdx.x - n_tk, smem, blockDim.x == 512u ? SH_RS_SEL : SH_RS_UP);
         return;
     }
-    __shared__ int32_t s_sel[DEC_MAX_TOK * 16];
-    __shared__ float s_wts[DEC_MAX_TOK * 16];
-    __shared__ uint32_t s_gi[3u + 2u * DEC_MAX_TOK * 16u], s_so[DEC_MAX_TOK * 16u];
-    __shared__ uint32_t s_last;
-    const uint32_t wave = threadIdx.x >> 6, P = p.T * p.topk;
-    const uint32_t t = blockIdx.x * 8u + wave, t0 = blockIdx.x * 8u;
-    const uint32_t p0 = t0 * p.topk, p1 = (p.T < t0 + 8u ? p.T : t0 + 8u) * p.topk;
+    // the top-k workgroups' tables live in the dynamic LDS the shared
+    // workgroups use (no static LDS: it would count against every workgroup)
+    int32_t *s_sel = (int32_t *)smem;
+    float *s_wts = (float *)(s_sel + DEC_MAX_TOK * 16u);
+    uint32_t *s_gi = (uint32_t *)(s_wts + DEC_MAX_TOK * 16u);
+    uint32_t *s_so = s_gi + 3u + 2u * DEC_MAX_TOK * 16u;
+    uint32_t *s_flag = s_so + DEC_MAX_TOK * 16u;
+    uint32_t *scr = s_flag + 1u;
+    const uint32_t wave = threadIdx.x >> 6, nw = blockDim.x >> 6, P = p.T * p.topk;
+    const uint32_t t = blockIdx.x * nw + wave, t0 = blockIdx.x * nw;
+    const uint32_t p0 = t0 * p.topk, p1 = (p.T < t0 + nw ? p.T : t0 + nw) * p.topk;
     if (p.flags & SF37_DEC_SELECT) {
         if (t < p.T) token_topk(p, t, s_sel + t * p.topk, s_wts + t * p.topk);
         __syncthreads();
@@ -992,15 +1007,15 @@ __global__ void __launch_bounds__(512) dec_select_kernel(dec_params p, uint32_t 
         __syncthreads();
         if (threadIdx.x == 0) {
             __threadfence();
-            s_last = atomicAdd(sel_arrivals(p), 1u) == n_tk - 1u;
+            *s_flag = atomicAdd(sel_arrivals(p), 1u) == n_tk - 1u;
         }
         __syncthreads();
-        if (!s_last) return;
+        if (!*s_flag) return;
         __threadfence();
         if (threadIdx.x < P && (threadIdx.x < p0 || threadIdx.x >= p1)) s_sel[threadIdx.x] = p.sel[threadIdx.x];
     }
     __syncthreads();
-    group_pairs(p, (const uint32_t *)s_sel, s_gi, s_so, true);
+    group_pairs(p, (const uint32_t *)s_sel, s_gi, s_so, true, scr);
 }
 
 // The routed part of the up launch on the block-pair DMA path (rows of 4, 8
@@ -1449,7 +1464,7 @@ namespace {
 
 struct dec_shape {
     bool up_wide;
-    uint32_t n_rt, n_xq, n_tk, n_shup, sh_rs, n_up, n_mid, n_dn, n_cb;
+    uint32_t n_rt, n_xq, n_tk, sel_threads, n_shup, sh_rs, n_up, n_mid, n_dn, n_cb;
     size_t lds_up, lds_shup, lds_dn;
     const void *dn_kernel;
 };
@@ -1508,14 +1523,18 @@ dec_shape dec_plan(const dec_params &p) {
     const uint32_t cus = device_cus();
     d.n_rt = (p.flags & (SF37_DEC_ROUTER | SF37_DEC_SELECT)) ? route_wgs(p.T, p.E) : 0u;
     d.n_xq = (p.T * nb + 3u) / 4u;
-    d.n_tk = (p.T + 7u) / 8u;
+    d.sel_threads = p.T <= 8u ? 512u : 256u;
+    d.n_tk = (p.T + d.sel_threads / 64u - 1u) / (d.sel_threads / 64u);
     // routed up: 8-wave block-pair DMA workgroups when the batch has a
     // select launch and they fit, else the row-pair loop
     const uint32_t P = p.T * p.topk;
     const bool upsel = (p.flags & SF37_DEC_UPSEL) != 0;
     d.up_wide = up_pairs(p.K) && !upsel && lds_up_dma(p.K, p.T, p.G, P, 8u) <= device_max_lds();
     d.lds_up = d.up_wide ? lds_up_dma(p.K, p.T, p.G, P, 8u) : lds_up_meta(p.K, p.T, p.G, P);
-    d.sh_rs = (p.flags & SF37_DEC_UPSEL) ? SH_RS_UP : SH_RS_SEL;
+    // the select launch takes 4 shared rows per 512-thread workgroup up to 8
+    // tokens; above that 2 per 256-thread workgroup (the terms of 16 tokens
+    // x 4 rows would hold one workgroup per CU)
+    d.sh_rs = (p.flags & SF37_DEC_UPSEL) || p.T > 8u ? SH_RS_UP : SH_RS_SEL;
     d.lds_shup = lds_up_shared(p.K, p.T, d.sh_rs);
     d.n_shup = sh ? p.F / d.sh_rs : 0u;                // shared gate/up workgroups (select or up launch)
     // persistent kernels: exactly as many workgroups as can be resident
@@ -1603,10 +1622,11 @@ extern "C" int sf37k_decode_route(const sf37_dec_params *pp, sf37_stream_t s) {
 extern "C" int sf37k_decode_select(const sf37_dec_params *pp, sf37_stream_t s) {
     const dec_shape d = dec_plan(*pp);
     static size_t opted = 65536;
-    const int err = set_lds((const void *)dec_select_kernel, d.n_shup ? d.lds_shup : 0u, &opted);
+    const size_t lds = d.n_shup && d.lds_shup > lds_select_topk() ? d.lds_shup : lds_select_topk();
+    const int err = set_lds((const void *)dec_select_kernel, lds, &opted);
     if (err) return err;
-    hipLaunchKernelGGL(dec_select_kernel, dim3(d.n_tk + d.n_shup), dim3(512), d.n_shup ? d.lds_shup : 0u,
-                       (hipStream_t)s, *pp, d.n_tk);
+    hipLaunchKernelGGL(dec_select_kernel, dim3(d.n_tk + d.n_shup), dim3(d.sel_threads), lds, (hipStream_t)s, *pp,
+                       d.n_tk);
     return (int)hipGetLastError();
 }
 
