@@ -854,8 +854,8 @@ __device__ __forceinline__ void dma16(uint32_t lds, uint32_t voff, const uint8_t
 // is computed while it loads.  xs holds each token's activation blocks with
 // the even blocks first, then the odd ones (bank-conflict-free: the NBP lanes
 // of a row read NBP distinct blocks 304 bytes apart).  Wave w takes items w,
-// w + nw, ... (no atomics: waiting for an atomic's result would also wait
-// for every load issued before it).
+// w + nw, ... up to 70% of them, then items from counters (the up queues),
+// which evens out the waves' finishing times.
 constexpr uint32_t ITEM_NONE = 0xffffffffu;
 template <int NBP>
 __device__ void up_items_pairs(const dec_params &p, const uint32_t *gi, const uint32_t *so, const uint32_t *xo,
@@ -867,11 +867,41 @@ __device__ void up_items_pairs(const dec_params &p, const uint32_t *gi, const ui
     const uint32_t nbK = 2u * (uint32_t)NBP;
     const uint32_t ipm = p.F / RPI, ipg = 2u * ipm, n_items = gi[0] * ipg;
     const uint64_t row_bytes = (uint64_t)nbK * SF37_Q3_BYTES, exp_bytes = (uint64_t)p.F * row_bytes;
-    uint32_t pos = gw;
-    auto next_item = [&]() -> uint32_t {
-        const uint32_t it = pos;
-        pos += nw;
-        return it < n_items ? it : ITEM_NONE;
+    // items [0, n_stat) round-robin (wave gw: gw, gw + nw, ...); the rest
+    // from a counter, each request issued with the refill before it is
+    // needed, so its answer is in by the wait for that tile
+    const uint32_t n_stat = nw * ((n_items * 9u / 10u) / nw);
+    // the dynamic items are split over UP_QUEUES counters, each owning a
+    // contiguous share (one counter for every wave of the chip serialises
+    // the requests); a queue's waves come from every XCD (workgroups are
+    // dealt to the XCDs round-robin), so a slower XCD hands work to faster
+    // ones
+    const uint32_t qi = ((gw >> 6) * 8u + (gw & 7u)) % UP_QUEUES, n_dyn = n_items - n_stat;
+    const uint32_t q0 = n_stat + (uint32_t)((uint64_t)n_dyn * qi / UP_QUEUES);
+    const uint32_t q1 = n_stat + (uint32_t)((uint64_t)n_dyn * (qi + 1u) / UP_QUEUES);
+    uint32_t *ctr = up_queue(p, qi);
+    uint32_t pos = gw, pend = 0;
+    // lane 0's atomic add, returning the old value; issued as plain code it
+    // would be rewritten into a wave-wide atomic whose answer is awaited on
+    // the spot (and with it every load issued before).  The answer is read
+    // only after a wait that names pend (wait_pend), which orders the read.
+    auto request = [&]() {
+        uint32_t v = 0;
+        if (lane == 0) {
+            const uint32_t one = 1u;
+            asm volatile("global_atomic_add %0, %1, %2, off sc0" : "=v"(v) : "v"(ctr), "v"(one) : "memory");
+        }
+        pend = v;
+    };
+    auto wait_pend = [&]() { asm volatile("s_waitcnt vmcnt(0)" : "+v"(pend) : : "memory"); };
+    auto take = [&]() -> uint32_t {
+        if (pos < n_stat) {
+            const uint32_t v = pos;
+            pos += nw;
+            return v;
+        }
+        const uint32_t v = q0 + (uint32_t)__builtin_amdgcn_readfirstlane((int)pend);
+        return v < q1 ? v : ITEM_NONE;
     };
     // an item's RPI rows are one contiguous 14080-byte span of the matrix
     auto tile_src = [&](uint32_t it) -> const uint8_t * {
@@ -933,18 +963,28 @@ __device__ void up_items_pairs(const dec_params &p, const uint32_t *gi, const ui
     // one item: wait for its tile (and the stores before it), read the
     // lane's pair, refill the tile with the next item, compute
     const uint32_t *pl = (const uint32_t *)tile + lane * 55u;
-    uint32_t it = next_item();
-    if (it != ITEM_NONE) fill(it);
+    if (pos >= n_stat) {
+        request();
+        wait_pend();
+    }
+    uint32_t it = take();
+    if (it != ITEM_NONE) {
+        fill(it);
+        if (pos >= n_stat) request();
+    }
     while (it != ITEM_NONE) {
-        const uint32_t nx = next_item();
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        wait_pend();                                // the tile, the pending request
+        const uint32_t nx = take();
         uint32_t w[PAIR_DW];
 #pragma unroll
         for (uint32_t i = 0; i < 55u; i++) w[i] = pl[i];
         w[55] = 0u;
         opaque<PAIR_DW>(w);                         // the reads are done before the tile is refilled
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        if (nx != ITEM_NONE) fill(nx);
+        if (nx != ITEM_NONE) {
+            fill(nx);
+            if (pos >= n_stat) request();
+        }
         compute(w, it);
         it = nx;
     }
