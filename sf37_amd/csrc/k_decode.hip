@@ -1080,8 +1080,9 @@ __device__ void up_routed_dma(const dec_params &p, unsigned char *smem, act_lds_
     }
 }
 
-// Batches with a select launch on the DMA path: 512-thread workgroups (8
-// waves, one LDS tile each, the activations staged once per workgroup).
+// Batches with a select launch on the DMA path: workgroups of 8 waves (4-7
+// where the activations of many tokens leave LDS for fewer tiles), one LDS
+// tile each, the activations staged once per workgroup.
 __global__ void __launch_bounds__(512) dec_up_dma_kernel(dec_params p) {
     extern __shared__ __align__(16) unsigned char smem[];
     const uint32_t nbK = p.K / SF37_QK, P = p.T * p.topk;
@@ -1504,7 +1505,7 @@ namespace {
 
 struct dec_shape {
     bool up_wide;
-    uint32_t n_rt, n_xq, n_tk, sel_threads, n_shup, sh_rs, n_up, n_mid, n_dn, n_cb;
+    uint32_t n_rt, n_xq, n_tk, sel_threads, n_shup, sh_rs, up_waves, n_up, n_mid, n_dn, n_cb;
     size_t lds_up, lds_shup, lds_dn;
     const void *dn_kernel;
 };
@@ -1565,12 +1566,16 @@ dec_shape dec_plan(const dec_params &p) {
     d.n_xq = (p.T * nb + 3u) / 4u;
     d.sel_threads = p.T <= 8u ? 512u : 256u;
     d.n_tk = (p.T + d.sel_threads / 64u - 1u) / (d.sel_threads / 64u);
-    // routed up: 8-wave block-pair DMA workgroups when the batch has a
-    // select launch and they fit, else the row-pair loop
+    // routed up: block-pair DMA workgroups when the batch has a select
+    // launch and at least 4 waves' tiles fit beside the activations (up to
+    // 8 waves), else the row-pair loop
     const uint32_t P = p.T * p.topk;
     const bool upsel = (p.flags & SF37_DEC_UPSEL) != 0;
-    d.up_wide = up_pairs(p.K) && !upsel && lds_up_dma(p.K, p.T, p.G, P, 8u) <= device_max_lds();
-    d.lds_up = d.up_wide ? lds_up_dma(p.K, p.T, p.G, P, 8u) : lds_up_meta(p.K, p.T, p.G, P);
+    const size_t tb = tile_base(p.K, p.T, p.G, P), ml = device_max_lds();
+    const uint32_t fit = tb < ml ? (uint32_t)((ml - tb) / 14336u) : 0u;
+    d.up_waves = fit < 8u ? fit : 8u;
+    d.up_wide = up_pairs(p.K) && !upsel && d.up_waves >= 4u;
+    d.lds_up = d.up_wide ? lds_up_dma(p.K, p.T, p.G, P, d.up_waves) : lds_up_meta(p.K, p.T, p.G, P);
     // the select launch takes 4 shared rows per 512-thread workgroup up to 8
     // tokens; above that 2 per 256-thread workgroup (the terms of 16 tokens
     // x 4 rows would hold one workgroup per CU)
@@ -1579,7 +1584,7 @@ dec_shape dec_plan(const dec_params &p) {
     d.n_shup = sh ? p.F / d.sh_rs : 0u;                // shared gate/up workgroups (select or up launch)
     // persistent kernels: exactly as many workgroups as can be resident
     const size_t up_lds = d.lds_up > d.lds_shup || !d.n_shup || !(p.flags & SF37_DEC_UPSEL) ? d.lds_up : d.lds_shup;
-    const uint32_t up_res = d.up_wide ? resident_wgs((const void *)dec_up_dma_kernel, 512, d.lds_up)
+    const uint32_t up_res = d.up_wide ? resident_wgs((const void *)dec_up_dma_kernel, 64 * (int)d.up_waves, d.lds_up)
                                       : resident_wgs((const void *)dec_up_kernel, 256, up_lds);
     d.n_up = (p.up_wgs && p.up_wgs < up_res ? p.up_wgs : up_res) * cus;
     d.n_mid = (p.T * p.topk * (p.F / SF37_QK) + (sh ? (p.T * (p.F / 32u) + 1u) / 2u : 0u) + 3u) / 4u;
@@ -1676,7 +1681,7 @@ extern "C" int sf37k_decode_up(const sf37_dec_params *pp, sf37_stream_t s) {
         static size_t opted_w = 65536;
         const int err = set_lds((const void *)dec_up_dma_kernel, d.lds_up, &opted_w);
         if (err) return err;
-        hipLaunchKernelGGL(dec_up_dma_kernel, dim3(d.n_up), dim3(512), d.lds_up, (hipStream_t)s, *pp);
+        hipLaunchKernelGGL(dec_up_dma_kernel, dim3(d.n_up), dim3(64u * d.up_waves), d.lds_up, (hipStream_t)s, *pp);
         return (int)hipGetLastError();
     }
     const bool upsel = (pp->flags & SF37_DEC_UPSEL) != 0u;
