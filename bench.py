@@ -268,14 +268,16 @@ def decode_bench(args, H, n_tok, layers=None, summary=False):
                           + 2 * n_tok * F * 4,
             # routed gate/up weights of the distinct experts + x blocks in, gate/up rows out
             "dec_up": distinct * GATE_UP_EXPERT_BYTES + n_tok * nb * 288 + 2 * P * F * 4,
-            # gate/up rows in, mid and its activation blocks out
-            "dec_mid": 2 * P * F * 4 + P * F * 4 + P * nbf * 288,
-            # shared gate/up in, Q8_0 shared mid out; routed down weights + mid blocks in,
-            # per-pair rows out
-            "dec_down": 2 * n_tok * F * 4 + n_tok * F + n_tok * (F // 32) * 4
-                        + distinct * DOWN_EXPERT_BYTES + P * nbf * 288 + P * K * 4,
-            # shared down weights + Q8_0 shared mid in, per-pair rows in, out
-            "dec_combine": lay.sh_down.nbytes + n_tok * F + n_tok * (F // 32) * 4 + P * K * 4 + n_tok * K * 4,
+            # gate/up rows in, mid and its activation blocks out; shared gate/up rows in,
+            # Q8_0 shared mid out
+            "dec_mid": 2 * P * F * 4 + P * F * 4 + P * nbf * 288 + 2 * n_tok * F * 4 + n_tok * F
+                       + n_tok * (F // 32) * 4,
+            # routed down weights + mid blocks in, per-pair rows out; shared down weights +
+            # Q8_0 shared mid in, shared rows out
+            "dec_down": distinct * DOWN_EXPERT_BYTES + P * nbf * 288 + P * K * 4
+                        + lay.sh_down.nbytes + n_tok * F + n_tok * (F // 32) * 4 + n_tok * K * 4,
+            # per-pair rows and shared rows in, out
+            "dec_combine": P * K * 4 + n_tok * K * 4 + n_tok * K * 4,
         })
     hip.synchronize()
 
