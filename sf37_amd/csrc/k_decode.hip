@@ -1532,6 +1532,24 @@ uint32_t device_max_lds() {
     return (uint32_t)lds;
 }
 
+// Opts kernel fn into at least `bytes` of dynamic LDS (above 64 KiB).  The
+// opt-in only ever rises: a batch needing less LDS never lowers what a
+// larger batch of the same kernel was given.
+int opt_in_lds(const void *fn, size_t bytes) {
+    struct entry { const void *fn; size_t bytes; };
+    static entry tab[16];
+    static int used = 0;
+    if (bytes <= 65536u) return 0;
+    int i = 0;
+    while (i < used && tab[i].fn != fn) i++;
+    if (i < used && tab[i].bytes >= bytes) return 0;
+    const hipError_t err = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+    if (err != hipSuccess) return (int)err;
+    if (i < used) tab[i].bytes = bytes;
+    else if (used < 16) tab[used++] = {fn, bytes};
+    return 0;
+}
+
 // Workgroups of this kernel one CU holds at once (from the occupancy
 // calculator, at least 1), cached per (kernel, block size, LDS bytes).
 // Dynamic LDS above 64 KiB is opted into first.
@@ -1541,7 +1559,7 @@ uint32_t resident_wgs(const void *fn, int threads, size_t lds) {
     static int used = 0;
     for (int i = 0; i < used; i++)
         if (cache[i].fn == fn && cache[i].threads == threads && cache[i].lds == lds) return cache[i].n;
-    if (lds > 65536u) (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    (void)opt_in_lds(fn, lds);
     int n = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, threads, lds) != hipSuccess || n < 1) n = 1;
     (void)hipGetLastError();
@@ -1648,16 +1666,6 @@ extern "C" int sf37k_decode_supported(uint32_t T, uint32_t topk, uint32_t E, uin
     return 1;
 }
 
-namespace {
-int set_lds(const void *fn, size_t bytes, size_t *opted) {
-    if (bytes <= *opted) return 0;
-    const hipError_t err = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
-    if (err != hipSuccess) return (int)err;
-    *opted = bytes;
-    return 0;
-}
-}  // namespace
-
 extern "C" int sf37k_decode_route(const sf37_dec_params *pp, sf37_stream_t s) {
     const dec_shape d = dec_plan(*pp);
     hipLaunchKernelGGL(dec_route_kernel, dim3(d.n_rt + d.n_xq), dim3(256), 0, (hipStream_t)s, *pp, d.n_rt);
@@ -1666,9 +1674,8 @@ extern "C" int sf37k_decode_route(const sf37_dec_params *pp, sf37_stream_t s) {
 
 extern "C" int sf37k_decode_select(const sf37_dec_params *pp, sf37_stream_t s) {
     const dec_shape d = dec_plan(*pp);
-    static size_t opted = 65536;
     const size_t lds = d.n_shup && d.lds_shup > lds_select_topk() ? d.lds_shup : lds_select_topk();
-    const int err = set_lds((const void *)dec_select_kernel, lds, &opted);
+    const int err = opt_in_lds((const void *)dec_select_kernel, lds);
     if (err) return err;
     hipLaunchKernelGGL(dec_select_kernel, dim3(d.n_tk + d.n_shup), dim3(d.sel_threads), lds, (hipStream_t)s, *pp,
                        d.n_tk);
@@ -1678,8 +1685,7 @@ extern "C" int sf37k_decode_select(const sf37_dec_params *pp, sf37_stream_t s) {
 extern "C" int sf37k_decode_up(const sf37_dec_params *pp, sf37_stream_t s) {
     const dec_shape d = dec_plan(*pp);
     if (d.up_wide) {
-        static size_t opted_w = 65536;
-        const int err = set_lds((const void *)dec_up_dma_kernel, d.lds_up, &opted_w);
+        const int err = opt_in_lds((const void *)dec_up_dma_kernel, d.lds_up);
         if (err) return err;
         hipLaunchKernelGGL(dec_up_dma_kernel, dim3(d.n_up), dim3(64u * d.up_waves), d.lds_up, (hipStream_t)s, *pp);
         return (int)hipGetLastError();
@@ -1687,8 +1693,7 @@ extern "C" int sf37k_decode_up(const sf37_dec_params *pp, sf37_stream_t s) {
     const bool upsel = (pp->flags & SF37_DEC_UPSEL) != 0u;
     const uint32_t n_sh = upsel ? d.n_shup : 0u;
     const size_t lds = d.lds_up > d.lds_shup || !n_sh ? d.lds_up : d.lds_shup;
-    static size_t opted = 65536;
-    const int err = set_lds((const void *)dec_up_kernel, lds, &opted);
+    const int err = opt_in_lds((const void *)dec_up_kernel, lds);
     if (err) return err;
     sf37_dec_params p = *pp;
     hipLaunchKernelGGL(dec_up_kernel, dim3(n_sh + d.n_up), dim3(256), lds, (hipStream_t)s, p, n_sh);
@@ -1704,6 +1709,8 @@ extern "C" int sf37k_decode_mid(const sf37_dec_params *pp, sf37_stream_t s) {
 extern "C" int sf37k_decode_down(const sf37_dec_params *pp, sf37_stream_t s) {
     const dec_shape d = dec_plan(*pp);
     void *args[] = {(void *)pp};
+    const int err = opt_in_lds(d.dn_kernel, d.lds_dn);
+    if (err) return err;
     const hipError_t e = hipLaunchKernel(d.dn_kernel, dim3(d.n_dn), dim3(256), args, d.lds_dn, (hipStream_t)s);
     return (int)(e != hipSuccess ? e : hipGetLastError());
 }

@@ -118,6 +118,26 @@ def test_fused_layer_equals_staged(H, layer, n_tok, routing):
     assert_bitexact(a[0], b[0], f"out ({n_tok} tokens, {routing})")
 
 
+def test_fused_layer_after_smaller_batches(H, layer):
+    """Batch sizes going down and up again in one process: each kernel's
+    dynamic-LDS opt-in must stay at the largest size asked for (a 16-token
+    launch after an 8-token one needs more LDS in the up and select launches
+    than the 8-token launch set up)."""
+    rng = np.random.default_rng(77)
+    outs = {}
+    for n_tok in (16, 8, 2, 16, 12, 16):
+        x = rng.standard_normal((n_tok, K)).astype(np.float32) if n_tok not in outs else outs[n_tok][0]
+        lg = rng.standard_normal((n_tok, E)).astype(np.float32) if n_tok not in outs else outs[n_tok][1]
+        say(f"batch sequence: {n_tok} tokens")
+        a = run_layer(H, layer, x, lg, True)
+        if n_tok in outs:
+            assert_bitexact(a[0], outs[n_tok][2], f"out ({n_tok} tokens, repeated)")
+        else:
+            b = run_layer(H, layer, x, lg, False)
+            assert_bitexact(a[0], b[0], f"out ({n_tok} tokens)")
+            outs[n_tok] = (x, lg, a[0])
+
+
 def test_fused_layer_router_on_device_and_clamps(H, layer):
     """Router logits computed in the fused route kernel (no injected logits),
     with the layer-43 clamps (routed 7, shared 16)."""
