@@ -868,8 +868,8 @@ __device__ void up_items_pairs(const dec_params &p, const uint32_t *gi, const ui
     const uint32_t ipm = p.F / RPI, ipg = 2u * ipm, n_items = gi[0] * ipg;
     const uint64_t row_bytes = (uint64_t)nbK * SF37_Q3_BYTES, exp_bytes = (uint64_t)p.F * row_bytes;
     // items [0, n_stat) round-robin (wave gw: gw, gw + nw, ...); the rest
-    // from a counter, each request issued with the refill before it is
-    // needed, so its answer is in by the wait for that tile
+    // from counters, each asked for after a compute while the next tile
+    // loads
     const uint32_t n_stat = nw * ((n_items * 9u / 10u) / nw);
     // the dynamic items are split over UP_QUEUES counters, each owning a
     // contiguous share (one counter for every wave of the chip serialises
@@ -880,28 +880,29 @@ __device__ void up_items_pairs(const dec_params &p, const uint32_t *gi, const ui
     const uint32_t q0 = n_stat + (uint32_t)((uint64_t)n_dyn * qi / UP_QUEUES);
     const uint32_t q1 = n_stat + (uint32_t)((uint64_t)n_dyn * (qi + 1u) / UP_QUEUES);
     uint32_t *ctr = up_queue(p, qi);
-    uint32_t pos = gw, pend = 0;
-    // lane 0's atomic add, returning the old value; issued as plain code it
-    // would be rewritten into a wave-wide atomic whose answer is awaited on
-    // the spot (and with it every load issued before).  The answer is read
-    // only after a wait that names pend (wait_pend), which orders the read.
-    auto request = [&]() {
-        uint32_t v = 0;
-        if (lane == 0) {
-            const uint32_t one = 1u;
-            asm volatile("global_atomic_add %0, %1, %2, off sc0" : "=v"(v) : "v"(ctr), "v"(one) : "memory");
-        }
-        pend = v;
-    };
-    auto wait_pend = [&]() { asm volatile("s_waitcnt vmcnt(0)" : "+v"(pend) : : "memory"); };
-    auto take = [&]() -> uint32_t {
+    uint32_t pos = gw;
+    bool more = n_dyn != 0u;
+    // the wave's next item (ITEM_NONE at the end).  A dynamic one is lane 0's
+    // atomic add on the counter, issued and awaited in one asm statement (the
+    // wait also covers the tile in flight, which the loop needs next anyway),
+    // so no register is read before the answer has arrived
+    auto next = [&]() -> uint32_t {
         if (pos < n_stat) {
             const uint32_t v = pos;
             pos += nw;
             return v;
         }
-        const uint32_t v = q0 + (uint32_t)__builtin_amdgcn_readfirstlane((int)pend);
-        return v < q1 ? v : ITEM_NONE;
+        if (!more) return ITEM_NONE;
+        uint32_t v = 0;
+        if (lane == 0) {
+            const uint32_t one = 1u;
+            asm volatile("global_atomic_add %0, %1, %2, off sc0\n\ts_waitcnt vmcnt(0)"
+                         : "=&v"(v) : "v"(ctr), "v"(one) : "memory");
+        }
+        v = q0 + (uint32_t)__builtin_amdgcn_readfirstlane((int)v);
+        if (v < q1) return v;
+        more = false;
+        return ITEM_NONE;
     };
     // an item's RPI rows are one contiguous 14080-byte span of the matrix
     auto tile_src = [&](uint32_t it) -> const uint8_t * {
@@ -963,30 +964,22 @@ __device__ void up_items_pairs(const dec_params &p, const uint32_t *gi, const ui
     // one item: wait for its tile (and the stores before it), read the
     // lane's pair, refill the tile with the next item, compute
     const uint32_t *pl = (const uint32_t *)tile + lane * 55u;
-    if (pos >= n_stat) {
-        request();
-        wait_pend();
-    }
-    uint32_t it = take();
-    if (it != ITEM_NONE) {
-        fill(it);
-        if (pos >= n_stat) request();
-    }
+    uint32_t it = next();
+    if (it != ITEM_NONE) fill(it);
+    uint32_t nx = it != ITEM_NONE ? next() : ITEM_NONE;
     while (it != ITEM_NONE) {
-        wait_pend();                                // the tile, the pending request
-        const uint32_t nx = take();
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");     // the tile (and the stores before it)
         uint32_t w[PAIR_DW];
 #pragma unroll
         for (uint32_t i = 0; i < 55u; i++) w[i] = pl[i];
         w[55] = 0u;
         opaque<PAIR_DW>(w);                         // the reads are done before the tile is refilled
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        if (nx != ITEM_NONE) {
-            fill(nx);
-            if (pos >= n_stat) request();
-        }
+        if (nx != ITEM_NONE) fill(nx);
         compute(w, it);
+        const uint32_t nn = nx != ITEM_NONE ? next() : ITEM_NONE;   // a ticket waits for the tile too
         it = nx;
+        nx = nn;
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");       // no load into LDS outlives the wave
 }
