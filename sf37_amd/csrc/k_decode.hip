@@ -107,8 +107,11 @@ __host__ __device__ constexpr size_t tile_base(uint32_t K, uint32_t T, uint32_t 
 __host__ __device__ constexpr size_t lds_up_dma(uint32_t K, uint32_t T, uint32_t G, uint32_t P, uint32_t waves) {
     return tile_base(K, T, G, P) + (size_t)waves * 14336u;
 }
+// Row stride (floats) of the shared gate/up terms: K/32 terms plus 4, so the
+// sums' lanes, one row each, read 16 distinct bank quads.
+__host__ __device__ constexpr uint32_t sh_red_stride(uint32_t K) { return K / 32u + 4u; }
 __host__ __device__ constexpr size_t lds_up_shared(uint32_t K, uint32_t T, uint32_t rs) {
-    return 2u * (size_t)tile_buf(up_shared_tile(K, rs)) + (size_t)T * 2u * rs * (K / 32u) * 4u;
+    return 2u * (size_t)tile_buf(up_shared_tile(K, rs)) + (size_t)T * 2u * rs * sh_red_stride(K) * 4u;
 }
 
 // Q8_0 block (34 bytes) at LDS byte offset L of base: scale, eight i8x4 words.
@@ -494,7 +497,8 @@ __device__ void shared_gate_up(const dec_params &p, uint32_t wg, unsigned char *
     const uint32_t tbytes = up_shared_tile(p.K, rs), wbuf = tile_buf(tbytes);
     const uint64_t row_bytes = (uint64_t)nb8 * SF37_Q8_0_BYTES;
     uint8_t *wl = smem;                                             // gate tile | up tile
-    float *red = (float *)(smem + 2u * wbuf);                       // [T][2][RS][nb8]
+    float *red = (float *)(smem + 2u * wbuf);                       // [T][2][RS][rstr]
+    const uint32_t rstr = sh_red_stride(p.K);
     const uint32_t og = lds_copy(wl, p.sh_gate + (uint64_t)row0 * row_bytes, tbytes);
     const uint32_t ou = wbuf + lds_copy(wl + wbuf, p.sh_up + (uint64_t)row0 * row_bytes, tbytes);
     // thread = (row, block) for both matrices; x blocks of 8 tokens at a time
@@ -530,8 +534,8 @@ __device__ void shared_gate_up(const dec_params &p, uint32_t wg, unsigned char *
                         ig = sdot4(qg[k], xv[k], ig);
                         iu = sdot4(qu[k], xv[k], iu);
                     }
-                    red[((t * 2u + 0u) * rs + r) * nb8 + b] = (float)ig * wg * xs[j];
-                    red[((t * 2u + 1u) * rs + r) * nb8 + b] = (float)iu * wu * xs[j];
+                    red[((t * 2u + 0u) * rs + r) * rstr + b] = (float)ig * wg * xs[j];
+                    red[((t * 2u + 1u) * rs + r) * rstr + b] = (float)iu * wu * xs[j];
                 }
             }
         }
@@ -540,7 +544,7 @@ __device__ void shared_gate_up(const dec_params &p, uint32_t wg, unsigned char *
     for (uint32_t i = threadIdx.x; i < p.T * 2u * rs; i += blockDim.x) {
         const uint32_t t = i / (2u * rs), mr = i - t * 2u * rs;
         const uint32_t m = mr / rs, r = mr - m * rs;
-        const float *rv = red + (uint64_t)i * nb8;
+        const float *rv = red + (uint64_t)i * rstr;
         float acc = 0.0f;
         if ((nb8 & 15u) == 0) {
             // the same sequential sum; 16 terms read per step so the LDS
