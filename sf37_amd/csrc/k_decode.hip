@@ -873,8 +873,9 @@ __device__ void up_items_pairs(const dec_params &p, const uint32_t *gi, const ui
     const uint64_t row_bytes = (uint64_t)nbK * SF37_Q3_BYTES, exp_bytes = (uint64_t)p.F * row_bytes;
     // items [0, n_stat) round-robin (wave gw: gw, gw + nw, ...); the rest
     // from counters, each asked for after a compute while the next tile
-    // loads
-    const uint32_t n_stat = nw * ((n_items * 9u / 10u) / nw);
+    // loads.  90% static up to 8 tokens, 80% above, where fewer waves share
+    // a CU (measured best at 8 and 16 tokens).
+    const uint32_t n_stat = nw * ((n_items * (p.T <= 8u ? 9u : 8u) / 10u) / nw);
     // the dynamic items are split over UP_QUEUES counters, each owning a
     // contiguous share (one counter for every wave of the chip serialises
     // the requests); a queue's waves come from every XCD (workgroups are
