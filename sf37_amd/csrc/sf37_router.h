@@ -260,7 +260,7 @@ __device__ __forceinline__ uint64_t sf37_topk_candidate(float logit, float bias,
 __device__ __forceinline__ uint32_t sf37_wave_max_u32(uint32_t v) {
 #define SF37_DPP_MAX32(ctrl, rows)                                                                     \
     do {                                                                                               \
-        const uint32_t n_ = (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, ctrl, rows, 0xf, false); \
+        const uint32_t n_ = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, ctrl, rows, 0xf, true);  \
         v = n_ > v ? n_ : v;                                                                           \
     } while (0)
     SF37_DPP_MAX32(0x111, 0xf);
