@@ -36,7 +36,9 @@ namespace {
 
 constexpr uint32_t DEC_MAX_TOK = 16;
 constexpr uint32_t DEC_TPC = 4;      // pairs per pass in the routed kernels
-constexpr uint32_t SH_RS_UP = 2;     // shared gate/up rows per workgroup in the up launch (256 threads)
+constexpr uint32_t SH_RS_UP = 2;     // shared gate/up rows per 256-thread workgroup of the select launch
+constexpr uint32_t SH_RS_UPSEL = 4;  // ... in the up launch (one token: fewer shared workgroups, so
+                                     // more routed ones start beside them; 2 and 8 measured slower)
 constexpr uint32_t SH_RS_SEL = 4;    // ... in the select launch (512 threads)
 constexpr uint32_t DN_MAX_NB = 5;    // down blocks per row held in registers (F <= 1280)
 constexpr uint32_t DN_TPC = 2;       // pairs per pass in the routed down kernel
@@ -1102,7 +1104,7 @@ __global__ void __launch_bounds__(512) dec_up_dma_kernel(dec_params p) {
 __global__ void __launch_bounds__(256) dec_up_kernel(dec_params p, uint32_t n_sh) {
     extern __shared__ __align__(16) unsigned char smem[];
     if (blockIdx.x < n_sh) {
-        shared_gate_up(p, blockIdx.x, smem, SH_RS_UP);
+        shared_gate_up(p, blockIdx.x, smem, SH_RS_UPSEL);
         return;
     }
     const uint32_t wg = blockIdx.x - n_sh, n_wg = gridDim.x - n_sh;
@@ -1594,8 +1596,9 @@ dec_shape dec_plan(const dec_params &p) {
     d.lds_up = d.up_wide ? lds_up_dma(p.K, p.T, p.G, P, d.up_waves) : lds_up_meta(p.K, p.T, p.G, P);
     // the select launch takes 4 shared rows per 512-thread workgroup up to 8
     // tokens; above that 2 per 256-thread workgroup (the terms of 16 tokens
-    // x 4 rows would hold one workgroup per CU)
-    d.sh_rs = (p.flags & SF37_DEC_UPSEL) || p.T > 8u ? SH_RS_UP : SH_RS_SEL;
+    // x 4 rows would hold one workgroup per CU); the one-token up launch 4
+    // per 256-thread workgroup
+    d.sh_rs = (p.flags & SF37_DEC_UPSEL) ? SH_RS_UPSEL : p.T > 8u ? SH_RS_UP : SH_RS_SEL;
     d.lds_shup = lds_up_shared(p.K, p.T, d.sh_rs);
     d.n_shup = sh ? p.F / d.sh_rs : 0u;                // shared gate/up workgroups (select or up launch)
     // persistent kernels: exactly as many workgroups as can be resident
@@ -1659,7 +1662,8 @@ extern "C" int sf37k_decode_supported(uint32_t T, uint32_t topk, uint32_t E, uin
     if (shared && shd_bps(F / 32u, shd_slices(T)) > SHD_MAX_BPS) return 0;
     const uint32_t P = T * topk, G = P < E ? P : E;
     if (lds_up_meta(K, T, G, P) > device_max_lds()) return 0;
-    if (shared && (lds_up_shared(K, T, SH_RS_UP) > device_max_lds() || lds_up_shared(K, T, SH_RS_SEL) > device_max_lds()))
+    if (shared && (lds_up_shared(K, T, SH_RS_UP) > device_max_lds() || lds_up_shared(K, T, SH_RS_SEL) > device_max_lds() ||
+                   lds_up_shared(K, T, SH_RS_UPSEL) > device_max_lds()))
         return 0;
     return 1;
 }
