@@ -1402,8 +1402,34 @@ __global__ void __launch_bounds__(256) dec_down_kernel(dec_params p) {
     };
     uint32_t staged_g = 0xffffffffu, staged_c0 = 0xffffffffu;
     uint32_t g = lo / spg, sub = lo - g * spg;
+    // The shared expert's down rows, handed out one row group at a time from
+    // DN_QUEUES queues (wave w asks queue w % DN_QUEUES, which owns a
+    // contiguous share): after the routed range, so waves that finish it
+    // early take more - except at one token, where a wave has at most one
+    // routed sub-item and takes its shared rows while that sub-item's weights
+    // load.  The next request is issued before the current group is computed.
+    auto shared_phase = [&]() {
+        const uint32_t R = 64u / (p.T * shd_slices(p.T)), n_sp = (p.K + R - 1u) / R;
+        const uint32_t qi = gw % DN_QUEUES;
+        const uint32_t q0 = (uint32_t)((uint64_t)n_sp * qi / DN_QUEUES), q1 = (uint32_t)((uint64_t)n_sp * (qi + 1u) / DN_QUEUES);
+        uint32_t *queue = dn_queue(p, qi);
+        auto request = [&]() -> uint32_t {
+            uint32_t v = 0;
+            if (lane == 0) v = atomicAdd(queue, 1u);
+            return v;
+        };
+        uint32_t pend = request();
+        for (;;) {
+            const uint32_t idx = q0 + (uint32_t)__builtin_amdgcn_readfirstlane((int)pend);
+            if (idx >= q1) break;
+            pend = request();
+            shared_down_pass<SHNB>(p, shq, shs, idx * R);
+        }
+    };
+    const bool sh_first = p.T == 1u;
     uint32_t nxt[21];
     if (lo < hi) load_q2(nxt, blk_ptr(g, sub));
+    if (sh && sh_first) shared_phase();
     for (uint32_t sidx = lo; sidx < hi; sidx++) {
         uint32_t w[21];
 #pragma unroll
@@ -1454,27 +1480,7 @@ __global__ void __launch_bounds__(256) dec_down_kernel(dec_params p) {
         g = ng;
         sub = nsub;
     }
-    if (!sh) return;
-    // Then the shared expert's down rows, handed out one row group at a time
-    // from DN_QUEUES queues (wave w asks queue w % DN_QUEUES, which owns a
-    // contiguous share): waves that finish their routed range early take
-    // more.  The next request is issued before the current group is computed.
-    const uint32_t R = 64u / (p.T * shd_slices(p.T)), n_sp = (p.K + R - 1u) / R;
-    const uint32_t qi = gw % DN_QUEUES;
-    const uint32_t q0 = (uint32_t)((uint64_t)n_sp * qi / DN_QUEUES), q1 = (uint32_t)((uint64_t)n_sp * (qi + 1u) / DN_QUEUES);
-    uint32_t *queue = dn_queue(p, qi);
-    auto request = [&]() -> uint32_t {
-        uint32_t v = 0;
-        if (lane == 0) v = atomicAdd(queue, 1u);
-        return v;
-    };
-    uint32_t pend = request();
-    for (;;) {
-        const uint32_t idx = q0 + (uint32_t)__builtin_amdgcn_readfirstlane((int)pend);
-        if (idx >= q1) break;
-        pend = request();
-        shared_down_pass<SHNB>(p, shq, shs, idx * R);
-    }
+    if (sh && !sh_first) shared_phase();
 }
 
 // ---------------------------------------------------------------------------
