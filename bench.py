@@ -72,6 +72,8 @@ def parse():
     ap.add_argument("--stack-steps", type=int, default=20, help="timed decode tokens through the stack")
     ap.add_argument("--stack-prefill-steps", type=int, default=2, help="timed 2048-token chunks through the stack")
     ap.add_argument("--stack-only", action="store_true", help="only the config 4 stack")
+    ap.add_argument("--opt", action="append", default=[], metavar="NAME=VALUE",
+                    help="library option (sf37_hip_set_option) set before measuring; repeatable")
     return ap.parse_args()
 
 
@@ -139,6 +141,9 @@ def main():
         sys.exit(2)
     # the router GEMV/GEMM runs inside the layer although injected logits select
     hip.set_option("router_with_logits", 1)
+    for kv in args.opt:
+        name, _, val = kv.partition("=")
+        hip.set_option(name, int(val))        # raises on an unknown name
     if args.prefill_only:
         lay = moe.SynthLayer(seed=moe.layer_seed(args.seed, 0))
         print(json.dumps({"prefill": [prefill_bench(args, H, lay, c) for c in (3, 2)]}), flush=True)
