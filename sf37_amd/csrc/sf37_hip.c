@@ -1214,6 +1214,10 @@ static int decode_run_in(const routed_args *a, const dec_extra *ex, float *out, 
     p.clamp_routed = a->clamp;
     p.clamp_shared = ex->clamp_shared;
     p.flags = ex->flags | ((uint64_t)T <= (uint64_t)g_opt_upsel_max_tok ? SF37_DEC_UPSEL : 0u);
+    /* one token: each slot its own group, in slot order (the slot-order
+     * combine makes the grouping order immaterial; the expert-sorted
+     * grouping only costs its scan) */
+    if (T == 1u && TK <= E) p.flags |= SF37_DEC_SLOTS;
     p.x = a->x;
     p.router_w = ex->router_w;
     p.router_bias = ex->router_bias;
