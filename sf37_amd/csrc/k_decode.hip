@@ -662,9 +662,10 @@ __device__ __forceinline__ void opaque(uint32_t *w) {
 // computes their terms; the sequential sum then walks the slices in order with
 // row_shr:1 (each slice adds its terms to the previous slice's total).  The
 // shared mid codes and scales of every token are in LDS (xq: T x F codes,
-// xsc: T x F/32 scales).
-template <int NB>
-__device__ void shared_down_pass(const dec_params &p, const int8_t *xq, const float *xsc, uint32_t r0) {
+// xsc: T x F/32 scales).  store(t, row, v) takes each (row, token) total.
+template <int NB, typename STORE>
+__device__ void shared_down_pass(const dec_params &p, const int8_t *xq, const float *xsc, uint32_t r0,
+                                 STORE &&store) {
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t S = shd_slices(p.T), TS = p.T * S, R = 64u / TS;
     const uint32_t nb8 = p.F / 32u, bps = shd_bps(nb8, S), ns = (nb8 + bps - 1u) / bps;
@@ -754,7 +755,7 @@ __device__ void shared_down_pass(const dec_params &p, const int8_t *xq, const fl
             acc = a2;
         }
     }
-    if (lane_ok && j == ns - 1u && row < p.K) p.sh_out[(uint64_t)t * p.K + row] = acc;
+    if (lane_ok && j == ns - 1u && row < p.K) store(t, row, acc);
 }
 
 // ---------------------------------------------------------------------------
@@ -1423,7 +1424,8 @@ __global__ void __launch_bounds__(256) dec_down_kernel(dec_params p) {
             const uint32_t idx = q0 + (uint32_t)__builtin_amdgcn_readfirstlane((int)pend);
             if (idx >= q1) break;
             pend = request();
-            shared_down_pass<SHNB>(p, shq, shs, idx * R);
+            shared_down_pass<SHNB>(p, shq, shs, idx * R,
+                                   [&](uint32_t t, uint32_t row, float v) { p.sh_out[(uint64_t)t * p.K + row] = v; });
         }
     };
     const bool sh_first = p.T == 1u;
@@ -1481,6 +1483,77 @@ __global__ void __launch_bounds__(256) dec_down_kernel(dec_params p) {
         sub = nsub;
     }
     if (sh && !sh_first) shared_phase();
+}
+
+// ---------------------------------------------------------------------------
+// One token, one group per slot (SF37_DEC_SLOTS): down and combine in one
+// launch.  A workgroup owns the rpw output rows of one routed sub-item (12
+// for F = 1280, lane = (row, block) as in dec_down_kernel): wave s < topk
+// computes slot s's rows of its expert, waves 0 .. nsh-1 first the shared
+// rows of the tile (R = 4 per wave), all into LDS; then one thread per row
+// forms out = [shared +] (slots summed in slot order) [+ out], the
+// arithmetic of dec_combine_kernel.  No per-pair rows reach memory.
+// ---------------------------------------------------------------------------
+constexpr uint32_t DN1_WAVES = 8;        // slots (topk <= 8) and shared passes (<= 8) per workgroup
+constexpr uint32_t DN1_MAX_RPW = 32;     // rows per tile (nb >= 2)
+
+__host__ __device__ constexpr uint32_t dn1_rpw(uint32_t F) { return 4u * (16u / (F / SF37_QK)); }
+
+template <int SHNB>
+__global__ void __launch_bounds__(DN1_WAVES * 64, 2) dec_down1_kernel(dec_params p) {
+    __shared__ __align__(16) int8_t shq[DN_MAX_NB * SF37_QK];
+    __shared__ float shs[DN_MAX_NB * SF37_QK / 32u];
+    __shared__ __align__(16) act_t xsl[DN1_WAVES][DN_MAX_NB];
+    __shared__ float res[DN1_WAVES][DN1_MAX_RPW];
+    __shared__ float shres[DN1_MAX_RPW];
+    const bool sh = (p.flags & SF37_DEC_SHARED) != 0;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63u;
+    const uint32_t nb = p.F / SF37_QK, rpd = 16u / nb, rpw = 4u * rpd, r0 = blockIdx.x * rpw;
+    const uint32_t q = lane & 15u, r_in = q / nb, b = q - r_in * nb;
+    const bool active = r_in < rpd;
+    const uint32_t rl = (lane >> 4) * rpd + (active ? r_in : 0u);
+    const bool routed = wave < p.topk;
+    uint32_t w[21];
+    if (routed) {
+        const uint32_t e = p.ginfo[2u + p.G + wave];
+        uint32_t row = r0 + rl;
+        row = row < p.K ? row : p.K - 1u;                                   // tail lanes stay in bounds
+        load_q2(w, p.down_w + ((uint64_t)e * p.K + row) * ((uint64_t)nb * SF37_Q2_BYTES) +
+                       (uint64_t)b * SF37_Q2_BYTES);
+    }
+    if (sh) {
+        for (uint32_t i = threadIdx.x; i < p.F / 16u; i += blockDim.x) ((u32x4 *)shq)[i] = ((const u32x4 *)p.sh_mq)[i];
+        for (uint32_t i = threadIdx.x; i < p.F / 32u; i += blockDim.x) shs[i] = p.sh_ms[i];
+    }
+    if (routed) {
+        const uint32_t per = nb * (uint32_t)(sizeof(act_t) / 16u);
+        for (uint32_t i = lane; i < per; i += 64u)
+            ((u32x4 *)xsl[wave])[i] = ((const u32x4 *)((const act_t *)p.midq + (uint64_t)p.sorted[wave] * nb))[i];
+    }
+    __syncthreads();
+    const uint32_t R = 64u / shd_slices(1u), nsh = (rpw + R - 1u) / R;
+    if (sh && wave < nsh)
+        shared_down_pass<SHNB>(p, shq, shs, r0 + wave * R,
+                               [&](uint32_t, uint32_t row, float v) { shres[row - r0] = v; });
+    if (routed) {
+        opaque<21>(w);
+        const act_t *x[DEC_TPC];
+#pragma unroll
+        for (uint32_t t = 0; t < DEC_TPC; t++) x[t] = xsl[wave] + b;
+        float bs[DEC_TPC], dd[1] = {x[0]->d}, acc[1];
+        q2_block_dots_lds<1>(w, x, bs);
+        seg_chains<1>(dd, bs, acc, b, nb);
+        if (active && b == nb - 1u && r0 + rl < p.K) res[wave][rl] = acc[0];
+    }
+    __syncthreads();
+    const uint32_t i = threadIdx.x;
+    if (i < rpw && r0 + i < p.K) {
+        const uint32_t r = r0 + i;
+        float acc = 0.0f;
+        for (uint32_t s2 = 0; s2 < p.topk; s2++) acc = acc + res[s2][i];
+        const float y = sh ? shres[i] + acc : (p.flags & SF37_DEC_SHBASE) ? p.sh_out[r] + acc : acc;
+        p.out[r] = (p.flags & SF37_DEC_RESID) ? p.out[r] + y : y;
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -1720,6 +1793,26 @@ extern "C" int sf37k_decode_down(const sf37_dec_params *pp, sf37_stream_t s) {
     const int err = opt_in_lds(d.dn_kernel, d.lds_dn);
     if (err) return err;
     const hipError_t e = hipLaunchKernel(d.dn_kernel, dim3(d.n_dn), dim3(256), args, d.lds_dn, (hipStream_t)s);
+    return (int)(e != hipSuccess ? e : hipGetLastError());
+}
+
+extern "C" int sf37k_decode_down_combine_supported(const sf37_dec_params *pp) {
+    const sf37_dec_params &p = *pp;
+    const uint32_t nb = p.F / SF37_QK;
+    return (p.flags & SF37_DEC_SLOTS) && p.T == 1u && p.topk <= DN1_WAVES && nb >= 2u && nb <= DN_MAX_NB &&
+           dn1_rpw(p.F) <= DN1_MAX_RPW && (dn1_rpw(p.F) + 3u) / 4u <= DN1_WAVES && p.K > 0u;
+}
+
+extern "C" int sf37k_decode_down_combine(const sf37_dec_params *pp, sf37_stream_t s) {
+    if (!sf37k_decode_down_combine_supported(pp)) return (int)hipErrorInvalidValue;
+    const sf37_dec_params &p = *pp;
+    const uint32_t nbat = (shd_bps(p.F / 32u, shd_slices(1u)) + SHD_CHUNK - 1u) / SHD_CHUNK;
+    const void *fn = (p.flags & SF37_DEC_SHARED) == 0u || nbat <= 1u ? (const void *)dec_down1_kernel<1>
+                     : nbat == 2u                                    ? (const void *)dec_down1_kernel<2>
+                                                                     : (const void *)dec_down1_kernel<3>;
+    const uint32_t rpw = dn1_rpw(p.F);
+    void *args[] = {(void *)pp};
+    const hipError_t e = hipLaunchKernel(fn, dim3((p.K + rpw - 1u) / rpw), dim3(DN1_WAVES * 64u), args, 0, (hipStream_t)s);
     return (int)(e != hipSuccess ? e : hipGetLastError());
 }
 

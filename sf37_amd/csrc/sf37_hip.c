@@ -51,6 +51,7 @@ static int64_t g_opt_write_gate_up = 0;
 static int64_t g_opt_decode = 1;
 static int64_t g_opt_router_always = 0;
 static int64_t g_opt_up_dyn_pct = -1, g_opt_up_wgs = 0, g_opt_dn_wgs = 0, g_opt_upsel_max_tok = 1;
+static int64_t g_opt_down_combine = 1;
 static int64_t g_opt_prefill = 1;
 static int64_t g_opt_prefill_min_pairs = 256;
 static int64_t g_opt_shared_min_tok = 64;
@@ -337,6 +338,7 @@ int sf37_hip_set_option(const char *name, int64_t value) {
     else if (!strcmp(name, "decode_up_wgs")) g_opt_up_wgs = value < 0 ? 0 : value;
     else if (!strcmp(name, "decode_down_wgs")) g_opt_dn_wgs = value < 0 ? 0 : value;
     else if (!strcmp(name, "decode_select_in_up_max_tokens")) g_opt_upsel_max_tok = value < 0 ? 0 : value;
+    else if (!strcmp(name, "decode_down_combine")) g_opt_down_combine = value ? 1 : 0;
     else if (!strcmp(name, "prefill_mfma")) g_opt_prefill = value ? 1 : 0;
     else if (!strcmp(name, "prefill_min_pairs")) g_opt_prefill_min_pairs = value < 0 ? 0 : value;
     else if (!strcmp(name, "shared_min_tokens")) g_opt_shared_min_tok = value < 0 ? 0 : value;
@@ -355,6 +357,7 @@ int64_t sf37_hip_get_option(const char *name) {
     if (!strcmp(name, "decode_up_wgs")) return g_opt_up_wgs;
     if (!strcmp(name, "decode_down_wgs")) return g_opt_dn_wgs;
     if (!strcmp(name, "decode_select_in_up_max_tokens")) return g_opt_upsel_max_tok;
+    if (!strcmp(name, "decode_down_combine")) return g_opt_down_combine;
     if (!strcmp(name, "prefill_mfma")) return g_opt_prefill;
     if (!strcmp(name, "prefill_min_pairs")) return g_opt_prefill_min_pairs;
     if (!strcmp(name, "shared_min_tokens")) return g_opt_shared_min_tok;
@@ -1326,8 +1329,10 @@ static int decode_run_in(const routed_args *a, const dec_extra *ex, float *out, 
             LAUNCH(SF37_HIP_STAGE_DEC_SELECT, sf37k_decode_select(&p, st), "decode select launch")) &&
            LAUNCH(SF37_HIP_STAGE_DEC_UP, sf37k_decode_up(&p, st), "decode up launch") &&
            LAUNCH(SF37_HIP_STAGE_DEC_MID, sf37k_decode_mid(&p, st), "decode mid launch") &&
-           LAUNCH(SF37_HIP_STAGE_DEC_DOWN, sf37k_decode_down(&p, st), "decode down launch") &&
-           LAUNCH(SF37_HIP_STAGE_DEC_COMBINE, sf37k_decode_combine(&p, st), "decode combine launch");
+           (g_opt_down_combine && sf37k_decode_down_combine_supported(&p)
+                ? LAUNCH(SF37_HIP_STAGE_DEC_DOWN, sf37k_decode_down_combine(&p, st), "decode down+combine launch")
+                : LAUNCH(SF37_HIP_STAGE_DEC_DOWN, sf37k_decode_down(&p, st), "decode down launch") &&
+                      LAUNCH(SF37_HIP_STAGE_DEC_COMBINE, sf37k_decode_combine(&p, st), "decode combine launch"));
 }
 
 static int decode_run(const routed_args *a, const dec_extra *ex, float *out, float *mid, float *down_pair,

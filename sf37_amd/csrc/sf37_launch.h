@@ -204,6 +204,10 @@ int sf37k_decode_up(const sf37_dec_params *p, sf37_stream_t s);
 int sf37k_decode_mid(const sf37_dec_params *p, sf37_stream_t s);
 int sf37k_decode_down(const sf37_dec_params *p, sf37_stream_t s);
 int sf37k_decode_combine(const sf37_dec_params *p, sf37_stream_t s);
+/* One token with SLOTS: down and combine as one launch (in place of the
+ * last two), when _supported says the shape fits. */
+int sf37k_decode_down_combine_supported(const sf37_dec_params *p);
+int sf37k_decode_down_combine(const sf37_dec_params *p, sf37_stream_t s);
 
 #ifdef __cplusplus
 }

@@ -208,7 +208,11 @@ def test_fused_routed_batch_mapped(H, O, layer):
 
 def test_fused_routed_one_duplicates(H, O, layer):
     """routed_moe_one (one group per slot) with a repeated expert and the
-    gate/up export option: all outputs equal the staged path."""
+    gate/up export option: out, gate, up and mid equal the staged path with
+    the one-token down+combine launch and without it; the per-slot down rows
+    (scratch, written only when down and combine are separate launches, as
+    the reference's direct down-sum path leaves them unwritten,
+    sf37_cuda.cu:5366-5371) equal the staged path's."""
     rng = np.random.default_rng(9)
     sel = rng.choice(E, TOPK, replace=False).astype(np.int32)
     sel[6] = sel[2]
@@ -218,8 +222,9 @@ def test_fused_routed_one_duplicates(H, O, layer):
     res = []
     H.set_option("moe_write_gate_up", 1)
     try:
-        for fused in (True, False):
+        for fused, down_combine in ((True, True), (True, False), (False, False)):
             H.set_option("decode_fused", 1 if fused else 0)
+            H.set_option("decode_down_combine", 1 if down_combine else 0)
             out, g, u, m, d = (H.Tensor.alloc(K * 4), H.Tensor.alloc(TOPK * F * 4), H.Tensor.alloc(TOPK * F * 4),
                                H.Tensor.alloc(TOPK * F * 4), H.Tensor.alloc(TOPK * K * 4))
             H.check(H.lib().sf37_hip_routed_moe_one(out, g, u, m, d, layer.gate, layer.up, layer.down, st, wt, E,
@@ -228,8 +233,11 @@ def test_fused_routed_one_duplicates(H, O, layer):
     finally:
         H.set_option("moe_write_gate_up", 0)
         H.set_option("decode_fused", 1)
-    for name, a, b in zip(("out", "gate", "up", "mid", "down"), res[0], res[1]):
-        assert_bitexact(a, b, f"routed_moe_one {name}")
+        H.set_option("decode_down_combine", 1)
+    for k in (0, 1):
+        for name, a, b in zip(("out", "gate", "up", "mid"), res[k], res[2]):
+            assert_bitexact(a, b, f"routed_moe_one {name} (run {k})")
+    assert_bitexact(res[1][4], res[2][4], "routed_moe_one down rows")
     host = layer.host_experts(sel)
     want, want_mid, _ = O.routed_moe_one_q8k(host["gate"], host["up"], host["down"], sel, w, E, K, F, K, 0.0, x)
     assert_bitexact(res[0][0], want, "routed_moe_one vs oracle")
