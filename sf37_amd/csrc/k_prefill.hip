@@ -26,6 +26,8 @@
 // buffers, one block ahead) and each wave streams its own weight rows into
 // registers one block ahead, dequantises them in registers and runs the
 // MFMAs: 4 token blocks x one 32-column weight block per wave.
+#include <type_traits>
+
 #include "sf37_blocks.h"
 #include "sf37_launch.h"
 
@@ -36,9 +38,20 @@ typedef float f16v __attribute__((ext_vector_type(16)));
 
 constexpr uint32_t PF_T = 64;           // pairs per tile
 constexpr uint32_t PF_TB = PF_T / 32u;  // 32-pair MFMA blocks per tile
-constexpr uint32_t PF_WAVES = 8;        // waves per workgroup (two per SIMD), 32 weight columns each
-constexpr uint32_t PF_GU_R = 128;       // F rows (gate and up) per gate/up workgroup
-constexpr uint32_t PF_DN_R = 256;       // output rows per down workgroup
+// Waves per workgroup (32 weight columns each) and activation buffers:
+// gate/up one 8-wave workgroup per CU (two waves per SIMD), activations
+// three buffers deep; down two 4-wave workgroups per CU (their barriers do
+// not stall each other's SIMDs), two buffers.  Measured: 4-wave down
+// workgroups 649 against 696 us at 4096 tokens; 4-wave gate/up 1307
+// against 1263 us.
+template <bool Q3> struct pf_cfg {
+    static constexpr uint32_t NW = Q3 ? 8u : 4u;
+    static constexpr uint32_t NBUF = Q3 ? 3u : 2u;
+    static constexpr uint32_t ROWS = (Q3 ? 16u : 32u) * NW;   // F rows (gate/up) or output rows per workgroup
+};
+constexpr uint32_t PF_GU_R = pf_cfg<true>::ROWS;    // 128
+constexpr uint32_t PF_DN_R = pf_cfg<false>::ROWS;   // 128
+constexpr uint32_t PF_CD_ROWS = 8;                  // table rows of LDS per buffer (5 used)
 constexpr uint32_t PF_TAB = 8;          // floats per (row, block) table entry: C0..C3, d
 // LDS layout of one activation block: 4 groups of 32 tile slots; in a group
 // slot t (0..31) starts at PF_RS * (t % 16) + 512 * (t / 16), so one 64-lane
@@ -231,7 +244,8 @@ __device__ __forceinline__ void lds_dma4(uint32_t lds, uint32_t voff, const void
 }
 __device__ __forceinline__ void wait_vm0() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 // All but the newest PF_DMA_PER_BLOCK vector-memory operations of the wave
-// done: the activation loads issued for the block after next stay in flight.
+// done: the activation loads issued for the block after next stay in flight
+// (8-wave workgroups, three buffers).
 constexpr int PF_DMA_PER_BLOCK = 5;   // 4 code rows + 1 table row per wave and block
 static_assert(PF_DMA_PER_BLOCK == 5, "the count in wait_vm_keep_next");
 __device__ __forceinline__ void wait_vm_keep_next() { asm volatile("s_waitcnt vmcnt(5)" ::: "memory"); }
@@ -447,14 +461,15 @@ __device__ __forceinline__ void pf_block(const RAW &r, const uint8_t *act_lds, c
 // 128 output rows, 32 per wave; epilogue down_pair[pair][row].
 template <bool Q3, int NTB, typename ISSUE>
 __device__ __forceinline__ void pf_body(const pf_params &p, const uint8_t *wrow, ISSUE &issue_act,
-                                        uint8_t (*s_act)[PF_ACT_BUF], float (*s_cd)[PF_WAVES * PF_T],
+                                        uint8_t (*s_act)[PF_ACT_BUF], float (*s_cd)[PF_CD_ROWS * PF_T],
                                         const uint32_t *s_pair, const float *s_w, uint32_t kh, uint32_t col,
                                         uint32_t wcol, uint32_t cnt);
 
 template <bool Q3>
-__global__ void __launch_bounds__(PF_WAVES * 64, 1) pf_expert_kernel(pf_params p) {
-    __shared__ __align__(16) uint8_t s_act[3][PF_ACT_BUF];
-    __shared__ __align__(16) float s_cd[3][PF_WAVES * PF_T];
+__global__ void __launch_bounds__(pf_cfg<Q3>::NW * 64, Q3 ? 1 : 2) pf_expert_kernel(pf_params p) {
+    constexpr uint32_t NW = pf_cfg<Q3>::NW, NBUF = pf_cfg<Q3>::NBUF;
+    __shared__ __align__(16) uint8_t s_act[NBUF][PF_ACT_BUF];
+    __shared__ __align__(16) float s_cd[NBUF][PF_CD_ROWS * PF_T];
     __shared__ uint32_t s_pair[PF_T];
     __shared__ float s_w[PF_T];
     const uint32_t wg = blockIdx.x, xcd = wg & 7u, slot = wg >> 3;
@@ -471,41 +486,50 @@ __global__ void __launch_bounds__(PF_WAVES * 64, 1) pf_expert_kernel(pf_params p
         s_pair[tid] = pr;
         if (Q3) s_w[tid] = p.weights[pr];
     }
-    // activation rows: tile slot `lane` for the tables; slot 32*(wave/4) + lane%32
-    // for the codes (pad slots repeat the last pair)
-    const uint32_t gi = wave >> 2, wq = wave & 3u;
-    uint32_t rowoff_c;
-    {
+    // activation rows: tile slot `lane` for the tables; slot 32*gi + lane%32
+    // for the codes (pad slots repeat the last pair).  8 waves: wave 4*gi + wq
+    // copies slot group gi; 4 waves: wave wq copies both groups.
+    constexpr uint32_t NG = NW == 8u ? 1u : 2u;      // slot groups a wave copies
+    const uint32_t wq = wave & 3u;
+    uint32_t rowoff_c[NG];
+#pragma unroll
+    for (uint32_t k = 0; k < NG; k++) {
+        const uint32_t gi = NW == 8u ? wave >> 2 : k;
         const uint32_t sl = 32u * gi + (lane & 31u);
         const uint32_t pr = p.sorted[p0 + (sl < cnt ? sl : cnt - 1u)];
-        rowoff_c = (Q3 ? pr / p.topk : pr) * nblk * (SF37_QK * 2u);
+        rowoff_c[k] = (Q3 ? pr / p.topk : pr) * nblk * (SF37_QK * 2u);
     }
     const uint32_t act_l = lds_addr(&s_act[0][0]), cd_l = lds_addr(&s_cd[0][0]);
-    // codes: waves 4*gi .. 4*gi+3 copy slot group gi; wave 4*gi + q loads slot
-    // pairs (t, t + 16), t = 4q .. 4q+3: lanes 0..31 read slot t's 512-byte
-    // row, lanes 32..63 slot t + 16's
-    // slice `part` of `nparts` (compile-time after inlining) of block b's loads
+    // codes: a wave loads slot pairs (t, t + 16), t = 4q .. 4q+3 of its slot
+    // group(s): lanes 0..31 read slot t's 512-byte row, lanes 32..63 slot
+    // t + 16's.  Slice `part` of `nparts` (compile-time after inlining) of
+    // block b's loads.
     auto issue_act = [&](uint32_t b, int part, int nparts) {
-        const uint32_t bf = b % 3u;
+        const uint32_t bf = b % NBUF;
         const uint8_t *cb = (const uint8_t *)p.act + (uint64_t)b * (SF37_QK * 2u);
-        const int j0 = 4 * part / nparts, j1 = 4 * (part + 1) / nparts;
+        constexpr int NJ = 4 * (int)NG;
+        const int j0 = NJ * part / nparts, j1 = NJ * (part + 1) / nparts;
 #pragma unroll
-        for (int j = j0; j < j1; j++) {
-            const uint32_t t = 4u * wq + (uint32_t)j;
-            const uint32_t r0 = (uint32_t)__builtin_amdgcn_readlane((int)rowoff_c, (int)t);
-            const uint32_t r1 = (uint32_t)__builtin_amdgcn_readlane((int)rowoff_c, (int)t + 16);
+        for (int jj = j0; jj < j1; jj++) {
+            const uint32_t k = (uint32_t)jj >> 2, gi = NW == 8u ? wave >> 2 : k;
+            const uint32_t t = 4u * wq + ((uint32_t)jj & 3u);
+            const uint32_t r0 = (uint32_t)__builtin_amdgcn_readlane((int)rowoff_c[k], (int)t);
+            const uint32_t r1 = (uint32_t)__builtin_amdgcn_readlane((int)rowoff_c[k], (int)t + 16);
             lds_dma16(act_l + bf * PF_ACT_BUF + gi * PF_GRP + t * PF_RS, (kh ? r1 : r0) + 16u * col, cb);
         }
-        if (part == 0) {   // tables: wave a < 5 loads C_a (a < 4) or d (a = 4) of all slots;
-                           // waves 5..7 fill spare rows (no branch inside the stage)
-            const uint32_t a = wave < 5u ? wave : 4u;
-            const float *tb = p.tab + ((uint64_t)b * 5u + a) * p.tab_stride + p0;
-            lds_dma4(cd_l + bf * (PF_WAVES * PF_T * 4u) + wave * PF_T * 4u, 4u * lane, tb);
+        if (part == 0) {   // tables of all slots: row a = C_a (a < 4) or d (a = 4).  8 waves:
+                           // wave a < 5 loads row a, waves 5..7 row 4 again; 4 waves: wave w
+                           // loads rows w and 4 (the same bytes from every wave; no branch)
+#pragma unroll
+            for (uint32_t k = 0; k < (NW == 8u ? 1u : 2u); k++) {
+                const uint32_t a = NW == 8u ? (wave < 5u ? wave : 4u) : (k ? 4u : wave);
+                const float *tb = p.tab + ((uint64_t)b * 5u + a) * p.tab_stride + p0;
+                lds_dma4(cd_l + bf * (PF_CD_ROWS * PF_T * 4u) + (NW == 8u ? wave : a) * PF_T * 4u, 4u * lane, tb);
+            }
         }
     };
     // this lane's weight row
     const uint32_t wcol = Q3 ? rt * PF_GU_R + 16u * wave + (col & 15u) : rt * PF_DN_R + 32u * wave + col;
-    static_assert(PF_GU_R == 16u * PF_WAVES && PF_DN_R == 32u * PF_WAVES, "32 columns per wave");
     const uint32_t blk_bytes = Q3 ? SF37_Q3_BYTES : SF37_Q2_BYTES;
     const uint64_t row_bytes = (uint64_t)nblk * blk_bytes;
     const uint8_t *wrow = (Q3 && col >= 16u ? p.w1 : p.w0) + ((uint64_t)e * p.out_rows + wcol) * row_bytes;
@@ -516,7 +540,7 @@ __global__ void __launch_bounds__(PF_WAVES * 64, 1) pf_expert_kernel(pf_params p
 // Main loop and epilogue for NTB 32-pair blocks (the tile's pair count rounded up).
 template <bool Q3, int NTB, typename ISSUE>
 __device__ __forceinline__ void pf_body(const pf_params &p, const uint8_t *wrow, ISSUE &issue_act,
-                                        uint8_t (*s_act)[PF_ACT_BUF], float (*s_cd)[PF_WAVES * PF_T],
+                                        uint8_t (*s_act)[PF_ACT_BUF], float (*s_cd)[PF_CD_ROWS * PF_T],
                                         const uint32_t *s_pair, const float *s_w, uint32_t kh, uint32_t col,
                                         uint32_t wcol, uint32_t cnt) {
     const uint32_t nblk = p.nblk;
@@ -528,73 +552,57 @@ __device__ __forceinline__ void pf_body(const pf_params &p, const uint8_t *wrow,
         for (int r2 = 0; r2 < 16; r2++) acc[i][r2] = 0.0f;
 
     // Pipeline: a block's weight words (registers) are loaded one block
-    // ahead, its activation rows and tables (LDS, three buffers) two blocks
-    // ahead.  During block b: first the weights of b+1, then the activation
-    // loads of b+2 spread over the stages; at the top of block b+1 the wave
-    // waits for all but those newest PF_DMA_PER_BLOCK loads.  Past the last
-    // block the loads repeat block nblk-1 (its buffer then receives the same
-    // bytes again; uniform code, no branch inside the stages); the final
-    // wait below keeps no load in flight at the end of the workgroup.
+    // ahead.  Three activation buffers (8 waves): the activation rows and
+    // tables of block b+2 are loaded during block b, spread over its stages,
+    // and the top of block b+1 waits for all but those newest
+    // PF_DMA_PER_BLOCK loads.  Two buffers (4 waves): those of block b+1 are
+    // issued at the start of block b, and the top of block b+1 waits for
+    // every load.  Past the last block the loads repeat block nblk-1 (its
+    // buffer then receives the same bytes again; uniform code, no branch
+    // inside the stages); the final wait below keeps no load in flight at
+    // the end of the workgroup.
+    constexpr uint32_t NBUF = pf_cfg<Q3>::NBUF;
     const uint32_t last = nblk - 1u;
     auto clampb = [&](uint32_t x) { return x < nblk ? x : last; };
-    if constexpr (Q3) {
-        // blocks in pairs: even blocks start dword-aligned, odd blocks 2 bytes in
-        q3_raw ra, rb;
-        auto wload = [&](q3_raw &r, uint32_t bn) {
+    auto top = [&]() {
+        if constexpr (NBUF == 3u) wait_vm_keep_next();
+        else wait_vm0();
+    };
+    using RAW = typename std::conditional<Q3, q3_raw, q2_raw>::type;
+    RAW ra, rb;
+    auto wload = [&](RAW &r, uint32_t bn) {
+        if constexpr (Q3) {
+            // blocks in pairs: even blocks start dword-aligned, odd blocks 2 bytes in
             const uint32_t o = SF37_Q3_BYTES * bn;
             q3_load(r, wrow + (o & ~3u), wrow + ((o + 12u + 12u * kh) & ~3u));
-        };
-        issue_act(0, 0, 1);
-        wload(ra, 0);
-        issue_act(clampb(1u), 0, 1);
-        for (uint32_t b = 0; b < nblk; b += 2u) {
-            wait_vm_keep_next();
-            raw_ready(ra);
-            __syncthreads();
-            const uint32_t b1 = clampb(b + 1u), b2 = clampb(b + 2u), b3 = clampb(b + 3u);
-            pf_block<true, 0, NTB>(ra, s_act[b % 3u], s_cd[b % 3u], kh, col, acc, blk, [&](int c, int nc) {
-                if (c == 0) wload(rb, b1);
-                issue_act(b2, c, nc);
-            });
-            if (b + 1u < nblk) {
-                wait_vm_keep_next();
-                raw_ready(rb);
-                __syncthreads();
-                pf_block<true, 16, NTB>(rb, s_act[(b + 1u) % 3u], s_cd[(b + 1u) % 3u], kh, col, acc, blk,
-                                        [&](int c, int nc) {
-                                            if (c == 0) wload(ra, b2);
-                                            issue_act(b3, c, nc);
-                                        });
-            }
-        }
-    } else {
-        q2_raw ra, rb;
-        auto wload = [&](q2_raw &r, uint32_t bn) {
+        } else {
             const uint8_t *bp = wrow + (uint64_t)SF37_Q2_BYTES * bn;
             q2_load(r, bp, bp + 12u + 8u * kh);
-        };
-        issue_act(0, 0, 1);
-        wload(ra, 0);
-        issue_act(clampb(1u), 0, 1);
-        for (uint32_t b = 0; b < nblk; b += 2u) {
-            wait_vm_keep_next();
-            raw_ready(ra);
+        }
+    };
+    // the block's loads: weights of bn into r, activations of ba
+    auto pre = [&](RAW &r, uint32_t bn, uint32_t ba, int c, int nc) {
+        if (c == 0) wload(r, bn);
+        if constexpr (NBUF == 3u) issue_act(ba, c, nc);
+        else if (c == 0) issue_act(ba, 0, 1);
+    };
+    issue_act(0, 0, 1);
+    wload(ra, 0);
+    if constexpr (NBUF == 3u) issue_act(clampb(1u), 0, 1);
+    constexpr int SH2 = Q3 ? 16 : 0;   // bit offset of an odd block's string in its words
+    for (uint32_t b = 0; b < nblk; b += 2u) {
+        top();
+        raw_ready(ra);
+        __syncthreads();
+        const uint32_t b1 = clampb(b + 1u), b2 = clampb(b + 2u), b3 = clampb(b + 3u);
+        pf_block<Q3, 0, NTB>(ra, s_act[b % NBUF], s_cd[b % NBUF], kh, col, acc, blk,
+                             [&](int c, int nc) { pre(rb, b1, NBUF == 3u ? b2 : b1, c, nc); });
+        if (b + 1u < nblk) {
+            top();
+            raw_ready(rb);
             __syncthreads();
-            const uint32_t b1 = clampb(b + 1u), b2 = clampb(b + 2u), b3 = clampb(b + 3u);
-            pf_block<false, 0, NTB>(ra, s_act[b % 3u], s_cd[b % 3u], kh, col, acc, blk, [&](int c, int nc) {
-                if (c == 0) wload(rb, b1);
-                issue_act(b2, c, nc);
-            });
-            if (b + 1u < nblk) {
-                wait_vm_keep_next();
-                raw_ready(rb);
-                __syncthreads();
-                pf_block<false, 0, NTB>(rb, s_act[(b + 1u) % 3u], s_cd[(b + 1u) % 3u], kh, col, acc, blk,
-                                        [&](int c, int nc) {
-                                            if (c == 0) wload(ra, b2);
-                                            issue_act(b3, c, nc);
-                                        });
-            }
+            pf_block<Q3, SH2, NTB>(rb, s_act[(b + 1u) % NBUF], s_cd[(b + 1u) % NBUF], kh, col, acc, blk,
+                                   [&](int c, int nc) { pre(ra, b2, NBUF == 3u ? b3 : b2, c, nc); });
         }
     }
     wait_vm0();
@@ -905,7 +913,7 @@ extern "C" int sf37k_pf_gate_up(float *mid, float *gate_out, float *up_out, cons
     p.n_rt = mid_dim / PF_GU_R;
     p.tab_stride = tab_stride;
     p.clamp = clamp;
-    hipLaunchKernelGGL(pf_expert_kernel<true>, dim3(pf_grid(max_tiles, p.n_rt)), dim3(PF_WAVES * 64), 0, (hipStream_t)s, p);
+    hipLaunchKernelGGL(pf_expert_kernel<true>, dim3(pf_grid(max_tiles, p.n_rt)), dim3(pf_cfg<true>::NW * 64), 0, (hipStream_t)s, p);
     return (int)hipGetLastError();
 }
 
@@ -923,7 +931,7 @@ extern "C" int sf37k_pf_down(float *down_pair, const uint8_t *down_w, const void
     p.out_rows = out_dim;
     p.n_rt = out_dim / PF_DN_R;
     p.tab_stride = tab_stride;
-    hipLaunchKernelGGL(pf_expert_kernel<false>, dim3(pf_grid(max_tiles, p.n_rt)), dim3(PF_WAVES * 64), 0, (hipStream_t)s, p);
+    hipLaunchKernelGGL(pf_expert_kernel<false>, dim3(pf_grid(max_tiles, p.n_rt)), dim3(pf_cfg<false>::NW * 64), 0, (hipStream_t)s, p);
     return (int)hipGetLastError();
 }
 
