@@ -143,6 +143,162 @@ __global__ void __launch_bounds__(1024) dispatch_kernel(uint32_t *__restrict__ g
     }
 }
 
+// ---------------------------------------------------------------------------
+// Dispatch of large batches over many workgroups, same order as
+// dispatch_kernel: chunk c of DC_CHUNK pairs goes to workgroup c.
+// dispatch_count_kernel: per-chunk expert histograms hist[c][e].
+// dispatch_scatter_kernel: every workgroup sums the histograms (expert
+// totals, and the counts of the chunks before its own), scans the totals
+// over the experts, and scatters its chunk in pair order: its waves take
+// consecutive quarters, each ranks 64 pairs at a time by ballot.  Workgroup
+// 0 writes the counts, offsets and group table.
+// ---------------------------------------------------------------------------
+constexpr uint32_t DC_CHUNK = 1024;   // pairs per workgroup
+constexpr uint32_t DC_THREADS = 256;
+constexpr uint32_t DC_WAVES = DC_THREADS / 64u;
+constexpr uint32_t DC_PER_LANE = DC_CHUNK / DC_THREADS;   // pairs per lane (a wave's quarter: 4 x 64)
+constexpr uint32_t DC_MIN_PAIRS = 8192;   // smaller batches: dispatch_kernel (one launch)
+constexpr uint32_t DC_HB = 16;            // histogram rows loaded together
+
+__global__ void __launch_bounds__(DC_THREADS) dispatch_count_kernel(uint32_t *__restrict__ hist,
+                                                                    const int32_t *__restrict__ selected,
+                                                                    uint32_t n_pairs, uint32_t n_expert) {
+    __shared__ uint32_t h[DISP_MAX_E];
+    for (uint32_t e = threadIdx.x; e < n_expert; e += DC_THREADS) h[e] = 0u;
+    __syncthreads();
+    const uint32_t c0 = blockIdx.x * DC_CHUNK;
+    const uint32_t c1 = c0 + DC_CHUNK < n_pairs ? c0 + DC_CHUNK : n_pairs;
+    uint32_t ev[DC_PER_LANE];
+#pragma unroll
+    for (uint32_t u = 0; u < DC_PER_LANE; u++) {   // every load issued before the first count
+        const uint32_t p = c0 + threadIdx.x + u * DC_THREADS;
+        ev[u] = p < c1 ? clamp_expert(selected[p], n_expert) : 0u;
+    }
+#pragma unroll
+    for (uint32_t u = 0; u < DC_PER_LANE; u++)
+        if (c0 + threadIdx.x + u * DC_THREADS < c1) atomicAdd(&h[ev[u]], 1u);
+    __syncthreads();
+    for (uint32_t e = threadIdx.x; e < n_expert; e += DC_THREADS) hist[(uint64_t)blockIdx.x * n_expert + e] = h[e];
+}
+
+__global__ void __launch_bounds__(DC_THREADS) dispatch_scatter_kernel(uint32_t *__restrict__ group_info,
+                                                                      uint32_t *__restrict__ sorted,
+                                                                      uint32_t *__restrict__ counts,
+                                                                      uint32_t *__restrict__ offsets,
+                                                                      const uint32_t *__restrict__ hist,
+                                                                      const int32_t *__restrict__ selected,
+                                                                      uint32_t n_pairs, uint32_t n_expert) {
+    __shared__ uint32_t tot[DISP_MAX_E], bef[DISP_MAX_E];
+    __shared__ uint32_t cnt[DC_WAVES][DISP_MAX_E];
+    __shared__ uint32_t wsum[2][DC_WAVES];
+    const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63u, nc = gridDim.x, c = blockIdx.x;
+    for (uint32_t e = tid; e < n_expert; e += DC_THREADS) {
+        uint32_t t = 0u, b = 0u;
+        for (uint32_t w0 = 0; w0 < nc; w0 += DC_HB) {   // DC_HB loads in flight
+            uint32_t v[DC_HB];
+#pragma unroll
+            for (uint32_t k = 0; k < DC_HB; k++) v[k] = w0 + k < nc ? hist[(uint64_t)(w0 + k) * n_expert + e] : 0u;
+#pragma unroll
+            for (uint32_t k = 0; k < DC_HB; k++) {
+                t += v[k];
+                b += w0 + k < c ? v[k] : 0u;
+            }
+        }
+        tot[e] = t;
+        bef[e] = b;
+    }
+    for (uint32_t i = tid; i < DC_WAVES * DISP_MAX_E; i += DC_THREADS) (&cnt[0][0])[i] = 0u;
+    __syncthreads();
+    // exclusive scans over the experts of the totals and of the non-empty
+    // flags: thread t owns experts 2t and 2t + 1 (n_expert <= 512)
+    const uint32_t e0 = 2u * tid, e1 = e0 + 1u;
+    const uint32_t t0 = e0 < n_expert ? tot[e0] : 0u, t1 = e1 < n_expert ? tot[e1] : 0u;
+    const uint32_t z0 = t0 ? 1u : 0u, z1 = t1 ? 1u : 0u;
+    uint32_t st = t0 + t1, sn = z0 + z1;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t a = __shfl_up(st, o, 64), b = __shfl_up(sn, o, 64);
+        if (lane >= (uint32_t)o) {
+            st += a;
+            sn += b;
+        }
+    }
+    if (lane == 63u) {
+        wsum[0][wave] = st;
+        wsum[1][wave] = sn;
+    }
+    __syncthreads();
+    uint32_t bt = 0u, bn = 0u, all_n = 0u;
+    for (uint32_t w = 0; w < DC_WAVES; w++) {
+        if (w < wave) {
+            bt += wsum[0][w];
+            bn += wsum[1][w];
+        }
+        all_n += wsum[1][w];
+    }
+    const uint32_t x0 = bt + st - t0 - t1, g0 = bn + sn - z0 - z1;   // exclusive prefix at e0
+    const uint32_t xs[2] = {x0, x0 + t0}, gs[2] = {g0, g0 + z0}, ts[2] = {t0, t1};
+    // the chunk's quarters: per-wave counts, then running offsets per expert
+    const uint32_t c0 = c * DC_CHUNK, c1 = c0 + DC_CHUNK < n_pairs ? c0 + DC_CHUNK : n_pairs;
+    const uint32_t span = DC_CHUNK / DC_WAVES;
+    const uint32_t beg = c0 + wave * span < c1 ? c0 + wave * span : c1;
+    const uint32_t end = beg + span < c1 ? beg + span : c1;
+    uint32_t ev[DC_PER_LANE];
+#pragma unroll
+    for (uint32_t u = 0; u < DC_PER_LANE; u++) {
+        const uint32_t p = beg + 64u * u + lane;
+        ev[u] = p < end ? clamp_expert(selected[p], n_expert) : 0u;
+    }
+#pragma unroll
+    for (uint32_t u = 0; u < DC_PER_LANE; u++)
+        if (beg + 64u * u + lane < end) atomicAdd(&cnt[wave][ev[u]], 1u);
+    __syncthreads();
+#pragma unroll
+    for (uint32_t k = 0; k < 2u; k++) {
+        const uint32_t e = e0 + k;
+        if (e >= n_expert) continue;
+        uint32_t run = xs[k] + bef[e];
+        for (uint32_t w = 0; w < DC_WAVES; w++) {
+            const uint32_t v = cnt[w][e];
+            cnt[w][e] = run;
+            run += v;
+        }
+        if (c == 0) {
+            counts[e] = ts[k];
+            offsets[e] = xs[k];
+            if (ts[k]) {
+                group_info[1u + gs[k]] = xs[k];
+                group_info[2u + n_expert + gs[k]] = e;
+            }
+        }
+    }
+    if (c == 0 && tid == 0) {
+        offsets[n_expert] = n_pairs;
+        group_info[0] = all_n;
+        group_info[1u + all_n] = n_pairs;
+    }
+    __syncthreads();
+    uint32_t nbits = 1;
+    while ((1u << nbits) < n_expert) nbits++;
+#pragma unroll
+    for (uint32_t u = 0; u < DC_PER_LANE; u++) {
+        const uint32_t p = beg + 64u * u + lane;
+        const bool act = p < end;
+        const uint32_t e = ev[u];
+        uint64_t peers = __ballot(act);
+        for (uint32_t b = 0; b < nbits; b++) {
+            const uint64_t m = __ballot(act && ((e >> b) & 1u));
+            peers &= ((e >> b) & 1u) ? m : ~m;
+        }
+        if (act) {
+            const uint64_t lt = lane ? (~0ull >> (64u - lane)) : 0ull;
+            const uint32_t rank = (uint32_t)__popcll(peers & lt);
+            sorted[cnt[wave][e] + rank] = p;
+            if ((peers & lt) == 0ull) cnt[wave][e] += (uint32_t)__popcll(peers);
+        }
+    }
+}
+
 // One group per slot of a single token (routed_moe_one): no sort needed.
 __global__ void slots_kernel(uint32_t *__restrict__ group_info, uint32_t *__restrict__ sorted,
                              const int32_t *__restrict__ selected, uint32_t topk, uint32_t n_expert) {
@@ -461,12 +617,25 @@ __global__ void __launch_bounds__(256) down_f32_kernel(float *__restrict__ down_
 
 }  // namespace
 
+extern "C" uint64_t sf37k_moe_dispatch_scratch_bytes(uint32_t n_pairs, uint32_t n_expert) {
+    return n_pairs > DC_MIN_PAIRS ? (uint64_t)((n_pairs + DC_CHUNK - 1u) / DC_CHUNK) * n_expert * 4u : 0u;
+}
+
 extern "C" int sf37k_moe_dispatch(uint32_t *group_info, uint32_t *sorted_pairs, uint32_t *counts,
                                   uint32_t *offsets, const int32_t *selected, uint32_t n_pairs,
-                                  uint32_t n_expert, sf37_stream_t s) {
+                                  uint32_t n_expert, uint32_t *hist, sf37_stream_t s) {
     if (n_expert == 0 || n_expert > DISP_MAX_E) return (int)hipErrorInvalidValue;
-    hipLaunchKernelGGL(dispatch_kernel, dim3(1), dim3(1024), 0, (hipStream_t)s, group_info,
-                       sorted_pairs, counts, offsets, selected, n_pairs, n_expert);
+    if (n_pairs <= DC_MIN_PAIRS) {
+        hipLaunchKernelGGL(dispatch_kernel, dim3(1), dim3(1024), 0, (hipStream_t)s, group_info,
+                           sorted_pairs, counts, offsets, selected, n_pairs, n_expert);
+        return (int)hipGetLastError();
+    }
+    if (!hist) return (int)hipErrorInvalidValue;
+    const uint32_t nc = (n_pairs + DC_CHUNK - 1u) / DC_CHUNK;
+    hipLaunchKernelGGL(dispatch_count_kernel, dim3(nc), dim3(DC_THREADS), 0, (hipStream_t)s, hist, selected, n_pairs,
+                       n_expert);
+    hipLaunchKernelGGL(dispatch_scatter_kernel, dim3(nc), dim3(DC_THREADS), 0, (hipStream_t)s, group_info,
+                       sorted_pairs, counts, offsets, hist, selected, n_pairs, n_expert);
     return (int)hipGetLastError();
 }
 

@@ -972,7 +972,7 @@ typedef struct {
  * into caller tensors.  Returns the byte size when base == NULL. */
 typedef struct {
     void *xq, *midq;
-    uint32_t *ginfo, *sorted, *counts, *offsets;
+    uint32_t *ginfo, *sorted, *counts, *offsets, *hist;
     float *mid, *down_pair;
     void *x16, *m16;        /* matrix-core path: fp16 codes in MFMA order */
     float *xtab, *mtab;     /* their per-block tables */
@@ -1008,6 +1008,7 @@ static uint64_t routed_layout(const routed_args *a, int slots, int pf, int need_
     RESERVE(sorted, uint32_t *, pairs * 4u);
     RESERVE(counts, uint32_t *, (uint64_t)a->n_expert * 4u);
     RESERVE(offsets, uint32_t *, ((uint64_t)a->n_expert + 1u) * 4u);
+    RESERVE(hist, uint32_t *, slots ? 0u : sf37k_moe_dispatch_scratch_bytes((uint32_t)pairs, a->n_expert));
     if (need_mid) RESERVE(mid, float *, pairs * a->mid_dim * 4u);
     if (need_down) RESERVE(down_pair, float *, pairs * a->out_dim * 4u);
 #undef RESERVE
@@ -1074,7 +1075,7 @@ static int routed_pf(const routed_args *a, const routed_scratch *s, float *out, 
     return LAUNCH(SF37_HIP_STAGE_PF_ACT_X, sf37k_pf_act(1, s->x16, s->xtab, a->x, a->in_dim, a->n_tok, st),
                   "routed_moe mfma input codes launch") &&
            LAUNCH(SF37_HIP_STAGE_DISPATCH, sf37k_moe_dispatch(s->ginfo, s->sorted, s->counts, s->offsets, a->selected,
-                                                              pairs, a->n_expert, st),
+                                                              pairs, a->n_expert, s->hist, st),
                   "routed_moe dispatch launch") &&
            LAUNCH(SF37_HIP_STAGE_PF_TILES, sf37k_pf_tiles(s->tiles, s->ginfo, groups, st), "routed_moe tiles launch") &&
            LAUNCH(SF37_HIP_STAGE_PF_TILES, sf37k_pf_tab_sort(s->xtabs, s->xtab, s->sorted, pairs, a->in_dim, a->topk, st),
@@ -1121,7 +1122,7 @@ static int routed_q8k(const routed_args *a, float *out, float *mid, float *down_
                        "routed_moe slot groups launch"))
             return 0;
     } else if (!LAUNCH(SF37_HIP_STAGE_DISPATCH, sf37k_moe_dispatch(s.ginfo, s.sorted, s.counts, s.offsets, a->selected, pairs,
-                                             a->n_expert, st),
+                                             a->n_expert, s.hist, st),
                           "routed_moe dispatch launch")) {
         return 0;
     }
@@ -1502,11 +1503,13 @@ int sf37_hip_moe_dispatch(sf37_hip_tensor *counts, sf37_hip_tensor *offsets, sf3
     if (counts->bytes < (uint64_t)n_expert * 4u || offsets->bytes < ((uint64_t)n_expert + 1u) * 4u ||
         sorted_pairs->bytes < (uint64_t)n_pairs * 4u || selected->bytes < (uint64_t)n_pairs * 4u)
         return 0;
-    uint32_t *ginfo = (uint32_t *)scratch_get((3u + 2u * (uint64_t)n_expert) * 4u, "dispatch groups");
-    if (!ginfo) return 0;
+    const uint64_t gbytes = align256((3u + 2u * (uint64_t)n_expert) * 4u);
+    char *scr = scratch_get(gbytes + sf37k_moe_dispatch_scratch_bytes(n_pairs, n_expert), "dispatch groups");
+    if (!scr) return 0;
+    uint32_t *ginfo = (uint32_t *)scr, *hist = (uint32_t *)(scr + gbytes);
     return LAUNCH(SF37_HIP_STAGE_DISPATCH, sf37k_moe_dispatch(ginfo, (uint32_t *)sorted_pairs->ptr, (uint32_t *)counts->ptr,
                                         (uint32_t *)offsets->ptr, (const int32_t *)selected->ptr, n_pairs,
-                                        n_expert, (sf37_stream_t)g_stream),
+                                        n_expert, hist, (sf37_stream_t)g_stream),
                      "dispatch launch");
 }
 

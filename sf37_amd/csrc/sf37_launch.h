@@ -73,10 +73,13 @@ int sf37k_moe_combine(float *out, const float *down_pair, const float *base, flo
                       uint32_t out_dim, uint32_t n_tok, sf37_stream_t s);
 /* Build the groups from selected experts: stable counting sort of pairs by
  * expert.  group_info layout: [0] = n_groups, [1 .. 1+E] = group pair
- * offsets, [2+E .. 2+2E) = group experts; counts/offsets per expert also. */
+ * offsets, [2+E .. 2+2E) = group experts; counts/offsets per expert also.
+ * hist: device scratch of sf37k_moe_dispatch_scratch_bytes (per-chunk
+ * histograms of batches sorted by many workgroups; NULL when that is 0). */
+uint64_t sf37k_moe_dispatch_scratch_bytes(uint32_t n_pairs, uint32_t n_expert);
 int sf37k_moe_dispatch(uint32_t *group_info, uint32_t *sorted_pairs, uint32_t *counts,
                        uint32_t *offsets, const int32_t *selected, uint32_t n_pairs,
-                       uint32_t n_expert, sf37_stream_t s);
+                       uint32_t n_expert, uint32_t *hist, sf37_stream_t s);
 /* One group per slot for a single token (no sort), as routed_moe_one. */
 int sf37k_moe_slots(uint32_t *group_info, uint32_t *sorted_pairs, const int32_t *selected,
                     uint32_t topk, uint32_t n_expert, sf37_stream_t s);

@@ -275,7 +275,9 @@ def test_router_reference_cases_and_random(H, O):
 
 def test_dispatch_bit_exact(H, O):
     r = np.random.default_rng(12)
-    for n_tok, n_exp in [(1, 288), (3, 4), (512, 288), (4096, 288), (100, 512)]:
+    # up to 8192 pairs one workgroup sorts; above, chunks of 1024 pairs over
+    # many workgroups (ragged last chunks: 8200 and 10400 pairs)
+    for n_tok, n_exp in [(1, 288), (3, 4), (512, 288), (4096, 288), (100, 512), (1025, 288), (1300, 512)]:
         sel = r.integers(-1, n_exp + 1, size=(n_tok, 8)).astype(np.int32)
         if n_tok == 512:
             sel[:, 0] = 17                                   # one hot expert
