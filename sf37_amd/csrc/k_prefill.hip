@@ -672,28 +672,35 @@ __global__ void __launch_bounds__(256) sh_w16_kernel(_Float16 *__restrict__ w16,
     }
 }
 
-// Q8_0 activations (arithmetic of q8_0_quantize_kernel, k_q8_0.hip): one
-// half-wave per 32-block; codes as fp16 in lane order, scale as float.
+// Q8_0 activations (arithmetic of q8_0_quantize_kernel, k_q8_0.hip): eight
+// lanes per 32-block, four consecutive values per lane; codes as fp16 in
+// lane order (a lane's four codes are contiguous there: one 8-byte store),
+// scale as float.
 __global__ void __launch_bounds__(256) sh_act_kernel(_Float16 *__restrict__ a16, float *__restrict__ xs,
                                                      const float *__restrict__ x, uint32_t nb, uint64_t n_tok) {
-    const uint64_t hw = (uint64_t)blockIdx.x * 8u + (threadIdx.x >> 5);
-    const uint32_t l = threadIdx.x & 31u;
-    const bool live = hw < nb * n_tok;
-    const uint64_t u = live ? hw : 0u;
-    const float v = x[u * 32u + l];
-    float amax = fabsf(v);
+    const uint64_t gid = (uint64_t)blockIdx.x * 256u + threadIdx.x;
+    const uint64_t blk = gid >> 3;
+    const uint32_t j = (uint32_t)gid & 7u;
+    const bool live = blk < nb * n_tok;
+    const uint64_t u = live ? blk : 0u;
+    const float4 v = *(const float4 *)(x + u * 32u + 4u * j);
+    float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
 #pragma unroll
-    for (int off = 16; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 32));
-    int q = 0;
+    for (int off = 4; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 8));
+    typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+    h4 q = {};
     float d = 0.0f;
     if (amax != 0.0f) {
         d = amax / 127.0f;
         const float iscale = 1.0f / d;
-        q = (int)fminf(fmaxf(__builtin_rintf(iscale * v), -128.0f), 127.0f);
+        const float vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int k = 0; k < 4; k++) q[k] = (_Float16)(int)fminf(fmaxf(__builtin_rintf(iscale * vv[k]), -128.0f), 127.0f);
     }
     if (!live) return;
-    a16[u * 32u + sh_pos(l)] = (_Float16)q;
-    if (l == 0) xs[u] = d;
+    static_assert(sh_pos(4u) == sh_pos(0u) + 4u && sh_pos(31u) == sh_pos(28u) + 3u, "a lane's codes are contiguous");
+    *(h4 *)(a16 + u * 32u + sh_pos(4u * j)) = q;
+    if (j == 0u) xs[u] = d;
 }
 
 struct sh_params {
@@ -952,7 +959,7 @@ extern "C" int sf37k_sh_repack(void *w16, float *ws, const uint8_t *w, uint64_t 
 extern "C" int sf37k_sh_act(void *a16, float *xs, const float *x, uint32_t dim, uint32_t n_tok, sf37_stream_t s) {
     const uint64_t n = (uint64_t)(dim / 32u) * n_tok;
     if (n == 0) return 0;
-    hipLaunchKernelGGL(sh_act_kernel, dim3((unsigned)((n + 7u) / 8u)), dim3(256), 0, (hipStream_t)s,
+    hipLaunchKernelGGL(sh_act_kernel, dim3((unsigned)((n + 31u) / 32u)), dim3(256), 0, (hipStream_t)s,
                        (_Float16 *)a16, xs, x, dim / 32u, (uint64_t)n_tok);
     return (int)hipGetLastError();
 }
