@@ -242,3 +242,45 @@ def test_fused_routed_one_duplicates(H, O, layer):
     want, want_mid, _ = O.routed_moe_one_q8k(host["gate"], host["up"], host["down"], sel, w, E, K, F, K, 0.0, x)
     assert_bitexact(res[0][0], want, "routed_moe_one vs oracle")
     assert_bitexact(res[0][3].reshape(TOPK, F), want_mid, "routed_moe_one mid vs oracle")
+
+
+@pytest.mark.parametrize("E_, D_, F_, topk", [(16, 1024, 512, 4), (16, 512, 768, 8), (12, 1024, 1280, 3)])
+def test_one_token_down_combine_shapes(H, O, E_, D_, F_, topk):
+    """The one-token down+combine launch on shapes other than the BASELINE
+    one: fewer slots than its 8 waves (top-3, top-4), 32- and 20-row tiles
+    (F = 512, 768: 8 and 5 shared passes), against the two-launch path,
+    the staged kernels and the oracle, bit for bit."""
+    from sf37_amd.moe import SynthLayer
+    say(f"one-token down+combine: E {E_}, D {D_}, F {F_}, top-{topk}")
+    lay = SynthLayer(seed=300 + topk, n_expert=E_, in_dim=D_, mid_dim=F_, topk=topk)
+    rng = np.random.default_rng(40 + topk)
+    x = rng.standard_normal((1, D_)).astype(np.float32)
+    lg = rng.standard_normal((1, E_)).astype(np.float32)
+    xt, lt = H.Tensor.from_array(x), H.Tensor.from_array(lg)
+    outs, profs = [], []
+    try:
+        for fused, dc in ((True, True), (True, False), (False, False)):
+            H.set_option("decode_fused", 1 if fused else 0)
+            H.set_option("decode_down_combine", 1 if dc else 0)
+            out, sel, wt = H.Tensor.alloc(D_ * 4), H.Tensor.alloc(topk * 4), H.Tensor.alloc(topk * 4)
+            H.lib().sf37_hip_profile_enable(1)
+            H.profile_read()
+            H.check(H.lib().sf37_hip_moe_layer(out, sel, wt, lay.weights_struct(), lt, xt, 1), "moe_layer")
+            profs.append(H.profile_read())
+            H.lib().sf37_hip_profile_enable(0)
+            outs.append((out.read(np.float32), sel.read(np.int32)))
+    finally:
+        H.lib().sf37_hip_profile_enable(0)
+        H.set_option("decode_fused", 1)
+        H.set_option("decode_down_combine", 1)
+    # the first run is the one-launch down+combine, the second two launches
+    assert profs[0]["dec_down"][1] == 1 and profs[0]["dec_combine"][1] == 0, profs[0]
+    assert profs[1]["dec_down"][1] == 1 and profs[1]["dec_combine"][1] == 1, profs[1]
+    for k in (1, 2):
+        assert np.array_equal(outs[0][1], outs[k][1])
+        assert_bitexact(outs[0][0], outs[k][0], f"out vs run {k}")
+    weights = dict(lay.host_experts(np.arange(E_)), **lay.host_dense(), n_expert=E_, mid_dim=F_)
+    want, want_sel, _ = O.moe_layer_q8k(weights, x, logits=lg, topk=topk)
+    assert np.array_equal(outs[0][1].reshape(1, topk), want_sel)
+    assert_bitexact(outs[0][0], want.reshape(-1), "out vs oracle")
+    lay.free()
