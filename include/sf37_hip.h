@@ -240,8 +240,19 @@ void *sf37_hip_get_stream(void);
  *   "moe_write_gate_up" 1 also writes gate/up outputs in routed_moe_one
  *                       (SF37_CUDA_MOE_WRITE_GATE_UP)
  *   "decode_fused"      1 (default): batches of up to 16 tokens on the Q8_K
- *                       path run as three fused launches; 0 uses one launch
- *                       per stage.  Results are identical either way.
+ *                       path run as the fused decode launches (route,
+ *                       select, up, mid, down, combine; fewer for one
+ *                       token); 0 uses the staged kernels.  Results are
+ *                       identical either way.
+ *   "decode_down_combine" 1 (default): one token's down and combine run as
+ *                       one launch; the per-slot `down` tensor of
+ *                       routed_moe_one is then scratch holding no rows (as
+ *                       the reference's direct down-sum path,
+ *                       sf37_cuda.cu:5366-5371); 0 writes them.
+ *   "decode_select_in_up_max_tokens", "decode_up_dyn_pct", "decode_up_wgs",
+ *   "decode_down_wgs"   decode tuning (results unchanged)
+ *   "prefill_mfma"      1 (default): grouped batches run on the matrix cores;
+ *   "prefill_min_pairs", "shared_min_tokens" the smallest batches that do
  *   "router_with_logits" 1: sf37_hip_moe_layer computes the router GEMV even
  *                       when logits_in is given (its result is unused; for
  *                       benchmarks that inject routing but keep the cost)
