@@ -109,43 +109,48 @@ template <bool Q3>
 __global__ void __launch_bounds__(256) pf_act_kernel(_Float16 *__restrict__ codes, float *__restrict__ tab,
                                                      const float *__restrict__ x, uint32_t nblk,
                                                      uint32_t n_rows) {
+    // each wave owns its LDS row and walks the (row, block) units wave by
+    // wave over the grid; nothing is shared between waves
     __shared__ int8_t qs[4][SF37_QK];
     const uint32_t wv = threadIdx.x >> 6, lane = threadIdx.x & 63u;
-    const uint32_t unit = blockIdx.x * 4u + wv;
-    const bool live = unit < nblk * n_rows;
-    const uint32_t u = live ? unit : 0u;
-    const float *xb = x + (uint64_t)u * SF37_QK + 4u * lane;
-    float v[4];
-#pragma unroll
-    for (int k = 0; k < 4; k++) v[k] = xb[k];
-    int8_t q[4];
-    int gs;
-    const float d = q8k_codes4(v, q, gs);
-    (void)gs;
-#pragma unroll
-    for (int k = 0; k < 4; k++) qs[wv][4u * lane + k] = q[k];
-    __syncthreads();
-    // lane produces positions 4*lane .. 4*lane+3, all in group lane/16
+    const uint32_t units = nblk * n_rows, stride = gridDim.x * 4u;
+    // lane produces positions 4*lane .. 4*lane+3, all in group lane/16: their
+    // source codes and biases do not depend on the unit
     const uint32_t g = lane >> 4;
-    int32_t s = 0;
-    _Float16 h[4];
+    uint32_t code[4];
+    int32_t bias[4];
 #pragma unroll
-    for (uint32_t c = 0; c < 4u; c++) {
-        uint32_t code;
-        int32_t bias;
-        pf_pos_code<Q3>(4u * (lane & 15u) + c, code, bias);
-        const int32_t a = qs[wv][64u * g + code];
-        h[c] = (_Float16)a;
-        s += bias * a;
+    for (uint32_t c = 0; c < 4u; c++) pf_pos_code<Q3>(4u * (lane & 15u) + c, code[c], bias[c]);
+    for (uint32_t u = blockIdx.x * 4u + wv; u < units; u += stride) {
+        const float *xb = x + (uint64_t)u * SF37_QK + 4u * lane;
+        float v[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) v[k] = xb[k];
+        int8_t q[4];
+        int gs;
+        const float d = q8k_codes4(v, q, gs);
+        (void)gs;
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // the previous unit's reads are done
+#pragma unroll
+        for (int k = 0; k < 4; k++) qs[wv][4u * lane + k] = q[k];
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // this unit's codes are in LDS
+        __builtin_amdgcn_wave_barrier();
+        int32_t s = 0;
+        _Float16 h[4];
+#pragma unroll
+        for (uint32_t c = 0; c < 4u; c++) {
+            const int32_t a = qs[wv][64u * g + code[c]];
+            h[c] = (_Float16)a;
+            s += bias[c] * a;
+        }
+        s = wave_sum_i32_width(s, 16);
+        typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+        const h4 hv = {h[0], h[1], h[2], h[3]};
+        *(h4 *)(codes + (uint64_t)u * SF37_QK + 4u * lane) = hv;
+        float *tb = tab + (uint64_t)u * PF_TAB;
+        if ((lane & 15u) == 0u) tb[g] = (float)(-s);
+        if (lane == 0u) tb[4] = d;
     }
-    s = wave_sum_i32_width(s, 16);
-    if (!live) return;
-    typedef _Float16 h4 __attribute__((ext_vector_type(4)));
-    const h4 hv = {h[0], h[1], h[2], h[3]};
-    *(h4 *)(codes + (uint64_t)u * SF37_QK + 4u * lane) = hv;
-    float *tb = tab + (uint64_t)u * PF_TAB;
-    if ((lane & 15u) == 0u) tb[g] = (float)(-s);
-    if (lane == 0u) tb[4] = d;
 }
 
 // ---------------------------------------------------------------------------
@@ -889,7 +894,11 @@ extern "C" int sf37k_pf_act(int q3, void *codes_v, float *tab, const float *x, u
     const uint32_t nblk = dim / SF37_QK;
     const uint64_t units = (uint64_t)nblk * n_rows;
     if (units == 0) return 0;
-    const dim3 grid((unsigned)((units + 3u) / 4u));
+    if (units > 0xffffffffu) return (int)hipErrorInvalidValue;
+    // four units per workgroup pass; at most 2048 workgroups, each wave then
+    // walks several units
+    const uint64_t wgs = (units + 3u) / 4u;
+    const dim3 grid((unsigned)(wgs < 2048u ? wgs : 2048u));
     if (q3)
         hipLaunchKernelGGL(pf_act_kernel<true>, grid, dim3(256), 0, (hipStream_t)s, codes, tab, x, nblk, n_rows);
     else
