@@ -498,35 +498,46 @@ __global__ void __launch_bounds__(256) combine_kernel(float *out, const float *_
     combine_store<MODE>(out, base, resid, i, acc);
 }
 
-// The same, four outputs per thread (out_dim % 4 == 0, 1 <= topk <= 16):
-// every slot's float4 is loaded before the first add.
-template <int MODE>
+// The same, four outputs per thread (out_dim % 4 == 0, 1 <= topk <= 16, the
+// row pointers 16-byte aligned): every slot's float4 is loaded before the
+// first add; TK = 8 loads exactly the eight slots (0: topk at run time, 16
+// loads of which those past topk repeat slot 0).  base and resid move as
+// float4; each component gets the scalar kernel's operations.
+template <int MODE, int TK>
 __global__ void __launch_bounds__(256) combine4_kernel(float *out, const float *__restrict__ down_pair,
                                                        const float *base, float *resid, uint32_t topk,
                                                        uint32_t out_dim, uint32_t n_tok) {
+    constexpr uint32_t NS = TK ? (uint32_t)TK : 16u;
+    const uint32_t tk = TK ? (uint32_t)TK : topk;
     const uint64_t i = ((uint64_t)blockIdx.x * 256u + threadIdx.x) * 4u;
     if (i >= (uint64_t)out_dim * n_tok) return;
     const uint64_t t = i / out_dim, r = i - t * out_dim;
-    float4 v[16];
+    float4 v[NS];
 #pragma unroll
-    for (uint32_t s = 0; s < 16u; s++) {
-        const uint32_t sc = s < topk ? s : 0u;   // every load in bounds
-        v[s] = *(const float4 *)(down_pair + (t * topk + sc) * out_dim + r);
+    for (uint32_t s = 0; s < NS; s++) {
+        const uint32_t sc = s < tk ? s : 0u;   // every load in bounds
+        v[s] = *(const float4 *)(down_pair + (t * tk + sc) * out_dim + r);
     }
     float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
-    for (uint32_t s = 0; s < 16u; s++) {
-        if (s < topk) {
+    for (uint32_t s = 0; s < NS; s++) {
+        if (s < tk) {
             acc.x = acc.x + v[s].x;
             acc.y = acc.y + v[s].y;
             acc.z = acc.z + v[s].z;
             acc.w = acc.w + v[s].w;
         }
     }
-    combine_store<MODE>(out, base, resid, i, acc.x);
-    combine_store<MODE>(out, base, resid, i + 1u, acc.y);
-    combine_store<MODE>(out, base, resid, i + 2u, acc.z);
-    combine_store<MODE>(out, base, resid, i + 3u, acc.w);
+    if constexpr (MODE == 0) {
+        *(float4 *)(out + i) = acc;
+    } else if constexpr (MODE == 1) {
+        const float4 bv = *(const float4 *)(base + i);
+        *(float4 *)(out + i) = make_float4(bv.x + acc.x, bv.y + acc.y, bv.z + acc.z, bv.w + acc.w);
+    } else {
+        const float4 bv = *(const float4 *)(base + i), rv = *(const float4 *)(resid + i);
+        *(float4 *)(resid + i) = make_float4(rv.x + (bv.x + acc.x), rv.y + (bv.y + acc.y), rv.z + (bv.z + acc.z),
+                                             rv.w + (bv.w + acc.w));
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -689,12 +700,23 @@ extern "C" int sf37k_moe_combine(float *out, const float *down_pair, const float
     if (n == 0) return 0;
     const int mode = resid ? 2 : (base ? 1 : 0);
     if ((resid || base) && !base) return (int)hipErrorInvalidValue;
-    const bool vec = out_dim % 4u == 0 && topk >= 1u && topk <= 16u && ((uintptr_t)down_pair & 15u) == 0;
+    const bool vec = out_dim % 4u == 0 && topk >= 1u && topk <= 16u &&
+                     (((uintptr_t)down_pair | (uintptr_t)out | (uintptr_t)base | (uintptr_t)resid) & 15u) == 0;
     const dim3 grid((unsigned)(((vec ? n / 4u : n) + 255) / 256));
     if (vec) {
-        if (mode == 0) hipLaunchKernelGGL(combine4_kernel<0>, grid, dim3(256), 0, (hipStream_t)s, out, down_pair, base, resid, topk, out_dim, n_tok);
-        else if (mode == 1) hipLaunchKernelGGL(combine4_kernel<1>, grid, dim3(256), 0, (hipStream_t)s, out, down_pair, base, resid, topk, out_dim, n_tok);
-        else hipLaunchKernelGGL(combine4_kernel<2>, grid, dim3(256), 0, (hipStream_t)s, out, down_pair, base, resid, topk, out_dim, n_tok);
+#define SF37_COMBINE4(M)                                                                                    \
+    do {                                                                                                      \
+        if (topk == 8u)                                                                                       \
+            hipLaunchKernelGGL((combine4_kernel<M, 8>), grid, dim3(256), 0, (hipStream_t)s, out, down_pair, base, \
+                               resid, topk, out_dim, n_tok);                                                  \
+        else                                                                                                  \
+            hipLaunchKernelGGL((combine4_kernel<M, 0>), grid, dim3(256), 0, (hipStream_t)s, out, down_pair, base, \
+                               resid, topk, out_dim, n_tok);                                                  \
+    } while (0)
+        if (mode == 0) SF37_COMBINE4(0);
+        else if (mode == 1) SF37_COMBINE4(1);
+        else SF37_COMBINE4(2);
+#undef SF37_COMBINE4
     } else {
         if (mode == 0) hipLaunchKernelGGL(combine_kernel<0>, grid, dim3(256), 0, (hipStream_t)s, out, down_pair, base, resid, topk, out_dim, n_tok);
         else if (mode == 1) hipLaunchKernelGGL(combine_kernel<1>, grid, dim3(256), 0, (hipStream_t)s, out, down_pair, base, resid, topk, out_dim, n_tok);
