@@ -224,13 +224,15 @@ __global__ void __launch_bounds__(256) dec_route_kernel(dec_params p, uint32_t n
     const uint32_t ntg = (p.T + 3u) / 4u;
     const uint32_t t0 = 4u * (blockIdx.x % ntg), e0 = 2u * (blockIdx.x / ntg);
     const uint32_t nt = p.T - t0 < 4u ? p.T - t0 : 4u, nr = p.E - e0 < 2u ? p.E - e0 : 2u;
-    if (norm && (p.flags & SF37_DEC_ROUTER)) {
+    // RMSNorm scales of the group's tokens (one wave per token), formed
+    // inside the router pass once its first loads are in flight
+    const auto scales = [&]() {
         if (wave < nt) {
             const float sc = sf37_rms_scale_wave(p.x + (uint64_t)(t0 + wave) * p.K, p.K, p.eps);
             if (lane == 0) s_scale[wave] = sc;
         }
         __syncthreads();
-    }
+    };
     stage_exp_tab_imm(tab);
     if (p.flags & SF37_DEC_ROUTER) {
         const float *wr = p.router_w + (uint64_t)e0 * p.K;
@@ -242,10 +244,10 @@ __global__ void __launch_bounds__(256) dec_route_kernel(dec_params p, uint32_t n
                 return sf37_norm_w1_bf16(v, s_scale[t - t0], nw16[k]);
             };
             switch (nt) {
-                case 1: sf37_router_wave<2, 1>(wr, nr, p.x, p.K, cg, t0, scr[wave], store, xf); break;
-                case 2: sf37_router_wave<2, 2>(wr, nr, p.x, p.K, cg, t0, scr[wave], store, xf); break;
-                case 3: sf37_router_wave<2, 3>(wr, nr, p.x, p.K, cg, t0, scr[wave], store, xf); break;
-                default: sf37_router_wave<2, 4>(wr, nr, p.x, p.K, cg, t0, scr[wave], store, xf); break;
+                case 1: sf37_router_wave<2, 1>(wr, nr, p.x, p.K, cg, t0, scr[wave], store, xf, scales); break;
+                case 2: sf37_router_wave<2, 2>(wr, nr, p.x, p.K, cg, t0, scr[wave], store, xf, scales); break;
+                case 3: sf37_router_wave<2, 3>(wr, nr, p.x, p.K, cg, t0, scr[wave], store, xf, scales); break;
+                default: sf37_router_wave<2, 4>(wr, nr, p.x, p.K, cg, t0, scr[wave], store, xf, scales); break;
             }
         } else {
             switch (nt) {

@@ -53,6 +53,9 @@ __device__ __forceinline__ double sf37_wave_sum_f64(double v) {
 struct sf37_x_identity {
     __device__ float operator()(uint32_t, uint32_t, float v) const { return v; }
 };
+struct sf37_no_pre {
+    __device__ void operator()() const {}
+};
 
 template <int NR, int NT, class STORE, class XF = sf37_x_identity>
 __device__ __forceinline__ void sf37_router_block(const float *wr, uint32_t nr, const float *x, uint32_t K,
@@ -147,9 +150,12 @@ __device__ __forceinline__ void sf37_router_rows_n(const float *wr, uint32_t nr,
 // sums of value v, so every value costs a few instructions instead of a DPP
 // chain of its own.  store(r, t, v) receives value v = r * NT + t (from
 // lane 8 v).  scr holds NR * NT * 64 doubles for this wave; NR * NT <= 8.
-template <int NR, int NT, class STORE, class XF = sf37_x_identity>
+// pre() runs once after the first chunk's loads are issued and before xf is
+// first applied (the fused norm forms its scales there while they load).
+template <int NR, int NT, class STORE, class XF = sf37_x_identity, class PRE = sf37_no_pre>
 __device__ __forceinline__ void sf37_router_wave(const float *wr, uint32_t nr, const float *x, uint32_t K,
-                                                 uint32_t cg, uint32_t t0, double *scr, STORE store, XF xf = XF()) {
+                                                 uint32_t cg, uint32_t t0, double *scr, STORE store, XF xf = XF(),
+                                                 PRE pre = PRE()) {
     static_assert(NR * NT <= 8, "eight values per wave at most");
     constexpr int NV = NR * NT;
     const uint32_t lane = threadIdx.x & 63u;
@@ -175,6 +181,7 @@ __device__ __forceinline__ void sf37_router_wave(const float *wr, uint32_t nr, c
                 for (int t = 0; t < NT; t++)
                     xv[t][j] = *(const sf37_f32x4 *)(x + (uint64_t)(t0 + t) * K + k0 + kk + 4u * jj);
             }
+            if (kk == 0u) pre();
 #pragma unroll
             for (int j = 0; j < 4; j++) {
                 if ((uint32_t)j < n4) {
@@ -193,6 +200,7 @@ __device__ __forceinline__ void sf37_router_wave(const float *wr, uint32_t nr, c
             }
         }
     } else {
+        pre();
         for (uint32_t k = k0; k < k0 + c; k++) {
 #pragma unroll
             for (int t = 0; t < NT; t++) {
