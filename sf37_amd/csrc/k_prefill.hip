@@ -674,11 +674,30 @@ __host__ __device__ constexpr uint32_t sh_pos(uint32_t k) {   // code index -> p
     return ((k >> 3) & 1u) * 16u + (k >> 4) * 8u + (k & 7u);
 }
 
-// one lane per Q8_0 block: 32 codes -> fp16 in lane order, scale -> float
-__global__ void __launch_bounds__(256) sh_w16_kernel(_Float16 *__restrict__ w16, float *__restrict__ ws,
-                                                     const uint8_t *__restrict__ w, uint64_t n_blocks) {
-    const uint64_t u = (uint64_t)blockIdx.x * 256u + threadIdx.x;
-    if (u >= n_blocks) return;
+// one lane per Q8_0 block: 32 codes -> fp16 in lane order, scale -> float;
+// the three shared matrices (gate, up, down) in one launch, block u of the
+// concatenation going to the matrix it falls in
+struct sh_w16_args {
+    _Float16 *w16[3];
+    float *ws[3];
+    const uint8_t *w[3];
+    uint64_t n[3];
+};
+__global__ void __launch_bounds__(256) sh_w16_kernel(sh_w16_args a) {
+    uint64_t u = (uint64_t)blockIdx.x * 256u + threadIdx.x;
+    uint32_t m = 0;
+    if (u >= a.n[0]) {
+        u -= a.n[0];
+        m = 1;
+        if (u >= a.n[1]) {
+            u -= a.n[1];
+            m = 2;
+            if (u >= a.n[2]) return;
+        }
+    }
+    _Float16 *const w16 = a.w16[m];
+    float *const ws = a.ws[m];
+    const uint8_t *const w = a.w[m];
     const uint8_t *b = w + u * SF37_Q8_0_BYTES;
     ws[u] = sf37_f16((uint32_t)b[0] | ((uint32_t)b[1] << 8));
     _Float16 h[32];
@@ -972,12 +991,19 @@ extern "C" int sf37k_sh_supported(uint32_t in_dim, uint32_t mid_dim, uint32_t ou
            out_dim % 128u == 0 && in_dim > 0 && mid_dim > 0;
 }
 
-extern "C" int sf37k_sh_repack(void *w16, float *ws, const uint8_t *w, uint64_t rows, uint32_t in_dim,
-                               sf37_stream_t s) {
-    const uint64_t n = rows * (in_dim / 32u);
+extern "C" int sf37k_sh_repack3(void *const w16[3], float *const ws[3], const uint8_t *const w[3],
+                                const uint64_t rows[3], const uint32_t in_dim[3], sf37_stream_t s) {
+    sh_w16_args a;
+    uint64_t n = 0;
+    for (int m = 0; m < 3; m++) {
+        a.w16[m] = (_Float16 *)w16[m];
+        a.ws[m] = ws[m];
+        a.w[m] = w[m];
+        a.n[m] = rows[m] * (in_dim[m] / 32u);
+        n += a.n[m];
+    }
     if (n == 0) return 0;
-    hipLaunchKernelGGL(sh_w16_kernel, dim3((unsigned)((n + 255u) / 256u)), dim3(256), 0, (hipStream_t)s,
-                       (_Float16 *)w16, ws, w, n);
+    hipLaunchKernelGGL(sh_w16_kernel, dim3((unsigned)((n + 255u) / 256u)), dim3(256), 0, (hipStream_t)s, a);
     return (int)hipGetLastError();
 }
 

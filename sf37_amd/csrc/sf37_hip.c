@@ -1051,9 +1051,12 @@ static int shared_mfma(float *out, float *mid, const uint8_t *gw, const uint8_t 
     if (!s) return 0;
     const sf37_stream_t st = (sf37_stream_t)g_stream;
     float *gs = (float *)(s + o_gs), *us = (float *)(s + o_us), *ds = (float *)(s + o_ds), *xs = (float *)(s + o_x);
-    return LAUNCH(SF37_HIP_STAGE_SH_REPACK, sf37k_sh_repack(s + o_g, gs, gw, F, D, st), "shared repack launch") &&
-           LAUNCH(SF37_HIP_STAGE_SH_REPACK, sf37k_sh_repack(s + o_u, us, uw, F, D, st), "shared repack launch") &&
-           LAUNCH(SF37_HIP_STAGE_SH_REPACK, sf37k_sh_repack(s + o_d, ds, dw, D, F, st), "shared repack launch") &&
+    void *const rw16[3] = {s + o_g, s + o_u, s + o_d};
+    float *const rws[3] = {gs, us, ds};
+    const uint8_t *const rw[3] = {gw, uw, dw};
+    const uint64_t rrows[3] = {F, F, D};
+    const uint32_t rin[3] = {D, D, F};
+    return LAUNCH(SF37_HIP_STAGE_SH_REPACK, sf37k_sh_repack3(rw16, rws, rw, rrows, rin, st), "shared repack launch") &&
            LAUNCH(SF37_HIP_STAGE_SH_ACT, sf37k_sh_act(s + o_a, xs, x, D, n_tok, st), "shared activation launch") &&
            LAUNCH(SF37_HIP_STAGE_SH_GATE_UP, sf37k_sh_gate_up(mid, s + o_g, gs, s + o_u, us, s + o_a, xs, n_tok, D, F,
                                                              clamp, st),

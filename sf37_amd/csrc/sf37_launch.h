@@ -134,7 +134,8 @@ int sf37k_pf_down(float *down_pair, const uint8_t *down_w, const void *act, cons
  * same order (a16: n_tok x dim halves, xs: n_tok x dim/32), gate/up with the
  * shared SwiGLU into mid, down into out.  Results equal q8_0_matmul + swiglu. */
 int sf37k_sh_supported(uint32_t in_dim, uint32_t mid_dim, uint32_t out_dim);
-int sf37k_sh_repack(void *w16, float *ws, const uint8_t *w, uint64_t rows, uint32_t in_dim, sf37_stream_t s);
+int sf37k_sh_repack3(void *const w16[3], float *const ws[3], const uint8_t *const w[3], const uint64_t rows[3],
+                     const uint32_t in_dim[3], sf37_stream_t s);
 int sf37k_sh_act(void *a16, float *xs, const float *x, uint32_t dim, uint32_t n_tok, sf37_stream_t s);
 int sf37k_sh_gate_up(float *mid, const void *g16, const float *gs, const void *u16, const float *us,
                      const void *a16, const float *xs, uint32_t n_tok, uint32_t in_dim, uint32_t mid_dim,
