@@ -42,13 +42,19 @@ __global__ void __launch_bounds__(256) rms_norm_kernel(float *__restrict__ out,
     if (row >= n_rows) return;
     const float *xr = x + (uint64_t)row * n;
     float *orow = out + (uint64_t)row * n;
-    if (bf16 && (n & 255u) == 0 && n <= 4096u) {
+    if (bf16 && (n & 255u) == 0 && n <= 4096u && ((uintptr_t)w & 7u) == 0) {
+        // the row and its weights in registers (16-byte x loads, 8-byte
+        // weight loads of four bf16 each, all issued before the sum)
         constexpr uint32_t MAXJ = 16;
         const uint32_t nj = n >> 8;
         sf37_f32x4 v[MAXJ];
+        uint2 wv[MAXJ];
 #pragma unroll
         for (uint32_t j = 0; j < MAXJ; j++)
-            if (j < nj) v[j] = *(const sf37_f32x4 *)(xr + 4u * lane + 256u * j);
+            if (j < nj) {
+                v[j] = *(const sf37_f32x4 *)(xr + 4u * lane + 256u * j);
+                wv[j] = *(const uint2 *)((const uint16_t *)w + 4u * lane + 256u * j);
+            }
         double ss = 0.0;
 #pragma unroll
         for (uint32_t j = 0; j < MAXJ; j++)
@@ -58,14 +64,15 @@ __global__ void __launch_bounds__(256) rms_norm_kernel(float *__restrict__ out,
             }
         const double tot = sf37_wave_sum_f64(ss);
         const float scale = 1.0f / __builtin_sqrtf((float)(tot / (double)n) + eps);
-        const uint16_t *wb = (const uint16_t *)w;
 #pragma unroll
         for (uint32_t j = 0; j < MAXJ; j++)
             if (j < nj) {
                 const uint32_t k = 4u * lane + 256u * j;
+                const uint16_t wq[4] = {(uint16_t)wv[j].x, (uint16_t)(wv[j].x >> 16), (uint16_t)wv[j].y,
+                                        (uint16_t)(wv[j].y >> 16)};
                 sf37_f32x4 o;
 #pragma unroll
-                for (int q = 0; q < 4; q++) o[q] = sf37_norm_w1_bf16(v[j][q], scale, wb[k + q]);
+                for (int q = 0; q < 4; q++) o[q] = sf37_norm_w1_bf16(v[j][q], scale, wq[q]);
                 *(sf37_f32x4 *)(orow + k) = o;
             }
         return;
