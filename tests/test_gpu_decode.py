@@ -167,6 +167,43 @@ def test_fused_layer_16_tokens_against_oracle(H, O, layer):
     assert_bitexact(out, want, "16-token layer")
 
 
+def tied_logits(rng, n_tok, kind):
+    """Router logits whose scores tie (router bias 0): rounded to integers,
+    all equal, or ten equal hot experts spread over every 64-expert column
+    (only the eight smallest positions may win)."""
+    if kind == "rounded":
+        return np.round(1.5 * rng.standard_normal((n_tok, E))).astype(np.float32)
+    if kind == "equal":
+        return np.zeros((n_tok, E), np.float32)
+    lg = (rng.standard_normal((n_tok, E)) - 4.0).astype(np.float32)
+    lg[:, [287, 250, 200, 130, 70, 64, 63, 31, 5, 1]] = 3.0
+    return lg
+
+
+@pytest.mark.parametrize("n_tok", [1, 3, 8])
+@pytest.mark.parametrize("kind", ["rounded", "equal", "hot_ties"])
+def test_fused_layer_tied_scores(H, O, layer, n_tok, kind):
+    """Tied router scores: the fused and staged paths select, order and
+    weight as the oracle does (equal scores go to the smaller expert)."""
+    rng = np.random.default_rng(500 + n_tok)
+    x = rng.standard_normal((n_tok, K)).astype(np.float32)
+    logits = tied_logits(rng, n_tok, kind)
+    say(f"tied scores: {n_tok} tokens, {kind}")
+    a = run_layer(H, layer, x, logits, True)
+    b = run_layer(H, layer, x, logits, False)
+    dense = layer.host_dense()
+    weights = dict(layer.host_experts(np.append(np.ravel(a[1]), 0)), **dense, n_expert=E, mid_dim=F)
+    want, wsel, ww = O.moe_layer_q8k(weights, x, logits=logits)
+    assert np.array_equal(a[1], wsel), (a[1], wsel)
+    assert np.array_equal(b[1], wsel)
+    if kind == "hot_ties":
+        assert np.array_equal(np.sort(a[1], axis=1), np.tile([1, 5, 31, 63, 64, 70, 130, 200], (n_tok, 1)))
+    assert_bitexact(a[2], ww, "weights")
+    assert_bitexact(b[2], ww, "staged weights")
+    assert_bitexact(a[0], want, f"out ({n_tok} tokens, {kind})")
+    assert_bitexact(b[0], want, f"staged out ({n_tok} tokens, {kind})")
+
+
 def test_fused_routed_batch_mapped(H, O, layer):
     """routed_moe_batch_mapped for 5 tokens at the full shape, with an invalid
     id and an expert repeated inside one token: out and per-pair mid equal
