@@ -130,6 +130,7 @@ def ref_lib():
         L = C.CDLL(path)
         sig = {
             "sf37_f16_to_f32": (C.c_float, [C.c_uint16]),
+            "sf37_bf16_to_f32": (C.c_float, [C.c_uint16]),
             "sf37_q3_asym_block_decode": (None, [_u8, _f]),
             "sf37_q2_asym_block_decode": (None, [_u8, _f]),
             "sf37_q8_0_block_decode": (None, [_u8, _f]),

@@ -16,6 +16,13 @@
 * orc_swiglu_mid against the reference's sf37_swiglu (sf37_ops.c:30-42)
   followed by the routing-weight product (sf37.c:2175-2177), bit for bit,
   clamps 0, 7 and 16.
+* orc_rms_norm_weight1_bf16 against the engine's own sequence (sf37.c:2243-
+  2244: the reference's sf37_bf16_to_f32 widening, then its
+  sf37_rms_norm_weight1), bit for bit, and the reference KAT with bf16
+  weights; plausible mistakes are shown to change the bits.
+* orc_f32_matvec_double (the F32 router, sf37.c:1970-1976) against a float64
+  matrix product (within 1 ulp), exact integer sums, and rows on which a
+  float accumulator or a transposed operand fails.
 """
 import ctypes as C
 
@@ -194,3 +201,180 @@ def test_swiglu_mid_matches_reference_swiglu_times_weight(orc, clamp):
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
     if clamp:
         assert (np.abs(g) > clamp).any() and (np.abs(u) > clamp).any()
+
+
+# --------------------------------------------------------------------------
+# RMSNorm(w + 1) with bf16 weights, and the F32 router GEMV (binary64 sums)
+# --------------------------------------------------------------------------
+
+def bf16_bits(a):
+    """bf16 codes of float32 values by truncation (any bf16 code is a valid weight)."""
+    return (np.asarray(a, np.float32).view(np.uint32) >> 16).astype(np.uint16)
+
+
+def ref_widened_rms(ref, x, wb, eps):
+    """The engine's sequence (sf37.c:2243-2244): tensor_bf16_to_f32 of the
+    norm weight through the reference's sf37_bf16_to_f32 (sf37_quant.c:32-37),
+    then sf37_rms_norm_weight1 (sf37_ops.c:22-28), both compiled from the
+    reference's sources."""
+    wf = np.array([ref.sf37_bf16_to_f32(int(v)) for v in wb], np.float32)
+    out = np.zeros(x.size, np.float32)
+    ref.sf37_rms_norm_weight1(fp(out), fp(x), fp(wf), x.size, eps)
+    return out, wf
+
+
+def rms_bf16_weights(seed, n):
+    """bf16 norm weights with ties (repeated codes), negatives, -1 (w + 1 = 0),
+    zeros of both signs, values that round when 1 is added, and tiny and huge
+    magnitudes."""
+    r = np.random.default_rng(seed)
+    w = (r.standard_normal(n) * 0.3).astype(np.float32)
+    w[::7] = w[min(3, n - 1)]          # ties
+    w[1::11] = -1.0                    # (w + 1) == 0
+    w[2::13] = 0.0
+    w[4::17] = -0.0
+    w[5::19] = 2.0 ** -30              # vanishes in w + 1
+    w[6::23] = 384.0
+    w[8::29] = -3.0e-3
+    return bf16_bits(w)
+
+
+def test_rms_norm_bf16_matches_reference_sequence(orc):
+    """orc_rms_norm_weight1_bf16 == reference widen + sf37_rms_norm_weight1,
+    bit for bit, at the engine's width 4096 and at odd widths; the inputs are
+    chosen so that a float sum of squares, another eps, a dropped +1, a
+    weight read as f16 or the scale applied as x * ((w + 1) * scale) give
+    other bits (each checked to differ, so the comparison has the power to
+    see them)."""
+    ref = orc.ref_lib()
+    if ref is None:
+        pytest.skip("reference build (oracle/_ref) absent")
+    L = orc.lib()
+    u16 = C.POINTER(C.c_uint16)
+    caught = set()
+    names = ("float sum of squares", "eps 1e-6", "no +1", "weight read as f16", "reassociated product")
+    for seed, n, xs, big in [(501, 4096, 3.0, True), (502, 4096, 1e-3, False), (503, 70, 50.0, False),
+                             (504, 1, 2.0, False), (505, 1280, 1.0, True), (506, 4096, 1.0, False)]:
+        r = np.random.default_rng(seed)
+        x = (r.standard_normal(n) * xs).astype(np.float32)
+        if big:
+            x[:4] = [1e4, -1e4, 3e-3, 0.0]      # large terms: a float sum of squares drifts
+        wb = rms_bf16_weights(seed, n)
+        for eps in (1e-5, 1e-6):
+            want, wf = ref_widened_rms(ref, x, wb, eps)
+            got = np.zeros(n, np.float32)
+            L.orc_rms_norm_weight1_bf16(fp(got), fp(x), wb.ctypes.data_as(u16), n, eps)
+            assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (seed, n, eps)
+            # the f32 variant on the widened weights gives the same bits
+            got32 = np.zeros(n, np.float32)
+            L.orc_rms_norm_weight1(fp(got32), fp(x), fp(wf), n, eps)
+            assert np.array_equal(got32.view(np.uint32), want.view(np.uint32))
+        # power of the comparison: plausible mistakes give other bits
+        want, wf = ref_widened_rms(ref, x, wb, 1e-5)
+        x64 = x.astype(np.float64)
+        ss32 = np.float32(0)
+        for v in x:                                     # float accumulator
+            ss32 = np.float32(ss32 + v * v)
+        mean64 = np.float32((x64 * x64).sum() / n)
+        good = np.float32(1) / np.sqrt(mean64 + np.float32(1e-5))
+        wp1 = wf + np.float32(1)
+        with np.errstate(over="ignore", invalid="ignore"):
+            mutants = {
+                "float sum of squares": (x * (np.float32(1) / np.sqrt(ss32 / np.float32(n) + np.float32(1e-5)))) * wp1,
+                "eps 1e-6": (x * (np.float32(1) / np.sqrt(mean64 + np.float32(1e-6)))) * wp1,
+                "no +1": (x * good) * wf,
+                "weight read as f16": (x * good) * (wb.view(np.float16).astype(np.float32) + np.float32(1)),
+                "reassociated product": x * (good * wp1),
+            }
+        assert np.array_equal(((x * good) * wp1).view(np.uint32), want.view(np.uint32))
+        for name, bad in mutants.items():
+            if not np.array_equal(bad.view(np.uint32), want.view(np.uint32)):
+                caught.add(name)
+    assert caught == set(names), set(names) - caught
+
+
+def test_rms_norm_bf16_reference_kat(orc):
+    """tests/test_sf37_ops.c:89-97 with the weights stored as bf16 (all four
+    are exact in bf16): within 1e-6 of the closed form, and equal to the f32
+    variant's bits."""
+    L = orc.lib()
+    x = np.array([1.0, -2.0, 3.0, -4.0], np.float32)
+    w = np.array([0.0, 0.5, -0.25, 1.0], np.float32)
+    wb = bf16_bits(w)
+    assert np.array_equal((wb.astype(np.uint32) << 16).view(np.float32), w)
+    out = np.zeros(4, np.float32)
+    L.orc_rms_norm_weight1_bf16(fp(out), fp(x), wb.ctypes.data_as(C.POINTER(C.c_uint16)), 4, 1e-5)
+    ss = float(np.sum(x.astype(np.float64) ** 2))
+    s = np.float32(1.0) / np.sqrt(np.float32(ss / 4.0) + np.float32(1e-5))
+    assert np.all(np.abs(out - x * s * (w + np.float32(1))) <= 1e-6)
+    out32 = np.zeros(4, np.float32)
+    L.orc_rms_norm_weight1(fp(out32), fp(x), fp(w), 4, 1e-5)
+    assert np.array_equal(out.view(np.uint32), out32.view(np.uint32))
+
+
+def f32_ulp_diff(a, b):
+    """Distance in units in the last place between float32 arrays (same sign)."""
+    ia = a.view(np.int32).astype(np.int64)
+    ib = b.view(np.int32).astype(np.int64)
+    ia = np.where(ia < 0, -(ia & 0x7fffffff), ia)
+    ib = np.where(ib < 0, -(ib & 0x7fffffff), ib)
+    return np.abs(ia - ib)
+
+
+def oracle_router(L, W, x):
+    E, D = W.shape
+    out = np.zeros((x.shape[0], E), np.float32)
+    Wc = np.ascontiguousarray(W)
+    for t in range(x.shape[0]):
+        L.orc_f32_matvec_double(fp(out[t]), fp(Wc), D, E, fp(np.ascontiguousarray(x[t])))
+    return out
+
+
+def test_f32_router_matvec_double_vs_float64_matmul(orc):
+    """orc_f32_matvec_double (the static F32 router, sf37.c:1970-1976:
+    binary64 products and sums, one rounding to float at the end) against
+    numpy's float64 matrix product rounded to float32: 288 x 4096 router,
+    16 token rows, within 1 ulp (the two sum the same exact products in other
+    orders), >= 99 % identical; a transposed operand fails that check."""
+    L = orc.lib()
+    r = np.random.default_rng(601)
+    E, D, T = 288, 4096, 16
+    W = (r.standard_normal((E, D)) * 0.02).astype(np.float32)
+    x = r.standard_normal((T, D)).astype(np.float32)
+    got = oracle_router(L, W, x)
+    want = (x.astype(np.float64) @ W.T.astype(np.float64)).astype(np.float32)
+    d = f32_ulp_diff(got, want)
+    assert d.max() <= 1 and (d == 0).mean() >= 0.99, (d.max(), (d == 0).mean())
+    # exact sums: integer operands whose every partial sum is exact in binary64
+    Wi = r.integers(-64, 64, (E, D)).astype(np.float32)
+    xi = r.integers(-64, 64, (T, D)).astype(np.float32)
+    gi = oracle_router(L, Wi, xi)
+    assert np.array_equal(gi, (xi.astype(np.int64) @ Wi.T.astype(np.int64)).astype(np.float32))
+    # power: the same weights read transposed ([D][E] memory as [E][D]) miss
+    Wt = np.ascontiguousarray(W.T).reshape(E, D)
+    bad = oracle_router(L, Wt, x)
+    assert f32_ulp_diff(bad, want).max() > 1000
+
+
+def test_f32_router_matvec_double_accumulator(orc):
+    """The binary64 accumulator of sf37.c:1974 against cases a float
+    accumulator gets wrong: terms 2^30, 1, -2^30 sum to 1 in binary64 and to
+    0 in binary32, and a long alternating row whose float sum drifts."""
+    L = orc.lib()
+    D = 4096
+    W = np.zeros((3, D), np.float32)
+    W[0, :3] = [2.0 ** 30, 1.0, -(2.0 ** 30)]
+    W[1, :] = np.where(np.arange(D) % 2 == 0, np.float32(1e8), np.float32(-1e8))
+    W[1, 5] += np.float32(8.0)
+    W[2, :] = np.float32(0.1)
+    x = np.ones((1, D), np.float32)
+    got = oracle_router(L, W, x)[0]
+    assert got[0] == 1.0
+    want1 = np.float32(np.sum(W[1].astype(np.float64)))
+    assert got[1] == want1
+    want2 = np.float32(np.float64(np.float32(0.1)) * D)
+    assert f32_ulp_diff(got[2:3], np.array([want2], np.float32)).max() <= 1
+    f32_acc = np.float32(0)
+    for v in W[0]:
+        f32_acc = np.float32(f32_acc + v)
+    assert f32_acc != got[0]       # a float accumulator would fail the first row
