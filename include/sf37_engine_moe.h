@@ -15,6 +15,11 @@
  * Return: 1 on success, 0 on failure with a line "sf37: HIP decode|prefill
  * layer <il> failed at <step>" on stderr (CUDA_LAYER_CHECK, sf37.c:3299-3305,
  * and its prefill twin).
+ *
+ * Precondition: il >= SF37_FIRST_MOE_LAYER.  Layers 0-2 are dense: the
+ * engine runs their Q8_0 FFN instead (sf37.c:3376-3390, sf37.c:2245-2249),
+ * which is not part of this block; both calls refuse them (return 0 and a
+ * "dense layer" line on stderr) before any launch.
  */
 #ifndef SF37_ENGINE_MOE_H
 #define SF37_ENGINE_MOE_H
@@ -26,6 +31,8 @@
 #ifdef __cplusplus
 extern "C" {
 #endif
+
+#define SF37_FIRST_MOE_LAYER 3u   /* sf37.c:2245: il < 3 runs the dense FFN */
 
 /* One MoE layer's tensors as absolute offsets into the model map (the
  * engine's sf37_tensor abs_offset, sf37.c:1760-1782). */

@@ -269,6 +269,16 @@ sf37_hip_tensor *sf37_hip_tensor_view(const sf37_hip_tensor *base, uint64_t offs
 int sf37_hip_register_device_range(const void *model_map, uint64_t model_size,
                                    uint64_t map_offset, uint64_t bytes,
                                    const sf37_hip_tensor *device);
+/* Registry query (no reference counterpart; for tests and tools): -1 when no
+ * registered range covers map[offset, offset+bytes), 0 when a range the
+ * caller registered covers it, else the number of open GGUF handles holding
+ * the range the layer binder made for it (freed when that reaches 0). */
+int sf37_hip_model_range_holds(const void *model_map, uint64_t offset, uint64_t bytes);
+/* Requests for device memory the library has served so far (its scratch,
+ * counters, layer buffers, model-range copies, widened weights and tensor
+ * allocations), counted whether or not a buffer had to grow.  No reference
+ * counterpart; tests use it to show that an entry point allocates nothing. */
+uint64_t sf37_hip_device_memory_requests(void);
 
 /* Q8_K activations of n_rows rows (the reference's 268-byte block layout). */
 int sf37_hip_q8k_quantize(sf37_hip_tensor *out, const sf37_hip_tensor *x,
@@ -321,7 +331,8 @@ int sf37_hip_moe_layer(sf37_hip_tensor *out, sf37_hip_tensor *selected,
  * device array of 10 MiB per GPU (held until the process ends); a batch whose
  * scratch would not fit is refused with a message (288 experts x 4096 x 1280
  * at top-8 take 5 MiB at 16 tokens).  Results equal sf37_hip_moe_layer's bit
- * for bit.  Every call on a GPU uses that GPU's one array: calls that overlap
+ * for bit.  Every call on a GPU uses that GPU's one array, whose address is
+ * looked up on the first call with that device current: calls that overlap
  * on one GPU (other streams, other threads) race. */
 int sf37_hip_moe_layer_noalloc(sf37_hip_tensor *out, sf37_hip_tensor *selected,
                                sf37_hip_tensor *weights, const sf37_hip_moe_layer_weights *w,

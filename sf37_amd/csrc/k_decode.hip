@@ -775,6 +775,8 @@ constexpr uint32_t TILE_BYTES = 14080; // an item: 64 pairs of 220 bytes, contig
 constexpr uint32_t TILE_LOADS = 14;    // 16-byte loads per lane to move a tile (64 x 16 bytes each)
 constexpr uint32_t TILE_LDS = TILE_LOADS * 1024u;   // a wave's LDS tile
 static_assert(TILE_BYTES <= TILE_LDS, "tile fits its LDS slot");
+static_assert(TILE_LDS == 14336u, "lds_up_dma sizes a wave's tile as 14336 bytes");
+static_assert(64u * 55u * 4u <= TILE_BYTES, "a lane's pair (55 dwords at 220 * lane) lies inside the tile");
 
 // Byte B / the f16 at even byte B of the dword array w (B folds to a constant).
 __device__ __forceinline__ uint32_t w_byte(const uint32_t *w, int B) { return (w[B >> 2] >> (8 * (B & 3))) & 0xffu; }
@@ -1588,8 +1590,38 @@ struct dec_shape {
     bool up_wide;
     uint32_t n_rt, n_xq, n_tk, sel_threads, n_shup, sh_rs, up_waves, n_up, n_mid, n_dn, n_cb;
     size_t lds_up, lds_shup, lds_dn;
+    size_t lds_sel_launch, lds_up_launch;   // dynamic LDS given to the select and up launches
     const void *dn_kernel;
 };
+
+// The LDS side of a launch plan, from the shapes and the device's LDS limit
+// per workgroup alone (no device query): the routed up kernel's form and
+// waves, the shared gate/up rows per workgroup, and the dynamic LDS of the
+// select, up and down launches.  dec_plan and sf37k_decode_lds_check use it.
+void dec_plan_lds(const dec_params &p, size_t ml, dec_shape &d) {
+    const bool sh = (p.flags & SF37_DEC_SHARED) != 0;
+    const bool upsel = (p.flags & SF37_DEC_UPSEL) != 0;
+    d.sel_threads = p.T <= 8u ? 512u : 256u;
+    // routed up: block-pair DMA workgroups when the batch has a select
+    // launch and at least 4 waves' tiles fit beside the activations (up to
+    // 8 waves), else the row-pair loop
+    const uint32_t P = p.T * p.topk;
+    const size_t tb = tile_base(p.K, p.T, p.G, P);
+    const uint32_t fit = tb < ml ? (uint32_t)((ml - tb) / TILE_LDS) : 0u;
+    d.up_waves = fit < 8u ? fit : 8u;
+    d.up_wide = up_pairs(p.K) && !upsel && d.up_waves >= 4u;
+    d.lds_up = d.up_wide ? lds_up_dma(p.K, p.T, p.G, P, d.up_waves) : lds_up_meta(p.K, p.T, p.G, P);
+    // the select launch takes 4 shared rows per 512-thread workgroup up to 8
+    // tokens; above that 2 per 256-thread workgroup (the terms of 16 tokens
+    // x 4 rows would hold one workgroup per CU); the one-token up launch 4
+    // per 256-thread workgroup
+    d.sh_rs = upsel ? SH_RS_UPSEL : p.T > 8u ? SH_RS_UP : SH_RS_SEL;
+    d.lds_shup = lds_up_shared(p.K, p.T, d.sh_rs);
+    d.n_shup = sh ? p.F / d.sh_rs : 0u;                // shared gate/up workgroups (select or up launch)
+    d.lds_sel_launch = d.n_shup && d.lds_shup > lds_select_topk() ? d.lds_shup : lds_select_topk();
+    d.lds_up_launch = d.up_wide ? d.lds_up : (d.lds_up > d.lds_shup || !d.n_shup || !upsel ? d.lds_up : d.lds_shup);
+    d.lds_dn = sh ? (size_t)p.T * p.F + (size_t)p.T * (p.F / 32u) * 4u : 0u;
+}
 
 uint32_t device_cus() {
     static int cus = 0;
@@ -1663,32 +1695,13 @@ dec_shape dec_plan(const dec_params &p) {
     const uint32_t cus = device_cus();
     d.n_rt = (p.flags & (SF37_DEC_ROUTER | SF37_DEC_SELECT)) ? route_wgs(p.T, p.E) : 0u;
     d.n_xq = (p.T * nb + 3u) / 4u;
-    d.sel_threads = p.T <= 8u ? 512u : 256u;
+    dec_plan_lds(p, device_max_lds(), d);
     d.n_tk = (p.T + d.sel_threads / 64u - 1u) / (d.sel_threads / 64u);
-    // routed up: block-pair DMA workgroups when the batch has a select
-    // launch and at least 4 waves' tiles fit beside the activations (up to
-    // 8 waves), else the row-pair loop
-    const uint32_t P = p.T * p.topk;
-    const bool upsel = (p.flags & SF37_DEC_UPSEL) != 0;
-    const size_t tb = tile_base(p.K, p.T, p.G, P), ml = device_max_lds();
-    const uint32_t fit = tb < ml ? (uint32_t)((ml - tb) / 14336u) : 0u;
-    d.up_waves = fit < 8u ? fit : 8u;
-    d.up_wide = up_pairs(p.K) && !upsel && d.up_waves >= 4u;
-    d.lds_up = d.up_wide ? lds_up_dma(p.K, p.T, p.G, P, d.up_waves) : lds_up_meta(p.K, p.T, p.G, P);
-    // the select launch takes 4 shared rows per 512-thread workgroup up to 8
-    // tokens; above that 2 per 256-thread workgroup (the terms of 16 tokens
-    // x 4 rows would hold one workgroup per CU); the one-token up launch 4
-    // per 256-thread workgroup
-    d.sh_rs = (p.flags & SF37_DEC_UPSEL) ? SH_RS_UPSEL : p.T > 8u ? SH_RS_UP : SH_RS_SEL;
-    d.lds_shup = lds_up_shared(p.K, p.T, d.sh_rs);
-    d.n_shup = sh ? p.F / d.sh_rs : 0u;                // shared gate/up workgroups (select or up launch)
     // persistent kernels: exactly as many workgroups as can be resident
-    const size_t up_lds = d.lds_up > d.lds_shup || !d.n_shup || !(p.flags & SF37_DEC_UPSEL) ? d.lds_up : d.lds_shup;
     const uint32_t up_res = d.up_wide ? resident_wgs((const void *)dec_up_dma_kernel, 64 * (int)d.up_waves, d.lds_up)
-                                      : resident_wgs((const void *)dec_up_kernel, 256, up_lds);
+                                      : resident_wgs((const void *)dec_up_kernel, 256, d.lds_up_launch);
     d.n_up = (p.up_wgs && p.up_wgs < up_res ? p.up_wgs : up_res) * cus;
     d.n_mid = (p.T * p.topk * (p.F / SF37_QK) + (sh ? (p.T * (p.F / 32u) + 1u) / 2u : 0u) + 3u) / 4u;
-    d.lds_dn = sh ? (size_t)p.T * p.F + (size_t)p.T * (p.F / 32u) * 4u : 0u;
     d.dn_kernel = down_kernel_for(p);
     const uint32_t dn_res = resident_wgs(d.dn_kernel, 256, d.lds_dn);
     d.n_dn = (p.dn_wgs && p.dn_wgs < dn_res ? p.dn_wgs : dn_res) * cus;
@@ -1735,18 +1748,79 @@ extern "C" void *sf37k_noalloc_scratch(void) {
     return g_noalloc_ptr[dev];
 }
 
-extern "C" int sf37k_decode_supported(uint32_t T, uint32_t topk, uint32_t E, uint32_t K, uint32_t F, int shared) {
+namespace {
+int decode_supported_at(uint32_t T, uint32_t topk, uint32_t E, uint32_t K, uint32_t F, int shared, size_t ml) {
     if (T == 0 || T > DEC_MAX_TOK || topk == 0 || K % SF37_QK || F % SF37_QK || K / SF37_QK > 16u ||
         F / SF37_QK > DN_MAX_NB)
         return 0;
     // shared down: the shared mid fits in the x area, a lane's slice in registers
     if (shared && shd_bps(F / 32u, shd_slices(T)) > SHD_MAX_BPS) return 0;
     const uint32_t P = T * topk, G = P < E ? P : E;
-    if (lds_up_meta(K, T, G, P) > device_max_lds()) return 0;
-    if (shared && (lds_up_shared(K, T, SH_RS_UP) > device_max_lds() || lds_up_shared(K, T, SH_RS_SEL) > device_max_lds() ||
-                   lds_up_shared(K, T, SH_RS_UPSEL) > device_max_lds()))
+    if (lds_up_meta(K, T, G, P) > ml) return 0;
+    if (shared && (lds_up_shared(K, T, SH_RS_UP) > ml || lds_up_shared(K, T, SH_RS_SEL) > ml ||
+                   lds_up_shared(K, T, SH_RS_UPSEL) > ml))
         return 0;
     return 1;
+}
+}  // namespace
+
+extern "C" int sf37k_decode_supported(uint32_t T, uint32_t topk, uint32_t E, uint32_t K, uint32_t F, int shared) {
+    return decode_supported_at(T, topk, E, K, F, shared, device_max_lds());
+}
+
+// Host-side check of the LDS direct loads of the decode launches for one
+// shape and flag set at a per-workgroup LDS limit (no device needed).  A
+// global_load_lds writes its 64 lanes' bytes at M0 + 16 * lane whatever the
+// source, so every M0 a kernel forms must leave that whole span inside the
+// region it targets, and every region must lie inside the LDS its launch is
+// given.  ext[0..5]: end of the last routed up tile's loads, LDS of the up
+// launch, end of the shared gate/up tile copies and terms, LDS of the launch
+// running them, end of the up kernel's activation area, start of its tiles.
+// Returns 0 when everything fits, -1 for a shape the library refuses before
+// any launch at that limit, else the number of the first failed check.
+extern "C" int sf37k_decode_lds_check(uint32_t T, uint32_t topk, uint32_t E, uint32_t K, uint32_t F,
+                                      uint32_t flags, uint32_t max_lds, uint64_t *ext) {
+    for (int i = 0; i < 6; i++) ext[i] = 0;
+    if (!decode_supported_at(T, topk, E, K, F, (flags & SF37_DEC_SHARED) != 0, max_lds)) return -1;
+    dec_params p = {};
+    p.T = T;
+    p.topk = topk;
+    p.E = E;
+    p.K = K;
+    p.F = F;
+    p.flags = flags;
+    const uint32_t P = T * topk;
+    p.G = P < E ? P : E;
+    dec_shape d = {};
+    dec_plan_lds(p, max_lds, d);
+    int fail = 0;
+    auto check = [&](bool ok, int code) {
+        if (!ok && !fail) fail = code;
+    };
+    if (d.up_wide) {
+        // wave w's tile at tile_base + w * TILE_LDS; load i of the fill writes
+        // [1024 i, 1024 i + 1024) of it (up_items_pairs)
+        ext[4] = lds_up_meta(K, T, p.G, P);
+        ext[5] = tile_base(K, T, p.G, P);
+        ext[0] = ext[5] + (uint64_t)(d.up_waves - 1u) * TILE_LDS + 1024u * (TILE_LOADS - 1u) + 64u * 16u;
+        ext[1] = d.lds_up_launch;
+        check(ext[4] <= ext[5], 1);
+        check(ext[0] <= ext[1], 2);
+        check(ext[1] <= max_lds && 64u * d.up_waves <= 512u, 3);
+    }
+    if (d.n_shup) {
+        // shared_gate_up: gate tile copy at 0, up tile copy at wbuf (lds_copy
+        // writes 16 * ceil((off + n) / 16) bytes, off <= 15), terms after 2 wbuf
+        const uint32_t tbytes = up_shared_tile(K, d.sh_rs), wbuf = tile_buf(tbytes);
+        const uint64_t span = 16ull * ((15ull + tbytes + 15ull) / 16ull);
+        const uint64_t terms_end = 2ull * wbuf + (uint64_t)T * 2u * d.sh_rs * sh_red_stride(K) * 4u;
+        ext[2] = wbuf + span > terms_end ? wbuf + span : terms_end;
+        ext[3] = (flags & SF37_DEC_UPSEL) ? d.lds_up_launch : d.lds_sel_launch;
+        check(span <= wbuf, 4);
+        check(terms_end <= ext[3], 5);
+        check(ext[3] <= max_lds, 6);
+    }
+    return fail;
 }
 
 extern "C" int sf37k_decode_route(const sf37_dec_params *pp, sf37_stream_t s) {
@@ -1757,7 +1831,7 @@ extern "C" int sf37k_decode_route(const sf37_dec_params *pp, sf37_stream_t s) {
 
 extern "C" int sf37k_decode_select(const sf37_dec_params *pp, sf37_stream_t s) {
     const dec_shape d = dec_plan(*pp);
-    const size_t lds = d.n_shup && d.lds_shup > lds_select_topk() ? d.lds_shup : lds_select_topk();
+    const size_t lds = d.lds_sel_launch;
     const int err = opt_in_lds((const void *)dec_select_kernel, lds);
     if (err) return err;
     hipLaunchKernelGGL(dec_select_kernel, dim3(d.n_tk + d.n_shup), dim3(d.sel_threads), lds, (hipStream_t)s, *pp,
@@ -1775,7 +1849,7 @@ extern "C" int sf37k_decode_up(const sf37_dec_params *pp, sf37_stream_t s) {
     }
     const bool upsel = (pp->flags & SF37_DEC_UPSEL) != 0u;
     const uint32_t n_sh = upsel ? d.n_shup : 0u;
-    const size_t lds = d.lds_up > d.lds_shup || !n_sh ? d.lds_up : d.lds_shup;
+    const size_t lds = d.lds_up_launch;
     const int err = opt_in_lds((const void *)dec_up_kernel, lds);
     if (err) return err;
     sf37_dec_params p = *pp;

@@ -53,6 +53,11 @@ constexpr uint32_t PF_GU_R = pf_cfg<true>::ROWS;    // 128
 constexpr uint32_t PF_DN_R = pf_cfg<false>::ROWS;   // 128
 constexpr uint32_t PF_CD_ROWS = 8;                  // table rows of LDS per buffer (5 used)
 constexpr uint32_t PF_TAB = 8;          // floats per (row, block) table entry: C0..C3, d
+// pf_expert table loads (dword): one row of PF_T floats per load, at row
+// index wave (8 waves, wave <= 7) or max(wave, 4) (4 waves).
+static_assert(PF_T * 4u == 256u, "a table load (64 dwords) writes exactly one row");
+static_assert(pf_cfg<true>::NW <= PF_CD_ROWS && pf_cfg<false>::NW <= PF_CD_ROWS && 4u < PF_CD_ROWS,
+              "pf_expert table rows stay in their buffer");
 // LDS layout of one activation block: 4 groups of 32 tile slots; in a group
 // slot t (0..31) starts at PF_RS * (t % 16) + 512 * (t / 16), so one 64-lane
 // load fills slots t and t + 16 (512 contiguous bytes each) and 16
@@ -60,6 +65,19 @@ constexpr uint32_t PF_TAB = 8;          // floats per (row, block) table entry: 
 constexpr uint32_t PF_RS = 2u * SF37_QK * 2u + 16u;  // 1040
 constexpr uint32_t PF_GRP = 16u * PF_RS;             // bytes of 32 slots
 constexpr uint32_t PF_ACT_BUF = PF_TB * PF_GRP;      // bytes of one LDS activation block
+
+// Extents of the LDS direct loads.  A global_load_lds writes its 64 lanes'
+// bytes at M0 + 16 * lane (dwordx4) or M0 + 4 * lane (dword) whatever the
+// source address, so every M0 a kernel forms must leave a whole 64-lane span
+// inside the buffer it targets.
+constexpr uint32_t DMA16_SPAN = 64u * 16u;
+constexpr uint32_t DMA4_SPAN = 64u * 4u;
+// pf_expert activation codes: M0 = buffer + gi * PF_GRP + t * PF_RS with slot
+// group gi <= PF_TB - 1 (8 waves: wave >> 2; 4 waves: k < 2) and t = 4 * wq +
+// (jj & 3) <= 15; lanes 32..63 fill slot t + 16, 512 bytes on.
+static_assert((PF_TB - 1u) * PF_GRP + 15u * PF_RS + DMA16_SPAN <= PF_ACT_BUF, "pf_expert code loads stay in their buffer");
+static_assert(DMA16_SPAN == 2u * 512u && 512u == 2u * SF37_QK, "one load = slots t and t + 16, 512 bytes each");
+static_assert(PF_RS >= 512u, "a slot row holds a block's 256 fp16 codes");
 
 // ---------------------------------------------------------------------------
 // Pair layouts.  Lane half kh of an MFMA holds 32 codes of every 64-group
@@ -669,6 +687,12 @@ constexpr uint32_t SH_TB = SH_T / 32u;         // 32-token blocks per tile
 constexpr uint32_t SH_CB = 4;                  // Q8_0 blocks per K chunk
 constexpr uint32_t SH_RS = SH_CB * 64u + 16u;  // LDS bytes per token row of a chunk (+16: banks)
 constexpr uint32_t SH_BUF = SH_T * SH_RS;
+// sh_gemm direct loads (dword): token row t = 16 * wave + j (4 waves, j < 16)
+// of a chunk buffer, one 256-byte row (SH_CB blocks x 32 fp16 codes) each;
+// activation scales: row `wave` of SH_T floats.
+static_assert(SH_CB * 64u == DMA4_SPAN, "a code load writes exactly one chunk row");
+static_assert(16u * 3u + 15u < SH_T && (SH_T - 1u) * SH_RS + DMA4_SPAN <= SH_BUF, "sh_gemm code loads stay in their buffer");
+static_assert(SH_T * 4u == DMA4_SPAN && 4u <= SH_CB, "sh_gemm scale rows stay in their buffer");
 
 __host__ __device__ constexpr uint32_t sh_pos(uint32_t k) {   // code index -> position in a block
     return ((k >> 3) & 1u) * 16u + (k >> 4) * 8u + (k & 7u);

@@ -53,9 +53,18 @@ static int hip_matmul_dense_mapped(sf37_hip_tensor *out, const sf37_engine_moe_l
         }                                                                                    \
     } while (0)
 
+/* Layers 0-2 are dense (sf37.c:3376-3390 run their Q8_0 FFN instead); they
+ * have no router or expert tensors, so the MoE block refuses them. */
+static int moe_layer_ok(const sf37_engine_moe_layer *l, const char *mode) {
+    if (l->il >= SF37_FIRST_MOE_LAYER) return 1;
+    fprintf(stderr, "sf37: HIP %s layer %u is a dense layer (MoE layers start at %u)\n", mode, l->il,
+            SF37_FIRST_MOE_LAYER);
+    return 0;
+}
+
 int sf37_engine_moe_decode(const sf37_engine_moe_layer *l, sf37_engine_moe_bufs *s) {
     static const char mode[] = "decode";
-    if (!l || !s) return 0;
+    if (!l || !s || !moe_layer_ok(l, mode)) return 0;
     const uint32_t il = l->il;
     HIP_LAYER_CHECK(sf37_hip_begin_layer(il), "begin layer");
 #ifdef SF37_USE_HIP
@@ -89,7 +98,7 @@ int sf37_engine_moe_decode(const sf37_engine_moe_layer *l, sf37_engine_moe_bufs 
 
 int sf37_engine_moe_prefill(const sf37_engine_moe_layer *l, sf37_engine_moe_bufs *p, uint32_t n_tok) {
     static const char mode[] = "prefill";
-    if (!l || !p || n_tok == 0) return 0;
+    if (!l || !p || n_tok == 0 || !moe_layer_ok(l, mode)) return 0;
     const uint32_t il = l->il;
     const uint64_t n = (uint64_t)n_tok;
     HIP_LAYER_CHECK(sf37_hip_begin_layer(il), "begin layer");

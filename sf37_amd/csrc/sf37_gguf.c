@@ -26,7 +26,7 @@
 #include "../../include/sf37_hip.h"
 
 sf37_hip_tensor *sf37i_map_tensor(const void *model_map, uint64_t model_size, uint64_t offset, uint64_t bytes,
-                                  const char *label, int *created);
+                                  const char *label, int *held, uint64_t *range_off, uint64_t *range_bytes);
 void sf37i_drop_range(const void *model_map, uint64_t offset, uint64_t bytes);
 void sf37i_drop_map(const void *model_map);
 
@@ -50,7 +50,7 @@ struct sf37_hip_gguf {
     gg_tensor *t;
     sf37_hip_tensor **owned;   /* handles given out by the binder (8 per bound layer) */
     uint32_t n_owned, cap_owned;
-    uint64_t (*made)[2];       /* registered ranges the binder created: offset, bytes */
+    uint64_t (*made)[2];       /* holds this handle has on binder-made ranges: offset, bytes */
     uint32_t n_made, cap_made;
 };
 
@@ -128,7 +128,8 @@ static void gg_free(sf37_hip_gguf *g) {
     if (!g) return;
     for (uint32_t i = 0; i < g->n_owned; i++) sf37_hip_tensor_free(g->owned[i]);
     free(g->owned);
-    /* a caller's map outlives the handle: drop only the ranges bound here */
+    /* a caller's map outlives the handle: give back this handle's holds (a
+     * range another open handle still holds stays) */
     if (g->fd < 0)
         for (uint32_t i = 0; i < g->n_made; i++) sf37i_drop_range(g->map, g->made[i][0], g->made[i][1]);
     free(g->made);
@@ -296,24 +297,25 @@ static sf37_hip_tensor *gg_keep(sf37_hip_gguf *g, sf37_hip_tensor *t) {
 }
 
 /* Device-resident tensor over a registered range: sf37_hip_evict_model_cache
- * leaves it alone; the range lives until the handle closes. */
+ * leaves it alone; the range lives while some handle holds it. */
 static sf37_hip_tensor *gg_resident(sf37_hip_gguf *g, const gg_tensor *t) {
-    int created = 0;
-    sf37_hip_tensor *d = sf37i_map_tensor(g->map, g->size, t->offset, t->bytes, t->name, &created);
-    if (d && created) {
+    int held = 0;
+    uint64_t roff = 0, rbytes = 0;
+    sf37_hip_tensor *d = sf37i_map_tensor(g->map, g->size, t->offset, t->bytes, t->name, &held, &roff, &rbytes);
+    if (d && held) {
         if (g->n_made == g->cap_made) {
             const uint32_t cap = g->cap_made ? 2u * g->cap_made : 64u;
             uint64_t(*n)[2] = (uint64_t(*)[2])realloc(g->made, cap * sizeof(*n));
             if (!n) {
                 sf37_hip_tensor_free(d);
-                sf37i_drop_range(g->map, t->offset, t->bytes);
+                sf37i_drop_range(g->map, roff, rbytes);
                 return NULL;
             }
             g->made = n;
             g->cap_made = cap;
         }
-        g->made[g->n_made][0] = t->offset;
-        g->made[g->n_made][1] = t->bytes;
+        g->made[g->n_made][0] = roff;
+        g->made[g->n_made][1] = rbytes;
         g->n_made++;
     }
     return gg_keep(g, d);

@@ -67,6 +67,7 @@ typedef struct {
     void *dev;
     int owned;   /* allocated here (freed on evict/cleanup) */
     int cache;   /* on-demand cache entry (dropped by evict) */
+    uint32_t holds;   /* GGUF binder handles holding it (0: registered by the caller) */
 } map_range;
 
 static map_range *g_ranges;
@@ -186,9 +187,17 @@ static int ensure_init(void) {
 
 static uint64_t align256(uint64_t v) { return (v + 255u) & ~(uint64_t)255u; }
 
+/* Requests for device memory the library serves (scratch, counters, layer
+ * buffers, range copies, widened weights, tensors), whether or not a buffer
+ * had to grow: the no-alloc entry point makes none. */
+static uint64_t g_mem_requests;
+
+uint64_t sf37_hip_device_memory_requests(void) { return g_mem_requests; }
+
 /* One reusable scratch area (the reference's cuda_tmp_alloc,
  * sf37_cuda.cu:1579-1592).  Growing it waits for queued work first. */
 static char *scratch_get(uint64_t bytes, const char *what) {
+    g_mem_requests++;
     if (bytes <= g_scratch_bytes && g_scratch) return (char *)g_scratch;
     if (g_scratch) {
         if (!hip_ok(hipStreamSynchronize(g_stream), "scratch sync")) return NULL;
@@ -378,6 +387,7 @@ static sf37_hip_tensor *tensor_new(void *ptr, uint64_t bytes, int owned) {
 }
 
 sf37_hip_tensor *sf37_hip_tensor_alloc(uint64_t bytes) {
+    g_mem_requests++;
     if (!ensure_init()) return NULL;
     void *p = NULL;
     if (!hip_ok(hipMalloc(&p, bytes + SF37_PAD), "tensor alloc")) return NULL;
@@ -387,6 +397,7 @@ sf37_hip_tensor *sf37_hip_tensor_alloc(uint64_t bytes) {
 }
 
 sf37_hip_tensor *sf37_hip_tensor_alloc_managed(uint64_t bytes) {
+    g_mem_requests++;
     if (!ensure_init()) return NULL;
     void *p = NULL;
     if (!hip_ok(hipMallocManaged(&p, bytes + SF37_PAD, hipMemAttachGlobal), "managed tensor alloc"))
@@ -464,12 +475,13 @@ static int range_push(const uint8_t *map, uint64_t off, uint64_t bytes, void *de
         g_ranges = n;
         g_cap_ranges = cap;
     }
-    map_range r = {map, off, bytes, dev, owned, cache};
+    map_range r = {map, off, bytes, dev, owned, cache, 0};
     g_ranges[g_nranges++] = r;
     return 1;
 }
 
 static int upload_range(const uint8_t *map, uint64_t off, uint64_t bytes, int cache, const char *label) {
+    g_mem_requests++;
     void *dev = NULL;
     char what[160];
     snprintf(what, sizeof(what), "model range upload (%s)", label ? label : "range");
@@ -513,33 +525,58 @@ void sf37i_drop_map(const void *model_map) {
     g_nranges = w;
 }
 
+void sf37i_drop_range(const void *model_map, uint64_t offset, uint64_t bytes);
+
 /* A non-owning tensor over a device copy of map[offset, offset+bytes) that
  * sf37_hip_evict_model_cache does not free, for the GGUF layer binder
  * (sf37_gguf.c): a registered (non-cache) range that covers it, else a new
- * registered range made here (*created = 1), which the binder drops with
- * sf37i_drop_range when its handle closes. */
+ * registered range made here.  Ranges made here are held by the binder
+ * handles that use them: *held = 1 and *range_off / *range_bytes name the
+ * range when the caller took a hold (a new range, or one another handle made
+ * and still holds), which it gives back with sf37i_drop_range when its handle
+ * closes; the range is freed when the last hold goes.  Ranges the caller
+ * registered (set_model_map_range/_spans, register_device_range) are used
+ * without a hold (*held = 0) and stay until evicted or cleaned up. */
 sf37_hip_tensor *sf37i_map_tensor(const void *model_map, uint64_t model_size, uint64_t offset, uint64_t bytes,
-                                  const char *label, int *created) {
-    *created = 0;
+                                  const char *label, int *held, uint64_t *range_off, uint64_t *range_bytes) {
+    *held = 0;
     if (!model_map || !bytes || !mapped_range_ok(model_size, offset, bytes) || !ensure_init()) return NULL;
     const uint8_t *map = (const uint8_t *)model_map;
     for (size_t i = g_nranges; i-- > 0;) {
-        const map_range *r = &g_ranges[i];
-        if (!r->cache && r->map == map && offset >= r->off && bytes <= r->bytes && offset - r->off <= r->bytes - bytes)
-            return tensor_new((char *)r->dev + (offset - r->off), bytes, 0);
+        map_range *r = &g_ranges[i];
+        if (!r->cache && r->map == map && offset >= r->off && bytes <= r->bytes && offset - r->off <= r->bytes - bytes) {
+            sf37_hip_tensor *t = tensor_new((char *)r->dev + (offset - r->off), bytes, 0);
+            if (t && r->holds) {
+                r->holds++;
+                *held = 1;
+                *range_off = r->off;
+                *range_bytes = r->bytes;
+            }
+            return t;
+        }
     }
     if (!upload_range(map, offset, bytes, 0, label)) return NULL;
-    *created = 1;
-    return tensor_new(g_ranges[g_nranges - 1].dev, bytes, 0);
+    g_ranges[g_nranges - 1].holds = 1;
+    sf37_hip_tensor *t = tensor_new(g_ranges[g_nranges - 1].dev, bytes, 0);
+    if (!t) {
+        sf37i_drop_range(map, offset, bytes);
+        return NULL;
+    }
+    *held = 1;
+    *range_off = offset;
+    *range_bytes = bytes;
+    return t;
 }
 
-/* Drop the registered range made for map[offset, offset+bytes) by
- * sf37i_map_tensor (the newest one of exactly that extent). */
+/* Give back one hold on the binder-made range map[offset, offset+bytes)
+ * (the newest held range of exactly that extent); the device copy is freed
+ * with the last hold. */
 void sf37i_drop_range(const void *model_map, uint64_t offset, uint64_t bytes) {
     if (!g_init || !model_map) return;
     for (size_t i = g_nranges; i-- > 0;) {
         map_range *r = &g_ranges[i];
-        if (!r->cache && r->map == (const uint8_t *)model_map && r->off == offset && r->bytes == bytes) {
+        if (!r->cache && r->holds && r->map == (const uint8_t *)model_map && r->off == offset && r->bytes == bytes) {
+            if (--r->holds) return;
             (void)hipStreamSynchronize(g_stream);
             widen_forget(r->dev, r->bytes);
             if (r->owned && r->dev) (void)hipFree(r->dev);
@@ -548,6 +585,20 @@ void sf37i_drop_range(const void *model_map, uint64_t offset, uint64_t bytes) {
             return;
         }
     }
+}
+
+/* Holds on the registered range that covers map[offset, offset+bytes):
+ * -1 when no registered range covers it, 0 for a caller-registered range,
+ * else the number of binder handles holding it. */
+int sf37_hip_model_range_holds(const void *model_map, uint64_t offset, uint64_t bytes) {
+    if (!g_init || !model_map) return -1;
+    for (size_t i = g_nranges; i-- > 0;) {
+        const map_range *r = &g_ranges[i];
+        if (!r->cache && r->map == (const uint8_t *)model_map && offset >= r->off && bytes <= r->bytes &&
+            offset - r->off <= r->bytes - bytes)
+            return (int)r->holds;
+    }
+    return -1;
 }
 
 int sf37_hip_set_model_fd(int fd) {
@@ -775,6 +826,7 @@ int sf37_hip_matmul_f32_mapped(sf37_hip_tensor *out, const void *model_map, uint
  * those kernels read; a tensor's weights (which may change between calls)
  * are widened into scratch on every call. */
 static const float *bf16_resident_f32(const void *w, uint64_t n) {
+    g_mem_requests++;
     for (size_t i = 0; i < g_nwide; i++)
         if (g_wide[i].src == w && g_wide[i].n == n) return g_wide[i].f32;
     if (g_nwide == g_cap_wide) {
@@ -1160,6 +1212,7 @@ typedef struct {
 } dec_extra;
 
 static uint32_t *dec_counters(uint64_t words) {
+    g_mem_requests++;
     if (g_dec_cnt && words <= g_dec_cnt_words) return g_dec_cnt;
     if (g_dec_cnt) {
         if (!hip_ok(hipStreamSynchronize(g_stream), "decode counter sync")) return NULL;
@@ -1541,6 +1594,7 @@ static uint64_t g_block_buf_bytes[2];
 
 /* Layer buffer i of at least bytes (kept and grown across calls). */
 static void *layer_buf(int i, uint64_t bytes) {
+    g_mem_requests++;
     if (!g_layer_bufs[i] || g_layer_buf_bytes[i] < bytes) {
         if (g_layer_bufs[i]) sf37_hip_tensor_free(g_layer_bufs[i]);
         g_layer_bufs[i] = sf37_hip_tensor_alloc(bytes);
@@ -1827,7 +1881,11 @@ int sf37_hip_moe_layer_noalloc(sf37_hip_tensor *out, sf37_hip_tensor *selected, 
                         "F32 router (or injected logits) and a Q8_0 shared expert\n", SF37_DEC_MAX_TOK);
         return 0;
     }
+    /* the array's address on the current device, looked up on the first
+     * call there (sf37_hip_init looks it up for device 0) */
     char *base = (char *)sf37k_noalloc_scratch();
+    if (!base && hip_ok((hipError_t)sf37k_noalloc_scratch_init(), "no-alloc scratch address"))
+        base = (char *)sf37k_noalloc_scratch();
     if (!base) {
         fprintf(stderr, "sf37: HIP moe_layer_noalloc: the static scratch of this device has no address\n");
         return 0;

@@ -201,6 +201,8 @@ int sf37k_noalloc_scratch_init(void);
 void *sf37k_noalloc_scratch(void);
 /* 1 if the fused kernels take this shape (token count, dims, LDS). */
 int sf37k_decode_supported(uint32_t T, uint32_t topk, uint32_t E, uint32_t K, uint32_t F, int shared);
+int sf37k_decode_lds_check(uint32_t T, uint32_t topk, uint32_t E, uint32_t K, uint32_t F, uint32_t flags,
+                           uint32_t max_lds, uint64_t *ext);
 /* The launches, in this order on one stream. */
 int sf37k_decode_route(const sf37_dec_params *p, sf37_stream_t s);
 int sf37k_decode_select(const sf37_dec_params *p, sf37_stream_t s);   /* skipped with UPSEL */

@@ -98,6 +98,8 @@ _SIGS = {
     "sf37_hip_tensor_device_ptr": (vp, [T]),
     "sf37_hip_tensor_view": (T, [T, u64, u64]),
     "sf37_hip_register_device_range": (C.c_int, [vp, u64, u64, u64, T]),
+    "sf37_hip_model_range_holds": (C.c_int, [vp, u64, u64]),
+    "sf37_hip_device_memory_requests": (u64, []),
     "sf37_hip_q8k_quantize": (C.c_int, [T, T, u32, u32]),
     "sf37_hip_moe_dispatch": (C.c_int, [T, T, T, T, u32, u32]),
     "sf37_hip_moe_layer": (C.c_int, [T, T, T, C.POINTER(LayerWeights), T, T, u32]),

@@ -34,6 +34,22 @@ def test_engine_hook_library_exports_its_header():
     assert all(hasattr(L, s) for s in syms)
 
 
+def test_engine_hook_refuses_dense_layers(capfd):
+    """Layers 0-2 are dense (sf37.c:2245-2249): the MoE block refuses them
+    with a 'dense layer' line before any HIP call, so no GPU is needed."""
+    import ctypes as C
+    from test_gpu_engine import EngineBufs, EngineLayer
+    L = C.CDLL(os.path.join(ROOT, "sf37_amd", "libsf37_engine_moe.so"))
+    L.sf37_engine_moe_decode.restype = L.sf37_engine_moe_prefill.restype = C.c_int
+    bufs = EngineBufs()
+    for il in (0, 1, 2):
+        lay = EngineLayer(il=il, n_expert=288, topk=8, embd=4096, expert_ff=1280)
+        assert L.sf37_engine_moe_decode(C.byref(lay), C.byref(bufs)) == 0
+        assert L.sf37_engine_moe_prefill(C.byref(lay), C.byref(bufs), C.c_uint32(4)) == 0
+    err = capfd.readouterr().err
+    assert err.count("is a dense layer") == 6, err
+
+
 def test_reference_entry_points_are_mirrored():
     """Each hot-path entry of the reference interface (sf37_cuda.h) has a
     sf37_hip_ twin with the same name suffix."""

@@ -189,6 +189,60 @@ def test_gguf_all_layers_one_handle_and_evict(H, O, tmp_path):
         lay.free()
 
 
+def test_gguf_two_handles_share_ranges(H, O):
+    """Two from_map handles on one caller map bind the same layer: the device
+    ranges are shared and held twice (registry query, no kernel); closing one
+    handle leaves the other's ranges registered and its layer exact against
+    the oracle; closing the second frees them."""
+    from sf37_amd import configs
+    from sf37_amd.moe import SynthLayer, bf16_bits
+    L = H.lib()
+    il = 44
+    lay = SynthLayer(seed=321, n_expert=E, in_dim=D, mid_dim=F, topk=8, il=il)
+    norm = bf16_bits((np.random.default_rng(321).standard_normal(D) * 0.02).astype(np.float32))
+    tensors, w_host = layer_file(O, lay, il, T_F32, norm)
+    data, _, _ = gguf_bytes([("general.architecture", "str", "sf37")], tensors)
+    buf = np.frombuffer(data, np.uint8).copy()          # the caller's map; outlives both handles
+    ga = L.sf37_hip_gguf_from_map(buf.ctypes.data, buf.nbytes)
+    gb = L.sf37_hip_gguf_from_map(buf.ctypes.data, buf.nbytes)
+    assert ga and gb
+    names = ["moe.gate_proj.weight", "moe.down_proj.weight", "share_expert.up_proj.weight", "moe.gate.weight"]
+    ext = []
+    for n in names:
+        off, nb, ty, nd = C.c_uint64(), C.c_uint64(), C.c_uint32(), C.c_uint32()
+        dims = (C.c_uint64 * 4)()
+        assert L.sf37_hip_gguf_tensor(ga, f"model.layers.{il}.{n}".encode(), C.byref(off), C.byref(nb),
+                                      C.byref(ty), C.byref(nd), dims)
+        ext.append((off.value, nb.value))
+    closed_b = False
+    try:
+        wa, wb, pa, pb = H.LayerWeights(), H.LayerWeights(), C.c_uint64(), C.c_uint64()
+        assert L.sf37_hip_gguf_bind_moe_layer(ga, il, C.byref(wa), C.byref(pa))
+        assert [L.sf37_hip_model_range_holds(buf.ctypes.data, o, b) for o, b in ext] == [1] * 4
+        assert L.sf37_hip_gguf_bind_moe_layer(gb, il, C.byref(wb), C.byref(pb))
+        assert [L.sf37_hip_model_range_holds(buf.ctypes.data, o, b) for o, b in ext] == [2] * 4
+        H.synchronize()
+        L.sf37_hip_gguf_close(ga)
+        ga = None
+        assert [L.sf37_hip_model_range_holds(buf.ctypes.data, o, b) for o, b in ext] == [1] * 4
+        h0 = (np.random.default_rng(5).standard_normal((3, D)) * 2).astype(np.float32)
+        lg_host = configs.logits_for(4, 4401, 3, n_expert=E)
+        h = H.Tensor.from_array(h0)
+        H.check(L.sf37_hip_moe_block(h, None, None, None, C.byref(wb), buf.ctypes.data, buf.nbytes, pb.value, 1e-5,
+                                     H.Tensor.from_array(lg_host), 3), "moe_block on the handle left open")
+        want = oracle_block(O, w_host, norm, h0, lg_host, il, T_F32, "q8_0")
+        assert_bitexact(h.read(np.float32).reshape(3, D), want, "layer after the other handle closed")
+        L.sf37_hip_gguf_close(gb)
+        closed_b = True
+        assert [L.sf37_hip_model_range_holds(buf.ctypes.data, o, b) for o, b in ext] == [-1] * 4
+    finally:
+        if ga:
+            L.sf37_hip_gguf_close(ga)
+        if not closed_b:
+            L.sf37_hip_gguf_close(gb)
+        lay.free()
+
+
 def test_undersized_weights_refused(H):
     """A layer whose gate tensor is one byte short returns 0 with no launch."""
     from sf37_amd.moe import SynthLayer
