@@ -671,76 +671,47 @@ __device__ __forceinline__ void pf_body(const pf_params &p, const uint8_t *wrow,
 }
 
 // ---------------------------------------------------------------------------
-// Shared expert (Q8_0, every token) on the matrix cores.
+// Shared expert (Q8_0, every token) on the int8 matrix cores.
 //
 // Canonical order of sf37_ops.c:92-108: acc = acc + ((float)isum_b * ws_b) * xs_b
-// per 32-block in block order.  isum_b comes from two 32x32x16 MFMAs on
-// fp16 operands holding the int8 codes exactly (|partial sums| < 2^20), so
-// it is exact; the epilogue is those three float operations per block.
-// The weights are repacked per call into fp16 codes in MFMA lane order
-// (position 16*kh + 8*m + e of a block holds code 16*m + 8*kh + e) with the
-// scales as floats; the activations are quantised straight into the same
-// order (bit-exact with sf37_ops.c:57-90).
+// per 32-block in block order.  One v_mfma_i32_32x32x32_i8 per (32-block,
+// 32-token block) forms isum_b exactly from the Q8_0 weight codes, read in
+// place from the tensor (no repacked copy), and the Q8_0 activation codes.
+// Its accumulator starts at the bits of SH_MAGIC = 1.5 * 2^23, so the int32
+// result read as a float is F = SH_MAGIC + isum_b exactly (|isum_b| <=
+// 32 * 127 * 128 < 2^22), and fma(F, ws_b, -SH_MAGIC * ws_b) is the exact
+// isum_b * ws_b (the second term is exact: 2 * 11 significant bits) rounded
+// once, the CPU's (float)isum * w_scale.  The epilogue is then the CPU's
+// three float operations per output and block.
+//
+// Layouts.  Activations: Q8_0 codes of each token in natural order (int8,
+// nb * 32 bytes per token) and a float scale per (token, block), bit-exact
+// with sf37_ops.c:57-90.  A workgroup stages a chunk of SH_CB blocks of its
+// 64 tokens in LDS: token row r holds 2 * SH_CB 16-byte pieces (block jj,
+// half kh = piece 2 jj + kh), piece q stored at slot q ^ (r & 7), so the
+// 8 rows a read of 8 lanes touches land on distinct banks.  MFMA operands:
+// lane (row or column l % 32, half kh = l / 32) holds the 16 codes
+// 16 kh .. 16 kh + 15 of a block, for activations and weights alike.
 // ---------------------------------------------------------------------------
 constexpr uint32_t SH_T = 64;                  // tokens per tile
 constexpr uint32_t SH_TB = SH_T / 32u;         // 32-token blocks per tile
 constexpr uint32_t SH_CB = 4;                  // Q8_0 blocks per K chunk
-constexpr uint32_t SH_RS = SH_CB * 64u + 16u;  // LDS bytes per token row of a chunk (+16: banks)
-constexpr uint32_t SH_BUF = SH_T * SH_RS;
-// sh_gemm direct loads (dword): token row t = 16 * wave + j (4 waves, j < 16)
-// of a chunk buffer, one 256-byte row (SH_CB blocks x 32 fp16 codes) each;
-// activation scales: row `wave` of SH_T floats.
-static_assert(SH_CB * 64u == DMA4_SPAN, "a code load writes exactly one chunk row");
-static_assert(16u * 3u + 15u < SH_T && (SH_T - 1u) * SH_RS + DMA4_SPAN <= SH_BUF, "sh_gemm code loads stay in their buffer");
+constexpr uint32_t SH_RS = SH_CB * 32u;        // LDS bytes per token row of a chunk (int8 codes)
+constexpr uint32_t SH_BUF = SH_T * SH_RS;      // one chunk buffer
+constexpr float SH_MAGIC = 12582912.0f;        // 1.5 * 2^23
+constexpr int32_t SH_MAGIC_BITS = 0x4B400000;
+// sh_gemm direct loads (dwordx4): load L of a chunk fills token rows
+// 8 L .. 8 L + 7 (1 KiB, contiguous), L < SH_T / 8, two per wave (4 waves);
+// activation scales (dword): row `wave` of SH_T floats.
+static_assert(SH_RS == 128u && DMA16_SPAN == 8u * SH_RS && SH_T / 8u == 2u * 4u,
+              "sh_gemm code loads: 8 rows each, two per wave, inside the buffer");
+static_assert(7u * DMA16_SPAN + DMA16_SPAN <= SH_BUF, "sh_gemm code loads stay in their buffer");
 static_assert(SH_T * 4u == DMA4_SPAN && 4u <= SH_CB, "sh_gemm scale rows stay in their buffer");
 
-__host__ __device__ constexpr uint32_t sh_pos(uint32_t k) {   // code index -> position in a block
-    return ((k >> 3) & 1u) * 16u + (k >> 4) * 8u + (k & 7u);
-}
-
-// one lane per Q8_0 block: 32 codes -> fp16 in lane order, scale -> float;
-// the three shared matrices (gate, up, down) in one launch, block u of the
-// concatenation going to the matrix it falls in
-struct sh_w16_args {
-    _Float16 *w16[3];
-    float *ws[3];
-    const uint8_t *w[3];
-    uint64_t n[3];
-};
-__global__ void __launch_bounds__(256) sh_w16_kernel(sh_w16_args a) {
-    uint64_t u = (uint64_t)blockIdx.x * 256u + threadIdx.x;
-    uint32_t m = 0;
-    if (u >= a.n[0]) {
-        u -= a.n[0];
-        m = 1;
-        if (u >= a.n[1]) {
-            u -= a.n[1];
-            m = 2;
-            if (u >= a.n[2]) return;
-        }
-    }
-    _Float16 *const w16 = a.w16[m];
-    float *const ws = a.ws[m];
-    const uint8_t *const w = a.w[m];
-    const uint8_t *b = w + u * SF37_Q8_0_BYTES;
-    ws[u] = sf37_f16((uint32_t)b[0] | ((uint32_t)b[1] << 8));
-    _Float16 h[32];
-#pragma unroll
-    for (uint32_t k = 0; k < 32u; k++) h[sh_pos(k)] = (_Float16)(int)(int8_t)b[2 + k];
-    typedef _Float16 h8v __attribute__((ext_vector_type(8)));
-#pragma unroll
-    for (int q = 0; q < 4; q++) {
-        const h8v v = {h[8 * q], h[8 * q + 1], h[8 * q + 2], h[8 * q + 3],
-                       h[8 * q + 4], h[8 * q + 5], h[8 * q + 6], h[8 * q + 7]};
-        *(h8v *)(w16 + u * 32u + 8u * q) = v;
-    }
-}
-
 // Q8_0 activations (arithmetic of q8_0_quantize_kernel, k_q8_0.hip): eight
-// lanes per 32-block, four consecutive values per lane; codes as fp16 in
-// lane order (a lane's four codes are contiguous there: one 8-byte store),
-// scale as float.
-__global__ void __launch_bounds__(256) sh_act_kernel(_Float16 *__restrict__ a16, float *__restrict__ xs,
+// lanes per 32-block, four consecutive values per lane, whose codes are one
+// dword store; the scale as a float.
+__global__ void __launch_bounds__(256) sh_act_kernel(int8_t *__restrict__ a8, float *__restrict__ xs,
                                                      const float *__restrict__ x, uint32_t nb, uint64_t n_tok) {
     const uint64_t gid = (uint64_t)blockIdx.x * 256u + threadIdx.x;
     const uint64_t blk = gid >> 3;
@@ -751,90 +722,114 @@ __global__ void __launch_bounds__(256) sh_act_kernel(_Float16 *__restrict__ a16,
     float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
 #pragma unroll
     for (int off = 4; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 8));
-    typedef _Float16 h4 __attribute__((ext_vector_type(4)));
-    h4 q = {};
+    uint32_t q = 0;
     float d = 0.0f;
     if (amax != 0.0f) {
         d = amax / 127.0f;
         const float iscale = 1.0f / d;
         const float vv[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-        for (int k = 0; k < 4; k++) q[k] = (_Float16)(int)fminf(fmaxf(__builtin_rintf(iscale * vv[k]), -128.0f), 127.0f);
+        for (int k = 0; k < 4; k++) {
+            const int c = (int)fminf(fmaxf(__builtin_rintf(iscale * vv[k]), -128.0f), 127.0f);
+            q |= ((uint32_t)c & 0xffu) << (8 * k);
+        }
     }
     if (!live) return;
-    static_assert(sh_pos(4u) == sh_pos(0u) + 4u && sh_pos(31u) == sh_pos(28u) + 3u, "a lane's codes are contiguous");
-    *(h4 *)(a16 + u * 32u + sh_pos(4u * j)) = q;
+    *(uint32_t *)(a8 + u * 32u + 4u * j) = q;
     if (j == 0u) xs[u] = d;
 }
 
 struct sh_params {
-    float *out0, *out1;            // gate/up: mid (SwiGLU) [tok][rows]; down: out [tok][rows]
-    const _Float16 *w0, *w1;       // gate, up (or down) in lane order
-    const float *ws0, *ws1;
-    const _Float16 *act;           // [tok][nb * 32]
+    float *out0;                   // gate/up: mid (SwiGLU) [tok][rows]; down: out [tok][rows]
+    const uint8_t *w0, *w1;        // Q8_0 gate, up (or down) [rows][nb blocks]
+    const int8_t *act;             // [tok][nb * 32]
     const float *xs;               // [tok][nb]
     uint32_t n_tok, nb, rows, n_ct, n_tt;
     float clamp;
 };
 
+// The lane's weight words of one K chunk: per block its 16 codes (half kh)
+// from the dwords around them (block jj of a chunk starts at byte 34 jj of
+// the chunk, so even blocks' codes sit 2 bytes into a dword and odd blocks'
+// on a dword boundary), and the dword holding the f16 scale.
 struct sh_raw {
-    uint32_t w[SH_CB][8];          // per block: the lane's 16 codes (two MFMA operands)
-    float s[SH_CB];
+    uint32_t c[18];                // 5 + 4 + 5 + 4 code dwords
+    uint32_t s[4];
 };
 
 __device__ __forceinline__ void sh_ready(sh_raw &r) {
-    asm volatile("" : "+v"(r.w[0][0]), "+v"(r.w[0][1]), "+v"(r.w[0][2]), "+v"(r.w[0][3]), "+v"(r.w[0][4]),
-                 "+v"(r.w[0][5]), "+v"(r.w[0][6]), "+v"(r.w[0][7]), "+v"(r.w[1][0]), "+v"(r.w[1][1]),
-                 "+v"(r.w[1][2]), "+v"(r.w[1][3]), "+v"(r.w[1][4]), "+v"(r.w[1][5]), "+v"(r.w[1][6]),
-                 "+v"(r.w[1][7]), "+v"(r.s[0]), "+v"(r.s[1]));
-    asm volatile("" : "+v"(r.w[2][0]), "+v"(r.w[2][1]), "+v"(r.w[2][2]), "+v"(r.w[2][3]), "+v"(r.w[2][4]),
-                 "+v"(r.w[2][5]), "+v"(r.w[2][6]), "+v"(r.w[2][7]), "+v"(r.w[3][0]), "+v"(r.w[3][1]),
-                 "+v"(r.w[3][2]), "+v"(r.w[3][3]), "+v"(r.w[3][4]), "+v"(r.w[3][5]), "+v"(r.w[3][6]),
-                 "+v"(r.w[3][7]), "+v"(r.s[2]), "+v"(r.s[3]));
+    asm volatile("" : "+v"(r.c[0]), "+v"(r.c[1]), "+v"(r.c[2]), "+v"(r.c[3]), "+v"(r.c[4]), "+v"(r.c[5]),
+                 "+v"(r.c[6]), "+v"(r.c[7]), "+v"(r.c[8]), "+v"(r.c[9]), "+v"(r.c[10]));
+    asm volatile("" : "+v"(r.c[11]), "+v"(r.c[12]), "+v"(r.c[13]), "+v"(r.c[14]), "+v"(r.c[15]), "+v"(r.c[16]),
+                 "+v"(r.c[17]), "+v"(r.s[0]), "+v"(r.s[1]), "+v"(r.s[2]), "+v"(r.s[3]));
 }
 
-__device__ __forceinline__ void sh_load(sh_raw &r, const _Float16 *wrow, const float *wsrow, uint32_t c,
-                                        uint32_t kh) {
+// dword offsets (within the chunk) of block jj's first code dword for half
+// kh = 0, and of the dword holding its scale; the scale is that dword's high
+// half for odd jj
+__host__ __device__ constexpr uint32_t sh_code_dw(uint32_t jj) { return (34u * jj + 2u) / 4u; }
+__host__ __device__ constexpr uint32_t sh_scale_dw(uint32_t jj) { return (34u * jj) / 4u; }
+// first of block jj's code dwords in sh_raw::c (5 for even blocks, 4 for odd)
+__host__ __device__ constexpr uint32_t sh_code_reg(uint32_t jj) { return (9u * jj + 1u) / 2u; }
+static_assert(sh_code_dw(0) == 0 && sh_code_dw(1) == 9 && sh_code_dw(2) == 17 && sh_code_dw(3) == 26 &&
+                  sh_scale_dw(1) == 8 && sh_scale_dw(3) == 25 && SH_CB == 4,
+              "chunk word offsets");
+static_assert(sh_code_reg(1) == 5 && sh_code_reg(2) == 9 && sh_code_reg(3) == 14 && sh_code_reg(4) == 18,
+              "code dword slots");
+
+__device__ __forceinline__ void sh_load(sh_raw &r, const uint8_t *wrow, uint32_t c, uint32_t kh) {
+    const uint32_t *q = (const uint32_t *)(wrow + (uint64_t)c * (SH_CB * SF37_Q8_0_BYTES));
 #pragma unroll
-    for (uint32_t j = 0; j < SH_CB; j++) {
-        const uint32_t *q = (const uint32_t *)(wrow + (uint64_t)(c * SH_CB + j) * 32u + 16u * kh);
+    for (uint32_t jj = 0; jj < SH_CB; jj++) {
 #pragma unroll
-        for (int i = 0; i < 8; i++) r.w[j][i] = q[i];
+        for (uint32_t i = 0; i < sh_code_reg(jj + 1u) - sh_code_reg(jj); i++)
+            r.c[sh_code_reg(jj) + i] = q[sh_code_dw(jj) + 4u * kh + i];
+        r.s[jj] = q[sh_scale_dw(jj)];
     }
-    const float4 sv = *(const float4 *)(wsrow + (uint64_t)c * SH_CB);
-    r.s[0] = sv.x; r.s[1] = sv.y; r.s[2] = sv.z; r.s[3] = sv.w;
 }
+
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+typedef int32_t i32x16 __attribute__((ext_vector_type(16)));
 
 // One K chunk (SH_CB Q8_0 blocks) for SH_TB token blocks.
 __device__ __forceinline__ void sh_chunk(const sh_raw &r, const uint8_t *act_lds, const float *xs_lds,
                                          uint32_t kh, uint32_t col, float (*acc)[16]) {
-    const uint8_t *a_lane = act_lds + col * SH_RS + 32u * kh;
+    const uint8_t *a_row = act_lds + col * SH_RS;     // token row col of token block 0
+    const uint32_t sw = col & 7u;                      // the row's slot swizzle (32 i + col has the same)
     const float *x_lane = xs_lds + 4u * kh;
+    const i32x16 magic = (i32x16)SH_MAGIC_BITS;
 #pragma unroll
-    for (uint32_t j = 0; j < SH_CB; j++) {
-        typedef uint32_t u4 __attribute__((ext_vector_type(4)));
-        const u4 t0 = {r.w[j][0], r.w[j][1], r.w[j][2], r.w[j][3]};
-        const u4 t1 = {r.w[j][4], r.w[j][5], r.w[j][6], r.w[j][7]};
+    for (uint32_t jj = 0; jj < SH_CB; jj++) {
+        const uint32_t o = sh_code_reg(jj);
+        i32x4 b;
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            b[i] = (int)((jj & 1u) ? r.c[o + i] : align_bytes(r.c[o + i + 1], r.c[o + i], 2u));
+        const float ws = sf37_f16((jj & 1u) ? r.s[jj] >> 16 : r.s[jj]);
+        const float nws = -SH_MAGIC * ws;
+        const uint32_t slot = ((2u * jj + kh) ^ sw) * 16u;
         // the MFMAs of every token block first, so the epilogue of one block
         // runs while the matrix cores still work on the next
-        f16v D[SH_TB];
+        i32x16 D[SH_TB];
 #pragma unroll
         for (uint32_t i = 0; i < SH_TB; i++) {
-            const uint8_t *ap = a_lane + i * 32u * SH_RS + j * 64u;
-            D[i] = f16v{};
-            D[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(*(const h8 *)ap, __builtin_bit_cast(h8, t0), D[i], 0, 0, 0);
-            D[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(*(const h8 *)(ap + 16), __builtin_bit_cast(h8, t1), D[i], 0, 0, 0);
+            const i32x4 a = *(const i32x4 *)(a_row + i * 32u * SH_RS + slot);
+            D[i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, magic, 0, 0, 0);
         }
 #pragma unroll
         for (uint32_t i = 0; i < SH_TB; i++) {
+            // the whole result reinterpreted at once (a bit_cast of one
+            // vector element would name the vector's storage, i.e. element 0)
+            const f16v F = __builtin_bit_cast(f16v, D[i]);
 #pragma unroll
-            for (int jj = 0; jj < 4; jj++) {
-                const float4 xv = *(const float4 *)(x_lane + j * SH_T + 32u * i + 8u * jj);
+            for (int jq = 0; jq < 4; jq++) {
+                const float4 xv = *(const float4 *)(x_lane + jj * SH_T + 32u * i + 8u * jq);
                 const float xa[4] = {xv.x, xv.y, xv.z, xv.w};
 #pragma unroll
                 for (int q = 0; q < 4; q++) {
-                    const float t = D[i][4 * jj + q] * r.s[j] * xa[q];
-                    acc[i][4 * jj + q] = acc[i][4 * jj + q] + t;
+                    const float p = __builtin_fmaf(F[4 * jq + q], ws, nws);
+                    const float t = p * xa[q];
+                    acc[i][4 * jq + q] = acc[i][4 * jq + q] + t;
                 }
             }
         }
@@ -856,22 +851,25 @@ __global__ void __launch_bounds__(256, 2) sh_gemm_kernel(sh_params p) {
     // this lane's weight row
     const uint32_t wcol = GU ? ct * 64u + 16u * wave + (col & 15u) : ct * 128u + 32u * wave + col;
     const bool second = GU && col >= 16u;
-    const _Float16 *wrow = (second ? p.w1 : p.w0) + (uint64_t)wcol * nb * 32u;
-    const float *wsrow = (second ? p.ws1 : p.ws0) + (uint64_t)wcol * nb;
-    // DMA: wave w copies token rows 16w .. 16w+15 (one 256-byte row per dword load);
-    // xs: one dword load per block (lane = token)
-    const uint32_t tl = t0 + (lane < SH_T ? lane : 0u);
+    const uint8_t *wrow = (second ? p.w1 : p.w0) + (uint64_t)wcol * nb * SF37_Q8_0_BYTES;
+    // DMA: load L = 2 wave + k fills rows 8 L .. 8 L + 7; lane l writes row
+    // 8 L + l / 8, slot l % 8, which holds piece (l % 8) ^ (l / 8) of it
+    uint32_t voff[2];
+#pragma unroll
+    for (uint32_t k = 0; k < 2u; k++) {
+        const uint32_t r = 8u * (2u * wave + k) + (lane >> 3);
+        const uint32_t tr = t0 + r < p.n_tok ? t0 + r : p.n_tok - 1u;
+        voff[k] = tr * nb * 32u + 16u * ((lane & 7u) ^ (lane >> 3));
+    }
+    const uint32_t tl = t0 + lane;
     const uint32_t tok_dma = tl < p.n_tok ? tl : p.n_tok - 1u;
     const uint32_t act_l = lds_addr(&s_act[0][0]), xs_l = lds_addr(&s_xs[0][0]);
     auto issue = [&](uint32_t c) {
         const uint32_t bf = c & 1u;
 #pragma unroll
-        for (uint32_t j = 0; j < 16u; j++) {
-            const uint32_t t = 16u * wave + j;
-            const uint32_t tr = t0 + t < p.n_tok ? t0 + t : p.n_tok - 1u;
-            lds_dma4(act_l + bf * SH_BUF + t * SH_RS, 4u * lane,
-                     (const uint8_t *)p.act + ((uint64_t)tr * nb + (uint64_t)c * SH_CB) * 64u);
-        }
+        for (uint32_t k = 0; k < 2u; k++)
+            lds_dma16(act_l + bf * SH_BUF + (2u * wave + k) * DMA16_SPAN, voff[k],
+                      (const uint8_t *)p.act + (uint64_t)c * (SH_CB * 32u));
         lds_dma4(xs_l + bf * (SH_CB * SH_T * 4u) + wave * SH_T * 4u, tok_dma * nb * 4u,
                  (const uint8_t *)p.xs + ((uint64_t)c * SH_CB + wave) * 4u);
     };
@@ -882,7 +880,7 @@ __global__ void __launch_bounds__(256, 2) sh_gemm_kernel(sh_params p) {
         for (int r2 = 0; r2 < 16; r2++) acc[i][r2] = 0.0f;
     sh_raw ra, rb;
     issue(0);
-    sh_load(ra, wrow, wsrow, 0, kh);
+    sh_load(ra, wrow, 0, kh);
     const uint32_t last = nchunk - 1u;
     for (uint32_t c = 0; c < nchunk; c += 2u) {
         const uint32_t c1 = c + 1u < nchunk ? c + 1u : last, c2 = c + 2u < nchunk ? c + 2u : last;
@@ -890,14 +888,14 @@ __global__ void __launch_bounds__(256, 2) sh_gemm_kernel(sh_params p) {
         sh_ready(ra);
         __syncthreads();
         issue(c1);
-        sh_load(rb, wrow, wsrow, c1, kh);
+        sh_load(rb, wrow, c1, kh);
         sh_chunk(ra, s_act[c & 1u], s_xs[c & 1u], kh, col, acc);
         if (c + 1u < nchunk) {
             wait_vm0();
             sh_ready(rb);
             __syncthreads();
             issue(c2);
-            sh_load(ra, wrow, wsrow, c2, kh);
+            sh_load(ra, wrow, c2, kh);
             sh_chunk(rb, s_act[(c + 1u) & 1u], s_xs[(c + 1u) & 1u], kh, col, acc);
         }
     }
@@ -1015,40 +1013,22 @@ extern "C" int sf37k_sh_supported(uint32_t in_dim, uint32_t mid_dim, uint32_t ou
            out_dim % 128u == 0 && in_dim > 0 && mid_dim > 0;
 }
 
-extern "C" int sf37k_sh_repack3(void *const w16[3], float *const ws[3], const uint8_t *const w[3],
-                                const uint64_t rows[3], const uint32_t in_dim[3], sf37_stream_t s) {
-    sh_w16_args a;
-    uint64_t n = 0;
-    for (int m = 0; m < 3; m++) {
-        a.w16[m] = (_Float16 *)w16[m];
-        a.ws[m] = ws[m];
-        a.w[m] = w[m];
-        a.n[m] = rows[m] * (in_dim[m] / 32u);
-        n += a.n[m];
-    }
-    if (n == 0) return 0;
-    hipLaunchKernelGGL(sh_w16_kernel, dim3((unsigned)((n + 255u) / 256u)), dim3(256), 0, (hipStream_t)s, a);
-    return (int)hipGetLastError();
-}
-
-extern "C" int sf37k_sh_act(void *a16, float *xs, const float *x, uint32_t dim, uint32_t n_tok, sf37_stream_t s) {
+extern "C" int sf37k_sh_act(void *a8, float *xs, const float *x, uint32_t dim, uint32_t n_tok, sf37_stream_t s) {
     const uint64_t n = (uint64_t)(dim / 32u) * n_tok;
     if (n == 0) return 0;
     hipLaunchKernelGGL(sh_act_kernel, dim3((unsigned)((n + 31u) / 32u)), dim3(256), 0, (hipStream_t)s,
-                       (_Float16 *)a16, xs, x, dim / 32u, (uint64_t)n_tok);
+                       (int8_t *)a8, xs, x, dim / 32u, (uint64_t)n_tok);
     return (int)hipGetLastError();
 }
 
-extern "C" int sf37k_sh_gate_up(float *mid, const void *g16, const float *gs, const void *u16, const float *us,
-                                const void *a16, const float *xs, uint32_t n_tok, uint32_t in_dim,
-                                uint32_t mid_dim, float clamp, sf37_stream_t s) {
+extern "C" int sf37k_sh_gate_up(float *mid, const uint8_t *gate_w, const uint8_t *up_w, const void *a8,
+                                const float *xs, uint32_t n_tok, uint32_t in_dim, uint32_t mid_dim, float clamp,
+                                sf37_stream_t s) {
     sh_params p = {};
     p.out0 = mid;
-    p.w0 = (const _Float16 *)g16;
-    p.w1 = (const _Float16 *)u16;
-    p.ws0 = gs;
-    p.ws1 = us;
-    p.act = (const _Float16 *)a16;
+    p.w0 = gate_w;
+    p.w1 = up_w;
+    p.act = (const int8_t *)a8;
     p.xs = xs;
     p.n_tok = n_tok;
     p.nb = in_dim / 32u;
@@ -1060,13 +1040,12 @@ extern "C" int sf37k_sh_gate_up(float *mid, const void *g16, const float *gs, co
     return (int)hipGetLastError();
 }
 
-extern "C" int sf37k_sh_down(float *out, const void *d16, const float *ds, const void *a16, const float *xs,
-                             uint32_t n_tok, uint32_t mid_dim, uint32_t out_dim, sf37_stream_t s) {
+extern "C" int sf37k_sh_down(float *out, const uint8_t *down_w, const void *a8, const float *xs, uint32_t n_tok,
+                             uint32_t mid_dim, uint32_t out_dim, sf37_stream_t s) {
     sh_params p = {};
     p.out0 = out;
-    p.w0 = (const _Float16 *)d16;
-    p.ws0 = ds;
-    p.act = (const _Float16 *)a16;
+    p.w0 = down_w;
+    p.act = (const int8_t *)a8;
     p.xs = xs;
     p.n_tok = n_tok;
     p.nb = mid_dim / 32u;
@@ -1076,4 +1055,3 @@ extern "C" int sf37k_sh_down(float *out, const void *d16, const float *ds, const
     hipLaunchKernelGGL(sh_gemm_kernel<false>, dim3(p.n_ct * p.n_tt), dim3(256), 0, (hipStream_t)s, p);
     return (int)hipGetLastError();
 }
-

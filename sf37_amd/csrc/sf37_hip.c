@@ -42,8 +42,8 @@ static void *g_scratch;
 static uint64_t g_scratch_bytes;
 static int g_model_fd = -1;
 
-static sf37_hip_tensor *g_layer_bufs[8];
-static uint64_t g_layer_buf_bytes[8];
+static sf37_hip_tensor *g_layer_bufs[10];
+static uint64_t g_layer_buf_bytes[10];
 
 static int64_t g_opt_q8k = 1;
 static int64_t g_opt_q8k_min_rows = 512;
@@ -55,6 +55,11 @@ static int64_t g_opt_down_combine = 1;
 static int64_t g_opt_prefill = 1;
 static int64_t g_opt_prefill_min_pairs = 256;
 static int64_t g_opt_shared_min_tok = 64;
+static int64_t g_opt_shared_stream = 1;
+/* the shared expert's side stream (default priority) and its fork / join
+ * events, made on first use */
+static hipStream_t g_side;
+static hipEvent_t g_ev_fork, g_ev_join;
 
 /* arrival counters of the fused decode kernels: zeroed once, left zero by
  * every completed launch */
@@ -118,18 +123,18 @@ static const char *const k_stage_names[SF37_HIP_N_STAGES] = {
     "pf_act_x", "pf_tiles", "pf_gate_up", "pf_act_mid", "pf_down",
     "sh_repack", "sh_act", "sh_gate_up", "sh_down"};
 
-static void prof_begin(void) {
+static void prof_begin(hipStream_t st) {
     if (!g_prof_on) return;
-    if (hipEventCreate(&g_prof_open) != hipSuccess || hipEventRecord(g_prof_open, g_stream) != hipSuccess) {
+    if (hipEventCreate(&g_prof_open) != hipSuccess || hipEventRecord(g_prof_open, st) != hipSuccess) {
         g_prof_open = NULL;
         (void)hipGetLastError();
     }
 }
 
-static void prof_end(uint32_t stage) {
+static void prof_end(uint32_t stage, hipStream_t st) {
     if (!g_prof_on || !g_prof_open) return;
     hipEvent_t e;
-    if (hipEventCreate(&e) != hipSuccess || hipEventRecord(e, g_stream) != hipSuccess) {
+    if (hipEventCreate(&e) != hipSuccess || hipEventRecord(e, st) != hipSuccess) {
         (void)hipGetLastError();
         return;
     }
@@ -147,8 +152,10 @@ static void prof_end(uint32_t stage) {
 
 static int launch_ok(int err, const char *what) { return hip_ok((hipError_t)err, what); }
 
-/* Launch wrapper: events around the launch when profiling. */
-#define LAUNCH(stage, call, what) (prof_begin(), launch_ok((call), (what)) ? (prof_end(stage), 1) : 0)
+/* Launch wrappers: events around the launch on its stream when profiling. */
+#define LAUNCH_ON(st, stage, call, what) \
+    (prof_begin(st), launch_ok((call), (what)) ? (prof_end((stage), (st)), 1) : 0)
+#define LAUNCH(stage, call, what) LAUNCH_ON(g_stream, stage, call, what)
 
 int sf37_hip_profile_enable(int on) {
     g_prof_on = on ? 1 : 0;
@@ -294,7 +301,12 @@ void sf37_hip_cleanup(void) {
     if (g_dec_cnt) (void)hipFree(g_dec_cnt);
     g_dec_cnt = NULL;
     g_dec_cnt_words = 0;
-    for (int i = 0; i < 8; i++) {
+    if (g_side) (void)hipStreamDestroy(g_side);
+    if (g_ev_fork) (void)hipEventDestroy(g_ev_fork);
+    if (g_ev_join) (void)hipEventDestroy(g_ev_join);
+    g_side = NULL;
+    g_ev_fork = g_ev_join = NULL;
+    for (int i = 0; i < 10; i++) {
         if (g_layer_bufs[i]) {
             (void)hipFree(g_layer_bufs[i]->ptr);
             free(g_layer_bufs[i]);
@@ -351,6 +363,7 @@ int sf37_hip_set_option(const char *name, int64_t value) {
     else if (!strcmp(name, "prefill_mfma")) g_opt_prefill = value ? 1 : 0;
     else if (!strcmp(name, "prefill_min_pairs")) g_opt_prefill_min_pairs = value < 0 ? 0 : value;
     else if (!strcmp(name, "shared_min_tokens")) g_opt_shared_min_tok = value < 0 ? 0 : value;
+    else if (!strcmp(name, "shared_stream")) g_opt_shared_stream = value ? 1 : 0;
     else return 0;
     return 1;
 }
@@ -370,6 +383,7 @@ int64_t sf37_hip_get_option(const char *name) {
     if (!strcmp(name, "prefill_mfma")) return g_opt_prefill;
     if (!strcmp(name, "prefill_min_pairs")) return g_opt_prefill_min_pairs;
     if (!strcmp(name, "shared_min_tokens")) return g_opt_shared_min_tok;
+    if (!strcmp(name, "shared_stream")) return g_opt_shared_stream;
     return -1;
 }
 
@@ -1018,7 +1032,16 @@ typedef struct {
     uint32_t n_tok;
     const float *comb_base;   /* combine: out = comb_base + sum (may be out) */
     float *comb_resid;        /* combine: comb_resid += comb_base + sum instead */
+    hipEvent_t comb_wait;     /* the combine waits for it (comb_base made on another stream) */
 } routed_args;
+
+/* The combine of a routed pipeline, after the work comb_base waits for. */
+static int routed_combine(const routed_args *a, float *out, const float *down_pair) {
+    if (a->comb_wait && !hip_ok(hipStreamWaitEvent(g_stream, a->comb_wait, 0), "shared expert join")) return 0;
+    return LAUNCH(SF37_HIP_STAGE_COMBINE, sf37k_moe_combine(out, down_pair, a->comb_base, a->comb_resid, a->topk,
+                                                            a->out_dim, a->n_tok, (sf37_stream_t)g_stream),
+                  "routed_moe combine launch");
+}
 
 /* Scratch of the Q8_K routed pipeline; mid/down_pair/gate/up may point
  * into caller tensors.  Returns the byte size when base == NULL. */
@@ -1084,38 +1107,36 @@ static int shared_mfma_eligible(uint32_t n_tok, uint32_t D, uint32_t F) {
            (uint64_t)n_tok * D * 2u < (1ull << 32) && (uint64_t)n_tok * F * 2u < (1ull << 32);
 }
 
+static void *layer_buf(int i, uint64_t bytes);
+
+/* On stream st with its own activation buffer (layer buffer 8), so it can
+ * run beside the routed pipeline, which uses the library scratch. */
 static int shared_mfma(float *out, float *mid, const uint8_t *gw, const uint8_t *uw, const uint8_t *dw, uint32_t D,
-                       uint32_t F, const float *x, uint32_t n_tok, float clamp) {
-    if (!aligned4(x) || !aligned4(out) || !aligned4(mid)) return 0;
-    const uint64_t wb = (uint64_t)F * D * 2u, sb = (uint64_t)F * (D / 32u) * 4u;
+                       uint32_t F, const float *x, uint32_t n_tok, float clamp, hipStream_t hs) {
+    if (!aligned4(x) || !aligned4(out) || !aligned4(mid) || !aligned4(gw) || !aligned4(uw) || !aligned4(dw)) return 0;
     const uint64_t maxd = D > F ? D : F;
-    const uint64_t ab = (uint64_t)n_tok * maxd * 2u, xb = (uint64_t)n_tok * (maxd / 32u) * 4u;
-    uint64_t off = 0, o_g, o_u, o_d, o_gs, o_us, o_ds, o_a, o_x;
-    o_g = off; off = align256(off + wb);
-    o_u = off; off = align256(off + wb);
-    o_d = off; off = align256(off + wb);
-    o_gs = off; off = align256(off + sb);
-    o_us = off; off = align256(off + sb);
-    o_ds = off; off = align256(off + sb);
-    o_a = off; off = align256(off + ab);
-    o_x = off; off = align256(off + xb);
-    char *s = scratch_get(off, "shared expert scratch");
+    const uint64_t ab = (uint64_t)n_tok * maxd, xb = (uint64_t)n_tok * (maxd / 32u) * 4u;
+    char *s = (char *)layer_buf(8, align256(ab) + xb);
     if (!s) return 0;
-    const sf37_stream_t st = (sf37_stream_t)g_stream;
-    float *gs = (float *)(s + o_gs), *us = (float *)(s + o_us), *ds = (float *)(s + o_ds), *xs = (float *)(s + o_x);
-    void *const rw16[3] = {s + o_g, s + o_u, s + o_d};
-    float *const rws[3] = {gs, us, ds};
-    const uint8_t *const rw[3] = {gw, uw, dw};
-    const uint64_t rrows[3] = {F, F, D};
-    const uint32_t rin[3] = {D, D, F};
-    return LAUNCH(SF37_HIP_STAGE_SH_REPACK, sf37k_sh_repack3(rw16, rws, rw, rrows, rin, st), "shared repack launch") &&
-           LAUNCH(SF37_HIP_STAGE_SH_ACT, sf37k_sh_act(s + o_a, xs, x, D, n_tok, st), "shared activation launch") &&
-           LAUNCH(SF37_HIP_STAGE_SH_GATE_UP, sf37k_sh_gate_up(mid, s + o_g, gs, s + o_u, us, s + o_a, xs, n_tok, D, F,
-                                                             clamp, st),
-                  "shared gate/up launch") &&
-           LAUNCH(SF37_HIP_STAGE_SH_ACT, sf37k_sh_act(s + o_a, xs, mid, F, n_tok, st), "shared mid activation launch") &&
-           LAUNCH(SF37_HIP_STAGE_SH_DOWN, sf37k_sh_down(out, s + o_d, ds, s + o_a, xs, n_tok, F, D, st),
-                  "shared down launch");
+    const sf37_stream_t st = (sf37_stream_t)hs;
+    void *a8 = s;
+    float *xs = (float *)(s + align256(ab));
+    return LAUNCH_ON(hs, SF37_HIP_STAGE_SH_ACT, sf37k_sh_act(a8, xs, x, D, n_tok, st), "shared activation launch") &&
+           LAUNCH_ON(hs, SF37_HIP_STAGE_SH_GATE_UP, sf37k_sh_gate_up(mid, gw, uw, a8, xs, n_tok, D, F, clamp, st),
+                     "shared gate/up launch") &&
+           LAUNCH_ON(hs, SF37_HIP_STAGE_SH_ACT, sf37k_sh_act(a8, xs, mid, F, n_tok, st), "shared mid activation launch") &&
+           LAUNCH_ON(hs, SF37_HIP_STAGE_SH_DOWN, sf37k_sh_down(out, dw, a8, xs, n_tok, F, D, st), "shared down launch");
+}
+
+/* The side stream and its events (default priority, no blocking with the
+ * null stream; ordering with the library stream only through the events). */
+static int side_stream_ready(void) {
+    if (g_side) return 1;
+    if (!hip_ok(hipEventCreateWithFlags(&g_ev_fork, hipEventDisableTiming), "side stream fork event") ||
+        !hip_ok(hipEventCreateWithFlags(&g_ev_join, hipEventDisableTiming), "side stream join event") ||
+        !hip_ok(hipStreamCreateWithFlags(&g_side, hipStreamNonBlocking), "side stream"))
+        return 0;
+    return 1;
 }
 
 /* Matrix-core pipeline (k_prefill.hip): x to fp16 MFMA codes, dispatch,
@@ -1146,8 +1167,7 @@ static int routed_pf(const routed_args *a, const routed_scratch *s, float *out, 
            LAUNCH(SF37_HIP_STAGE_PF_DOWN, sf37k_pf_down(down_pair, a->down_w, s->m16, s->mtabs, s->tiles, s->sorted,
                                                        max_tiles, tstride, a->mid_dim, a->out_dim, st),
                   "routed_moe mfma down launch") &&
-           LAUNCH(SF37_HIP_STAGE_COMBINE, sf37k_moe_combine(out, down_pair, a->comb_base, a->comb_resid, a->topk, a->out_dim, a->n_tok, st),
-                  "routed_moe combine launch");
+           routed_combine(a, out, down_pair);
 }
 
 /* Q8_K pipeline: quantize x, group pairs by expert (slots = one group per
@@ -1191,8 +1211,7 @@ static int routed_q8k(const routed_args *a, float *out, float *mid, float *down_
                                   a->out_dim, st),
                    "routed_moe q8k down launch"))
         return 0;
-    return LAUNCH(SF37_HIP_STAGE_COMBINE, sf37k_moe_combine(out, down_pair, a->comb_base, a->comb_resid, a->topk, a->out_dim, a->n_tok, st),
-                     "routed_moe combine launch");
+    return routed_combine(a, out, down_pair);
 }
 
 /* ---- fused decode path (k_decode.hip) ------------------------------------ */
@@ -1458,7 +1477,7 @@ int sf37_hip_routed_moe_one(sf37_hip_tensor *out, sf37_hip_tensor *gate, sf37_hi
     if (moe_gate->bytes < gb || moe_up->bytes < gb || moe_down->bytes < db) return 0;
     routed_args a = {(const uint8_t *)moe_gate->ptr, (const uint8_t *)moe_up->ptr, (const uint8_t *)moe_down->ptr,
                      (const int32_t *)selected->ptr, (const float *)weights->ptr, n_total_expert, topk, in_dim,
-                     expert_mid_dim, out_dim, clamp, (const float *)x->ptr, 1, NULL, NULL};
+                     expert_mid_dim, out_dim, clamp, (const float *)x->ptr, 1, NULL, NULL, NULL};
     return routed_one_impl(out, gate, up, mid, down, &a);
 }
 
@@ -1488,7 +1507,7 @@ int sf37_hip_routed_moe_one_mapped(sf37_hip_tensor *out, sf37_hip_tensor *gate, 
                               expert_mid_dim, out_dim, x, 1))
         return 0;
     routed_args a = {NULL, NULL, NULL, (const int32_t *)selected->ptr, (const float *)weights->ptr, n_total_expert,
-                     topk, in_dim, expert_mid_dim, out_dim, clamp, (const float *)x->ptr, 1, NULL, NULL};
+                     topk, in_dim, expert_mid_dim, out_dim, clamp, (const float *)x->ptr, 1, NULL, NULL, NULL};
     if (!resolve_experts(model_map, model_size, gate_offset, up_offset, down_offset, n_total_expert, in_dim,
                          expert_mid_dim, out_dim, &a.gate_w, &a.up_w, &a.down_w))
         return 0;
@@ -1507,7 +1526,7 @@ int sf37_hip_routed_moe_batch_mapped(sf37_hip_tensor *out, sf37_hip_tensor *gate
                               expert_mid_dim, out_dim, x, n_tok))
         return 0;
     routed_args a = {NULL, NULL, NULL, (const int32_t *)selected->ptr, (const float *)weights->ptr, n_total_expert,
-                     topk, in_dim, expert_mid_dim, out_dim, clamp, (const float *)x->ptr, n_tok, NULL, NULL};
+                     topk, in_dim, expert_mid_dim, out_dim, clamp, (const float *)x->ptr, n_tok, NULL, NULL, NULL};
     if (!resolve_experts(model_map, model_size, gate_offset, up_offset, down_offset, n_total_expert, in_dim,
                          expert_mid_dim, out_dim, &a.gate_w, &a.up_w, &a.down_w))
         return 0;
@@ -1596,6 +1615,11 @@ static uint64_t g_block_buf_bytes[2];
 static void *layer_buf(int i, uint64_t bytes) {
     g_mem_requests++;
     if (!g_layer_bufs[i] || g_layer_buf_bytes[i] < bytes) {
+        /* a buffer the side stream may still read or write is freed only
+         * after both streams' queued work */
+        if (g_layer_bufs[i] && (!hip_ok(hipStreamSynchronize(g_stream), "layer buffer sync") ||
+                                (g_side && !hip_ok(hipStreamSynchronize(g_side), "side stream sync"))))
+            return NULL;
         if (g_layer_bufs[i]) sf37_hip_tensor_free(g_layer_bufs[i]);
         g_layer_bufs[i] = sf37_hip_tensor_alloc(bytes);
         g_layer_buf_bytes[i] = g_layer_bufs[i] ? bytes : 0;
@@ -1677,7 +1701,7 @@ static int layer_shared_q3q2(float *out, const sf37_hip_moe_layer_weights *w, co
         !hip_ok(hipMemsetD32Async((hipDeviceptr_t)wts, 0x3f800000, n_tok, g_stream), "shared weight fill"))
         return 0;
     routed_args a = {(const uint8_t *)w->sh_gate->ptr, (const uint8_t *)w->sh_up->ptr,
-                     (const uint8_t *)w->sh_down->ptr, sel, wts, 1u, 1u, D, F, D, w->clamp_shared, x, n_tok, NULL, NULL};
+                     (const uint8_t *)w->sh_down->ptr, sel, wts, 1u, 1u, D, F, D, w->clamp_shared, x, n_tok, NULL, NULL, NULL};
     if (decode_eligible(&a, 0)) {
         dec_extra ex;
         memset(&ex, 0, sizeof(ex));
@@ -1744,7 +1768,7 @@ static int moe_layer_impl(sf37_hip_tensor *out, sf37_hip_tensor *selected, sf37_
     }
     const sf37_stream_t st = (sf37_stream_t)g_stream;
     routed_args a = {(const uint8_t *)w->gate->ptr, (const uint8_t *)w->up->ptr, (const uint8_t *)w->down->ptr, NULL,
-                     NULL, E, K, D, F, D, w->clamp_routed, (const float *)x->ptr, n_tok, NULL, NULL};
+                     NULL, E, K, D, F, D, w->clamp_routed, (const float *)x->ptr, n_tok, NULL, NULL, NULL};
     const int fused = decode_eligible(&a, SF37_DEC_SELECT | (shared_q3 ? 0u : SF37_DEC_SHARED));
     if (bn && !fused) {
         const uint64_t bytes = (uint64_t)n_tok * D * 4u;
@@ -1773,6 +1797,19 @@ static int moe_layer_impl(sf37_hip_tensor *out, sf37_hip_tensor *selected, sf37_
                            "moe block rms_norm launch"))
             return 0;
         xl = xn;
+    }
+    /* the Q8_0 shared expert of a prefill batch on the side stream, from
+     * here to the routed combine: it depends on the rows alone, so it runs
+     * beside the router, top-k, dispatch and routed experts */
+    const int side = !fused && !shared_q3 && g_opt_shared_stream && shared_mfma_eligible(n_tok, D, F);
+    if (side) {
+        float *sh = (float *)layer_buf(3, (uint64_t)n_tok * F * 4u);
+        if (!sh || !side_stream_ready() || !hip_ok(hipEventRecord(g_ev_fork, g_stream), "shared expert fork") ||
+            !hip_ok(hipStreamWaitEvent(g_side, g_ev_fork, 0), "shared expert fork wait") ||
+            !shared_mfma((float *)out->ptr, sh, (const uint8_t *)w->sh_gate->ptr, (const uint8_t *)w->sh_up->ptr,
+                         (const uint8_t *)w->sh_down->ptr, D, F, xl, n_tok, w->clamp_shared, g_side) ||
+            !hip_ok(hipEventRecord(g_ev_join, g_side), "shared expert join record"))
+            return 0;
     }
     /* logits: injected, or a BF16 / Q8_0 router computed here; the F32
      * router runs in the decode route launch or below */
@@ -1813,10 +1850,12 @@ static int moe_layer_impl(sf37_hip_tensor *out, sf37_hip_tensor *selected, sf37_
      * pair -> SwiGLU -> Q8_0 down */
     if (shared_q3) {
         if (!layer_shared_q3q2((float *)out->ptr, w, xl, n_tok)) return 0;
+    } else if (side) {
+        a.comb_wait = g_ev_join;   /* launched above; the routed combine joins it */
     } else if (shared_mfma_eligible(n_tok, D, F)) {
         float *sh = (float *)layer_buf(3, (uint64_t)n_tok * F * 4u);
         if (!sh || !shared_mfma((float *)out->ptr, sh, (const uint8_t *)w->sh_gate->ptr, (const uint8_t *)w->sh_up->ptr,
-                                (const uint8_t *)w->sh_down->ptr, D, F, xl, n_tok, w->clamp_shared))
+                                (const uint8_t *)w->sh_down->ptr, D, F, xl, n_tok, w->clamp_shared, g_stream))
             return 0;
     } else {
         float *sh = (float *)layer_buf(3, (uint64_t)n_tok * F * 4u * 3u);   /* gate | up | mid */
@@ -1838,6 +1877,7 @@ static int moe_layer_impl(sf37_hip_tensor *out, sf37_hip_tensor *selected, sf37_
     float *routed = NULL;
     if (!q8k_use_for(F) || !q8k_use_for(D)) {
         if (n_tok != 1u) return 0;
+        if (side && !hip_ok(hipStreamWaitEvent(g_stream, g_ev_join, 0), "shared expert join")) return 0;
         routed = (float *)layer_buf(4, (uint64_t)D * 4u);
         float *mid_down = (float *)layer_buf(5, (uint64_t)K * ((uint64_t)F + D) * 4u);
         if (!routed || !mid_down || !routed_f32(&a, routed, mid_down, mid_down + (uint64_t)K * F, NULL, NULL))
@@ -1874,7 +1914,7 @@ int sf37_hip_moe_layer_noalloc(sf37_hip_tensor *out, sf37_hip_tensor *selected, 
     const int run_router = !logits_in || (g_opt_router_always && w->router);
     if (!layer_weights_ok(w, run_router)) return 0;
     routed_args a = {(const uint8_t *)w->gate->ptr, (const uint8_t *)w->up->ptr, (const uint8_t *)w->down->ptr, NULL,
-                     NULL, E, K, D, F, D, w->clamp_routed, (const float *)x->ptr, n_tok, NULL, NULL};
+                     NULL, E, K, D, F, D, w->clamp_routed, (const float *)x->ptr, n_tok, NULL, NULL, NULL};
     if ((run_router && w->router_type != SF37_HIP_TYPE_F32) || w->shared_type == SF37_HIP_TYPE_Q3GU ||
         !decode_eligible(&a, SF37_DEC_SELECT | SF37_DEC_SHARED)) {
         fprintf(stderr, "sf37: HIP moe_layer_noalloc takes decode batches of 1..%u tokens on the Q8_K path with an "

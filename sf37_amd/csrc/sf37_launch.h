@@ -128,20 +128,17 @@ int sf37k_pf_down(float *down_pair, const uint8_t *down_w, const void *act, cons
                   const uint32_t *tiles, const uint32_t *sorted_pairs, uint32_t max_tiles,
                   uint32_t tab_stride, uint32_t mid_dim, uint32_t out_dim, sf37_stream_t s);
 
-/* Shared expert (Q8_0) on the matrix cores for many tokens (k_prefill.hip):
- * repack weight rows to fp16 codes in MFMA lane order + float scales
- * (w16: rows x in_dim halves, ws: rows x in_dim/32), Q8_0 activations in the
- * same order (a16: n_tok x dim halves, xs: n_tok x dim/32), gate/up with the
- * shared SwiGLU into mid, down into out.  Results equal q8_0_matmul + swiglu. */
+/* Shared expert (Q8_0) on the int8 matrix cores for many tokens
+ * (k_prefill.hip): Q8_0 activations (a8: n_tok x dim int8 codes, xs: n_tok x
+ * dim/32 float scales), gate/up straight from the Q8_0 weight tensors with
+ * the shared SwiGLU into mid, down into out.  Results equal q8_0_matmul +
+ * swiglu bit for bit. */
 int sf37k_sh_supported(uint32_t in_dim, uint32_t mid_dim, uint32_t out_dim);
-int sf37k_sh_repack3(void *const w16[3], float *const ws[3], const uint8_t *const w[3], const uint64_t rows[3],
-                     const uint32_t in_dim[3], sf37_stream_t s);
-int sf37k_sh_act(void *a16, float *xs, const float *x, uint32_t dim, uint32_t n_tok, sf37_stream_t s);
-int sf37k_sh_gate_up(float *mid, const void *g16, const float *gs, const void *u16, const float *us,
-                     const void *a16, const float *xs, uint32_t n_tok, uint32_t in_dim, uint32_t mid_dim,
-                     float clamp, sf37_stream_t s);
-int sf37k_sh_down(float *out, const void *d16, const float *ds, const void *a16, const float *xs,
-                  uint32_t n_tok, uint32_t mid_dim, uint32_t out_dim, sf37_stream_t s);
+int sf37k_sh_act(void *a8, float *xs, const float *x, uint32_t dim, uint32_t n_tok, sf37_stream_t s);
+int sf37k_sh_gate_up(float *mid, const uint8_t *gate_w, const uint8_t *up_w, const void *a8, const float *xs,
+                     uint32_t n_tok, uint32_t in_dim, uint32_t mid_dim, float clamp, sf37_stream_t s);
+int sf37k_sh_down(float *out, const uint8_t *down_w, const void *a8, const float *xs, uint32_t n_tok,
+                  uint32_t mid_dim, uint32_t out_dim, sf37_stream_t s);
 
 /* Fused decode layer (up to 16 tokens): route, select, up, mid, down,
  * combine (k_decode.hip).  Pointers are device addresses; flags select the parts

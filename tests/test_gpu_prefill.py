@@ -182,13 +182,16 @@ def test_config3_layer_sample_vs_oracle(H, O, layer):
 def test_layer_mfma_equals_staged(H, layer, n_tok):
     """Whole layer (router on the device, shared expert and routed experts on
     the matrix cores) against the dot-product kernels (prefill_mfma=0), bit for
-    bit; token counts that leave partial 32- and 64-token tiles."""
+    bit; token counts that leave partial 32- and 64-token tiles.  The matrix-
+    core layer runs with the shared expert on the side stream (joined before
+    the routed combine) and in order on the library stream."""
     from sf37_amd import moe
     rng = np.random.default_rng(300 + n_tok)
     x = rng.standard_normal((n_tok, K)).astype(np.float32)
     res = []
-    for mfma in (1, 0):
+    for mfma, side in ((1, 1), (1, 0), (0, 1)):
         H.set_option("prefill_mfma", mfma)
+        H.set_option("shared_stream", side)
         H.lib().sf37_hip_profile_enable(1)
         H.profile_read()
         try:
@@ -199,8 +202,10 @@ def test_layer_mfma_equals_staged(H, layer, n_tok):
         finally:
             H.lib().sf37_hip_profile_enable(0)
             H.set_option("prefill_mfma", 1)
+            H.set_option("shared_stream", 1)
         ran = prof["sh_gate_up"][1] + prof["pf_gate_up"][1]
         assert ran == (2 if mfma else 0), f"matrix-core kernels ran {ran} times with prefill_mfma={mfma}"
         res.append((out.read(np.float32), sel.read(np.int32)))
-    assert np.array_equal(res[0][1], res[1][1])
-    assert_bitexact(res[0][0], res[1][0], f"layer out, {n_tok} tokens")
+    for r, what in ((res[0], "side stream"), (res[1], "one stream")):
+        assert np.array_equal(r[1], res[2][1])
+        assert_bitexact(r[0], res[2][0], f"layer out ({what}), {n_tok} tokens")
