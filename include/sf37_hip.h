@@ -253,6 +253,10 @@ void *sf37_hip_get_stream(void);
  *   "decode_down_wgs"   decode tuning (results unchanged)
  *   "prefill_mfma"      1 (default): grouped batches run on the matrix cores;
  *   "prefill_min_pairs", "shared_min_tokens" the smallest batches that do
+ *   "shared_stream"     1 (default): a prefill batch's Q8_0 shared expert
+ *                       runs on a second stream of the library (default
+ *                       priority), forked after its input rows and joined
+ *                       before the routed combine; 0: in order
  *   "router_with_logits" 1: sf37_hip_moe_layer computes the router GEMV even
  *                       when logits_in is given (its result is unused; for
  *                       benchmarks that inject routing but keep the cost)

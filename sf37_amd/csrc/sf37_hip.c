@@ -1400,12 +1400,13 @@ static int decode_run_in(const routed_args *a, const dec_extra *ex, float *out, 
     p.xn = ex->xn;
     p.cnt = cnt;
     const sf37_stream_t st = (sf37_stream_t)g_stream;
+    const int down_combine = g_opt_down_combine && sf37k_decode_down_combine_supported(&p);
     return LAUNCH(SF37_HIP_STAGE_DEC_ROUTE, sf37k_decode_route(&p, st), "decode route launch") &&
            ((p.flags & SF37_DEC_UPSEL) ||
             LAUNCH(SF37_HIP_STAGE_DEC_SELECT, sf37k_decode_select(&p, st), "decode select launch")) &&
            LAUNCH(SF37_HIP_STAGE_DEC_UP, sf37k_decode_up(&p, st), "decode up launch") &&
            LAUNCH(SF37_HIP_STAGE_DEC_MID, sf37k_decode_mid(&p, st), "decode mid launch") &&
-           (g_opt_down_combine && sf37k_decode_down_combine_supported(&p)
+           (down_combine
                 ? LAUNCH(SF37_HIP_STAGE_DEC_DOWN, sf37k_decode_down_combine(&p, st), "decode down+combine launch")
                 : LAUNCH(SF37_HIP_STAGE_DEC_DOWN, sf37k_decode_down(&p, st), "decode down launch") &&
                       LAUNCH(SF37_HIP_STAGE_DEC_COMBINE, sf37k_decode_combine(&p, st), "decode combine launch"));
