@@ -154,6 +154,7 @@ def main():
 
     dec = decode_bench(args, H, n_tok)
     dec1 = decode_bench(args, H, 1, layers=dec["layers"], summary=True) if n_tok != 1 else None
+    q3q2 = {f"decode_{t}tok": shared_q3q2_bench(args, H, dec["layers"], t) for t in sorted({n_tok, 1}, reverse=True)}
     prefill = [prefill_bench(args, H, dec["layers"][0], c) for c in (3, 2)] if args.prefill_steps > 0 else None
 
     cpu, parity = None, None
@@ -209,6 +210,7 @@ def main():
         "stages": dec["stages"],
         "stage_timing": STAGE_TIMING_NOTE,
         "config0": dec1,
+        "shared_q3q2": q3q2,
         "parity": parity,
         "prefill": prefill,
         "stack": stack,
@@ -317,7 +319,7 @@ def decode_bench(args, H, n_tok, layers=None, summary=False):
     k_avg_ms = k_ms / k_n
     k_mean_bytes = float(np.mean([kern_bytes[i % args.layers][kern] for i in range(args.steps)]))
     achieved = k_mean_bytes / (k_avg_ms * 1e-3) / 1e9
-    traffic = measured_traffic(kern) if n_tok == 8 else None
+    traffic = measured_traffic(kern, n_tok)
     stages = {k: {"ms_per_launch": round(v[0] / max(v[1], 1), 5), "launches": v[1]} for k, v in prof.items() if v[1]}
     roof = {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
@@ -339,6 +341,63 @@ def decode_bench(args, H, n_tok, layers=None, summary=False):
                 "roofline": roof, "stages": stages}
     res.update(layers=layers, xs=xs, sels=sels, step_bytes=step_bytes)
     return res
+
+
+def shared_q3q2_bench(args, H, layers, n_tok):
+    """The decode step with the shared expert in Q3GU gate/up and Q2D down
+    (the BASELINE configurations' "same formats" option, 6,225,920 bytes),
+    on the same routed experts, inputs and injected routing as the headline,
+    whose shared expert is the reference engine's own Q8_0 (sf37.c:1780-1782).
+    The library runs that shared expert as one more expert of weight 1 with
+    the shared clamp through the Q8_K decode launches, then the routed
+    launches add it."""
+    from sf37_amd import configs, hip, moe
+    K, F, TOPK = moe.EMBD, moe.EXPERT_FF, moe.EXPERT_USED
+    L = hip.lib()
+    shared, structs, xs, lgs, step_bytes = [], [], [], [], []
+    for l, lay in enumerate(layers):
+        seed = moe.layer_seed(args.seed, l)
+        sg = hip.synth_quant("q3", F, K, seed, moe.STREAM["sh_gate"])
+        su = hip.synth_quant("q3", F, K, seed, moe.STREAM["sh_up"])
+        sd = hip.synth_quant("q2", K, F, seed, moe.STREAM["sh_down"])
+        shared.append((sg, su, sd))
+        structs.append(hip.LayerWeights(lay.router.h, lay.router_bias.h, lay.gate.h, lay.up.h, lay.down.h, sg.h,
+                                        su.h, sd.h, lay.n_expert, lay.topk, lay.in_dim, lay.mid_dim, 3.0,
+                                        lay.clamp_routed, lay.clamp_shared, hip.TYPE_F32, hip.TYPE_Q3GU))
+        xs.append(configs.x_device(1, seed, n_tok))
+        lgs.append(hip.Tensor.from_array(configs.logits_for(1, seed, n_tok)))
+    out = hip.Tensor.alloc(n_tok * K * 4)
+    sel = hip.Tensor.alloc(n_tok * TOPK * 4)
+    wts = hip.Tensor.alloc(n_tok * TOPK * 4)
+    n = len(layers)
+
+    def step(i):
+        hip.check(L.sf37_hip_moe_layer(out, sel, wts, structs[i % n], lgs[i % n], xs[i % n], n_tok),
+                  "moe layer (q3q2 shared)")
+
+    for l in range(n):
+        step(l)
+        distinct = len(np.unique(sel.read(np.int32)))
+        sh = sum(t.nbytes for t in shared[l])
+        step_bytes.append(distinct * EXPERT_BYTES + sh + layers[l].router_bytes() + n_tok * K * 4 * 2)
+    for i in range(args.warmup):
+        step(i)
+    H.sync()
+    a, b = H.event(), H.event()
+    H.record(a)
+    for i in range(args.steps):
+        step(i)
+    H.record(b)
+    ms = H.elapsed_ms(a, b) / args.steps
+    H.sync()
+    mean_bytes = float(np.mean([step_bytes[i % n] for i in range(args.steps)]))
+    value = mean_bytes / (ms * 1e-3) / 1e9
+    for t in [out, sel, wts] + xs + lgs + [x for sh in shared for x in sh]:
+        t.free()
+    return {"workload": (f"BASELINE configs[{1 if n_tok == 8 else 0}] with " if n_tok in (1, 8) else "")
+                        + f"the shared expert in Q3GU/Q2D, {n_tok} token(s)",
+            "value": round(value, 2), "unit": "GB/s", "ms_per_step": round(ms, 5),
+            "hbm_bytes_per_step": int(mean_bytes), "pct_of_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 2)}
 
 
 def parity_vs_cpu(layer, x, n_check=None):
@@ -473,7 +532,7 @@ def prefill_bench(args, H, layer, config):
             raise SystemExit(f"bench.py: {k} did not run for config {config}")
         t = f / (k_ms / k_n * 1e-3) / 1e12
         mfma[k] = {"achieved": round(t, 1), "ms_per_launch": round(k_ms / k_n, 4),
-                   "frac": round(t / MFMA_F16_PEAK_TFLOPS, 4)}
+                   "frac": round(t / MFMA_F16_PEAK_TFLOPS, 4), "timing": "HIP events"}
     routed_ms = sum(prof[k][0] / prof[k][1] for k in flops)
     routed_t = sum(flops.values()) / (routed_ms * 1e-3) / 1e12
     counts = np.bincount(sel.read(np.int32).ravel(), minlength=E)
@@ -482,7 +541,9 @@ def prefill_bench(args, H, layer, config):
             "tokens_per_s_per_layer": round(n_tok / (ms * 1e-3), 1),
             "routed_mfma": {"bound": "mfma", "achieved": round(routed_t, 1), "peak": MFMA_F16_PEAK_TFLOPS,
                             "unit": "TFLOP/s", "frac": round(routed_t / MFMA_F16_PEAK_TFLOPS, 4),
-                            "dtype": "f16 operands holding exact small integers, fp32 accumulate"},
+                            "dtype": "f16 operands holding exact small integers, fp32 accumulate",
+                            "timing": "HIP events around each launch on its stream (include the dispatch; "
+                                      "profiles/prefill_layer_kernel_trace.md has rocprofv3 kernel durations)"},
             "kernels": mfma, "max_pairs_per_expert": int(counts.max()), "idle_experts": int((counts == 0).sum()),
             "stage_ms": stages}
 
@@ -564,16 +625,18 @@ def stack_bench(args, H):
     return res
 
 
-def measured_traffic(kern):
-    """HBM bytes per launch of kern from the counter summary in profiles/
-    (rocprofv3 FETCH_SIZE / WRITE_SIZE scaled by a copy calibration), or None."""
-    path = os.path.join(ROOT, "profiles", "decode8_hbm_traffic.md")
+def measured_traffic(kern, n_tok):
+    """HBM bytes per launch of kern at n_tok tokens from the counter summary
+    in profiles/ (rocprofv3 FETCH_SIZE / WRITE_SIZE scaled by a copy
+    calibration, table rows "| kernel | tokens | fetch | write | hbm bytes |"),
+    or None."""
+    path = os.path.join(ROOT, "profiles", "decode_hbm_traffic.md")
     if not os.path.exists(path):
         return None
     for line in open(path):
         cells = [c.strip() for c in line.strip().strip("|").split("|")]
-        if len(cells) == 4 and cells[0] == kern and cells[3].isdigit():
-            return int(cells[3])
+        if len(cells) == 5 and cells[0] == kern and cells[1] == str(n_tok) and cells[4].isdigit():
+            return int(cells[4])
     return None
 
 
