@@ -536,6 +536,21 @@ def prefill_bench(args, H, layer, config):
     routed_ms = sum(prof[k][0] / prof[k][1] for k in flops)
     routed_t = sum(flops.values()) / (routed_ms * 1e-3) / 1e12
     counts = np.bincount(sel.read(np.int32).ravel(), minlength=E)
+    # VALU issue the exact arithmetic needs at least (the matrix-core kernels'
+    # bound): per padded pair, output and 256-block the canonical epilogue's 5
+    # operations; per tile the weights' dequantisation (1.5 operations per Q3
+    # code, 1 per Q2 code); at 16 lanes per cycle per SIMD, 1024 SIMDs, 2.4 GHz
+    tiles = [min(64, c - 64 * i) for c in counts for i in range((int(c) + 63) // 64)]
+    padded = sum(32 * ((t + 31) // 32) for t in tiles)
+    nbk, nbf = K // 256, F // 256
+    valu = {"pf_gate_up": padded * 2 * F * nbk * 5 + len(tiles) * 2 * F * K * 1.5,
+            "pf_down": padded * K * nbf * 5 + len(tiles) * K * F * 1.0}
+    lane_ops_per_s = 1024 * 16 * 2.4e9
+    for k, v in valu.items():
+        ceil_ms = v / lane_ops_per_s * 1e3
+        mfma[k]["valu_ceiling_ms"] = round(ceil_ms, 4)
+        mfma[k]["frac_of_valu_ceiling"] = round(ceil_ms / mfma[k]["ms_per_launch"], 4)
+    mfma["executed_over_algorithmic_flops"] = round(padded / P, 4)
     stages = {k: round(v[0] / v[1], 4) for k, v in prof.items() if v[1]}
     return {"config": config, "tokens": n_tok, "ms_per_layer": round(ms, 4),
             "tokens_per_s_per_layer": round(n_tok / (ms * 1e-3), 1),
