@@ -1228,6 +1228,7 @@ typedef struct {
     float eps;
     float *xn;
     float *sh_out;           /* SHBASE: the shared expert's rows, added by the combine */
+    hipEvent_t comb_wait;    /* SHBASE: the combine waits for it (sh_out made on another stream) */
 } dec_extra;
 
 static uint32_t *dec_counters(uint64_t words) {
@@ -1270,9 +1271,11 @@ static int decode_eligible(const routed_args *a, uint32_t flags) {
  * D), else scratch is used. */
 /* fixed_base != NULL: lay the scratch out in [fixed_base, + fixed_bytes) and
  * use fixed_cnt as the item queues instead of the library's allocations. */
+/* With size_only, only the scratch bytes this call needs are returned there
+ * (nothing is launched). */
 static int decode_run_in(const routed_args *a, const dec_extra *ex, float *out, float *mid, float *down_pair,
                          float *gate_out, float *up_out, char *fixed_base, uint64_t fixed_bytes,
-                         uint32_t *fixed_cnt) {
+                         uint32_t *fixed_cnt, uint64_t *size_only) {
     if (!aligned4(a->gate_w) || !aligned4(a->up_w) || !aligned4(a->down_w) || !aligned4(a->x) ||
         !aligned4(out) || (mid && !aligned4(mid)) || (down_pair && !aligned4(down_pair)) ||
         (gate_out && !aligned4(gate_out)) || (up_out && !aligned4(up_out)))
@@ -1340,6 +1343,10 @@ static int decode_run_in(const routed_args *a, const dec_extra *ex, float *out, 
     if ((ex->flags & SF37_DEC_SELECT) && !ex->sel) TAKE(o_sel, P * 4u);
     if ((ex->flags & SF37_DEC_SELECT) && !ex->wts) TAKE(o_wts, P * 4u);
 #undef TAKE
+    if (size_only) {
+        *size_only = off;
+        return 1;
+    }
     char *base;
     uint32_t *cnt;
     if (fixed_base) {
@@ -1401,20 +1408,24 @@ static int decode_run_in(const routed_args *a, const dec_extra *ex, float *out, 
     p.cnt = cnt;
     const sf37_stream_t st = (sf37_stream_t)g_stream;
     const int down_combine = g_opt_down_combine && sf37k_decode_down_combine_supported(&p);
+    /* a shared expert made on another stream joins before the launch that adds it */
+    const hipEvent_t join = (ex->flags & SF37_DEC_SHBASE) ? ex->comb_wait : NULL;
     return LAUNCH(SF37_HIP_STAGE_DEC_ROUTE, sf37k_decode_route(&p, st), "decode route launch") &&
            ((p.flags & SF37_DEC_UPSEL) ||
             LAUNCH(SF37_HIP_STAGE_DEC_SELECT, sf37k_decode_select(&p, st), "decode select launch")) &&
            LAUNCH(SF37_HIP_STAGE_DEC_UP, sf37k_decode_up(&p, st), "decode up launch") &&
            LAUNCH(SF37_HIP_STAGE_DEC_MID, sf37k_decode_mid(&p, st), "decode mid launch") &&
            (down_combine
-                ? LAUNCH(SF37_HIP_STAGE_DEC_DOWN, sf37k_decode_down_combine(&p, st), "decode down+combine launch")
+                ? (!join || hip_ok(hipStreamWaitEvent(g_stream, join, 0), "shared expert join")) &&
+                      LAUNCH(SF37_HIP_STAGE_DEC_DOWN, sf37k_decode_down_combine(&p, st), "decode down+combine launch")
                 : LAUNCH(SF37_HIP_STAGE_DEC_DOWN, sf37k_decode_down(&p, st), "decode down launch") &&
+                      (!join || hip_ok(hipStreamWaitEvent(g_stream, join, 0), "shared expert join")) &&
                       LAUNCH(SF37_HIP_STAGE_DEC_COMBINE, sf37k_decode_combine(&p, st), "decode combine launch"));
 }
 
 static int decode_run(const routed_args *a, const dec_extra *ex, float *out, float *mid, float *down_pair,
                       float *gate_out, float *up_out) {
-    return decode_run_in(a, ex, out, mid, down_pair, gate_out, up_out, NULL, 0, NULL);
+    return decode_run_in(a, ex, out, mid, down_pair, gate_out, up_out, NULL, 0, NULL, NULL);
 }
 
 /* fp32-activation path for one token (sf37_cuda.cu:5382-5446). */
@@ -1691,23 +1702,52 @@ static int layer_router_typed(float *logits, const sf37_hip_moe_layer_weights *w
 }
 
 /* The Q3GU/Q2D shared expert of n_tok rows: one expert, every token selects
- * it with weight 1.0, the shared clamp (the Q8_K routed pipeline). */
-static int layer_shared_q3q2(float *out, const sf37_hip_moe_layer_weights *w, const float *x, uint32_t n_tok) {
+ * it with weight 1.0, the shared clamp (the Q8_K routed pipeline).  With
+ * joined (decode batches of several tokens, option shared_stream) it runs
+ * on the side stream with scratch of its own (layer buffer 9: its decode
+ * scratch, the counters after it), forked after the rows are ready, beside
+ * the routed launches; *joined then names the event the launch that adds
+ * the rows must wait for (8 tokens: 147 -> 129 us per layer; one token
+ * measured 56 -> 59 us, so a single token stays in order). */
+static int layer_shared_q3q2(float *out, const sf37_hip_moe_layer_weights *w, const float *x, uint32_t n_tok,
+                             hipEvent_t *joined) {
     const uint32_t D = w->in_dim, F = w->mid_dim;
     char *sw = (char *)layer_buf(6, align256((uint64_t)n_tok * 4u) + (uint64_t)n_tok * 4u);
     if (!sw) return 0;
     int32_t *sel = (int32_t *)sw;
     float *wts = (float *)(sw + align256((uint64_t)n_tok * 4u));
+    routed_args a = {(const uint8_t *)w->sh_gate->ptr, (const uint8_t *)w->sh_up->ptr,
+                     (const uint8_t *)w->sh_down->ptr, sel, wts, 1u, 1u, D, F, D, w->clamp_shared, x, n_tok, NULL, NULL,
+                     NULL};
+    const int dec = decode_eligible(&a, 0);
+    dec_extra ex;
+    memset(&ex, 0, sizeof(ex));
+    if (joined) *joined = NULL;
+    if (dec && joined && g_opt_shared_stream && n_tok > 1u) {
+        uint64_t need = 0;
+        if (!decode_run_in(&a, &ex, out, NULL, NULL, NULL, NULL, NULL, 0, NULL, &need)) return 0;
+        const uint64_t cnt_bytes = align256((uint64_t)sf37k_decode_counters(n_tok, 1u, 1u, D, F) * 4u);
+        const int fresh = !g_layer_bufs[9] || g_layer_buf_bytes[9] < cnt_bytes + need;
+        char *buf = (char *)layer_buf(9, cnt_bytes + need);
+        /* the kernels leave their counters zero; a new buffer starts so */
+        if (!buf || (fresh && !hip_ok(hipMemset(buf, 0, cnt_bytes), "shared expert counters clear")) ||
+            !side_stream_ready() || !hip_ok(hipEventRecord(g_ev_fork, g_stream), "shared expert fork") ||
+            !hip_ok(hipStreamWaitEvent(g_side, g_ev_fork, 0), "shared expert fork wait"))
+            return 0;
+        hipStream_t main = g_stream;
+        g_stream = g_side;   /* the library's launches of this call go to the side stream */
+        const int ok = hip_ok(hipMemsetAsync(sel, 0, (uint64_t)n_tok * 4u, g_stream), "shared selection fill") &&
+                       hip_ok(hipMemsetD32Async((hipDeviceptr_t)wts, 0x3f800000, n_tok, g_stream), "shared weight fill") &&
+                       decode_run_in(&a, &ex, out, NULL, NULL, NULL, NULL, buf + cnt_bytes, need, (uint32_t *)buf, NULL) &&
+                       hip_ok(hipEventRecord(g_ev_join, g_side), "shared expert join record");
+        g_stream = main;
+        if (ok) *joined = g_ev_join;
+        return ok;
+    }
     if (!hip_ok(hipMemsetAsync(sel, 0, (uint64_t)n_tok * 4u, g_stream), "shared selection fill") ||
         !hip_ok(hipMemsetD32Async((hipDeviceptr_t)wts, 0x3f800000, n_tok, g_stream), "shared weight fill"))
         return 0;
-    routed_args a = {(const uint8_t *)w->sh_gate->ptr, (const uint8_t *)w->sh_up->ptr,
-                     (const uint8_t *)w->sh_down->ptr, sel, wts, 1u, 1u, D, F, D, w->clamp_shared, x, n_tok, NULL, NULL, NULL};
-    if (decode_eligible(&a, 0)) {
-        dec_extra ex;
-        memset(&ex, 0, sizeof(ex));
-        return decode_run(&a, &ex, out, NULL, NULL, NULL, NULL);
-    }
+    if (dec) return decode_run(&a, &ex, out, NULL, NULL, NULL, NULL);
     return routed_q8k(&a, out, NULL, NULL, NULL, NULL, 0);
 }
 
@@ -1824,12 +1864,14 @@ static int moe_layer_impl(sf37_hip_tensor *out, sf37_hip_tensor *selected, sf37_
     if (fused) {
         /* a Q3GU/Q2D shared expert first, then the routed launches add it */
         float *sh_out = NULL;
+        hipEvent_t join = NULL;
         if (shared_q3) {
             sh_out = (float *)layer_buf(4, (uint64_t)n_tok * D * 4u);
-            if (!sh_out || !layer_shared_q3q2(sh_out, w, xl, n_tok)) return 0;
+            if (!sh_out || !layer_shared_q3q2(sh_out, w, xl, n_tok, &join)) return 0;
         }
         dec_extra ex;
         layer_fused_extra(&ex, w, logits, selected, weights, bn, run_router && router_f32, sh_out);
+        ex.comb_wait = join;
         return decode_run(&a, &ex, (float *)out->ptr, NULL, NULL, NULL, NULL);
     }
     /* layer-owned buffers (separate from the routed scratch): selection,
@@ -1850,7 +1892,7 @@ static int moe_layer_impl(sf37_hip_tensor *out, sf37_hip_tensor *selected, sf37_
     /* shared expert into out: Q3GU/Q2D on the Q8_K path, or Q8_0 gate/up
      * pair -> SwiGLU -> Q8_0 down */
     if (shared_q3) {
-        if (!layer_shared_q3q2((float *)out->ptr, w, xl, n_tok)) return 0;
+        if (!layer_shared_q3q2((float *)out->ptr, w, xl, n_tok, NULL)) return 0;
     } else if (side) {
         a.comb_wait = g_ev_join;   /* launched above; the routed combine joins it */
     } else if (shared_mfma_eligible(n_tok, D, F)) {
@@ -1935,7 +1977,7 @@ int sf37_hip_moe_layer_noalloc(sf37_hip_tensor *out, sf37_hip_tensor *selected, 
     layer_fused_extra(&ex, w, logits_in ? (const float *)logits_in->ptr : NULL, selected, weights, NULL, run_router,
                       NULL);
     return decode_run_in(&a, &ex, (float *)out->ptr, NULL, NULL, NULL, NULL, base + SF37_NOALLOC_QUEUE_BYTES,
-                         SF37_NOALLOC_SCRATCH_BYTES - SF37_NOALLOC_QUEUE_BYTES, (uint32_t *)base);
+                         SF37_NOALLOC_SCRATCH_BYTES - SF37_NOALLOC_QUEUE_BYTES, (uint32_t *)base, NULL);
 }
 
 int sf37_hip_moe_block(sf37_hip_tensor *hidden, sf37_hip_tensor *normed, sf37_hip_tensor *selected,
