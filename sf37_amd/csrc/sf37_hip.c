@@ -1701,6 +1701,31 @@ static int layer_router_typed(float *logits, const sf37_hip_moe_layer_weights *w
                        "moe_layer bf16 router launch");
 }
 
+/* One decode_run_in on the side stream with scratch of its own (layer
+ * buffer 9: the counters, then the decode scratch), forked from the library
+ * stream now; *joined names the event the launch that uses its output must
+ * wait for. */
+static int decode_run_side(const routed_args *a, const dec_extra *ex, float *out, hipEvent_t *joined) {
+    uint64_t need = 0;
+    if (!decode_run_in(a, ex, out, NULL, NULL, NULL, NULL, NULL, 0, NULL, &need)) return 0;
+    const uint64_t cnt_bytes =
+        align256((uint64_t)sf37k_decode_counters(a->n_tok, a->topk, a->n_expert, a->in_dim, a->mid_dim) * 4u);
+    const int fresh = !g_layer_bufs[9] || g_layer_buf_bytes[9] < cnt_bytes + need;
+    char *buf = (char *)layer_buf(9, cnt_bytes + need);
+    /* the kernels leave their counters zero; a new buffer starts so */
+    if (!buf || (fresh && !hip_ok(hipMemset(buf, 0, cnt_bytes), "side counters clear")) || !side_stream_ready() ||
+        !hip_ok(hipEventRecord(g_ev_fork, g_stream), "side fork") ||
+        !hip_ok(hipStreamWaitEvent(g_side, g_ev_fork, 0), "side fork wait"))
+        return 0;
+    hipStream_t main = g_stream;
+    g_stream = g_side;   /* the library's launches of this call go to the side stream */
+    const int ok = decode_run_in(a, ex, out, NULL, NULL, NULL, NULL, buf + cnt_bytes, need, (uint32_t *)buf, NULL) &&
+                   hip_ok(hipEventRecord(g_ev_join, g_side), "side join record");
+    g_stream = main;
+    *joined = ok ? g_ev_join : NULL;
+    return ok;
+}
+
 /* The Q3GU/Q2D shared expert of n_tok rows: one expert, every token selects
  * it with weight 1.0, the shared clamp (the Q8_K routed pipeline).  With
  * joined (decode batches of several tokens, option shared_stream) it runs
@@ -1724,25 +1749,10 @@ static int layer_shared_q3q2(float *out, const sf37_hip_moe_layer_weights *w, co
     memset(&ex, 0, sizeof(ex));
     if (joined) *joined = NULL;
     if (dec && joined && g_opt_shared_stream && n_tok > 1u) {
-        uint64_t need = 0;
-        if (!decode_run_in(&a, &ex, out, NULL, NULL, NULL, NULL, NULL, 0, NULL, &need)) return 0;
-        const uint64_t cnt_bytes = align256((uint64_t)sf37k_decode_counters(n_tok, 1u, 1u, D, F) * 4u);
-        const int fresh = !g_layer_bufs[9] || g_layer_buf_bytes[9] < cnt_bytes + need;
-        char *buf = (char *)layer_buf(9, cnt_bytes + need);
-        /* the kernels leave their counters zero; a new buffer starts so */
-        if (!buf || (fresh && !hip_ok(hipMemset(buf, 0, cnt_bytes), "shared expert counters clear")) ||
-            !side_stream_ready() || !hip_ok(hipEventRecord(g_ev_fork, g_stream), "shared expert fork") ||
-            !hip_ok(hipStreamWaitEvent(g_side, g_ev_fork, 0), "shared expert fork wait"))
-            return 0;
-        hipStream_t main = g_stream;
-        g_stream = g_side;   /* the library's launches of this call go to the side stream */
-        const int ok = hip_ok(hipMemsetAsync(sel, 0, (uint64_t)n_tok * 4u, g_stream), "shared selection fill") &&
-                       hip_ok(hipMemsetD32Async((hipDeviceptr_t)wts, 0x3f800000, n_tok, g_stream), "shared weight fill") &&
-                       decode_run_in(&a, &ex, out, NULL, NULL, NULL, NULL, buf + cnt_bytes, need, (uint32_t *)buf, NULL) &&
-                       hip_ok(hipEventRecord(g_ev_join, g_side), "shared expert join record");
-        g_stream = main;
-        if (ok) *joined = g_ev_join;
-        return ok;
+        /* the fills go to the library stream, before the fork */
+        return hip_ok(hipMemsetAsync(sel, 0, (uint64_t)n_tok * 4u, g_stream), "shared selection fill") &&
+               hip_ok(hipMemsetD32Async((hipDeviceptr_t)wts, 0x3f800000, n_tok, g_stream), "shared weight fill") &&
+               decode_run_side(&a, &ex, out, joined);
     }
     if (!hip_ok(hipMemsetAsync(sel, 0, (uint64_t)n_tok * 4u, g_stream), "shared selection fill") ||
         !hip_ok(hipMemsetD32Async((hipDeviceptr_t)wts, 0x3f800000, n_tok, g_stream), "shared weight fill"))
