@@ -757,11 +757,18 @@ struct sh_raw {
     uint32_t s[4];
 };
 
-__device__ __forceinline__ void sh_ready(sh_raw &r) {
-    asm volatile("" : "+v"(r.c[0]), "+v"(r.c[1]), "+v"(r.c[2]), "+v"(r.c[3]), "+v"(r.c[4]), "+v"(r.c[5]),
-                 "+v"(r.c[6]), "+v"(r.c[7]), "+v"(r.c[8]), "+v"(r.c[9]), "+v"(r.c[10]));
-    asm volatile("" : "+v"(r.c[11]), "+v"(r.c[12]), "+v"(r.c[13]), "+v"(r.c[14]), "+v"(r.c[15]), "+v"(r.c[16]),
-                 "+v"(r.c[17]), "+v"(r.s[0]), "+v"(r.s[1]), "+v"(r.s[2]), "+v"(r.s[3]));
+// What a lane loads of a K chunk: its half of the row's 136 bytes, dwords
+// 17 kh .. 17 kh + 16, contiguous (five loads instead of one per block
+// piece; lanes l and l + 32 hold the same row).
+struct sh_half {
+    uint32_t w[17];
+};
+
+__device__ __forceinline__ void sh_ready(sh_half &h) {
+    asm volatile("" : "+v"(h.w[0]), "+v"(h.w[1]), "+v"(h.w[2]), "+v"(h.w[3]), "+v"(h.w[4]), "+v"(h.w[5]),
+                 "+v"(h.w[6]), "+v"(h.w[7]), "+v"(h.w[8]));
+    asm volatile("" : "+v"(h.w[9]), "+v"(h.w[10]), "+v"(h.w[11]), "+v"(h.w[12]), "+v"(h.w[13]), "+v"(h.w[14]),
+                 "+v"(h.w[15]), "+v"(h.w[16]));
 }
 
 // dword offsets (within the chunk) of block jj's first code dword for half
@@ -776,16 +783,41 @@ static_assert(sh_code_dw(0) == 0 && sh_code_dw(1) == 9 && sh_code_dw(2) == 17 &&
               "chunk word offsets");
 static_assert(sh_code_reg(1) == 5 && sh_code_reg(2) == 9 && sh_code_reg(3) == 14 && sh_code_reg(4) == 18,
               "code dword slots");
+static_assert(2u * 17u * 4u == SH_CB * SF37_Q8_0_BYTES, "the two halves cover the chunk exactly");
 
-__device__ __forceinline__ void sh_load(sh_raw &r, const uint8_t *wrow, uint32_t c, uint32_t kh) {
-    const uint32_t *q = (const uint32_t *)(wrow + (uint64_t)c * (SH_CB * SF37_Q8_0_BYTES));
+__device__ __forceinline__ void sh_load(sh_half &h, const uint8_t *wrow, uint32_t c, uint32_t kh) {
+    const uint32_t *q = (const uint32_t *)(wrow + (uint64_t)c * (SH_CB * SF37_Q8_0_BYTES)) + 17u * kh;
 #pragma unroll
-    for (uint32_t jj = 0; jj < SH_CB; jj++) {
+    for (uint32_t i = 0; i < 17u; i++) h.w[i] = q[i];
+}
+
+// The chunk's words in the MFMA layout: half kh needs, per block, the code
+// dwords sh_code_dw(jj) + 4 kh .. (+4 or +5) and the scale dwords 0, 8, 17,
+// 25.  permlane32_swap(A, B) gives [A of lanes 0-31, B of lanes 0-31] and
+// [A of lanes 32-63, B of lanes 32-63]: with A = dword i and B = dword
+// 4 + i of each half, the first is block 0's dword i of both halves (dword i
+// for kh = 0, dword 4 + i for kh = 1), the second block 2's (17 + i, 21 + i);
+// blocks 1 and 3 likewise from dwords 9 + i and 13 + i; a swap of a dword
+// with itself hands both halves the scale dwords 0 and 17 (8 and 25).
+__device__ __forceinline__ void sh_swap(sh_raw &r, const sh_half &h) {
 #pragma unroll
-        for (uint32_t i = 0; i < sh_code_reg(jj + 1u) - sh_code_reg(jj); i++)
-            r.c[sh_code_reg(jj) + i] = q[sh_code_dw(jj) + 4u * kh + i];
-        r.s[jj] = q[sh_scale_dw(jj)];
+    for (uint32_t i = 0; i < 5u; i++) {
+        const auto v = __builtin_amdgcn_permlane32_swap(h.w[i], h.w[4u + i], false, false);
+        r.c[sh_code_reg(0) + i] = v[0];
+        r.c[sh_code_reg(2) + i] = v[1];
     }
+#pragma unroll
+    for (uint32_t i = 0; i < 4u; i++) {
+        const auto v = __builtin_amdgcn_permlane32_swap(h.w[9u + i], h.w[13u + i], false, false);
+        r.c[sh_code_reg(1) + i] = v[0];
+        r.c[sh_code_reg(3) + i] = v[1];
+    }
+    const auto s0 = __builtin_amdgcn_permlane32_swap(h.w[0], h.w[0], false, false);
+    const auto s1 = __builtin_amdgcn_permlane32_swap(h.w[8], h.w[8], false, false);
+    r.s[0] = s0[0];
+    r.s[2] = s0[1];
+    r.s[1] = s1[0];
+    r.s[3] = s1[1];
 }
 
 typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
@@ -878,25 +910,31 @@ __global__ void __launch_bounds__(256, 2) sh_gemm_kernel(sh_params p) {
     for (uint32_t i = 0; i < SH_TB; i++)
 #pragma unroll
         for (int r2 = 0; r2 < 16; r2++) acc[i][r2] = 0.0f;
-    sh_raw ra, rb;
+    sh_half ha, hb;
     issue(0);
-    sh_load(ra, wrow, 0, kh);
+    sh_load(ha, wrow, 0, kh);
     const uint32_t last = nchunk - 1u;
     for (uint32_t c = 0; c < nchunk; c += 2u) {
         const uint32_t c1 = c + 1u < nchunk ? c + 1u : last, c2 = c + 2u < nchunk ? c + 2u : last;
         wait_vm0();
-        sh_ready(ra);
+        sh_ready(ha);
         __syncthreads();
         issue(c1);
-        sh_load(rb, wrow, c1, kh);
-        sh_chunk(ra, s_act[c & 1u], s_xs[c & 1u], kh, col, acc);
+        {
+            sh_raw r;
+            sh_swap(r, ha);
+            sh_load(hb, wrow, c1, kh);
+            sh_chunk(r, s_act[c & 1u], s_xs[c & 1u], kh, col, acc);
+        }
         if (c + 1u < nchunk) {
             wait_vm0();
-            sh_ready(rb);
+            sh_ready(hb);
             __syncthreads();
             issue(c2);
-            sh_load(ra, wrow, c2, kh);
-            sh_chunk(rb, s_act[(c + 1u) & 1u], s_xs[(c + 1u) & 1u], kh, col, acc);
+            sh_raw r;
+            sh_swap(r, hb);
+            sh_load(ha, wrow, c2, kh);
+            sh_chunk(r, s_act[(c + 1u) & 1u], s_xs[(c + 1u) & 1u], kh, col, acc);
         }
     }
     wait_vm0();
