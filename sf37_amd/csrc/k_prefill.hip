@@ -304,23 +304,23 @@ struct q2_raw {
     uint32_t w[4][2];
 };
 
+
 __device__ __forceinline__ void raw_ready(q3_raw &r) {
     asm volatile("" : "+v"(r.h[0]), "+v"(r.h[1]), "+v"(r.h[2]), "+v"(r.h[3]), "+v"(r.w[0][0]), "+v"(r.w[0][1]),
                  "+v"(r.w[0][2]), "+v"(r.w[0][3]), "+v"(r.w[1][0]), "+v"(r.w[1][1]), "+v"(r.w[1][2]),
                  "+v"(r.w[1][3]), "+v"(r.w[2][0]), "+v"(r.w[2][1]), "+v"(r.w[2][2]), "+v"(r.w[2][3]),
                  "+v"(r.w[3][0]), "+v"(r.w[3][1]), "+v"(r.w[3][2]), "+v"(r.w[3][3]));
 }
-__device__ __forceinline__ void raw_ready(q2_raw &r) {
-    asm volatile("" : "+v"(r.h[0]), "+v"(r.h[1]), "+v"(r.h[2]), "+v"(r.w[0][0]), "+v"(r.w[0][1]), "+v"(r.w[1][0]),
-                 "+v"(r.w[1][1]), "+v"(r.w[2][0]), "+v"(r.w[2][1]), "+v"(r.w[3][0]), "+v"(r.w[3][1]));
-}
 
 typedef uint32_t u32x4a __attribute__((ext_vector_type(4), aligned(4)));
 typedef uint32_t u32x3a __attribute__((ext_vector_type(3), aligned(4)));
 typedef uint32_t u32x2a __attribute__((ext_vector_type(2), aligned(4)));
 
-// Dword loads (no register tuples): the words go straight into the
-// registers the loop carries them in, so no copy waits for the data.
+// Q3 words as dword loads (no register tuples): the words go straight into
+// the registers the loop carries them in, so no copy waits for the data.
+// (Contiguous half-block loads with lane swaps, as the Q2 blocks below,
+// measured 1.5 % slower here: twelve swaps per block cost more VALU than
+// the sixteen fewer loads save in this VALU-bound kernel.)
 __device__ __forceinline__ void q3_load(q3_raw &r, const uint8_t *hp, const uint8_t *pp) {
     const uint32_t *h = (const uint32_t *)hp;
 #pragma unroll
@@ -332,17 +332,46 @@ __device__ __forceinline__ void q3_load(q3_raw &r, const uint8_t *hp, const uint
         for (int i = 0; i < 4; i++) r.w[g][i] = q[i];
     }
 }
-__device__ __forceinline__ void q2_load(q2_raw &r, const uint8_t *hp, const uint8_t *pp) {
-    const uint32_t *h = (const uint32_t *)hp;
-#pragma unroll
-    for (int i = 0; i < 3; i++) r.h[i] = h[i];
-#pragma unroll
-    for (int g = 0; g < 4; g++) {
-        const uint32_t *q = (const uint32_t *)(pp + 16 * g);
-        r.w[g][0] = q[0];
-        r.w[g][1] = q[1];
-    }
+
+
+// What a lane loads of a Q2 block (21 dwords): dwords 8 kh .. 8 kh + 10,
+// contiguous (three loads instead of eleven); pf_words then trades what each
+// half needs from the other with v_permlane32_swap (lanes l and l + 32 hold
+// the same row).
+struct q2_half {
+    uint32_t w[11];
+};
+__device__ __forceinline__ void raw_ready(q2_half &r) {
+    asm volatile("" : "+v"(r.w[0]), "+v"(r.w[1]), "+v"(r.w[2]), "+v"(r.w[3]), "+v"(r.w[4]), "+v"(r.w[5]),
+                 "+v"(r.w[6]), "+v"(r.w[7]), "+v"(r.w[8]), "+v"(r.w[9]), "+v"(r.w[10]));
 }
+__device__ __forceinline__ void q2_load_half(q2_half &r, const uint8_t *bp, uint32_t kh) {
+    const uint32_t *q = (const uint32_t *)bp + 8u * kh;
+#pragma unroll
+    for (int i = 0; i < 11; i++) r.w[i] = q[i];
+}
+// q2_raw of both halves: the header dwords 0..2 and group g's dwords
+// 3 + 4 g + 2 kh, +1.  permlane32_swap(A, B) gives [A of lanes 0-31, B of
+// lanes 0-31] and [A of lanes 32-63, B of lanes 32-63]; with A, B = loaded
+// dwords (3, 5), (4, 6), (7, 9), (8, 10) the first is a word of group 0 or 1
+// for both halves, the second the same word of group 2 or 3 (8 dwords on);
+// a swap of dword j with itself hands both halves header dword j.
+__device__ __forceinline__ q2_raw pf_words(const q2_half &h) {
+    q2_raw r;
+#pragma unroll
+    for (int j = 0; j < 3; j++) r.h[j] = __builtin_amdgcn_permlane32_swap(h.w[j], h.w[j], false, false)[0];
+#pragma unroll
+    for (int g = 0; g < 2; g++) {
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const auto v = __builtin_amdgcn_permlane32_swap(h.w[3 + 4 * g + i], h.w[5 + 4 * g + i], false, false);
+            r.w[g][i] = v[0];
+            r.w[g + 2][i] = v[1];
+        }
+    }
+    return r;
+}
+__device__ __forceinline__ const q3_raw &pf_words(const q3_raw &r) { return r; }
 
 // 32 bits of the lane's string starting at bit SH + o of the loaded words.
 template <int SH, int O>
@@ -607,7 +636,7 @@ __device__ __forceinline__ void pf_body(const pf_params &p, const uint8_t *wrow,
         if constexpr (NBUF == 3u) wait_vm_keep_next();
         else wait_vm0();
     };
-    using RAW = typename std::conditional<Q3, q3_raw, q2_raw>::type;
+    using RAW = typename std::conditional<Q3, q3_raw, q2_half>::type;
     RAW ra, rb;
     auto wload = [&](RAW &r, uint32_t bn) {
         if constexpr (Q3) {
@@ -615,8 +644,7 @@ __device__ __forceinline__ void pf_body(const pf_params &p, const uint8_t *wrow,
             const uint32_t o = SF37_Q3_BYTES * bn;
             q3_load(r, wrow + (o & ~3u), wrow + ((o + 12u + 12u * kh) & ~3u));
         } else {
-            const uint8_t *bp = wrow + (uint64_t)SF37_Q2_BYTES * bn;
-            q2_load(r, bp, bp + 12u + 8u * kh);
+            q2_load_half(r, wrow + (uint64_t)SF37_Q2_BYTES * bn, kh);
         }
     };
     // the block's loads: weights of bn into r, activations of ba
@@ -634,13 +662,13 @@ __device__ __forceinline__ void pf_body(const pf_params &p, const uint8_t *wrow,
         raw_ready(ra);
         __syncthreads();
         const uint32_t b1 = clampb(b + 1u), b2 = clampb(b + 2u), b3 = clampb(b + 3u);
-        pf_block<Q3, 0, NTB>(ra, s_act[b % NBUF], s_cd[b % NBUF], kh, col, acc, blk,
+        pf_block<Q3, 0, NTB>(pf_words(ra), s_act[b % NBUF], s_cd[b % NBUF], kh, col, acc, blk,
                              [&](int c, int nc) { pre(rb, b1, NBUF == 3u ? b2 : b1, c, nc); });
         if (b + 1u < nblk) {
             top();
             raw_ready(rb);
             __syncthreads();
-            pf_block<Q3, SH2, NTB>(rb, s_act[(b + 1u) % NBUF], s_cd[(b + 1u) % NBUF], kh, col, acc, blk,
+            pf_block<Q3, SH2, NTB>(pf_words(rb), s_act[(b + 1u) % NBUF], s_cd[(b + 1u) % NBUF], kh, col, acc, blk,
                                    [&](int c, int nc) { pre(ra, b2, NBUF == 3u ? b3 : b2, c, nc); });
         }
     }
