@@ -722,7 +722,6 @@ __device__ __forceinline__ void pf_body(const pf_params &p, const uint8_t *wrow,
 // 16 kh .. 16 kh + 15 of a block, for activations and weights alike.
 // ---------------------------------------------------------------------------
 constexpr uint32_t SH_T = 64;                  // tokens per tile
-constexpr uint32_t SH_TB = SH_T / 32u;         // 32-token blocks per tile
 constexpr uint32_t SH_CB = 4;                  // Q8_0 blocks per K chunk
 constexpr uint32_t SH_RS = SH_CB * 32u;        // LDS bytes per token row of a chunk (int8 codes)
 constexpr uint32_t SH_BUF = SH_T * SH_RS;      // one chunk buffer
@@ -851,12 +850,13 @@ __device__ __forceinline__ void sh_swap(sh_raw &r, const sh_half &h) {
 typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 typedef int32_t i32x16 __attribute__((ext_vector_type(16)));
 
-// One K chunk (SH_CB Q8_0 blocks) for SH_TB token blocks.
+// One K chunk (SH_CB Q8_0 blocks) for TBW token blocks from token block tb0.
+template <int TBW>
 __device__ __forceinline__ void sh_chunk(const sh_raw &r, const uint8_t *act_lds, const float *xs_lds,
-                                         uint32_t kh, uint32_t col, float (*acc)[16]) {
-    const uint8_t *a_row = act_lds + col * SH_RS;     // token row col of token block 0
+                                         uint32_t kh, uint32_t col, uint32_t tb0, float (*acc)[16]) {
+    const uint8_t *a_row = act_lds + (32u * tb0 + col) * SH_RS;   // token row col of token block tb0
     const uint32_t sw = col & 7u;                      // the row's slot swizzle (32 i + col has the same)
-    const float *x_lane = xs_lds + 4u * kh;
+    const float *x_lane = xs_lds + 32u * tb0 + 4u * kh;
     const i32x16 magic = (i32x16)SH_MAGIC_BITS;
 #pragma unroll
     for (uint32_t jj = 0; jj < SH_CB; jj++) {
@@ -870,14 +870,14 @@ __device__ __forceinline__ void sh_chunk(const sh_raw &r, const uint8_t *act_lds
         const uint32_t slot = ((2u * jj + kh) ^ sw) * 16u;
         // the MFMAs of every token block first, so the epilogue of one block
         // runs while the matrix cores still work on the next
-        i32x16 D[SH_TB];
+        i32x16 D[TBW];
 #pragma unroll
-        for (uint32_t i = 0; i < SH_TB; i++) {
+        for (uint32_t i = 0; i < TBW; i++) {
             const i32x4 a = *(const i32x4 *)(a_row + i * 32u * SH_RS + slot);
             D[i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, magic, 0, 0, 0);
         }
 #pragma unroll
-        for (uint32_t i = 0; i < SH_TB; i++) {
+        for (uint32_t i = 0; i < TBW; i++) {
             // the whole result reinterpreted at once (a bit_cast of one
             // vector element would name the vector's storage, i.e. element 0)
             const f16v F = __builtin_bit_cast(f16v, D[i]);
@@ -896,20 +896,26 @@ __device__ __forceinline__ void sh_chunk(const sh_raw &r, const uint8_t *act_lds
     }
 }
 
-// GU: gate/up, 128 weight columns per workgroup = 16 gate + 16 up rows per
-// wave, epilogue mid = (g*sig(g))*u (shared clamp).  Otherwise down: 32
-// output rows per wave, out written directly.
-template <bool GU>
+// GU: gate/up, 16 gate + 16 up rows per wave, epilogue mid = (g*sig(g))*u
+// (shared clamp).  Otherwise down: 32 output rows per wave, out written
+// directly.  TBW = 2: a wave takes both 32-token blocks of the tile, the
+// workgroup 128 weight columns; TBW = 1 (batches whose TBW = 2 grid would
+// leave CUs idle): waves 2 c and 2 c + 1 take token block 0 and 1 of the
+// same 32 columns, the workgroup 64 columns.
+template <bool GU, int TBW>
 __global__ void __launch_bounds__(256, 2) sh_gemm_kernel(sh_params p) {
     __shared__ __align__(16) uint8_t s_act[2][SH_BUF];
     __shared__ __align__(16) float s_xs[2][SH_CB * SH_T];
+    static_assert(TBW == 1 || TBW == 2, "token blocks per wave");
     const uint32_t tt = blockIdx.x % p.n_tt, ct = blockIdx.x / p.n_tt;
     const uint32_t tid = threadIdx.x, lane = tid & 63u, kh = lane >> 5, col = lane & 31u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t tb0 = TBW == 2 ? 0u : (wave & 1u), cg = TBW == 2 ? wave : wave >> 1;
+    constexpr uint32_t COLS = 64u * TBW;               // weight columns per workgroup
     const uint32_t t0 = tt * SH_T;
     const uint32_t nb = p.nb, nchunk = nb / SH_CB;
     // this lane's weight row
-    const uint32_t wcol = GU ? ct * 64u + 16u * wave + (col & 15u) : ct * 128u + 32u * wave + col;
+    const uint32_t wcol = GU ? ct * (COLS / 2u) + 16u * cg + (col & 15u) : ct * COLS + 32u * cg + col;
     const bool second = GU && col >= 16u;
     const uint8_t *wrow = (second ? p.w1 : p.w0) + (uint64_t)wcol * nb * SF37_Q8_0_BYTES;
     // DMA: load L = 2 wave + k fills rows 8 L .. 8 L + 7; lane l writes row
@@ -933,9 +939,9 @@ __global__ void __launch_bounds__(256, 2) sh_gemm_kernel(sh_params p) {
         lds_dma4(xs_l + bf * (SH_CB * SH_T * 4u) + wave * SH_T * 4u, tok_dma * nb * 4u,
                  (const uint8_t *)p.xs + ((uint64_t)c * SH_CB + wave) * 4u);
     };
-    float acc[SH_TB][16];
+    float acc[TBW][16];
 #pragma unroll
-    for (uint32_t i = 0; i < SH_TB; i++)
+    for (uint32_t i = 0; i < (uint32_t)TBW; i++)
 #pragma unroll
         for (int r2 = 0; r2 < 16; r2++) acc[i][r2] = 0.0f;
     sh_half ha, hb;
@@ -952,7 +958,7 @@ __global__ void __launch_bounds__(256, 2) sh_gemm_kernel(sh_params p) {
             sh_raw r;
             sh_swap(r, ha);
             sh_load(hb, wrow, c1, kh);
-            sh_chunk(r, s_act[c & 1u], s_xs[c & 1u], kh, col, acc);
+            sh_chunk<TBW>(r, s_act[c & 1u], s_xs[c & 1u], kh, col, tb0, acc);
         }
         if (c + 1u < nchunk) {
             wait_vm0();
@@ -962,15 +968,15 @@ __global__ void __launch_bounds__(256, 2) sh_gemm_kernel(sh_params p) {
             sh_raw r;
             sh_swap(r, hb);
             sh_load(ha, wrow, c2, kh);
-            sh_chunk(r, s_act[(c + 1u) & 1u], s_xs[(c + 1u) & 1u], kh, col, acc);
+            sh_chunk<TBW>(r, s_act[(c + 1u) & 1u], s_xs[(c + 1u) & 1u], kh, col, tb0, acc);
         }
     }
     wait_vm0();
 #pragma unroll
-    for (uint32_t i = 0; i < SH_TB; i++) {
+    for (uint32_t i = 0; i < (uint32_t)TBW; i++) {
 #pragma unroll
         for (int r2 = 0; r2 < 16; r2++) {
-            const uint32_t t = t0 + 32u * i + 8u * (r2 >> 2) + 4u * kh + (r2 & 3);
+            const uint32_t t = t0 + 32u * (tb0 + i) + 8u * (r2 >> 2) + 4u * kh + (r2 & 3);
             const float v = acc[i][r2];
             if constexpr (GU) {
                 const float o = __shfl_xor(v, 16, 64);
@@ -1074,6 +1080,19 @@ extern "C" int sf37k_pf_down(float *down_pair, const uint8_t *down_w, const void
     return (int)hipGetLastError();
 }
 
+// The 64-column shared GEMM when the 128-column grid (n_ct x n_tt
+// workgroups) would not fill the resident slots once (three per CU).
+static bool sh_narrow(uint32_t n_ct, uint32_t n_tt) {
+    static int cus = 0;
+    if (!cus) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+            cus = 256;
+    }
+    return (uint64_t)n_ct * n_tt < 3ull * (uint64_t)cus;
+}
+
 extern "C" int sf37k_sh_supported(uint32_t in_dim, uint32_t mid_dim, uint32_t out_dim) {
     return in_dim % (32u * SH_CB * 2u) == 0 && mid_dim % (32u * SH_CB * 2u) == 0 && mid_dim % 64u == 0 &&
            out_dim % 128u == 0 && in_dim > 0 && mid_dim > 0;
@@ -1099,10 +1118,15 @@ extern "C" int sf37k_sh_gate_up(float *mid, const uint8_t *gate_w, const uint8_t
     p.n_tok = n_tok;
     p.nb = in_dim / 32u;
     p.rows = mid_dim;
-    p.n_ct = mid_dim / 64u;
     p.n_tt = (n_tok + SH_T - 1u) / SH_T;
     p.clamp = clamp;
-    hipLaunchKernelGGL(sh_gemm_kernel<true>, dim3(p.n_ct * p.n_tt), dim3(256), 0, (hipStream_t)s, p);
+    if (sh_narrow(mid_dim / 64u, p.n_tt)) {
+        p.n_ct = mid_dim / 32u;
+        hipLaunchKernelGGL((sh_gemm_kernel<true, 1>), dim3(p.n_ct * p.n_tt), dim3(256), 0, (hipStream_t)s, p);
+    } else {
+        p.n_ct = mid_dim / 64u;
+        hipLaunchKernelGGL((sh_gemm_kernel<true, 2>), dim3(p.n_ct * p.n_tt), dim3(256), 0, (hipStream_t)s, p);
+    }
     return (int)hipGetLastError();
 }
 
@@ -1116,8 +1140,13 @@ extern "C" int sf37k_sh_down(float *out, const uint8_t *down_w, const void *a8, 
     p.n_tok = n_tok;
     p.nb = mid_dim / 32u;
     p.rows = out_dim;
-    p.n_ct = out_dim / 128u;
     p.n_tt = (n_tok + SH_T - 1u) / SH_T;
-    hipLaunchKernelGGL(sh_gemm_kernel<false>, dim3(p.n_ct * p.n_tt), dim3(256), 0, (hipStream_t)s, p);
+    if (sh_narrow(out_dim / 128u, p.n_tt)) {
+        p.n_ct = out_dim / 64u;
+        hipLaunchKernelGGL((sh_gemm_kernel<false, 1>), dim3(p.n_ct * p.n_tt), dim3(256), 0, (hipStream_t)s, p);
+    } else {
+        p.n_ct = out_dim / 128u;
+        hipLaunchKernelGGL((sh_gemm_kernel<false, 2>), dim3(p.n_ct * p.n_tt), dim3(256), 0, (hipStream_t)s, p);
+    }
     return (int)hipGetLastError();
 }
