@@ -1081,7 +1081,9 @@ extern "C" int sf37k_pf_down(float *down_pair, const uint8_t *down_w, const void
 }
 
 // The 64-column shared GEMM when the 128-column grid (n_ct x n_tt
-// workgroups) would not fill the resident slots once (three per CU).
+// workgroups) is under two workgroups per CU (measured crossover: at 2048
+// tokens the 128-column gate/up grid of 640 workgroups takes 128 us, the
+// 64-column one 157 us; at 512 tokens 64 columns win, 73 against 75 us).
 static bool sh_narrow(uint32_t n_ct, uint32_t n_tt) {
     static int cus = 0;
     if (!cus) {
@@ -1090,7 +1092,7 @@ static bool sh_narrow(uint32_t n_ct, uint32_t n_tt) {
             hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
             cus = 256;
     }
-    return (uint64_t)n_ct * n_tt < 3ull * (uint64_t)cus;
+    return (uint64_t)n_ct * n_tt < 2ull * (uint64_t)cus;
 }
 
 extern "C" int sf37k_sh_supported(uint32_t in_dim, uint32_t mid_dim, uint32_t out_dim) {
