@@ -56,6 +56,19 @@ __device__ __forceinline__ uint32_t clamp_expert(int32_t e, uint32_t n) {
     return (e < 0 || (uint32_t)e >= n) ? 0u : (uint32_t)e;
 }
 
+// Expert ids a grouping sees: the E routed experts, and with SH9 the shared
+// expert as id E.
+__device__ __forceinline__ uint32_t n_ids(const sf37_dec_params &p) {
+    return p.E + ((p.flags & SF37_DEC_SH9) ? 1u : 0u);
+}
+
+// Weight bytes of expert e of a matrix (w: the routed experts, exp_bytes
+// apart; sh: the shared expert, id E with SH9).
+__device__ __forceinline__ const uint8_t *expert_base(const sf37_dec_params &p, const uint8_t *w, const uint8_t *sh,
+                                                      uint32_t e, uint64_t exp_bytes) {
+    return e < p.E ? w + (uint64_t)e * exp_bytes : sh;
+}
+
 }  // namespace
 
 using dec_params = sf37_dec_params;
@@ -290,12 +303,17 @@ __device__ void token_topk(const dec_params &p, uint32_t t, int32_t *sel_out, fl
     const float *cp = p.cand_p + (uint64_t)t * p.E;
     int32_t *so[1] = {sel_out};
     float *wo[1] = {w_out};
+    const uint32_t sh9 = (p.flags & SF37_DEC_SH9) ? 1u : 0u;
     sf37_wave_topk_cand<1>(
         [ck, cp](uint32_t, uint32_t e, float &pr) {
             pr = cp[e];
             return ck[e];
         },
-        p.E, p.topk, p.scale, so, wo);
+        p.E, p.topk - sh9, p.scale, so, wo);
+    if (sh9 && (threadIdx.x & 63u) == 0u) {   // the shared expert's slot: id E, weight 1
+        sel_out[p.topk - 1u] = (int32_t)p.E;
+        w_out[p.topk - 1u] = 1.0f;
+    }
 }
 
 // Inclusive sum over the wave's lanes (DPP row shifts, then rows 0-1 into
@@ -329,10 +347,10 @@ __device__ void group_pairs(const dec_params &p, const uint32_t *s_sel, uint32_t
     uint32_t *s_e = st + GROUP_MAX_E, *s_se = s_e + DEC_MAX_TOK * 16u;
     uint32_t *s_tot = s_se + DEC_MAX_TOK * 16u, *s_wcnt = s_tot + 2u;
     const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u, nthr = blockDim.x;
-    const uint32_t P = p.T * p.topk;
+    const uint32_t P = p.T * p.topk, ne = n_ids(p);
     if (p.flags & SF37_DEC_SLOTS) {
         if (threadIdx.x < p.topk) {
-            const uint32_t s = threadIdx.x, e = clamp_expert((int32_t)s_sel[s], p.E);
+            const uint32_t s = threadIdx.x, e = clamp_expert((int32_t)s_sel[s], ne);
             so[s] = s;
             gi[1u + s] = s;
             gi[2u + p.G + s] = e;
@@ -353,46 +371,46 @@ __device__ void group_pairs(const dec_params &p, const uint32_t *s_sel, uint32_t
         __syncthreads();
         return;
     }
-    const bool masks = p.E <= GROUP_MAX_E;
+    const bool masks = ne <= GROUP_MAX_E;
     if (masks) {
-        for (uint32_t e = threadIdx.x; e < p.E; e += nthr) msk[e] = 0u;
+        for (uint32_t e = threadIdx.x; e < ne; e += nthr) msk[e] = 0u;
         __syncthreads();
         if (threadIdx.x < P)
-            atomicOr(&msk[clamp_expert((int32_t)s_sel[threadIdx.x], p.E)], 1u << (threadIdx.x / p.topk));
+            atomicOr(&msk[clamp_expert((int32_t)s_sel[threadIdx.x], ne)], 1u << (threadIdx.x / p.topk));
         __syncthreads();
         if (wave == 0) {
             // lane l: experts [c l, c l + c); exclusive scans of the pair
             // counts and of the non-empty experts
-            const uint32_t c = (p.E + 63u) >> 6, e0 = lane * c;
+            const uint32_t c = (ne + 63u) >> 6, e0 = lane * c;
             uint32_t n = 0, g = 0;
             for (uint32_t i = 0; i < c; i++) {
                 const uint32_t e = e0 + i;
-                if (e < p.E) {
+                if (e < ne) {
                     const uint32_t m = msk[e];
                     n += (uint32_t)__builtin_popcount(m);
                     g += m != 0u;
                 }
             }
             const uint32_t ni = wave_incl_sum(n), gin = wave_incl_sum(g);
-            uint32_t ne = ni - n, ge = gin - g;
+            uint32_t np = ni - n, ge = gin - g;
             if (lane == 63u) {
                 s_tot[0] = ni;
                 s_tot[1] = gin;
             }
             for (uint32_t i = 0; i < c; i++) {
                 const uint32_t e = e0 + i;
-                if (e < p.E) {
+                if (e < ne) {
                     const uint32_t m = msk[e];
-                    st[e] = ne;
+                    st[e] = np;
                     if (m) {
-                        gi[1u + ge] = ne;
+                        gi[1u + ge] = np;
                         gi[2u + p.G + ge] = e;
                         if (publish) {
-                            p.ginfo[1u + ge] = ne;
+                            p.ginfo[1u + ge] = np;
                             p.ginfo[2u + p.G + ge] = e;
                         }
                         ge++;
-                        ne += (uint32_t)__builtin_popcount(m);
+                        np += (uint32_t)__builtin_popcount(m);
                     }
                 }
             }
@@ -410,7 +428,7 @@ __device__ void group_pairs(const dec_params &p, const uint32_t *s_sel, uint32_t
             }
         }
         if (threadIdx.x < P) {
-            const uint32_t i = threadIdx.x, e = clamp_expert((int32_t)s_sel[i], p.E), t = i / p.topk;
+            const uint32_t i = threadIdx.x, e = clamp_expert((int32_t)s_sel[i], ne), t = i / p.topk;
             const uint32_t pos = st[e] + (uint32_t)__builtin_popcount(msk[e] & ((1u << t) - 1u));
             so[pos] = i;
             if (publish) p.sorted[pos] = i;
@@ -419,7 +437,7 @@ __device__ void group_pairs(const dec_params &p, const uint32_t *s_sel, uint32_t
         return;
     }
     // a token holds an expert twice: each pair counts the pairs before it
-    if (threadIdx.x < P) s_e[threadIdx.x] = clamp_expert((int32_t)s_sel[threadIdx.x], p.E);
+    if (threadIdx.x < P) s_e[threadIdx.x] = clamp_expert((int32_t)s_sel[threadIdx.x], ne);
     __syncthreads();
     if (threadIdx.x < P) {
         const uint32_t i = threadIdx.x, e = s_e[i];
@@ -920,8 +938,8 @@ __device__ void up_items_pairs(const dec_params &p, const uint32_t *gi, const ui
     auto tile_src = [&](uint32_t it) -> const uint8_t * {
         const uint32_t g = it / ipg, r2 = it - g * ipg;
         const uint32_t m = r2 >= ipm ? 1u : 0u, k = r2 - m * ipm;
-        const uint8_t *W = m ? p.up_w : p.gate_w;
-        return W + (uint64_t)gi[2u + p.G + g] * exp_bytes + (uint64_t)(k * RPI) * row_bytes;
+        const uint8_t *W = expert_base(p, m ? p.up_w : p.gate_w, m ? p.sh_up : p.sh_gate, gi[2u + p.G + g], exp_bytes);
+        return W + (uint64_t)(k * RPI) * row_bytes;
     };
     const uint32_t tile_lds = (uint32_t)(uintptr_t)tile;
     auto fill = [&](uint32_t it) {
@@ -1142,11 +1160,11 @@ __global__ void __launch_bounds__(256) dec_up_kernel(dec_params p, uint32_t n_sh
     const uint32_t q1 = n_stat + (uint32_t)((uint64_t)n_dyn * (qi + 1u) / UP_QUEUES);
     uint32_t *queue = up_queue(p, qi);
     const uint64_t row_bytes = (uint64_t)nbK * SF37_Q3_BYTES, exp_bytes = (uint64_t)p.F * row_bytes;
-    const uint8_t *W = m ? p.up_w : p.gate_w;
+    const uint8_t *W = m ? p.up_w : p.gate_w, *Wsh = m ? p.sh_up : p.sh_gate;
     // an item is carried as (group, row pair): static successors step it,
     // dynamic answers divide once
     auto block_ptr = [&](uint32_t g, uint32_t rp) -> const uint8_t * {
-        return W + (uint64_t)gi[2u + p.G + g] * exp_bytes + (uint64_t)(2u * rp + rr) * row_bytes +
+        return expert_base(p, W, Wsh, gi[2u + p.G + g], exp_bytes) + (uint64_t)(2u * rp + rr) * row_bytes +
                (uint64_t)bl * SF37_Q3_BYTES;
     };
     // a dynamic request: lane 0's atomic; its index is read when needed
@@ -1268,6 +1286,8 @@ __global__ void __launch_bounds__(256) dec_mid_kernel(dec_params p) {
     const uint32_t pr = w / nbm, blk = w - pr * nbm;
     const uint64_t o = (uint64_t)pr * p.F + (uint64_t)blk * SF37_QK + 4u * lane;
     const float wt = p.wts[pr];
+    // the shared expert's slot (SH9) takes the shared clamp
+    const float clamp = (p.flags & SF37_DEC_SH9) && pr % p.topk == p.topk - 1u ? p.clamp_shared : p.clamp_routed;
     float gv[4], uv[4], v[4];
 #pragma unroll
     for (int k = 0; k < 4; k++) {
@@ -1276,7 +1296,7 @@ __global__ void __launch_bounds__(256) dec_mid_kernel(dec_params p) {
     }
 #pragma unroll
     for (int k = 0; k < 4; k++) {
-        v[k] = sf37_swiglu_mid_t(gv[k], uv[k], wt, p.clamp_routed, tab);
+        v[k] = sf37_swiglu_mid_t(gv[k], uv[k], wt, clamp, tab);
         p.mid[o + k] = v[k];
     }
     int8_t qk[4];
@@ -1403,7 +1423,8 @@ __global__ void __launch_bounds__(256) dec_down_kernel(dec_params p) {
     auto blk_ptr = [&](uint32_t g_, uint32_t sub_) -> const uint8_t * {
         uint32_t row = sub_ * rpw + rl;
         row = row < p.K ? row : p.K - 1u;                                    // keep tail lanes in bounds
-        return p.down_w + ((uint64_t)gi[2u + p.G + g_] * p.K + row) * row_bytes + (uint64_t)b * SF37_Q2_BYTES;
+        return expert_base(p, p.down_w, p.sh_down, gi[2u + p.G + g_], (uint64_t)p.K * row_bytes) + row * row_bytes +
+               (uint64_t)b * SF37_Q2_BYTES;
     };
     uint32_t staged_g = 0xffffffffu, staged_c0 = 0xffffffffu;
     uint32_t g = lo / spg, sub = lo - g * spg;
@@ -1522,7 +1543,8 @@ __global__ void __launch_bounds__(DN1_WAVES * 64, 2) dec_down1_kernel(dec_params
         const uint32_t e = p.ginfo[2u + p.G + wave];
         uint32_t row = r0 + rl;
         row = row < p.K ? row : p.K - 1u;                                   // tail lanes stay in bounds
-        load_q2(w, p.down_w + ((uint64_t)e * p.K + row) * ((uint64_t)nb * SF37_Q2_BYTES) +
+        const uint64_t rb = (uint64_t)nb * SF37_Q2_BYTES;
+        load_q2(w, expert_base(p, p.down_w, p.sh_down, e, (uint64_t)p.K * rb) + (uint64_t)row * rb +
                        (uint64_t)b * SF37_Q2_BYTES);
     }
     if (sh) {

@@ -42,8 +42,9 @@ static void *g_scratch;
 static uint64_t g_scratch_bytes;
 static int g_model_fd = -1;
 
-static sf37_hip_tensor *g_layer_bufs[10];
-static uint64_t g_layer_buf_bytes[10];
+#define N_LAYER_BUFS 11
+static sf37_hip_tensor *g_layer_bufs[N_LAYER_BUFS];
+static uint64_t g_layer_buf_bytes[N_LAYER_BUFS];
 
 static int64_t g_opt_q8k = 1;
 static int64_t g_opt_q8k_min_rows = 512;
@@ -56,6 +57,7 @@ static int64_t g_opt_prefill = 1;
 static int64_t g_opt_prefill_min_pairs = 256;
 static int64_t g_opt_shared_min_tok = 64;
 static int64_t g_opt_shared_stream = 1;
+static int64_t g_opt_shared_slot = 1;
 /* the shared expert's side stream (default priority) and its fork / join
  * events, made on first use */
 static hipStream_t g_side;
@@ -306,7 +308,7 @@ void sf37_hip_cleanup(void) {
     if (g_ev_join) (void)hipEventDestroy(g_ev_join);
     g_side = NULL;
     g_ev_fork = g_ev_join = NULL;
-    for (int i = 0; i < 10; i++) {
+    for (int i = 0; i < N_LAYER_BUFS; i++) {
         if (g_layer_bufs[i]) {
             (void)hipFree(g_layer_bufs[i]->ptr);
             free(g_layer_bufs[i]);
@@ -364,6 +366,7 @@ int sf37_hip_set_option(const char *name, int64_t value) {
     else if (!strcmp(name, "prefill_min_pairs")) g_opt_prefill_min_pairs = value < 0 ? 0 : value;
     else if (!strcmp(name, "shared_min_tokens")) g_opt_shared_min_tok = value < 0 ? 0 : value;
     else if (!strcmp(name, "shared_stream")) g_opt_shared_stream = value ? 1 : 0;
+    else if (!strcmp(name, "decode_shared_slot")) g_opt_shared_slot = value ? 1 : 0;
     else return 0;
     return 1;
 }
@@ -384,6 +387,7 @@ int64_t sf37_hip_get_option(const char *name) {
     if (!strcmp(name, "prefill_min_pairs")) return g_opt_prefill_min_pairs;
     if (!strcmp(name, "shared_min_tokens")) return g_opt_shared_min_tok;
     if (!strcmp(name, "shared_stream")) return g_opt_shared_stream;
+    if (!strcmp(name, "decode_shared_slot")) return g_opt_shared_slot;
     return -1;
 }
 
@@ -1282,7 +1286,8 @@ static int decode_run_in(const routed_args *a, const dec_extra *ex, float *out, 
         return 0;
     const uint32_t T = a->n_tok, E = a->n_expert, K = a->in_dim, F = a->mid_dim, TK = a->topk;
     const uint64_t P = (uint64_t)T * TK;
-    const uint32_t G = (uint32_t)(P < E ? P : E);
+    const uint32_t n_ids = E + ((ex->flags & SF37_DEC_SH9) ? 1u : 0u);   /* SH9: the shared expert is id E */
+    const uint32_t G = (uint32_t)(P < n_ids ? P : n_ids);
     const int sh = (ex->flags & SF37_DEC_SHARED) != 0;
     sf37_dec_params p;
     memset(&p, 0, sizeof(p));
@@ -1391,7 +1396,9 @@ static int decode_run_in(const routed_args *a, const dec_extra *ex, float *out, 
         p.wts = (float *)a->weights;
     }
     if ((ex->flags & SF37_DEC_ROUTER) && !p.router_w) return 0;
-    if (sh && (!p.sh_gate || !p.sh_up || !p.sh_down)) return 0;
+    if ((sh || (ex->flags & SF37_DEC_SH9)) && (!p.sh_gate || !p.sh_up || !p.sh_down)) return 0;
+    if ((ex->flags & SF37_DEC_SH9) && (sh || (ex->flags & SF37_DEC_SHBASE) || !(ex->flags & SF37_DEC_SELECT) || TK < 2u))
+        return 0;
     if (ex->flags & SF37_DEC_SHBASE) {
         if (sh || !ex->sh_out) return 0;
         p.sh_out = ex->sh_out;
@@ -1789,6 +1796,38 @@ static void layer_fused_extra(dec_extra *ex, const sf37_hip_moe_layer_weights *w
     ex->wts = weights ? (float *)weights->ptr : NULL;
 }
 
+/* The decode launches of a layer whose shared expert is in the routed
+ * formats (Q3GU gate/up, Q2D down) with that expert as one more slot of
+ * every token (SH9; the layer takes it for one token): the top-k fills slots 0..K-1 of K + 1 per token, slot K
+ * is the shared expert (id E, weight 1, the shared clamp), so it is one more
+ * group of n_tok pairs in the same up, mid and down launches, and the
+ * combine's slot-order sum adds its row last - (slots 0..K-1) + shared,
+ * the same single addition as shared + (slots 0..K-1).  The K + 1 slots
+ * live in a layer buffer; the caller's selections and weights receive
+ * slots 0..K-1. */
+static int layer_fused_sh9(const routed_args *a9, const sf37_hip_moe_layer_weights *w, const float *logits,
+                           sf37_hip_tensor *selected, sf37_hip_tensor *weights, const block_norm *bn, int f32_router,
+                           float *out) {
+    const uint32_t T = a9->n_tok, S = a9->topk, K = S - 1u;
+    const uint64_t slots = (uint64_t)T * S * 4u;
+    char *buf = (char *)layer_buf(10, 2u * align256(slots));
+    if (!buf) return 0;
+    int32_t *sel9 = (int32_t *)buf;
+    float *wts9 = (float *)(buf + align256(slots));
+    dec_extra ex;
+    layer_fused_extra(&ex, w, logits, NULL, NULL, bn, f32_router, NULL);
+    ex.flags = (ex.flags & ~SF37_DEC_SHARED) | SF37_DEC_SH9;
+    ex.sel = sel9;
+    ex.wts = wts9;
+    if (!decode_run(a9, &ex, out, NULL, NULL, NULL, NULL)) return 0;
+    return (!selected || hip_ok(hipMemcpy2DAsync(selected->ptr, (size_t)K * 4u, sel9, (size_t)S * 4u, (size_t)K * 4u, T,
+                                                 hipMemcpyDeviceToDevice, g_stream),
+                                "selection copy")) &&
+           (!weights || hip_ok(hipMemcpy2DAsync(weights->ptr, (size_t)K * 4u, wts9, (size_t)S * 4u, (size_t)K * 4u, T,
+                                                hipMemcpyDeviceToDevice, g_stream),
+                               "routing weight copy"));
+}
+
 /* With bn, out is the hidden state (and x the same tensor): out += layer(
  * RMSNorm(out)).  The fused decode launches take the norm and residual
  * themselves; otherwise rms_norm into a block buffer and the layer into
@@ -1821,6 +1860,15 @@ static int moe_layer_impl(sf37_hip_tensor *out, sf37_hip_tensor *selected, sf37_
     routed_args a = {(const uint8_t *)w->gate->ptr, (const uint8_t *)w->up->ptr, (const uint8_t *)w->down->ptr, NULL,
                      NULL, E, K, D, F, D, w->clamp_routed, (const float *)x->ptr, n_tok, NULL, NULL, NULL};
     const int fused = decode_eligible(&a, SF37_DEC_SELECT | (shared_q3 ? 0u : SF37_DEC_SHARED));
+    /* one token: a Q3GU/Q2D shared expert as one more slot inside the routed
+     * decode launches (above one token its group of n_tok pairs would make
+     * the up and down items that hold it several times heavier than the
+     * routed ones: measured 163 against 125 us per 8-token layer, so there it
+     * runs as launches of its own on the second stream) */
+    routed_args a9 = a;
+    a9.topk = K + 1u;
+    const int sh9 = shared_q3 && g_opt_shared_slot && fused && n_tok == 1u && K + 1u <= 16u &&
+                    decode_eligible(&a9, SF37_DEC_SELECT);
     if (bn && !fused) {
         const uint64_t bytes = (uint64_t)n_tok * D * 4u;
         for (int i = 0; i < 2; i++) {
@@ -1841,7 +1889,7 @@ static int moe_layer_impl(sf37_hip_tensor *out, sf37_hip_tensor *selected, sf37_
      * on the fused path (whose launches normalise x themselves), the rows
      * normalised here for the steps that run before those launches */
     const float *xl = (const float *)x->ptr;
-    if (bn && ((run_router && !router_f32) || shared_q3)) {
+    if (bn && ((run_router && !router_f32) || (shared_q3 && !sh9))) {
         float *xn = bn->xn ? bn->xn : (float *)layer_buf(5, (uint64_t)n_tok * D * 4u);
         if (!xn || !LAUNCH(SF37_HIP_STAGE_OTHER, sf37k_rms_norm(xn, (const float *)x->ptr, bn->norm_w, 1, D, n_tok,
                                                                 bn->eps, st),
@@ -1871,6 +1919,7 @@ static int moe_layer_impl(sf37_hip_tensor *out, sf37_hip_tensor *selected, sf37_
         if (!layer_router_typed(lg_buf, w, xl, n_tok)) return 0;
         if (!logits) logits = lg_buf;
     }
+    if (sh9) return layer_fused_sh9(&a9, w, logits, selected, weights, bn, run_router && router_f32, (float *)out->ptr);
     if (fused) {
         /* a Q3GU/Q2D shared expert first, then the routed launches add it */
         float *sh_out = NULL;

@@ -153,6 +153,9 @@ int sf37k_sh_down(float *out, const uint8_t *down_w, const void *a8, const float
 #define SF37_DEC_RESID 32u   /* out += layer output (out is the hidden state) */
 #define SF37_DEC_UPSEL 64u   /* no select launch: the up launch forms the top-k and runs the shared gate/up */
 #define SF37_DEC_SHBASE 128u /* out = sh_out (computed before) + routed; no shared expert here */
+#define SF37_DEC_SH9 256u    /* the shared expert in the routed formats (Q3GU gate/up, Q2D down at sh_gate,
+                                sh_up, sh_down) as expert id E in the last of topk slots per token: the
+                                top-k fills topk - 1 slots, the last is (E, weight 1.0, clamp_shared) */
 #define SF37_DEC_ACT_BYTES 288u  /* activation block: 256 codes, d, 4 sums, pad */
 typedef struct sf37_dec_params {
     uint32_t T, E, K, F, topk, G;

@@ -4,7 +4,9 @@ weight 1.0 and the shared clamp (shared_type 11), against the oracle's
 composition of the same (oracle.moe_layer_q8k(shared_format="q3q2")), bit for
 bit, at the BASELINE shape: config 0 (one token, router logits computed on
 the device and fed to the oracle), config 1 (8 tokens), config 3 (4096
-tokens, uniform routing) on a token sample, and layer 43's clamps.
+tokens, uniform routing) on a token sample, and layer 43's clamps; and the
+decode form that runs it as one more slot of every token inside the routed
+launches against the form that runs it as launches of its own.
 """
 import sys
 
@@ -81,3 +83,34 @@ def test_shared_q3q2_layer_vs_oracle(H, O, layer, config):
     assert np.array_equal(sel[idx], wsel)
     assert_bitexact(w[idx], ww, "routing weights")
     assert_bitexact(out[idx], want, f"config {config} layer {layer.il} output")
+
+
+@pytest.mark.parametrize("n_tok", [1, 3, 8])
+def test_shared_slot_equals_separate_launches(H, layer, n_tok):
+    """One-token decodes run the Q3GU/Q2D shared expert as one more slot
+    inside the routed launches (option decode_shared_slot, on by default: one
+    route launch per layer); with the option off, and for batches of several
+    tokens, it runs as launches of its own (two route launches).  Outputs,
+    selections and routing weights agree bit for bit."""
+    from sf37_amd import moe
+    rng = np.random.default_rng(900 + n_tok)
+    x = rng.standard_normal((n_tok, K)).astype(np.float32)
+    logits = rng.standard_normal((n_tok, E)).astype(np.float32)
+    got = {}
+    for slot in (1, 0):
+        say(f"shared slot {slot}: {n_tok} tokens, layer {layer.il}")
+        H.set_option("decode_shared_slot", slot)
+        H.lib().sf37_hip_profile_enable(1)
+        H.profile_read()
+        try:
+            out, sel, w = H.Tensor.alloc(n_tok * K * 4), H.Tensor.alloc(n_tok * 32), H.Tensor.alloc(n_tok * 32)
+            moe.moe_layer(layer, H.Tensor.from_array(x), n_tok, out, sel, w, H.Tensor.from_array(logits))
+            prof = H.profile_read()
+            got[slot] = (out.read(np.float32), sel.read(np.int32), w.read(np.float32))
+        finally:
+            H.lib().sf37_hip_profile_enable(0)
+            H.set_option("decode_shared_slot", 1)
+        assert prof["dec_route"][1] == (1 if slot and n_tok == 1 else 2), prof["dec_route"]
+    assert np.array_equal(got[1][1], got[0][1])
+    assert_bitexact(got[1][2], got[0][2], "routing weights")
+    assert_bitexact(got[1][0], got[0][0], f"output, {n_tok} tokens")
