@@ -1513,13 +1513,14 @@ __global__ void __launch_bounds__(256) dec_down_kernel(dec_params p) {
 // ---------------------------------------------------------------------------
 // One token, one group per slot (SF37_DEC_SLOTS): down and combine in one
 // launch.  A workgroup owns the rpw output rows of one routed sub-item (12
-// for F = 1280, lane = (row, block) as in dec_down_kernel): wave s < topk
-// computes slot s's rows of its expert, waves 0 .. nsh-1 first the shared
+// for F = 1280, lane = (row, block) as in dec_down_kernel): wave w computes
+// slot w's rows of its expert (and slot w + 8's past eight slots, up to 16),
+// waves 0 .. nsh-1 first the shared
 // rows of the tile (R = 4 per wave), all into LDS; then one thread per row
 // forms out = [shared +] (slots summed in slot order) [+ out], the
 // arithmetic of dec_combine_kernel.  No per-pair rows reach memory.
 // ---------------------------------------------------------------------------
-constexpr uint32_t DN1_WAVES = 8;        // slots (topk <= 8) and shared passes (<= 8) per workgroup
+constexpr uint32_t DN1_WAVES = 8;        // waves: slots (two each past eight) and shared passes (<= 8)
 constexpr uint32_t DN1_MAX_RPW = 32;     // rows per tile (nb >= 2)
 
 __host__ __device__ constexpr uint32_t dn1_rpw(uint32_t F) { return 4u * (16u / (F / SF37_QK)); }
@@ -1528,8 +1529,8 @@ template <int SHNB>
 __global__ void __launch_bounds__(DN1_WAVES * 64, 2) dec_down1_kernel(dec_params p) {
     __shared__ __align__(16) int8_t shq[DN_MAX_NB * SF37_QK];
     __shared__ float shs[DN_MAX_NB * SF37_QK / 32u];
-    __shared__ __align__(16) act_t xsl[DN1_WAVES][DN_MAX_NB];
-    __shared__ float res[DN1_WAVES][DN1_MAX_RPW];
+    __shared__ __align__(16) act_t xsl[SHNB == 1 ? 2 : 1][DN1_WAVES][DN_MAX_NB];
+    __shared__ float res[(SHNB == 1 ? 2 : 1) * DN1_WAVES][DN1_MAX_RPW];
     __shared__ float shres[DN1_MAX_RPW];
     const bool sh = (p.flags & SF37_DEC_SHARED) != 0;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63u;
@@ -1537,39 +1538,51 @@ __global__ void __launch_bounds__(DN1_WAVES * 64, 2) dec_down1_kernel(dec_params
     const uint32_t q = lane & 15u, r_in = q / nb, b = q - r_in * nb;
     const bool active = r_in < rpd;
     const uint32_t rl = (lane >> 4) * rpd + (active ? r_in : 0u);
-    const bool routed = wave < p.topk;
-    uint32_t w[21];
-    if (routed) {
-        const uint32_t e = p.ginfo[2u + p.G + wave];
-        uint32_t row = r0 + rl;
-        row = row < p.K ? row : p.K - 1u;                                   // tail lanes stay in bounds
-        const uint64_t rb = (uint64_t)nb * SF37_Q2_BYTES;
-        load_q2(w, expert_base(p, p.down_w, p.sh_down, e, (uint64_t)p.K * rb) + (uint64_t)row * rb +
-                       (uint64_t)b * SF37_Q2_BYTES);
+    // wave w takes slot w and, past eight slots, slot w + 8 (the instance
+    // without shared-down batches; the others take up to eight slots)
+    constexpr uint32_t NJ = SHNB == 1 ? 2u : 1u;
+    bool routed[NJ];
+    uint32_t w[NJ][21];
+#pragma unroll
+    for (uint32_t j = 0; j < NJ; j++) {
+        const uint32_t s = wave + DN1_WAVES * j;
+        routed[j] = s < p.topk;
+        if (routed[j]) {
+            const uint32_t e = p.ginfo[2u + p.G + s];
+            uint32_t row = r0 + rl;
+            row = row < p.K ? row : p.K - 1u;                               // tail lanes stay in bounds
+            const uint64_t rb = (uint64_t)nb * SF37_Q2_BYTES;
+            load_q2(w[j], expert_base(p, p.down_w, p.sh_down, e, (uint64_t)p.K * rb) + (uint64_t)row * rb +
+                              (uint64_t)b * SF37_Q2_BYTES);
+        }
     }
     if (sh) {
         for (uint32_t i = threadIdx.x; i < p.F / 16u; i += blockDim.x) ((u32x4 *)shq)[i] = ((const u32x4 *)p.sh_mq)[i];
         for (uint32_t i = threadIdx.x; i < p.F / 32u; i += blockDim.x) shs[i] = p.sh_ms[i];
     }
-    if (routed) {
-        const uint32_t per = nb * (uint32_t)(sizeof(act_t) / 16u);
+#pragma unroll
+    for (uint32_t j = 0; j < NJ; j++) {
+        if (!routed[j]) continue;
+        const uint32_t per = nb * (uint32_t)(sizeof(act_t) / 16u), s = wave + DN1_WAVES * j;
         for (uint32_t i = lane; i < per; i += 64u)
-            ((u32x4 *)xsl[wave])[i] = ((const u32x4 *)((const act_t *)p.midq + (uint64_t)p.sorted[wave] * nb))[i];
+            ((u32x4 *)xsl[j][wave])[i] = ((const u32x4 *)((const act_t *)p.midq + (uint64_t)p.sorted[s] * nb))[i];
     }
     __syncthreads();
     const uint32_t R = 64u / shd_slices(1u), nsh = (rpw + R - 1u) / R;
     if (sh && wave < nsh)
         shared_down_pass<SHNB>(p, shq, shs, r0 + wave * R,
                                [&](uint32_t, uint32_t row, float v) { shres[row - r0] = v; });
-    if (routed) {
-        opaque<21>(w);
+#pragma unroll
+    for (uint32_t j = 0; j < NJ; j++) {
+        if (!routed[j]) continue;
+        opaque<21>(w[j]);
         const act_t *x[DEC_TPC];
 #pragma unroll
-        for (uint32_t t = 0; t < DEC_TPC; t++) x[t] = xsl[wave] + b;
+        for (uint32_t t = 0; t < DEC_TPC; t++) x[t] = xsl[j][wave] + b;
         float bs[DEC_TPC], dd[1] = {x[0]->d}, acc[1];
-        q2_block_dots_lds<1>(w, x, bs);
+        q2_block_dots_lds<1>(w[j], x, bs);
         seg_chains<1>(dd, bs, acc, b, nb);
-        if (active && b == nb - 1u && r0 + rl < p.K) res[wave][rl] = acc[0];
+        if (active && b == nb - 1u && r0 + rl < p.K) res[wave + DN1_WAVES * j][rl] = acc[0];
     }
     __syncthreads();
     const uint32_t i = threadIdx.x;
@@ -1897,7 +1910,10 @@ extern "C" int sf37k_decode_down(const sf37_dec_params *pp, sf37_stream_t s) {
 extern "C" int sf37k_decode_down_combine_supported(const sf37_dec_params *pp) {
     const sf37_dec_params &p = *pp;
     const uint32_t nb = p.F / SF37_QK;
-    return (p.flags & SF37_DEC_SLOTS) && p.T == 1u && p.topk <= DN1_WAVES && nb >= 2u && nb <= DN_MAX_NB &&
+    // slots: two per wave in the instance without shared-down batches
+    const uint32_t nbat = (shd_bps(p.F / 32u, shd_slices(1u)) + SHD_CHUNK - 1u) / SHD_CHUNK;
+    const uint32_t max_slots = (p.flags & SF37_DEC_SHARED) == 0u || nbat <= 1u ? 2u * DN1_WAVES : DN1_WAVES;
+    return (p.flags & SF37_DEC_SLOTS) && p.T == 1u && p.topk <= max_slots && nb >= 2u && nb <= DN_MAX_NB &&
            dn1_rpw(p.F) <= DN1_MAX_RPW && (dn1_rpw(p.F) + 3u) / 4u <= DN1_WAVES && p.K > 0u;
 }
 

@@ -281,12 +281,14 @@ def test_fused_routed_one_duplicates(H, O, layer):
     assert_bitexact(res[0][3].reshape(TOPK, F), want_mid, "routed_moe_one mid vs oracle")
 
 
-@pytest.mark.parametrize("E_, D_, F_, topk", [(16, 1024, 512, 4), (16, 512, 768, 8), (12, 1024, 1280, 3)])
+@pytest.mark.parametrize("E_, D_, F_, topk", [(16, 1024, 512, 4), (16, 512, 768, 8), (12, 1024, 1280, 3),
+                                             (32, 1024, 1280, 12)])
 def test_one_token_down_combine_shapes(H, O, E_, D_, F_, topk):
     """The one-token down+combine launch on shapes other than the BASELINE
-    one: fewer slots than its 8 waves (top-3, top-4), 32- and 20-row tiles
-    (F = 512, 768: 8 and 5 shared passes), against the two-launch path,
-    the staged kernels and the oracle, bit for bit."""
+    one: fewer slots than its 8 waves (top-3, top-4), more (top-12: waves
+    0-3 take two slots), 32- and 20-row tiles (F = 512, 768: 8 and 5 shared
+    passes), against the two-launch path, the staged kernels and the
+    oracle, bit for bit."""
     from sf37_amd.moe import SynthLayer
     say(f"one-token down+combine: E {E_}, D {D_}, F {F_}, top-{topk}")
     lay = SynthLayer(seed=300 + topk, n_expert=E_, in_dim=D_, mid_dim=F_, topk=topk)

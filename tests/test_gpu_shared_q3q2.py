@@ -111,6 +111,8 @@ def test_shared_slot_equals_separate_launches(H, layer, n_tok):
             H.lib().sf37_hip_profile_enable(0)
             H.set_option("decode_shared_slot", 1)
         assert prof["dec_route"][1] == (1 if slot and n_tok == 1 else 2), prof["dec_route"]
+        if slot and n_tok == 1:   # nine slots: down and combine still one launch
+            assert prof["dec_down"][1] == 1 and prof["dec_combine"][1] == 0, prof
     assert np.array_equal(got[1][1], got[0][1])
     assert_bitexact(got[1][2], got[0][2], "routing weights")
     assert_bitexact(got[1][0], got[0][0], f"output, {n_tok} tokens")
