@@ -257,10 +257,10 @@ void *sf37_hip_get_stream(void);
  *                       runs on a second stream of the library (default
  *                       priority), forked after its input rows and joined
  *                       before the routed combine; 0: in order
- *   "decode_shared_slot" 1 (default): a one-token decode's Q3GU/Q2D shared
- *                       expert runs as one more slot inside the routed
- *                       decode launches (slot topk, weight 1, the shared
- *                       clamp); 0: as launches of its own before them
+ *   "decode_shared_slot" 1 (default): a decode batch's Q3GU/Q2D shared
+ *                       expert runs as one more slot of every token inside
+ *                       the routed decode launches (slot topk, weight 1, the
+ *                       shared clamp); 0: as launches of its own
  *   "router_with_logits" 1: sf37_hip_moe_layer computes the router GEMV even
  *                       when logits_in is given (its result is unused; for
  *                       benchmarks that inject routing but keep the cost)

@@ -62,6 +62,14 @@ __device__ __forceinline__ uint32_t n_ids(const sf37_dec_params &p) {
     return p.E + ((p.flags & SF37_DEC_SH9) ? 1u : 0u);
 }
 
+// With SH9 the shared expert's pairs (one per token) form groups of at
+// most SH9_PAIRS pairs, so no up or down item holds more pairs than a
+// routed expert shared by two tokens.
+constexpr uint32_t SH9_PAIRS = 2;
+__device__ __forceinline__ uint32_t expert_groups(const sf37_dec_params &p, uint32_t e, uint32_t pairs) {
+    return (p.flags & SF37_DEC_SH9) && e == p.E ? (pairs + SH9_PAIRS - 1u) / SH9_PAIRS : (pairs ? 1u : 0u);
+}
+
 // Weight bytes of expert e of a matrix (w: the routed experts, exp_bytes
 // apart; sh: the shared expert, id E with SH9).
 __device__ __forceinline__ const uint8_t *expert_base(const sf37_dec_params &p, const uint8_t *w, const uint8_t *sh,
@@ -386,9 +394,9 @@ __device__ void group_pairs(const dec_params &p, const uint32_t *s_sel, uint32_t
             for (uint32_t i = 0; i < c; i++) {
                 const uint32_t e = e0 + i;
                 if (e < ne) {
-                    const uint32_t m = msk[e];
-                    n += (uint32_t)__builtin_popcount(m);
-                    g += m != 0u;
+                    const uint32_t m = msk[e], pc = (uint32_t)__builtin_popcount(m);
+                    n += pc;
+                    g += expert_groups(p, e, pc);
                 }
             }
             const uint32_t ni = wave_incl_sum(n), gin = wave_incl_sum(g);
@@ -400,18 +408,18 @@ __device__ void group_pairs(const dec_params &p, const uint32_t *s_sel, uint32_t
             for (uint32_t i = 0; i < c; i++) {
                 const uint32_t e = e0 + i;
                 if (e < ne) {
-                    const uint32_t m = msk[e];
+                    const uint32_t m = msk[e], pc = (uint32_t)__builtin_popcount(m), ng_e = expert_groups(p, e, pc);
                     st[e] = np;
-                    if (m) {
-                        gi[1u + ge] = np;
+                    for (uint32_t k = 0; k < ng_e; k++) {   // one group, or the shared expert's pair chunks
+                        gi[1u + ge] = np + SH9_PAIRS * k;
                         gi[2u + p.G + ge] = e;
                         if (publish) {
-                            p.ginfo[1u + ge] = np;
+                            p.ginfo[1u + ge] = np + SH9_PAIRS * k;
                             p.ginfo[2u + p.G + ge] = e;
                         }
                         ge++;
-                        np += (uint32_t)__builtin_popcount(m);
                     }
+                    np += pc;
                 }
             }
         }
@@ -457,7 +465,10 @@ __device__ void group_pairs(const dec_params &p, const uint32_t *s_sel, uint32_t
     const uint32_t i = threadIdx.x;
     const bool act = i < P;
     const uint32_t e = act ? s_se[i] : 0u;
-    const bool start = act && (i == 0u || s_se[i - 1u] != e);
+    // the shared expert (SH9, id E: the last run of the sorted order, one
+    // pair per token) starts a group every SH9_PAIRS pairs
+    const bool sh_chunk = (p.flags & SF37_DEC_SH9) && e == p.E && (i - (P - p.T)) % SH9_PAIRS == 0u;
+    const bool start = act && (i == 0u || s_se[i - 1u] != e || sh_chunk);
     const uint64_t m = __ballot(start);
     const uint32_t below = (uint32_t)__builtin_popcountll(m & ((1ull << lane) - 1ull));
     if (lane == 0) s_wcnt[wave] = (uint32_t)__builtin_popcountll(m);

@@ -1286,8 +1286,10 @@ static int decode_run_in(const routed_args *a, const dec_extra *ex, float *out, 
         return 0;
     const uint32_t T = a->n_tok, E = a->n_expert, K = a->in_dim, F = a->mid_dim, TK = a->topk;
     const uint64_t P = (uint64_t)T * TK;
-    const uint32_t n_ids = E + ((ex->flags & SF37_DEC_SH9) ? 1u : 0u);   /* SH9: the shared expert is id E */
-    const uint32_t G = (uint32_t)(P < n_ids ? P : n_ids);
+    /* groups: one per expert id, and with SH9 the shared expert (id E) as
+     * up to n_tok groups of its pairs */
+    const uint32_t n_grp = E + ((ex->flags & SF37_DEC_SH9) ? T : 0u);
+    const uint32_t G = (uint32_t)(P < n_grp ? P : n_grp);
     const int sh = (ex->flags & SF37_DEC_SHARED) != 0;
     sf37_dec_params p;
     memset(&p, 0, sizeof(p));
@@ -1798,7 +1800,7 @@ static void layer_fused_extra(dec_extra *ex, const sf37_hip_moe_layer_weights *w
 
 /* The decode launches of a layer whose shared expert is in the routed
  * formats (Q3GU gate/up, Q2D down) with that expert as one more slot of
- * every token (SH9; the layer takes it for one token): the top-k fills slots 0..K-1 of K + 1 per token, slot K
+ * every token (SH9): the top-k fills slots 0..K-1 of K + 1 per token, slot K
  * is the shared expert (id E, weight 1, the shared clamp), so it is one more
  * group of n_tok pairs in the same up, mid and down launches, and the
  * combine's slot-order sum adds its row last - (slots 0..K-1) + shared,
@@ -1860,15 +1862,13 @@ static int moe_layer_impl(sf37_hip_tensor *out, sf37_hip_tensor *selected, sf37_
     routed_args a = {(const uint8_t *)w->gate->ptr, (const uint8_t *)w->up->ptr, (const uint8_t *)w->down->ptr, NULL,
                      NULL, E, K, D, F, D, w->clamp_routed, (const float *)x->ptr, n_tok, NULL, NULL, NULL};
     const int fused = decode_eligible(&a, SF37_DEC_SELECT | (shared_q3 ? 0u : SF37_DEC_SHARED));
-    /* one token: a Q3GU/Q2D shared expert as one more slot inside the routed
-     * decode launches (above one token its group of n_tok pairs would make
-     * the up and down items that hold it several times heavier than the
-     * routed ones: measured 163 against 125 us per 8-token layer, so there it
-     * runs as launches of its own on the second stream) */
+    /* a Q3GU/Q2D shared expert as one more slot inside the routed decode
+     * launches (its pairs grouped two at a time, so its up and down items
+     * weigh what a routed expert's do: as one group of n_tok pairs the 8-token
+     * layer measured 163 against 125 us with its own launches) */
     routed_args a9 = a;
     a9.topk = K + 1u;
-    const int sh9 = shared_q3 && g_opt_shared_slot && fused && n_tok == 1u && K + 1u <= 16u &&
-                    decode_eligible(&a9, SF37_DEC_SELECT);
+    const int sh9 = shared_q3 && g_opt_shared_slot && fused && K + 1u <= 16u && decode_eligible(&a9, SF37_DEC_SELECT);
     if (bn && !fused) {
         const uint64_t bytes = (uint64_t)n_tok * D * 4u;
         for (int i = 0; i < 2; i++) {
