@@ -1868,7 +1868,10 @@ static int moe_layer_impl(sf37_hip_tensor *out, sf37_hip_tensor *selected, sf37_
      * layer measured 163 against 125 us with its own launches) */
     routed_args a9 = a;
     a9.topk = K + 1u;
-    const int sh9 = shared_q3 && g_opt_shared_slot && fused && K + 1u <= 16u && decode_eligible(&a9, SF37_DEC_SELECT);
+    /* (pairs <= experts: then the launch plan's group count, the pair
+     * count, is the same with the shared expert's groups) */
+    const int sh9 = shared_q3 && g_opt_shared_slot && fused && K + 1u <= 16u &&
+                    (uint64_t)n_tok * (K + 1u) <= E && decode_eligible(&a9, SF37_DEC_SELECT);
     if (bn && !fused) {
         const uint64_t bytes = (uint64_t)n_tok * D * 4u;
         for (int i = 0; i < 2; i++) {
