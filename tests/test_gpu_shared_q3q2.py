@@ -16,6 +16,7 @@ import pytest
 pytestmark = pytest.mark.gpu
 
 E, K, F = 288, 4096, 1280
+_KEEP = []
 
 
 def say(msg):
@@ -116,3 +117,35 @@ def test_shared_slot_equals_separate_launches(H, layer, n_tok):
     assert np.array_equal(got[1][1], got[0][1])
     assert_bitexact(got[1][2], got[0][2], "routing weights")
     assert_bitexact(got[1][0], got[0][0], f"output, {n_tok} tokens")
+
+
+@pytest.mark.parametrize("n_tok", [1, 8])
+def test_shared_slot_in_ffn_block(H, layer, n_tok):
+    """sf37_hip_moe_block (RMSNorm(w+1) of the hidden rows, the layer, the
+    residual) with the Q3GU/Q2D shared expert as a decode slot equals the
+    same block with the shared expert's own launches, bit for bit, and the
+    normalised rows it returns equal the standalone RMSNorm's."""
+    import ctypes as C
+    from sf37_amd import moe
+    rng = np.random.default_rng(1300 + n_tok)
+    norm = H.Tensor.from_array(moe.bf16_bits((rng.standard_normal(K) * 0.02).astype(np.float32)))
+    key = np.zeros(64, np.uint8)                 # host address used as the map key
+    _KEEP.append((key, norm))                    # registered for the session: no later key reuses it
+    H.check(H.lib().sf37_hip_register_device_range(key.ctypes.data, norm.nbytes, 0, norm.nbytes, norm.h),
+            "register norm weights")
+    h0 = (rng.standard_normal((n_tok, K)) * 3).astype(np.float32)
+    logits = rng.standard_normal((n_tok, E)).astype(np.float32)
+    got = {}
+    try:
+        for slot in (1, 0):
+            say(f"FFN block, shared slot {slot}: {n_tok} tokens, layer {layer.il}")
+            H.set_option("decode_shared_slot", slot)
+            h, normed = H.Tensor.from_array(h0), H.Tensor.alloc(n_tok * K * 4)
+            H.check(H.lib().sf37_hip_moe_block(h, normed, None, None, C.byref(layer.weights_struct()),
+                                               key.ctypes.data, norm.nbytes, 0, 1e-5,
+                                               H.Tensor.from_array(logits), n_tok), "moe_block")
+            got[slot] = (h.read(np.float32), normed.read(np.float32))
+    finally:
+        H.set_option("decode_shared_slot", 1)
+    assert_bitexact(got[1][1], got[0][1], "normalised rows")
+    assert_bitexact(got[1][0], got[0][0], f"hidden rows, {n_tok} tokens")
