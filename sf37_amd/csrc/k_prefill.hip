@@ -514,8 +514,8 @@ __device__ __forceinline__ void pf_block(const RAW &r, const uint8_t *act_lds, c
 template <bool Q3, int NTB, typename ISSUE>
 __device__ __forceinline__ void pf_body(const pf_params &p, const uint8_t *wrow, ISSUE &issue_act,
                                         uint8_t (*s_act)[PF_ACT_BUF], float (*s_cd)[PF_CD_ROWS * PF_T],
-                                        const uint32_t *s_pair, const float *s_w, uint32_t kh, uint32_t col,
-                                        uint32_t wcol, uint32_t cnt);
+                                        const uint32_t *s_pair, const float *s_w, const uint64_t *s_tab,
+                                        uint32_t kh, uint32_t col, uint32_t wcol, uint32_t cnt);
 
 template <bool Q3>
 __global__ void __launch_bounds__(pf_cfg<Q3>::NW * 64, Q3 ? 1 : 2) pf_expert_kernel(pf_params p) {
@@ -524,6 +524,7 @@ __global__ void __launch_bounds__(pf_cfg<Q3>::NW * 64, Q3 ? 1 : 2) pf_expert_ker
     __shared__ __align__(16) float s_cd[NBUF][PF_CD_ROWS * PF_T];
     __shared__ uint32_t s_pair[PF_T];
     __shared__ float s_w[PF_T];
+    __shared__ uint64_t s_tab[Q3 ? 32 : 1];    // the exp table of the SwiGLU epilogue
     const uint32_t wg = blockIdx.x, xcd = wg & 7u, slot = wg >> 3;
     const uint32_t t = xcd + 8u * (slot / p.n_rt), rt = slot % p.n_rt;
     if (t >= p.tiles[0]) return;
@@ -538,6 +539,7 @@ __global__ void __launch_bounds__(pf_cfg<Q3>::NW * 64, Q3 ? 1 : 2) pf_expert_ker
         s_pair[tid] = pr;
         if (Q3) s_w[tid] = p.weights[pr];
     }
+    if (Q3) sf37_stage_exp_tab(s_tab);          // read after the main loop's barriers
     // activation rows: tile slot `lane` for the tables; slot 32*gi + lane%32
     // for the codes (pad slots repeat the last pair).  8 waves: wave 4*gi + wq
     // copies slot group gi; 4 waves: wave wq copies both groups.
@@ -601,16 +603,16 @@ __global__ void __launch_bounds__(pf_cfg<Q3>::NW * 64, Q3 ? 1 : 2) pf_expert_ker
     const uint32_t blk_bytes = Q3 ? SF37_Q3_BYTES : SF37_Q2_BYTES;
     const uint64_t row_bytes = (uint64_t)nblk * blk_bytes;
     const uint8_t *wrow = (Q3 && col >= 16u ? p.w1 : p.w0) + ((uint64_t)e * p.out_rows + wcol) * row_bytes;
-    if (ntb == 1) pf_body<Q3, 1>(p, wrow, issue_act, s_act, s_cd, s_pair, s_w, kh, col, wcol, cnt);
-    else pf_body<Q3, 2>(p, wrow, issue_act, s_act, s_cd, s_pair, s_w, kh, col, wcol, cnt);
+    if (ntb == 1) pf_body<Q3, 1>(p, wrow, issue_act, s_act, s_cd, s_pair, s_w, s_tab, kh, col, wcol, cnt);
+    else pf_body<Q3, 2>(p, wrow, issue_act, s_act, s_cd, s_pair, s_w, s_tab, kh, col, wcol, cnt);
 }
 
 // Main loop and epilogue for NTB 32-pair blocks (the tile's pair count rounded up).
 template <bool Q3, int NTB, typename ISSUE>
 __device__ __forceinline__ void pf_body(const pf_params &p, const uint8_t *wrow, ISSUE &issue_act,
                                         uint8_t (*s_act)[PF_ACT_BUF], float (*s_cd)[PF_CD_ROWS * PF_T],
-                                        const uint32_t *s_pair, const float *s_w, uint32_t kh, uint32_t col,
-                                        uint32_t wcol, uint32_t cnt) {
+                                        const uint32_t *s_pair, const float *s_w, const uint64_t *s_tab,
+                                        uint32_t kh, uint32_t col, uint32_t wcol, uint32_t cnt) {
     const uint32_t nblk = p.nblk;
     float acc[NTB][16];
     f16v blk[PF_TB];
@@ -677,22 +679,30 @@ __device__ __forceinline__ void pf_body(const pf_params &p, const uint8_t *wrow,
     // epilogue: D layout - lane holds column col, tokens 8*(r/4) + 4*kh + r%4
 #pragma unroll
     for (uint32_t i = 0; i < (uint32_t)NTB; i++) {
-        {
+        if constexpr (Q3) {
+            // lanes col and col ^ 16 hold the gate and up rows of one mid row:
+            // after swapping values the gate lane forms the SwiGLU of tokens
+            // r2 = k and the up lane of r2 = k + 8, so every lane takes half
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                const float va = acc[i][k], vb = acc[i][k + 8];
+                const float oa = __shfl_xor(va, 16, 64), ob = __shfl_xor(vb, 16, 64);
+                const bool up_lane = col >= 16u;
+                const int r2 = up_lane ? k + 8 : k;
+                const float g = up_lane ? ob : va, u = up_lane ? vb : oa;
+                const uint32_t tl = 32u * i + 8u * ((uint32_t)r2 >> 2) + 4u * kh + ((uint32_t)r2 & 3u);
+                if (tl < cnt) {
+                    const uint64_t at = (uint64_t)s_pair[tl] * p.out_rows + wcol;
+                    p.mid[at] = sf37_swiglu_mid_t(g, u, s_w[tl], p.clamp, s_tab);
+                    if (p.gate_out) p.gate_out[at] = g;
+                    if (p.up_out) p.up_out[at] = u;
+                }
+            }
+        } else {
 #pragma unroll
             for (int r2 = 0; r2 < 16; r2++) {
                 const uint32_t tl = 32u * i + 8u * (r2 >> 2) + 4u * kh + (r2 & 3);
-                const float v = acc[i][r2];
-                if constexpr (Q3) {
-                    const float o = __shfl_xor(v, 16, 64);
-                    if (col < 16u && tl < cnt) {
-                        const uint64_t at = (uint64_t)s_pair[tl] * p.out_rows + wcol;
-                        p.mid[at] = sf37_swiglu_mid(v, o, s_w[tl], p.clamp);
-                        if (p.gate_out) p.gate_out[at] = v;
-                        if (p.up_out) p.up_out[at] = o;
-                    }
-                } else {
-                    if (tl < cnt) p.down_pair[(uint64_t)s_pair[tl] * p.out_rows + wcol] = v;
-                }
+                if (tl < cnt) p.down_pair[(uint64_t)s_pair[tl] * p.out_rows + wcol] = acc[i][r2];
             }
         }
     }
@@ -906,7 +916,9 @@ template <bool GU, int TBW>
 __global__ void __launch_bounds__(256, 2) sh_gemm_kernel(sh_params p) {
     __shared__ __align__(16) uint8_t s_act[2][SH_BUF];
     __shared__ __align__(16) float s_xs[2][SH_CB * SH_T];
+    __shared__ uint64_t s_tab[GU ? 32 : 1];    // the exp table of the SwiGLU epilogue
     static_assert(TBW == 1 || TBW == 2, "token blocks per wave");
+    if (GU) sf37_stage_exp_tab(s_tab);          // read after the chunk loop's barriers
     const uint32_t tt = blockIdx.x % p.n_tt, ct = blockIdx.x / p.n_tt;
     const uint32_t tid = threadIdx.x, lane = tid & 63u, kh = lane >> 5, col = lane & 31u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -974,15 +986,25 @@ __global__ void __launch_bounds__(256, 2) sh_gemm_kernel(sh_params p) {
     wait_vm0();
 #pragma unroll
     for (uint32_t i = 0; i < (uint32_t)TBW; i++) {
+        if constexpr (GU) {
+            // lanes col and col ^ 16 hold the gate and up rows of one mid row:
+            // the gate lane forms the SwiGLU of tokens r2 = k, the up lane of
+            // r2 = k + 8
 #pragma unroll
-        for (int r2 = 0; r2 < 16; r2++) {
-            const uint32_t t = t0 + 32u * (tb0 + i) + 8u * (r2 >> 2) + 4u * kh + (r2 & 3);
-            const float v = acc[i][r2];
-            if constexpr (GU) {
-                const float o = __shfl_xor(v, 16, 64);
-                if (col < 16u && t < p.n_tok) p.out0[(uint64_t)t * p.rows + wcol] = sf37_swiglu_mid(v, o, 1.0f, p.clamp);
-            } else {
-                if (t < p.n_tok) p.out0[(uint64_t)t * p.rows + wcol] = v;
+            for (int k = 0; k < 8; k++) {
+                const float va = acc[i][k], vb = acc[i][k + 8];
+                const float oa = __shfl_xor(va, 16, 64), ob = __shfl_xor(vb, 16, 64);
+                const bool up_lane = col >= 16u;
+                const uint32_t r2 = up_lane ? (uint32_t)k + 8u : (uint32_t)k;
+                const float g = up_lane ? ob : va, u = up_lane ? vb : oa;
+                const uint32_t t = t0 + 32u * (tb0 + i) + 8u * (r2 >> 2) + 4u * kh + (r2 & 3u);
+                if (t < p.n_tok) p.out0[(uint64_t)t * p.rows + wcol] = sf37_swiglu_mid_t(g, u, 1.0f, p.clamp, s_tab);
+            }
+        } else {
+#pragma unroll
+            for (int r2 = 0; r2 < 16; r2++) {
+                const uint32_t t = t0 + 32u * (tb0 + i) + 8u * (r2 >> 2) + 4u * kh + (r2 & 3);
+                if (t < p.n_tok) p.out0[(uint64_t)t * p.rows + wcol] = acc[i][r2];
             }
         }
     }
