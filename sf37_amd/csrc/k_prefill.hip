@@ -507,130 +507,55 @@ __device__ __forceinline__ void pf_block(const RAW &r, const uint8_t *act_lds, c
     }
 }
 
-// Gate/up (Q3 = true): row tile = 64 F rows, wave w has gate rows
-// rt*64 + 16w + c and up rows (c < 16: gate, else up) as its 32 columns;
-// epilogue mid = ((g*sig(g))*u)*w per pair.  Down (Q3 = false): row tile =
-// 128 output rows, 32 per wave; epilogue down_pair[pair][row].
-template <bool Q3, int NTB, typename ISSUE>
-__device__ __forceinline__ void pf_body(const pf_params &p, const uint8_t *wrow, ISSUE &issue_act,
-                                        uint8_t (*s_act)[PF_ACT_BUF], float (*s_cd)[PF_CD_ROWS * PF_T],
-                                        const uint32_t *s_pair, const float *s_w, const uint64_t *s_tab,
-                                        uint32_t kh, uint32_t col, uint32_t wcol, uint32_t cnt);
+template <bool Q3> using pf_raw_t = typename std::conditional<Q3, q3_raw, q2_half>::type;
 
+// One tile's view for the routed kernels: its expert, pairs and weight row,
+// and the per-lane direct-load offsets of its activation rows.
 template <bool Q3>
-__global__ void __launch_bounds__(pf_cfg<Q3>::NW * 64, Q3 ? 1 : 2) pf_expert_kernel(pf_params p) {
-    constexpr uint32_t NW = pf_cfg<Q3>::NW, NBUF = pf_cfg<Q3>::NBUF;
-    __shared__ __align__(16) uint8_t s_act[NBUF][PF_ACT_BUF];
-    __shared__ __align__(16) float s_cd[NBUF][PF_CD_ROWS * PF_T];
-    __shared__ uint32_t s_pair[PF_T];
-    __shared__ float s_w[PF_T];
-    __shared__ uint64_t s_tab[Q3 ? 32 : 1];    // the exp table of the SwiGLU epilogue
-    const uint32_t wg = blockIdx.x, xcd = wg & 7u, slot = wg >> 3;
-    const uint32_t t = xcd + 8u * (slot / p.n_rt), rt = slot % p.n_rt;
-    if (t >= p.tiles[0]) return;
-    const uint4 ti = ((const uint4 *)p.tiles)[1 + t];
-    const uint32_t e = ti.x, p0 = ti.y, cnt = ti.z;
-    const uint32_t tid = threadIdx.x, lane = tid & 63u, kh = lane >> 5, col = lane & 31u;
-    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const uint32_t ntb = (cnt + 31u) / 32u;
-    const uint32_t nblk = p.nblk;
-    if (tid < PF_T) {
-        const uint32_t pr = p.sorted[p0 + (tid < cnt ? tid : cnt - 1u)];
-        s_pair[tid] = pr;
-        if (Q3) s_w[tid] = p.weights[pr];
+struct pf_item {
+    uint32_t e, p0, cnt, ntb;
+    const uint8_t *wrow;
+    uint32_t wcol;
+    uint32_t voff[pf_cfg<Q3>::NW == 8u ? 4 : 1];
+    uint32_t rowoff_c[pf_cfg<Q3>::NW == 8u ? 1 : 2];
+};
+
+// A block's weight words into r (even blocks start dword-aligned, odd Q3
+// blocks 2 bytes in).
+template <bool Q3>
+__device__ __forceinline__ void pf_wload(pf_raw_t<Q3> &r, const uint8_t *wrow, uint32_t bn, uint32_t kh) {
+    if constexpr (Q3) {
+        const uint32_t o = SF37_Q3_BYTES * bn;
+        q3_load(r, wrow + (o & ~3u), wrow + ((o + 12u + 12u * kh) & ~3u));
+    } else {
+        q2_load_half(r, wrow + (uint64_t)SF37_Q2_BYTES * bn, kh);
     }
-    if (Q3) sf37_stage_exp_tab(s_tab);          // read after the main loop's barriers
-    // activation rows: tile slot `lane` for the tables; slot 32*gi + lane%32
-    // for the codes (pad slots repeat the last pair).  8 waves: wave 4*gi + wq
-    // copies slot group gi; 4 waves: wave wq copies both groups.
-    constexpr uint32_t NG = NW == 8u ? 1u : 2u;      // slot groups a wave copies
-    const uint32_t wq = wave & 3u;
-    uint32_t rowoff_c[NG];
-#pragma unroll
-    for (uint32_t k = 0; k < NG; k++) {
-        const uint32_t gi = NW == 8u ? wave >> 2 : k;
-        const uint32_t sl = 32u * gi + (lane & 31u);
-        const uint32_t pr = p.sorted[p0 + (sl < cnt ? sl : cnt - 1u)];
-        rowoff_c[k] = (Q3 ? pr / p.topk : pr) * nblk * (SF37_QK * 2u);
-    }
-    const uint32_t act_l = lds_addr(&s_act[0][0]), cd_l = lds_addr(&s_cd[0][0]);
-    // codes: a wave loads slot pairs (t, t + 16), t = 4q .. 4q+3 of its slot
-    // group(s): lanes 0..31 read slot t's 512-byte row, lanes 32..63 slot
-    // t + 16's.  Slice `part` of `nparts` (compile-time after inlining) of
-    // block b's loads.
-    // each load's per-lane byte offset within a block's codes is the same
-    // for every block: the 8-wave kernel forms its four once (measured 1-3 %
-    // faster); the 4-wave kernel re-forms its eight per block (eight more
-    // VGPRs measured 2 % slower there)
-    constexpr int NJ = 4 * (int)NG;
-    auto lane_off = [&](int jj) -> uint32_t {
-        const uint32_t k = (uint32_t)jj >> 2, t = 4u * wq + ((uint32_t)jj & 3u);
-        const uint32_t r0 = (uint32_t)__builtin_amdgcn_readlane((int)rowoff_c[k], (int)t);
-        const uint32_t r1 = (uint32_t)__builtin_amdgcn_readlane((int)rowoff_c[k], (int)t + 16);
-        return (kh ? r1 : r0) + 16u * col;
-    };
-    uint32_t voff[NW == 8u ? NJ : 1];
-    if constexpr (NW == 8u) {
-#pragma unroll
-        for (int jj = 0; jj < NJ; jj++) voff[jj] = lane_off(jj);
-    }
-    auto issue_act = [&](uint32_t b, int part, int nparts) {
-        const uint32_t bf = b % NBUF;
-        const uint8_t *cb = (const uint8_t *)p.act + (uint64_t)b * (SF37_QK * 2u);
-        const int j0 = NJ * part / nparts, j1 = NJ * (part + 1) / nparts;
-#pragma unroll
-        for (int jj = j0; jj < j1; jj++) {
-            const uint32_t k = (uint32_t)jj >> 2, gi = NW == 8u ? wave >> 2 : k;
-            const uint32_t t = 4u * wq + ((uint32_t)jj & 3u);
-            uint32_t vo;
-            if constexpr (NW == 8u) vo = voff[jj];
-            else vo = lane_off(jj);
-            lds_dma16(act_l + bf * PF_ACT_BUF + gi * PF_GRP + t * PF_RS, vo, cb);
-        }
-        if (part == 0) {   // tables of all slots: row a = C_a (a < 4) or d (a = 4).  8 waves:
-                           // wave a < 5 loads row a, waves 5..7 row 4 again; 4 waves: wave w
-                           // loads rows w and 4 (the same bytes from every wave; no branch)
-#pragma unroll
-            for (uint32_t k = 0; k < (NW == 8u ? 1u : 2u); k++) {
-                const uint32_t a = NW == 8u ? (wave < 5u ? wave : 4u) : (k ? 4u : wave);
-                const float *tb = p.tab + ((uint64_t)b * 5u + a) * p.tab_stride + p0;
-                lds_dma4(cd_l + bf * (PF_CD_ROWS * PF_T * 4u) + (NW == 8u ? wave : a) * PF_T * 4u, 4u * lane, tb);
-            }
-        }
-    };
-    // this lane's weight row
-    const uint32_t wcol = Q3 ? rt * PF_GU_R + 16u * wave + (col & 15u) : rt * PF_DN_R + 32u * wave + col;
-    const uint32_t blk_bytes = Q3 ? SF37_Q3_BYTES : SF37_Q2_BYTES;
-    const uint64_t row_bytes = (uint64_t)nblk * blk_bytes;
-    const uint8_t *wrow = (Q3 && col >= 16u ? p.w1 : p.w0) + ((uint64_t)e * p.out_rows + wcol) * row_bytes;
-    if (ntb == 1) pf_body<Q3, 1>(p, wrow, issue_act, s_act, s_cd, s_pair, s_w, s_tab, kh, col, wcol, cnt);
-    else pf_body<Q3, 2>(p, wrow, issue_act, s_act, s_cd, s_pair, s_w, s_tab, kh, col, wcol, cnt);
 }
 
-// Main loop and epilogue for NTB 32-pair blocks (the tile's pair count rounded up).
+// The block loop for NTB 32-pair blocks (the tile's pair count rounded up).
+// On entry block 0's weights are loading into ra and its activation rows
+// (with NBUF = 3, block 1's too) are issued; on exit every load is done.
+//
+// Pipeline: a block's weight words (registers) are loaded one block
+// ahead.  Three activation buffers (8 waves): the activation rows and
+// tables of block b+2 are loaded during block b, spread over its stages,
+// and the top of block b+1 waits for all but those newest
+// PF_DMA_PER_BLOCK loads.  Two buffers (4 waves): those of block b+1 are
+// issued at the start of block b, and the top of block b+1 waits for
+// every load.  Past the last block the loads repeat block nblk-1 (its
+// buffer then receives the same bytes again; uniform code, no branch
+// inside the stages); the final wait keeps no load in flight at the end
+// of the workgroup.
 template <bool Q3, int NTB, typename ISSUE>
-__device__ __forceinline__ void pf_body(const pf_params &p, const uint8_t *wrow, ISSUE &issue_act,
+__device__ __forceinline__ void pf_loop(const pf_params &p, const uint8_t *wrow, ISSUE &&issue_act,
                                         uint8_t (*s_act)[PF_ACT_BUF], float (*s_cd)[PF_CD_ROWS * PF_T],
-                                        const uint32_t *s_pair, const float *s_w, const uint64_t *s_tab,
-                                        uint32_t kh, uint32_t col, uint32_t wcol, uint32_t cnt) {
+                                        uint32_t kh, uint32_t col, pf_raw_t<Q3> &ra, float (*acc)[16]) {
     const uint32_t nblk = p.nblk;
-    float acc[NTB][16];
     f16v blk[PF_TB];
 #pragma unroll
     for (int i = 0; i < NTB; i++)
 #pragma unroll
         for (int r2 = 0; r2 < 16; r2++) acc[i][r2] = 0.0f;
-
-    // Pipeline: a block's weight words (registers) are loaded one block
-    // ahead.  Three activation buffers (8 waves): the activation rows and
-    // tables of block b+2 are loaded during block b, spread over its stages,
-    // and the top of block b+1 waits for all but those newest
-    // PF_DMA_PER_BLOCK loads.  Two buffers (4 waves): those of block b+1 are
-    // issued at the start of block b, and the top of block b+1 waits for
-    // every load.  Past the last block the loads repeat block nblk-1 (its
-    // buffer then receives the same bytes again; uniform code, no branch
-    // inside the stages); the final wait below keeps no load in flight at
-    // the end of the workgroup.
     constexpr uint32_t NBUF = pf_cfg<Q3>::NBUF;
     const uint32_t last = nblk - 1u;
     auto clampb = [&](uint32_t x) { return x < nblk ? x : last; };
@@ -638,26 +563,13 @@ __device__ __forceinline__ void pf_body(const pf_params &p, const uint8_t *wrow,
         if constexpr (NBUF == 3u) wait_vm_keep_next();
         else wait_vm0();
     };
-    using RAW = typename std::conditional<Q3, q3_raw, q2_half>::type;
-    RAW ra, rb;
-    auto wload = [&](RAW &r, uint32_t bn) {
-        if constexpr (Q3) {
-            // blocks in pairs: even blocks start dword-aligned, odd blocks 2 bytes in
-            const uint32_t o = SF37_Q3_BYTES * bn;
-            q3_load(r, wrow + (o & ~3u), wrow + ((o + 12u + 12u * kh) & ~3u));
-        } else {
-            q2_load_half(r, wrow + (uint64_t)SF37_Q2_BYTES * bn, kh);
-        }
-    };
+    pf_raw_t<Q3> rb;
     // the block's loads: weights of bn into r, activations of ba
-    auto pre = [&](RAW &r, uint32_t bn, uint32_t ba, int c, int nc) {
-        if (c == 0) wload(r, bn);
+    auto pre = [&](pf_raw_t<Q3> &r, uint32_t bn, uint32_t ba, int c, int nc) {
+        if (c == 0) pf_wload<Q3>(r, wrow, bn, kh);
         if constexpr (NBUF == 3u) issue_act(ba, c, nc);
         else if (c == 0) issue_act(ba, 0, 1);
     };
-    issue_act(0, 0, 1);
-    wload(ra, 0);
-    if constexpr (NBUF == 3u) issue_act(clampb(1u), 0, 1);
     constexpr int SH2 = Q3 ? 16 : 0;   // bit offset of an odd block's string in its words
     for (uint32_t b = 0; b < nblk; b += 2u) {
         top();
@@ -675,8 +587,15 @@ __device__ __forceinline__ void pf_body(const pf_params &p, const uint8_t *wrow,
         }
     }
     wait_vm0();
+}
 
-    // epilogue: D layout - lane holds column col, tokens 8*(r/4) + 4*kh + r%4
+// The tile's outputs.  D layout: lane holds column col, tokens
+// 8*(r/4) + 4*kh + r%4.  Gate/up: mid = ((g*sig(g))*u)*w per pair; down:
+// the per-pair rows.
+template <bool Q3, int NTB>
+__device__ __forceinline__ void pf_epilogue(const pf_params &p, const float (*acc)[16], const uint32_t *s_pair,
+                                            const float *s_w, const uint64_t *s_tab, uint32_t kh, uint32_t col,
+                                            uint32_t wcol, uint32_t cnt) {
 #pragma unroll
     for (uint32_t i = 0; i < (uint32_t)NTB; i++) {
         if constexpr (Q3) {
@@ -705,6 +624,122 @@ __device__ __forceinline__ void pf_body(const pf_params &p, const uint8_t *wrow,
                 if (tl < cnt) p.down_pair[(uint64_t)s_pair[tl] * p.out_rows + wcol] = acc[i][r2];
             }
         }
+    }
+}
+
+// Gate/up (Q3 = true): row tile = 64 F rows, wave w has gate rows
+// rt*64 + 16w + c and up rows (c < 16: gate, else up) as its 32 columns;
+// epilogue mid = ((g*sig(g))*u)*w per pair.  Down (Q3 = false): row tile =
+// 128 output rows, 32 per wave; epilogue down_pair[pair][row].  One item
+// (tile, row tile) per workgroup: tiles interleaved over the XCDs, a tile's
+// row tiles consecutive on one.  (A persistent form, each workgroup taking
+// every G-th item and issuing the next item's first loads before the
+// current item's epilogue, measured slower: down 652 -> 677 us at config 3
+// with 40 more VGPRs; gate/up did not fit its registers.)
+template <bool Q3>
+__global__ void __launch_bounds__(pf_cfg<Q3>::NW * 64, Q3 ? 1 : 2) pf_expert_kernel(pf_params p) {
+    constexpr uint32_t NW = pf_cfg<Q3>::NW, NBUF = pf_cfg<Q3>::NBUF;
+    __shared__ __align__(16) uint8_t s_act[NBUF][PF_ACT_BUF];
+    __shared__ __align__(16) float s_cd[NBUF][PF_CD_ROWS * PF_T];
+    __shared__ uint32_t s_pair[PF_T];
+    __shared__ float s_w[PF_T];
+    __shared__ uint64_t s_tab[Q3 ? 32 : 1];    // the exp table of the SwiGLU epilogue
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, kh = lane >> 5, col = lane & 31u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t nblk = p.nblk;
+    // activation rows: tile slot `lane` for the tables; slot 32*gi + lane%32
+    // for the codes (pad slots repeat the last pair).  8 waves: wave 4*gi + wq
+    // copies slot group gi; 4 waves: wave wq copies both groups.
+    constexpr uint32_t NG = NW == 8u ? 1u : 2u;      // slot groups a wave copies
+    constexpr int NJ = 4 * (int)NG;
+    const uint32_t wq = wave & 3u;
+    const uint32_t act_l = lds_addr(&s_act[0][0]), cd_l = lds_addr(&s_cd[0][0]);
+    const uint32_t blk_bytes = Q3 ? SF37_Q3_BYTES : SF37_Q2_BYTES;
+    const uint64_t row_bytes = (uint64_t)nblk * blk_bytes;
+    // codes: a wave loads slot pairs (t, t + 16), t = 4q .. 4q+3 of its slot
+    // group(s): lanes 0..31 read slot t's 512-byte row, lanes 32..63 slot
+    // t + 16's.  Each load's per-lane byte offset within a block's codes is
+    // the same for every block: the 8-wave kernel forms its four once
+    // (measured 1-3 % faster); the 4-wave kernel re-forms its eight per
+    // block (eight more VGPRs measured 2 % slower there)
+    auto lane_off = [&](const pf_item<Q3> &it, int jj) -> uint32_t {
+        const uint32_t k = (uint32_t)jj >> 2, t = 4u * wq + ((uint32_t)jj & 3u);
+        const uint32_t r0 = (uint32_t)__builtin_amdgcn_readlane((int)it.rowoff_c[k], (int)t);
+        const uint32_t r1 = (uint32_t)__builtin_amdgcn_readlane((int)it.rowoff_c[k], (int)t + 16);
+        return (kh ? r1 : r0) + 16u * col;
+    };
+    // the workgroup's item (tile, row tile), its pairs and routing weights
+    // in s_pair / s_w
+    pf_item<Q3> it;
+    {
+        const uint32_t idx = blockIdx.x, xcd = idx & 7u, slot = idx >> 3;
+        const uint32_t t = xcd + 8u * (slot / p.n_rt), rt = slot % p.n_rt;
+        if (t >= p.tiles[0]) return;
+        const uint4 ti = ((const uint4 *)p.tiles)[1 + t];
+        it.e = ti.x;
+        it.p0 = ti.y;
+        it.cnt = ti.z;
+        it.ntb = (it.cnt + 31u) / 32u;
+        if (tid < PF_T) {
+            const uint32_t pr = p.sorted[it.p0 + (tid < it.cnt ? tid : it.cnt - 1u)];
+            s_pair[tid] = pr;
+            if (Q3) s_w[tid] = p.weights[pr];
+        }
+#pragma unroll
+        for (uint32_t g = 0; g < NG; g++) {
+            const uint32_t gi = NW == 8u ? wave >> 2 : g;
+            const uint32_t sl = 32u * gi + (lane & 31u);
+            const uint32_t pr = p.sorted[it.p0 + (sl < it.cnt ? sl : it.cnt - 1u)];
+            it.rowoff_c[g] = (Q3 ? pr / p.topk : pr) * nblk * (SF37_QK * 2u);
+        }
+        if constexpr (NW == 8u) {
+#pragma unroll
+            for (int jj = 0; jj < NJ; jj++) it.voff[jj] = lane_off(it, jj);
+        }
+        // this lane's weight row
+        it.wcol = Q3 ? rt * PF_GU_R + 16u * wave + (col & 15u) : rt * PF_DN_R + 32u * wave + col;
+        it.wrow = (Q3 && col >= 16u ? p.w1 : p.w0) + ((uint64_t)it.e * p.out_rows + it.wcol) * row_bytes;
+    }
+    if (Q3) sf37_stage_exp_tab(s_tab);          // read after the block loop's barriers
+    // slice `part` of `nparts` (compile-time after inlining) of block b's
+    // activation loads
+    auto issue_act = [&](uint32_t b, int part, int nparts) {
+        const uint32_t bf = b % NBUF;
+        const uint8_t *cb = (const uint8_t *)p.act + (uint64_t)b * (SF37_QK * 2u);
+        const int j0 = NJ * part / nparts, j1 = NJ * (part + 1) / nparts;
+#pragma unroll
+        for (int jj = j0; jj < j1; jj++) {
+            const uint32_t k = (uint32_t)jj >> 2, gi = NW == 8u ? wave >> 2 : k;
+            const uint32_t t = 4u * wq + ((uint32_t)jj & 3u);
+            uint32_t vo;
+            if constexpr (NW == 8u) vo = it.voff[jj];
+            else vo = lane_off(it, jj);
+            lds_dma16(act_l + bf * PF_ACT_BUF + gi * PF_GRP + t * PF_RS, vo, cb);
+        }
+        if (part == 0) {   // tables of all slots: row a = C_a (a < 4) or d (a = 4).  8 waves:
+                           // wave a < 5 loads row a, waves 5..7 row 4 again; 4 waves: wave w
+                           // loads rows w and 4 (the same bytes from every wave; no branch)
+#pragma unroll
+            for (uint32_t k = 0; k < (NW == 8u ? 1u : 2u); k++) {
+                const uint32_t a = NW == 8u ? (wave < 5u ? wave : 4u) : (k ? 4u : wave);
+                const float *tb = p.tab + ((uint64_t)b * 5u + a) * p.tab_stride + it.p0;
+                lds_dma4(cd_l + bf * (PF_CD_ROWS * PF_T * 4u) + (NW == 8u ? wave : a) * PF_T * 4u, 4u * lane, tb);
+            }
+        }
+    };
+    // the first loads: block 0's weights, its activation rows (and block 1's
+    // with three buffers)
+    pf_raw_t<Q3> ra;
+    issue_act(0, 0, 1);
+    pf_wload<Q3>(ra, it.wrow, 0, kh);
+    if constexpr (NBUF == 3u) issue_act(nblk > 1u ? 1u : 0u, 0, 1);
+    float acc[2][16];
+    if (it.ntb == 1) {
+        pf_loop<Q3, 1>(p, it.wrow, issue_act, s_act, s_cd, kh, col, ra, acc);
+        pf_epilogue<Q3, 1>(p, acc, s_pair, s_w, s_tab, kh, col, it.wcol, it.cnt);
+    } else {
+        pf_loop<Q3, 2>(p, it.wrow, issue_act, s_act, s_cd, kh, col, ra, acc);
+        pf_epilogue<Q3, 2>(p, acc, s_pair, s_w, s_tab, kh, col, it.wcol, it.cnt);
     }
 }
 
