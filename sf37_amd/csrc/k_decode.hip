@@ -1401,6 +1401,17 @@ __device__ __forceinline__ void seg_chains(const float *d, const float *bs, floa
 // of these sub-items (mostly inside one group); the group's activation
 // blocks for up to four pairs sit in the wave's LDS slice.  The next
 // sub-item's blocks are loaded while the current one is computed.
+// Words [0, n) of src into LDS dst by direct global->LDS dword loads (lane
+// i of an instruction writes dst word c0 + i; lanes past n masked off).  All
+// threads of the workgroup call it; lds_copy_wait() must follow.
+__device__ __forceinline__ void lds_copy_words(uint32_t *dst, const uint32_t *src, uint32_t n) {
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u, nw = blockDim.x >> 6;
+    for (uint32_t c0 = wave * 64u; c0 < n; c0 += nw * 64u) {
+        const uint32_t c = c0 + lane;
+        if (c < n) __builtin_amdgcn_global_load_lds((const void *)(src + c), dst + c0, 4, 0, 0);
+    }
+}
+
 template <int SHNB>
 __global__ void __launch_bounds__(256) dec_down_kernel(dec_params p) {
     extern __shared__ __align__(16) unsigned char smem[];        // shared mid codes, then scales
@@ -1412,14 +1423,14 @@ __global__ void __launch_bounds__(256) dec_down_kernel(dec_params p) {
     uint32_t *so = gi + 3u + 2u * p.G;
     int8_t *shq = (int8_t *)smem;
     float *shs = (float *)(smem + p.T * p.F);
-    for (uint32_t i = threadIdx.x; i < 3u + 2u * p.G; i += blockDim.x) gi[i] = p.ginfo[i];
-    for (uint32_t i = threadIdx.x; i < P; i += blockDim.x) so[i] = p.sorted[i];
+    // tables and the shared mid into LDS by direct loads, all in flight at once
+    lds_copy_words(gi, p.ginfo, 3u + 2u * p.G);
+    lds_copy_words(so, p.sorted, P);
     if (sh) {
-        for (uint32_t i = threadIdx.x; i < p.T * p.F / 16u; i += blockDim.x)
-            ((u32x4 *)shq)[i] = ((const u32x4 *)p.sh_mq)[i];
-        for (uint32_t i = threadIdx.x; i < p.T * (p.F / 32u); i += blockDim.x) shs[i] = p.sh_ms[i];
+        lds_copy_words((uint32_t *)shq, (const uint32_t *)p.sh_mq, p.T * p.F / 4u);
+        lds_copy_words((uint32_t *)shs, (const uint32_t *)p.sh_ms, p.T * (p.F / 32u));
     }
-    __syncthreads();
+    lds_copy_wait();
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63u;
     act_t *xw = xsl[wave];
     const uint32_t nb = p.F / SF37_QK, rpd = 16u / nb, rpw = 4u * rpd;     // rows per DPP row / wave
