@@ -941,14 +941,75 @@ __device__ __forceinline__ void sh_chunk(const sh_raw &r, const uint8_t *act_lds
     }
 }
 
+// The same chunk with its LDS reads (activation operands and scales) all
+// issued first and its MFMAs next, then the epilogues in block order (same
+// arithmetic, same order per output).  For grids of at most two workgroups
+// per CU, where about one wave per SIMD leaves the LDS and MFMA latencies
+// unhidden: they are then paid once per chunk instead of once per read, at
+// ~225 VGPRs.
+template <int TBW>
+__device__ __forceinline__ void sh_chunk_batched(const sh_raw &r, const uint8_t *act_lds, const float *xs_lds,
+                                                 uint32_t kh, uint32_t col, uint32_t tb0, float (*acc)[16]) {
+    const uint8_t *a_row = act_lds + (32u * tb0 + col) * SH_RS;
+    const uint32_t sw = col & 7u;
+    const float *x_lane = xs_lds + 32u * tb0 + 4u * kh;
+    const i32x16 magic = (i32x16)SH_MAGIC_BITS;
+    i32x4 a[SH_CB][TBW];
+    float4 xv[SH_CB][TBW][4];
+#pragma unroll
+    for (uint32_t jj = 0; jj < SH_CB; jj++) {
+        const uint32_t slot = ((2u * jj + kh) ^ sw) * 16u;
+#pragma unroll
+        for (uint32_t i = 0; i < TBW; i++) {
+            a[jj][i] = *(const i32x4 *)(a_row + i * 32u * SH_RS + slot);
+#pragma unroll
+            for (int jq = 0; jq < 4; jq++) xv[jj][i][jq] = *(const float4 *)(x_lane + jj * SH_T + 32u * i + 8u * jq);
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    i32x16 D[SH_CB][TBW];
+    float ws[SH_CB], nws[SH_CB];
+#pragma unroll
+    for (uint32_t jj = 0; jj < SH_CB; jj++) {
+        const uint32_t o = sh_code_reg(jj);
+        i32x4 b;
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            b[i] = (int)((jj & 1u) ? r.c[o + i] : align_bytes(r.c[o + i + 1], r.c[o + i], 2u));
+        ws[jj] = sf37_f16((jj & 1u) ? r.s[jj] >> 16 : r.s[jj]);
+        nws[jj] = -SH_MAGIC * ws[jj];
+#pragma unroll
+        for (uint32_t i = 0; i < TBW; i++) D[jj][i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[jj][i], b, magic, 0, 0, 0);
+    }
+#pragma unroll
+    for (uint32_t jj = 0; jj < SH_CB; jj++) {
+#pragma unroll
+        for (uint32_t i = 0; i < TBW; i++) {
+            const f16v F = __builtin_bit_cast(f16v, D[jj][i]);
+#pragma unroll
+            for (int jq = 0; jq < 4; jq++) {
+                const float xa[4] = {xv[jj][i][jq].x, xv[jj][i][jq].y, xv[jj][i][jq].z, xv[jj][i][jq].w};
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const float p = __builtin_fmaf(F[4 * jq + q], ws[jj], nws[jj]);
+                    const float t = p * xa[q];
+                    acc[i][4 * jq + q] = acc[i][4 * jq + q] + t;
+                }
+            }
+        }
+    }
+}
+
 // GU: gate/up, 16 gate + 16 up rows per wave, epilogue mid = (g*sig(g))*u
 // (shared clamp).  Otherwise down: 32 output rows per wave, out written
 // directly.  TBW = 2: a wave takes both 32-token blocks of the tile, the
 // workgroup 128 weight columns; TBW = 1 (batches whose TBW = 2 grid would
 // leave CUs idle): waves 2 c and 2 c + 1 take token block 0 and 1 of the
-// same 32 columns, the workgroup 64 columns.
-template <bool GU, int TBW>
+// same 32 columns, the workgroup 64 columns.  BAT (TBW = 1 only): the chunk
+// body with its reads batched (sh_chunk_batched).
+template <bool GU, int TBW, bool BAT = false>
 __global__ void __launch_bounds__(256, 2) sh_gemm_kernel(sh_params p) {
+    static_assert(!BAT || TBW == 1, "the batched chunk body is the narrow form's");
     __shared__ __align__(16) uint8_t s_act[2][SH_BUF];
     __shared__ __align__(16) float s_xs[2][SH_CB * SH_T];
     __shared__ uint64_t s_tab[GU ? 32 : 1];    // the exp table of the SwiGLU epilogue
@@ -1005,7 +1066,8 @@ __global__ void __launch_bounds__(256, 2) sh_gemm_kernel(sh_params p) {
             sh_raw r;
             sh_swap(r, ha);
             sh_load(hb, wrow, c1, kh);
-            sh_chunk<TBW>(r, s_act[c & 1u], s_xs[c & 1u], kh, col, tb0, acc);
+            if constexpr (BAT) sh_chunk_batched<TBW>(r, s_act[c & 1u], s_xs[c & 1u], kh, col, tb0, acc);
+            else sh_chunk<TBW>(r, s_act[c & 1u], s_xs[c & 1u], kh, col, tb0, acc);
         }
         if (c + 1u < nchunk) {
             wait_vm0();
@@ -1015,7 +1077,8 @@ __global__ void __launch_bounds__(256, 2) sh_gemm_kernel(sh_params p) {
             sh_raw r;
             sh_swap(r, hb);
             sh_load(ha, wrow, c2, kh);
-            sh_chunk<TBW>(r, s_act[(c + 1u) & 1u], s_xs[(c + 1u) & 1u], kh, col, tb0, acc);
+            if constexpr (BAT) sh_chunk_batched<TBW>(r, s_act[(c + 1u) & 1u], s_xs[(c + 1u) & 1u], kh, col, tb0, acc);
+            else sh_chunk<TBW>(r, s_act[(c + 1u) & 1u], s_xs[(c + 1u) & 1u], kh, col, tb0, acc);
         }
     }
     wait_vm0();
@@ -1141,7 +1204,7 @@ extern "C" int sf37k_pf_down(float *down_pair, const uint8_t *down_w, const void
 // workgroups) is under two workgroups per CU (measured crossover: at 2048
 // tokens the 128-column gate/up grid of 640 workgroups takes 128 us, the
 // 64-column one 157 us; at 512 tokens 64 columns win, 73 against 75 us).
-static bool sh_narrow(uint32_t n_ct, uint32_t n_tt) {
+static uint32_t sh_cus() {
     static int cus = 0;
     if (!cus) {
         int dev = 0;
@@ -1149,8 +1212,14 @@ static bool sh_narrow(uint32_t n_ct, uint32_t n_tt) {
             hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
             cus = 256;
     }
-    return (uint64_t)n_ct * n_tt < 2ull * (uint64_t)cus;
+    return (uint32_t)cus;
 }
+static bool sh_narrow(uint32_t n_ct, uint32_t n_tt) { return (uint64_t)n_ct * n_tt < 2ull * sh_cus(); }
+// The narrow form's batched chunk body when its grid (n_ct x n_tt, 64
+// columns) is one round at two workgroups per CU (measured, gate/up + down:
+// 256 tokens 57 + 21 -> 46 + 16 us, 512 tokens 73 + 27 -> 70 + 24 us; at
+// 1024 tokens, 1.25 rounds, 97 -> 100 us, so that grid keeps the other body).
+static bool sh_batched(uint32_t n_ct, uint32_t n_tt) { return (uint64_t)n_ct * n_tt <= 2ull * sh_cus(); }
 
 extern "C" int sf37k_sh_supported(uint32_t in_dim, uint32_t mid_dim, uint32_t out_dim) {
     return in_dim % (32u * SH_CB * 2u) == 0 && mid_dim % (32u * SH_CB * 2u) == 0 && mid_dim % 64u == 0 &&
@@ -1181,7 +1250,10 @@ extern "C" int sf37k_sh_gate_up(float *mid, const uint8_t *gate_w, const uint8_t
     p.clamp = clamp;
     if (sh_narrow(mid_dim / 64u, p.n_tt)) {
         p.n_ct = mid_dim / 32u;
-        hipLaunchKernelGGL((sh_gemm_kernel<true, 1>), dim3(p.n_ct * p.n_tt), dim3(256), 0, (hipStream_t)s, p);
+        if (sh_batched(p.n_ct, p.n_tt))
+            hipLaunchKernelGGL((sh_gemm_kernel<true, 1, true>), dim3(p.n_ct * p.n_tt), dim3(256), 0, (hipStream_t)s, p);
+        else
+            hipLaunchKernelGGL((sh_gemm_kernel<true, 1>), dim3(p.n_ct * p.n_tt), dim3(256), 0, (hipStream_t)s, p);
     } else {
         p.n_ct = mid_dim / 64u;
         hipLaunchKernelGGL((sh_gemm_kernel<true, 2>), dim3(p.n_ct * p.n_tt), dim3(256), 0, (hipStream_t)s, p);
@@ -1202,7 +1274,10 @@ extern "C" int sf37k_sh_down(float *out, const uint8_t *down_w, const void *a8, 
     p.n_tt = (n_tok + SH_T - 1u) / SH_T;
     if (sh_narrow(out_dim / 128u, p.n_tt)) {
         p.n_ct = out_dim / 64u;
-        hipLaunchKernelGGL((sh_gemm_kernel<false, 1>), dim3(p.n_ct * p.n_tt), dim3(256), 0, (hipStream_t)s, p);
+        if (sh_batched(p.n_ct, p.n_tt))
+            hipLaunchKernelGGL((sh_gemm_kernel<false, 1, true>), dim3(p.n_ct * p.n_tt), dim3(256), 0, (hipStream_t)s, p);
+        else
+            hipLaunchKernelGGL((sh_gemm_kernel<false, 1>), dim3(p.n_ct * p.n_tt), dim3(256), 0, (hipStream_t)s, p);
     } else {
         p.n_ct = out_dim / 128u;
         hipLaunchKernelGGL((sh_gemm_kernel<false, 2>), dim3(p.n_ct * p.n_tt), dim3(256), 0, (hipStream_t)s, p);

@@ -178,11 +178,13 @@ def test_config3_layer_sample_vs_oracle(H, O, layer):
     assert_bitexact(out[idx], want, "config 3 sample")
 
 
-@pytest.mark.parametrize("n_tok", [77, 300])
+@pytest.mark.parametrize("n_tok", [77, 300, 1100])
 def test_layer_mfma_equals_staged(H, layer, n_tok):
     """Whole layer (router on the device, shared expert and routed experts on
     the matrix cores) against the dot-product kernels (prefill_mfma=0), bit for
-    bit; token counts that leave partial 32- and 64-token tiles.  The matrix-
+    bit; token counts that leave partial 32- and 64-token tiles (77 and 300:
+    the shared GEMM's 64-column form with its batched chunk body, 1100: the
+    same form over more than one round, with the other body).  The matrix-
     core layer runs with the shared expert on the side stream (joined before
     the routed combine) and in order on the library stream."""
     from sf37_amd import moe
