@@ -899,7 +899,7 @@ __device__ __forceinline__ void dma16(uint32_t lds, uint32_t voff, const uint8_t
 constexpr uint32_t ITEM_NONE = 0xffffffffu;
 template <int NBP>
 __device__ void up_items_pairs(const dec_params &p, const uint32_t *gi, const uint32_t *so, const uint32_t *xo,
-                               const act_lds_t *xs, uint8_t *tile, uint32_t gw, uint32_t nw) {
+                               const act_lds_t *xs, uint8_t *tile, uint32_t gw, uint32_t nw, bool prefilled) {
     constexpr uint32_t RPI = 64u / (uint32_t)NBP;           // rows per item
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t r = lane / (uint32_t)NBP, j = lane % (uint32_t)NBP;
@@ -1005,8 +1005,8 @@ __device__ void up_items_pairs(const dec_params &p, const uint32_t *gi, const ui
     // one item: wait for its tile (and the stores before it), read the
     // lane's pair, refill the tile with the next item, compute
     const uint32_t *pl = (const uint32_t *)tile + lane * 55u;
-    uint32_t it = next();
-    if (it != ITEM_NONE) fill(it);
+    uint32_t it = next();                 // gw itself when the launch prologue already filled its tile
+    if (it != ITEM_NONE && !prefilled) fill(it);
     uint32_t nx = it != ITEM_NONE ? next() : ITEM_NONE;
     while (it != ITEM_NONE) {
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");     // the tile (and the stores before it)
@@ -1093,25 +1093,37 @@ __global__ void __launch_bounds__(512) dec_select_kernel(dec_params p, uint32_t 
 }
 
 // The routed part of the up launch on the block-pair DMA path (rows of 4, 8
-// or 16 blocks): each token's activation blocks staged even blocks first,
-// then odd ones, and a 14 KiB tile per wave after them.
+// or 16 blocks), after the launch prologue has staged each token's
+// activation blocks (even blocks first, then odd ones) and, with prefilled,
+// started the wave's first tile: the pairs' activation offsets, then the
+// items.  A 14 KiB tile per wave sits after the activations.
 __device__ void up_routed_dma(const dec_params &p, unsigned char *smem, act_lds_t *xs, const uint32_t *gi,
-                              const uint32_t *so, uint32_t *xo, uint32_t gw, uint32_t nw, uint32_t wave) {
+                              const uint32_t *so, uint32_t *xo, uint32_t gw, uint32_t nw, uint32_t wave,
+                              bool prefilled) {
     const uint32_t nbK = p.K / SF37_QK, P = p.T * p.topk;
-    constexpr uint32_t A16 = sizeof(act_t) / 16u, L16 = sizeof(act_lds_t) / 16u;
-    for (uint32_t i = threadIdx.x; i < p.T * nbK * A16; i += blockDim.x) {
-        const uint32_t blk = i / A16, c = i - blk * A16;
-        const uint32_t t = blk / nbK, b = blk - t * nbK;
-        ((u32x4 *)xs)[(t * nbK + (b & 1u) * (nbK >> 1) + (b >> 1)) * L16 + c] = ((const u32x4 *)p.xq)[i];
-    }
     for (uint32_t i = threadIdx.x; i < P; i += blockDim.x) xo[i] = (so[i] / p.topk) * nbK;
     __syncthreads();
     uint8_t *tile = smem + tile_base(p.K, p.T, p.G, P) + wave * TILE_LDS;
     switch (nbK) {
-        case 4: up_items_pairs<2>(p, gi, so, xo, xs, tile, gw, nw); break;
-        case 8: up_items_pairs<4>(p, gi, so, xo, xs, tile, gw, nw); break;
-        default: up_items_pairs<8>(p, gi, so, xo, xs, tile, gw, nw); break;
+        case 4: up_items_pairs<2>(p, gi, so, xo, xs, tile, gw, nw, prefilled); break;
+        case 8: up_items_pairs<4>(p, gi, so, xo, xs, tile, gw, nw, prefilled); break;
+        default: up_items_pairs<8>(p, gi, so, xo, xs, tile, gw, nw, prefilled); break;
     }
+}
+
+// LDS direct loads with a per-lane source address: lane i writes LDS bytes
+// [m0 + 4 i, + 4) (dword) or [m0 + 16 i, + 16) (dwordx4); masked lanes write
+// nothing.  Issued through inline asm, so the compiler neither tracks nor
+// waits for them: the caller waits (s_waitcnt vmcnt) before reading.
+__device__ __forceinline__ void dma4_lane(uint32_t lds, const void *src) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, off" ::"s"(__builtin_amdgcn_readfirstlane(lds)),
+                 "v"(src)
+                 : "memory");
+}
+__device__ __forceinline__ void dma16_lane(uint32_t lds, const void *src) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(__builtin_amdgcn_readfirstlane(lds)),
+                 "v"(src)
+                 : "memory");
 }
 
 // Batches with a select launch on the DMA path: workgroups of 8 waves (4-7
@@ -1124,12 +1136,70 @@ __global__ void __launch_bounds__(512) dec_up_dma_kernel(dec_params p) {
     uint32_t *gi = (uint32_t *)(xs + p.T * nbK);
     uint32_t *so = gi + 3u + 2u * p.G;
     uint32_t *xo = so + P;
-    for (uint32_t i = threadIdx.x; i < 3u + 2u * p.G; i += blockDim.x) gi[i] = p.ginfo[i];
-    for (uint32_t i = threadIdx.x; i < P; i += blockDim.x) so[i] = p.sorted[i];
-    __syncthreads();
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), nwg = blockDim.x >> 6;
-    up_routed_dma(p, smem, xs, gi, so, xo, blockIdx.x * nwg + wave, gridDim.x * nwg, wave);
+    const uint32_t lane = threadIdx.x & 63u, gw = blockIdx.x * nwg + wave, nw = gridDim.x * nwg;
+    // everything the workgroup stages goes by direct loads issued at once:
+    // the group table and pair order (dwords), the activation blocks (even
+    // blocks first, then odd; lane = destination 16-byte chunk, the pad
+    // chunks of act_lds_t masked), then this wave's first tile (its static
+    // item gw, whose expert is read from the table in memory), so the tile
+    // is in flight while the rest arrives
+    {
+        const uint32_t n_gi = 3u + 2u * p.G;
+        for (uint32_t c0 = wave * 64u; c0 < n_gi; c0 += nwg * 64u)
+            if (c0 + lane < n_gi) dma4_lane((uint32_t)(uintptr_t)(gi + c0), p.ginfo + c0 + lane);
+        for (uint32_t c0 = wave * 64u; c0 < P; c0 += nwg * 64u)
+            if (c0 + lane < P) dma4_lane((uint32_t)(uintptr_t)(so + c0), p.sorted + c0 + lane);
+        constexpr uint32_t A16 = sizeof(act_t) / 16u, L16 = sizeof(act_lds_t) / 16u;
+        const uint32_t n_x = p.T * nbK * L16, half = nbK >> 1;
+        for (uint32_t c0 = wave * 64u; c0 < n_x; c0 += nwg * 64u) {
+            const uint32_t d = c0 + lane, bp = d / L16, c = d - bp * L16;
+            const uint32_t t = bp / nbK, sl = bp - t * nbK;
+            const uint32_t b = sl < half ? 2u * sl : 2u * (sl - half) + 1u;
+            if (d < n_x && c < A16)
+                dma16_lane((uint32_t)(uintptr_t)xs + 16u * c0, (const u32x4 *)p.xq + ((uint64_t)(t * nbK + b) * A16 + c));
+        }
+    }
+    bool prefilled = false;
+    {
+        const uint32_t NBP = nbK / 2u, RPI = 64u / NBP, ipm = p.F / RPI, ipg = 2u * ipm;
+        const uint32_t g0 = gw / ipg, g0c = g0 < p.G ? g0 : p.G - 1u;
+        // the group count and this group's expert by scalar loads (the
+        // compiler's vector loads would wait for the direct loads above)
+        uint32_t n_grp, e0;
+        {
+            const uint64_t gp = (uint64_t)(uintptr_t)p.ginfo;
+            const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)gp), hi = __builtin_amdgcn_readfirstlane((uint32_t)(gp >> 32));
+            const uint64_t base = ((uint64_t)hi << 32) | lo;
+            const uint32_t off = __builtin_amdgcn_readfirstlane(4u * (2u + p.G + g0c));
+            asm volatile("s_load_dword %0, %2, 0x0\n\ts_load_dword %1, %2, %3\n\ts_waitcnt lgkmcnt(0)"
+                         : "=&s"(n_grp), "=&s"(e0)
+                         : "s"(base), "s"(off)
+                         : "memory");
+        }
+        const uint32_t n_items = n_grp * ipg;
+        const uint32_t n_stat = nw * ((n_items * (p.T <= 8u ? 9u : 8u) / 10u) / nw);
+        if (gw < n_stat && (nbK == 4u || nbK == 8u || nbK == 16u)) {
+            const uint32_t r2 = gw - g0 * ipg, m = r2 >= ipm ? 1u : 0u, k = r2 - m * ipm;
+            const uint64_t row_bytes = (uint64_t)nbK * SF37_Q3_BYTES, exp_bytes = (uint64_t)p.F * row_bytes;
+            const uint8_t *src = expert_base(p, m ? p.up_w : p.gate_w, m ? p.sh_up : p.sh_gate, e0, exp_bytes) +
+                                 (uint64_t)(k * RPI) * row_bytes;
+            const uint32_t tile_lds = (uint32_t)(uintptr_t)(smem + tile_base(p.K, p.T, p.G, P) + wave * TILE_LDS);
+            constexpr uint32_t last = TILE_BYTES / 16u - 1u;
+#pragma unroll
+            for (uint32_t i = 0; i < TILE_LOADS; i++) {
+                const uint32_t c = i * 64u + lane;
+                dma16(tile_lds + 1024u * i, 16u * (c < last ? c : last), src);
+            }
+            prefilled = true;
+        }
+    }
+    if (prefilled) asm volatile("s_waitcnt vmcnt(14)" ::: "memory");      // all but the tile's TILE_LOADS
+    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    up_routed_dma(p, smem, xs, gi, so, xo, gw, nw, wave, prefilled);
 }
+static_assert(TILE_LOADS == 14u, "the prologue's wait leaves exactly one tile's loads in flight");
 
 // With UPSEL (few tokens, no select launch): workgroups [0, n_sh) run the
 // shared gate/up rows, the rest the routed items after each has formed the
