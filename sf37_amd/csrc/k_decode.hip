@@ -897,6 +897,12 @@ __device__ __forceinline__ void dma16(uint32_t lds, uint32_t voff, const uint8_t
 // w + nw, ... up to 70% of them, then items from counters (the up queues),
 // which evens out the waves' finishing times.
 constexpr uint32_t ITEM_NONE = 0xffffffffu;
+// Items of the DMA up launch dealt round-robin before the counters take
+// over: 90 % up to 8 tokens, 80 % above, where fewer waves share a CU
+// (measured best at 8 and 16 tokens); a multiple of the waves.
+__device__ __forceinline__ uint32_t up_static_items(uint32_t n_items, uint32_t nw, uint32_t T) {
+    return nw * ((n_items * (T <= 8u ? 9u : 8u) / 10u) / nw);
+}
 template <int NBP>
 __device__ void up_items_pairs(const dec_params &p, const uint32_t *gi, const uint32_t *so, const uint32_t *xo,
                                const act_lds_t *xs, uint8_t *tile, uint32_t gw, uint32_t nw, bool prefilled) {
@@ -909,9 +915,8 @@ __device__ void up_items_pairs(const dec_params &p, const uint32_t *gi, const ui
     const uint64_t row_bytes = (uint64_t)nbK * SF37_Q3_BYTES, exp_bytes = (uint64_t)p.F * row_bytes;
     // items [0, n_stat) round-robin (wave gw: gw, gw + nw, ...); the rest
     // from counters, each asked for after a compute while the next tile
-    // loads.  90% static up to 8 tokens, 80% above, where fewer waves share
-    // a CU (measured best at 8 and 16 tokens).
-    const uint32_t n_stat = nw * ((n_items * (p.T <= 8u ? 9u : 8u) / 10u) / nw);
+    // loads
+    const uint32_t n_stat = up_static_items(n_items, nw, p.T);
     // the dynamic items are split over UP_QUEUES counters, each owning a
     // contiguous share (one counter for every wave of the chip serialises
     // the requests); a queue's waves come from every XCD (workgroups are
@@ -1177,9 +1182,7 @@ __global__ void __launch_bounds__(512) dec_up_dma_kernel(dec_params p) {
                          : "s"(base), "s"(off)
                          : "memory");
         }
-        const uint32_t n_items = n_grp * ipg;
-        const uint32_t n_stat = nw * ((n_items * (p.T <= 8u ? 9u : 8u) / 10u) / nw);
-        if (gw < n_stat && (nbK == 4u || nbK == 8u || nbK == 16u)) {
+        if (gw < up_static_items(n_grp * ipg, nw, p.T) && (nbK == 4u || nbK == 8u || nbK == 16u)) {
             const uint32_t r2 = gw - g0 * ipg, m = r2 >= ipm ? 1u : 0u, k = r2 - m * ipm;
             const uint64_t row_bytes = (uint64_t)nbK * SF37_Q3_BYTES, exp_bytes = (uint64_t)p.F * row_bytes;
             const uint8_t *src = expert_base(p, m ? p.up_w : p.gate_w, m ? p.sh_up : p.sh_gate, e0, exp_bytes) +
