@@ -118,6 +118,23 @@ def test_fused_layer_equals_staged(H, layer, n_tok, routing):
     assert_bitexact(a[0], b[0], f"out ({n_tok} tokens, {routing})")
 
 
+@pytest.mark.parametrize("n_tok", [2, 4, 5, 6, 7, 9, 10, 11, 12, 14, 15])
+def test_fused_layer_every_batch_size(H, layer, n_tok):
+    """The batch sizes the cases above skip (each launch plan of 1..16
+    tokens: the DMA up launch with and without its first tiles started in
+    the prologue, the select launch's top-k workgroup counts, the down
+    kernel's shared-down batch instances), fused against staged."""
+    rng = np.random.default_rng(2000 + n_tok)
+    x = rng.standard_normal((n_tok, K)).astype(np.float32)
+    logits = rng.standard_normal((n_tok, E)).astype(np.float32)
+    say(f"fused vs staged: {n_tok} tokens")
+    a = run_layer(H, layer, x, logits, True)
+    b = run_layer(H, layer, x, logits, False)
+    assert np.array_equal(a[1], b[1])
+    assert_bitexact(a[2], b[2], "weights")
+    assert_bitexact(a[0], b[0], f"out ({n_tok} tokens)")
+
+
 def test_fused_layer_after_smaller_batches(H, layer):
     """Batch sizes going down and up again in one process: each kernel's
     dynamic-LDS opt-in must stay at the largest size asked for (a 16-token
