@@ -135,6 +135,26 @@ def test_fused_layer_every_batch_size(H, layer, n_tok):
     assert_bitexact(a[0], b[0], f"out ({n_tok} tokens)")
 
 
+@pytest.mark.parametrize("seed", range(12))
+def test_fused_layer_random_batches(H, layer, seed):
+    """Seeded random batches (1..16 tokens, hot experts of random count and
+    strength, so groups of 1..16 pairs and launch plans of every shape),
+    fused against staged, bit for bit."""
+    rng = np.random.default_rng(5000 + seed)
+    n_tok = int(rng.integers(1, 17))
+    hot = tuple(int(e) for e in rng.choice(E, size=int(rng.integers(0, 9)), replace=False))
+    logits = rng.standard_normal((n_tok, E)).astype(np.float32)
+    if hot:
+        logits[:, list(hot)] += np.float32(rng.uniform(0.5, 8.0))
+    x = (rng.standard_normal((n_tok, K)) * rng.uniform(0.5, 4.0)).astype(np.float32)
+    say(f"random batch {seed}: {n_tok} tokens, {len(hot)} hot experts")
+    a = run_layer(H, layer, x, logits, True)
+    b = run_layer(H, layer, x, logits, False)
+    assert np.array_equal(a[1], b[1])
+    assert_bitexact(a[2], b[2], "weights")
+    assert_bitexact(a[0], b[0], f"out (seed {seed}, {n_tok} tokens)")
+
+
 def test_fused_layer_after_smaller_batches(H, layer):
     """Batch sizes going down and up again in one process: each kernel's
     dynamic-LDS opt-in must stay at the largest size asked for (a 16-token
