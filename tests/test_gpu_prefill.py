@@ -6,8 +6,9 @@ staged path (option prefill_mfma=0) and the CPU oracle bit for bit.  Cases:
 a small layer with an odd number of 256-blocks per row, a group larger than
 one 128-pair tile, an invalid expert id and an expert repeated inside a
 token; the BASELINE layer at config 2 (Zipf routing, idle experts, groups
-of hundreds of pairs) against the staged path; config 3 (4096 tokens) on a
-sample of tokens against the oracle.
+of hundreds of pairs) and skewed batches (eight experts taken by all or half
+of the tokens) against the staged path; config 3 (4096 tokens) on a sample
+of tokens against the oracle.
 """
 import sys
 
@@ -146,6 +147,34 @@ def test_config2_batch_mfma_equals_staged(H, layer):
     assert a[2] == 2 and b[2] == 0
     assert_bitexact(a[1], b[1], "config 2 mid")
     assert_bitexact(a[0], b[0], "config 2 out")
+
+
+@pytest.mark.parametrize("n_tok,hot_frac", [(200, 1.0), (700, 1.0), (700, 0.5)])
+def test_batch_hot_experts_mfma_equals_staged(H, layer, n_tok, hot_frac):
+    """Skewed batches: a share of the tokens (all, or every other one) select
+    the same eight experts (boosted logits, distinct boosts so the slot
+    order is fixed), the rest route at random: groups of hundreds of pairs
+    cut into many 64-pair tiles, beside groups of a few pairs or (all hot)
+    280 idle experts.  out and every pair's mid equal the staged path bit
+    for bit."""
+    import oracle as O
+    rng = np.random.default_rng(8100 + n_tok + int(hot_frac * 10))
+    x = rng.standard_normal((n_tok, K)).astype(np.float32)
+    logits = rng.standard_normal((n_tok, E)).astype(np.float32)
+    hot = rng.choice(E, size=TOPK, replace=False)
+    rows = np.arange(n_tok) if hot_frac == 1.0 else np.arange(0, n_tok, 2)
+    for k, e in enumerate(hot):
+        logits[rows, e] += np.float32(12.0 + k)
+    sel, w, _ = O.router_select(logits, np.zeros(E, np.float32), TOPK, 3.0)
+    counts = np.bincount(sel.ravel(), minlength=E)
+    assert counts[hot].min() >= len(rows)
+    assert hot_frac < 1.0 or (counts == 0).sum() == E - TOPK
+    say(f"hot batch: {n_tok} tokens, {len(rows)} on the hot experts, largest group {counts.max()} pairs")
+    a = batch_run(H, layer, sel, w, x, True)
+    b = batch_run(H, layer, sel, w, x, False)
+    assert a[2] == 2 and b[2] == 0
+    assert_bitexact(a[1], b[1], f"hot batch mid ({n_tok} tokens)")
+    assert_bitexact(a[0], b[0], f"hot batch out ({n_tok} tokens)")
 
 
 def test_config3_layer_sample_vs_oracle(H, O, layer):
