@@ -61,89 +61,26 @@ __global__ void __launch_bounds__(256) f32_matmul_kernel(float *__restrict__ out
 // Prefill logits on the fp64 matrix cores (v_mfma_f64_16x16x4f64): the
 // fp32 operands convert exactly to binary64, every product is exact and the
 // sums are binary64, so the logits stay within 1 ulp of the CPU's ordered
-// sum.  A wave owns 16 tokens x 16 experts, a workgroup four expert tiles
-// of the same tokens (they share the x rows in the caches).  Lane l loads
-// float4 runs x[t0 + l%16][k + 4(l/16) ..] and W[e0 + l%16][same k]; MFMA
-// step s of a 16-wide k slice takes element s of both, so the MFMA's k
-// index g = l/16 is k + 4g + s in both operands.  Chunks of 64 k are
-// double-buffered in registers.  K must be a multiple of 128.
-typedef double rt_f64x4 __attribute__((ext_vector_type(4)));
-constexpr uint32_t RM_CH = 4;   // 16-wide k slices per chunk
-
-__device__ __forceinline__ void rm_load(sf37_f32x4 (&a)[RM_CH], sf37_f32x4 (&b)[RM_CH], const float *xa,
-                                        const float *wb, uint32_t k) {
-#pragma unroll
-    for (uint32_t c = 0; c < RM_CH; c++) {
-        a[c] = *(const sf37_f32x4 *)(xa + k + 16u * c);
-        b[c] = *(const sf37_f32x4 *)(wb + k + 16u * c);
-    }
-}
-
-// Two accumulation chains (even / odd slices) so consecutive MFMAs of a
-// wave do not wait on each other; they are added once at the end.
-__device__ __forceinline__ void rm_mfma(rt_f64x4 (&acc)[2], const sf37_f32x4 (&a)[RM_CH],
-                                        const sf37_f32x4 (&b)[RM_CH]) {
-#pragma unroll
-    for (int s = 0; s < 4; s++)
-#pragma unroll
-        for (uint32_t c = 0; c < RM_CH; c++)
-            acc[c & 1u] = __builtin_amdgcn_mfma_f64_16x16x4f64((double)a[c][s], (double)b[c][s], acc[c & 1u], 0, 0, 0);
-}
-
-// Workgroups go to the 8 XCDs round-robin by id: XCD k takes the token
-// tiles t = k (mod 8) and walks them expert-tile by expert-tile, so its L2
-// holds one 64-row slice of W at a time and each x row is read by one XCD.
-__global__ void __launch_bounds__(256) f64mm_router_kernel(float *__restrict__ out, const float *__restrict__ w,
-                                                           const float *__restrict__ x, uint32_t K, uint32_t E,
-                                                           uint32_t T) {
-    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
-    const uint32_t nt = (T + 15u) / 16u, ne = (E + 63u) / 64u;
-    const uint32_t xcd = blockIdx.x & 7u, q = blockIdx.x >> 3;
-    const uint32_t ct = nt > xcd ? (nt - xcd + 7u) / 8u : 0u;      // token tiles of this XCD
-    if (q >= ct * ne) return;
-    const uint32_t et = q / ct, tt = xcd + 8u * (q - et * ct);
-    const uint32_t e0 = (et * 4u + wave) * 16u;
-    if (e0 >= E) return;
-    const uint32_t t0 = tt * 16u, i = lane & 15u, g = lane >> 4;
-    const uint32_t tr = t0 + i < T ? t0 + i : T - 1u, er = e0 + i < E ? e0 + i : E - 1u;   // loads stay in bounds
-    const float *xa = x + (uint64_t)tr * K + 4u * g;
-    const float *wb = w + (uint64_t)er * K + 4u * g;
-    rt_f64x4 acc[2] = {{0.0, 0.0, 0.0, 0.0}, {0.0, 0.0, 0.0, 0.0}};
-    sf37_f32x4 a0[RM_CH], b0[RM_CH], a1[RM_CH], b1[RM_CH];
-    rm_load(a0, b0, xa, wb, 0);
-    for (uint32_t k = 0; k < K; k += 128u) {
-        rm_load(a1, b1, xa, wb, k + 64u);
-        rm_mfma(acc, a0, b0);
-        if (k + 128u < K) rm_load(a0, b0, xa, wb, k + 128u);
-        rm_mfma(acc, a1, b1);
-    }
-    // D: lane l holds rows l/16 + 4r (tokens), column l%16 (expert)
-    const uint32_t e = e0 + i;
-#pragma unroll
-    for (uint32_t r = 0; r < 4; r++) {
-        const uint32_t t = t0 + g + 4u * r;
-        if (t < T && e < E) out[(uint64_t)t * E + e] = (float)(acc[0][r] + acc[1][r]);
-    }
-}
-
-// The same product with both operands staged in LDS: a workgroup owns 32
-// tokens x RL_E experts (64, or 96: 288 = 3 x 96 has no padded expert
-// columns and needs fewer workgroups) and walks K in 64-wide chunks (x and W
-// rows copied with float4 loads, the next chunk held in registers while the
-// current one is consumed); wave w takes tokens 16(w & 1).. and experts
-// RL_E/2 (w >> 1).., RL_E/32 MFMA tiles sharing the token operand.  Rows are
+// sum.  A workgroup owns 32 tokens x RL_E experts (96 when that pads E less
+// than 64 does: 288 = 3 x 96) and one of S contiguous K slices, walked in
+// 64-wide chunks: x and W rows copied with float4 loads into LDS (rows
 // padded by four floats so a step's 16 rows x 4 columns fall in distinct
-// banks.  K % 128 == 0.  The expert tile is chosen per call by the number of
-// rounds of one workgroup per CU each shape needs (a CU running two of these
-// workgroups takes twice as long; a 96-expert workgroup takes 1.5x a 64-expert
-// one).
-constexpr uint32_t RL_T = 32, RL_K = 64, RL_P = RL_K + 4;
-#ifndef RL_MIN_TOK
-#define RL_MIN_TOK 1024u   // smaller batches keep the register kernel (more workgroups)
-#endif
+// banks), the next chunk held in registers while the current one is
+// consumed.  Wave w takes tokens 16(w & 1).. and experts RL_E/2 (w >> 1)..,
+// RL_E/32 MFMA tiles sharing the token operand; MFMA step s4 takes column
+// s4 + l/16 of both operands, so the k index is the same in A and B.
+// Token tiles go to the 8 XCDs round-robin (XCD k takes tiles k mod 8), so
+// each x row is read by one XCD.  With S > 1 each slice writes its binary64
+// partial sums and rl_reduce_kernel adds the slices in slice order (a fixed
+// order: the logits do not depend on scheduling); S is chosen so the grid
+// holds about three workgroups per CU (at 512 tokens 16 slices: 48 tiles
+// alone would leave 208 CUs idle while each walked all of K).
+typedef double rt_f64x4 __attribute__((ext_vector_type(4)));
+constexpr uint32_t RL_T = 32, RL_K = 64, RL_P = RL_K + 4, RL_MAX_SLICES = 16;
 
 template <uint32_t RL_E>
-__global__ void __launch_bounds__(256) f64mm_router_lds_kernel(float *__restrict__ out, const float *__restrict__ w,
+__global__ void __launch_bounds__(256) f64mm_router_lds_kernel(float *__restrict__ out, double *__restrict__ part,
+                                                               const float *__restrict__ w,
                                                                const float *__restrict__ x, uint32_t K, uint32_t E,
                                                                uint32_t T) {
     static_assert(RL_T == 32 && RL_E % 32 == 0 && RL_K % 32 == 0, "copy: 32 rows x 8 float4 lanes per pass");
@@ -157,15 +94,16 @@ __global__ void __launch_bounds__(256) f64mm_router_lds_kernel(float *__restrict
     if (q >= ct * ne) return;
     const uint32_t et = q / ct, tt = xcd + 8u * (q - et * ct);
     const uint32_t t0 = tt * RL_T, e0 = et * RL_E;
+    const uint32_t S = gridDim.y, ks = K / S, kb = blockIdx.y * ks;   // this workgroup's K slice
     // copy assignments: x row tid/8 (float4 tid%8); W rows 32m + tid/8
     const uint32_t cr = tid >> 3, cc = (tid & 7u) * 4u;
     const uint32_t xr = t0 + cr < T ? t0 + cr : T - 1u;               // loads stay in bounds
-    const float *xp = x + (uint64_t)xr * K + cc;
+    const float *xp = x + (uint64_t)xr * K + kb + cc;
     const float *wp[RL_WT];
 #pragma unroll
     for (uint32_t m = 0; m < RL_WT; m++) {
         const uint32_t wr = e0 + 32u * m + cr < E ? e0 + 32u * m + cr : E - 1u;
-        wp[m] = w + (uint64_t)wr * K + cc;
+        wp[m] = w + (uint64_t)wr * K + kb + cc;
     }
     constexpr uint32_t NC = RL_K / 32u;    // float4 columns per thread and row
     sf37_f32x4 rx[NC], rw[RL_WT][NC];
@@ -196,7 +134,7 @@ __global__ void __launch_bounds__(256) f64mm_router_lds_kernel(float *__restrict
     rt_f64x4 acc[NT];
 #pragma unroll
     for (uint32_t h = 0; h < NT; h++) acc[h] = rt_f64x4{0.0, 0.0, 0.0, 0.0};
-    const uint32_t nk = K / RL_K;
+    const uint32_t nk = ks / RL_K;
     for (uint32_t kc = 0; kc < nk; kc++) {
         const uint32_t buf = kc & 1u;
         if (kc + 1u < nk) fetch((kc + 1u) * RL_K);
@@ -215,15 +153,29 @@ __global__ void __launch_bounds__(256) f64mm_router_lds_kernel(float *__restrict
         __syncthreads();
     }
     // D: lane l holds rows l/16 + 4r (tokens), column l%16 (expert)
+    double *ps = part + (uint64_t)blockIdx.y * T * E;
 #pragma unroll
     for (uint32_t h = 0; h < NT; h++) {
         const uint32_t e = e0 + (wave >> 1) * (RL_E / 2u) + 16u * h + i;
 #pragma unroll
         for (uint32_t r = 0; r < 4; r++) {
             const uint32_t t = t0 + (wave & 1u) * 16u + g + 4u * r;
-            if (t < T && e < E) out[(uint64_t)t * E + e] = (float)acc[h][r];
+            if (t < T && e < E) {
+                if (S == 1u) out[(uint64_t)t * E + e] = (float)acc[h][r];
+                else ps[(uint64_t)t * E + e] = acc[h][r];
+            }
         }
     }
+}
+
+// out[j] = the S slices' binary64 partial sums added in slice order, rounded once.
+__global__ void __launch_bounds__(256) rl_reduce_kernel(float *__restrict__ out, const double *__restrict__ part,
+                                                        uint32_t S, uint64_t n) {
+    const uint64_t j = (uint64_t)blockIdx.x * 256u + threadIdx.x;
+    if (j >= n) return;
+    double v = part[j];
+    for (uint32_t s = 1; s < S; s++) v += part[(uint64_t)s * n + j];
+    out[j] = (float)v;
 }
 
 // Decode GEMV (n_tok small): one workgroup per expert row and 8 tokens.
@@ -299,29 +251,52 @@ uint32_t router_cus() {
     return (uint32_t)cus;
 }
 
+// Matrix-core plan for n_tok > 16: expert tile (96 or 64, the one that pads
+// E less) and the number of K slices (a power of two up to 16 that divides K
+// into 64-wide chunks, the smallest giving about three workgroups per CU).
+// Returns 0 where the GEMV or the generic kernel runs instead.
+int rl_plan(uint64_t in_dim, uint64_t out_dim, uint64_t n_tok, uint32_t *te, uint32_t *S) {
+    if (n_tok <= 16 || in_dim % 128u != 0 || in_dim > 0xffffffffu || out_dim > 0xffffffffu || n_tok > 0xffffffffu)
+        return 0;
+    const uint64_t pad96 = (out_dim + 95) / 96 * 96 - out_dim, pad64 = (out_dim + 63) / 64 * 64 - out_dim;
+    *te = pad96 <= pad64 ? 96u : 64u;
+    const uint64_t tiles = (n_tok + RL_T - 1) / RL_T * ((out_dim + *te - 1) / *te), want = 3u * router_cus();
+    uint32_t s = 1;
+    while (s < RL_MAX_SLICES && tiles * s < want && in_dim % (2u * s * RL_K) == 0) s *= 2u;
+    *S = s;
+    return 1;
+}
+
 }  // namespace
 
+extern "C" uint64_t sf37k_f32_matmul_part_bytes(uint64_t in_dim, uint64_t out_dim, uint64_t n_tok) {
+    uint32_t te, S;
+    return rl_plan(in_dim, out_dim, n_tok, &te, &S) && S > 1u ? (uint64_t)S * n_tok * out_dim * 8u : 0u;
+}
+
 extern "C" int sf37k_f32_matmul(float *out, const float *w, const float *x, uint64_t in_dim,
-                                uint64_t out_dim, uint64_t n_tok, sf37_stream_t s) {
+                                uint64_t out_dim, uint64_t n_tok, double *part, uint64_t part_bytes,
+                                sf37_stream_t s) {
     if (out_dim == 0 || n_tok == 0) return 0;
+    uint32_t te, S;
     if (n_tok <= 16) {
         hipLaunchKernelGGL(f32_matvec_kernel, dim3((unsigned)out_dim, (unsigned)((n_tok + 7) / 8)),
                            dim3(256), 0, (hipStream_t)s, out, w, x, in_dim, out_dim, (uint32_t)n_tok);
-    } else if (in_dim % 128u == 0 && in_dim <= 0xffffffffu && out_dim <= 0xffffffffu && n_tok <= 0xffffffffu &&
-               n_tok >= RL_MIN_TOK) {
-        const uint64_t nt = (n_tok + RL_T - 1) / RL_T, cus = router_cus();
-        const uint64_t ne64 = (out_dim + 63) / 64, ne96 = (out_dim + 95) / 96;
-        const uint64_t r64 = (nt * ne64 + cus - 1) / cus, r96 = (nt * ne96 + cus - 1) / cus;
-        if (3u * r96 < 2u * r64)
-            hipLaunchKernelGGL(f64mm_router_lds_kernel<96>, dim3((unsigned)(8u * ((nt + 7) / 8) * ne96)), dim3(256),
-                               0, (hipStream_t)s, out, w, x, (uint32_t)in_dim, (uint32_t)out_dim, (uint32_t)n_tok);
+    } else if (rl_plan(in_dim, out_dim, n_tok, &te, &S)) {
+        if (S > 1u && (!part || part_bytes < (uint64_t)S * n_tok * out_dim * 8u)) S = 1;   // no workspace: one slice
+        const uint64_t nt = (n_tok + RL_T - 1) / RL_T, ne = (out_dim + te - 1) / te;
+        const dim3 grid((unsigned)(8u * ((nt + 7) / 8) * ne), S);
+        if (te == 96u)
+            hipLaunchKernelGGL(f64mm_router_lds_kernel<96>, grid, dim3(256), 0, (hipStream_t)s, out, part, w, x,
+                               (uint32_t)in_dim, (uint32_t)out_dim, (uint32_t)n_tok);
         else
-            hipLaunchKernelGGL(f64mm_router_lds_kernel<64>, dim3((unsigned)(8u * ((nt + 7) / 8) * ne64)), dim3(256),
-                               0, (hipStream_t)s, out, w, x, (uint32_t)in_dim, (uint32_t)out_dim, (uint32_t)n_tok);
-    } else if (in_dim % 128u == 0 && in_dim <= 0xffffffffu && out_dim <= 0xffffffffu && n_tok <= 0xffffffffu) {
-        const uint64_t nt = (n_tok + 15) / 16, ne = (out_dim + 63) / 64;
-        hipLaunchKernelGGL(f64mm_router_kernel, dim3((unsigned)(8u * ((nt + 7) / 8) * ne)), dim3(256), 0,
-                           (hipStream_t)s, out, w, x, (uint32_t)in_dim, (uint32_t)out_dim, (uint32_t)n_tok);
+            hipLaunchKernelGGL(f64mm_router_lds_kernel<64>, grid, dim3(256), 0, (hipStream_t)s, out, part, w, x,
+                               (uint32_t)in_dim, (uint32_t)out_dim, (uint32_t)n_tok);
+        if (S > 1u) {
+            const uint64_t n = n_tok * out_dim;
+            hipLaunchKernelGGL(rl_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)s, out,
+                               (const double *)part, S, n);
+        }
     } else {
         hipLaunchKernelGGL(f32_matmul_kernel,
                            dim3((unsigned)((out_dim + RT_E - 1) / RT_E), (unsigned)((n_tok + RT_T - 1) / RT_T)),

@@ -42,7 +42,7 @@ static void *g_scratch;
 static uint64_t g_scratch_bytes;
 static int g_model_fd = -1;
 
-#define N_LAYER_BUFS 11
+#define N_LAYER_BUFS 12
 static sf37_hip_tensor *g_layer_bufs[N_LAYER_BUFS];
 static uint64_t g_layer_buf_bytes[N_LAYER_BUFS];
 
@@ -219,6 +219,19 @@ static char *scratch_get(uint64_t bytes, const char *what) {
     g_scratch = p;
     g_scratch_bytes = bytes;
     return (char *)p;
+}
+
+static void *layer_buf(int i, uint64_t bytes);
+
+/* Router logits with binary64 sums.  Above 16 tokens the product is split
+ * over K into slices whose partial sums go to layer buffer 11 and are added
+ * in slice order; if that buffer cannot be had it runs unsplit (same sums,
+ * fewer workgroups). */
+static int router_matmul(float *out, const float *w, const float *x, uint64_t in_dim, uint64_t out_dim,
+                         uint64_t n_tok, sf37_stream_t s) {
+    const uint64_t pb = sf37k_f32_matmul_part_bytes(in_dim, out_dim, n_tok);
+    double *part = pb ? (double *)layer_buf(11, pb) : NULL;
+    return sf37k_f32_matmul(out, w, x, in_dim, out_dim, n_tok, part, part ? pb : 0, s);
 }
 
 /* Weight rows and activations are read with dword loads. */
@@ -811,7 +824,7 @@ int sf37_hip_matvec_f32(sf37_hip_tensor *out, const sf37_hip_tensor *weights, ui
                         uint64_t out_dim, const sf37_hip_tensor *x) {
     if (!out || !weights || !x || !ensure_init()) return 0;
     if (out->bytes < out_dim * 4u || x->bytes < in_dim * 4u || weights->bytes < out_dim * in_dim * 4u) return 0;
-    return LAUNCH(SF37_HIP_STAGE_ROUTER, sf37k_f32_matmul((float *)out->ptr, (const float *)weights->ptr, (const float *)x->ptr, in_dim,
+    return LAUNCH(SF37_HIP_STAGE_ROUTER, router_matmul((float *)out->ptr, (const float *)weights->ptr, (const float *)x->ptr, in_dim,
                                       out_dim, 1, (sf37_stream_t)g_stream),
                      "f32 matvec launch");
 }
@@ -832,7 +845,7 @@ int sf37_hip_matmul_f32_mapped(sf37_hip_tensor *out, const void *model_map, uint
         return 0;
     const float *w = (const float *)model_ptr(model_map, weight_offset, wb, "f32 weights");
     if (!w) return 0;
-    return LAUNCH(SF37_HIP_STAGE_ROUTER, sf37k_f32_matmul((float *)out->ptr, w, (const float *)x->ptr, in_dim, out_dim, n_tok,
+    return LAUNCH(SF37_HIP_STAGE_ROUTER, router_matmul((float *)out->ptr, w, (const float *)x->ptr, in_dim, out_dim, n_tok,
                                       (sf37_stream_t)g_stream),
                      "f32 matmul launch");
 }
@@ -875,7 +888,7 @@ int sf37_hip_matvec_bf16(sf37_hip_tensor *out, const sf37_hip_tensor *weights, u
     if (!f) return 0;
     return LAUNCH(SF37_HIP_STAGE_OTHER, sf37k_bf16_widen(f, (const uint16_t *)weights->ptr, n, (sf37_stream_t)g_stream),
                   "bf16 widen launch") &&
-           LAUNCH(SF37_HIP_STAGE_ROUTER, sf37k_f32_matmul((float *)out->ptr, f, (const float *)x->ptr, in_dim, out_dim,
+           LAUNCH(SF37_HIP_STAGE_ROUTER, router_matmul((float *)out->ptr, f, (const float *)x->ptr, in_dim, out_dim,
                                                           1, (sf37_stream_t)g_stream),
                   "bf16 matvec launch");
 }
@@ -897,7 +910,7 @@ int sf37_hip_matmul_bf16_mapped(sf37_hip_tensor *out, const void *model_map, uin
     const void *w = model_ptr(model_map, weight_offset, wb, "bf16 weights");
     const float *f = w ? bf16_resident_f32(w, out_dim * in_dim) : NULL;
     if (!f) return 0;
-    return LAUNCH(SF37_HIP_STAGE_ROUTER, sf37k_f32_matmul((float *)out->ptr, f, (const float *)x->ptr, in_dim, out_dim,
+    return LAUNCH(SF37_HIP_STAGE_ROUTER, router_matmul((float *)out->ptr, f, (const float *)x->ptr, in_dim, out_dim,
                                                           n_tok, (sf37_stream_t)g_stream),
                   "bf16 matmul launch");
 }
@@ -1110,8 +1123,6 @@ static int shared_mfma_eligible(uint32_t n_tok, uint32_t D, uint32_t F) {
     return g_opt_prefill && n_tok >= (uint64_t)g_opt_shared_min_tok && sf37k_sh_supported(D, F, D) &&
            (uint64_t)n_tok * D * 2u < (1ull << 32) && (uint64_t)n_tok * F * 2u < (1ull << 32);
 }
-
-static void *layer_buf(int i, uint64_t bytes);
 
 /* On stream st with its own activation buffer (layer buffer 8), so it can
  * run beside the routed pipeline, which uses the library scratch. */
@@ -1691,7 +1702,7 @@ static int dev_registered(const void *p, uint64_t bytes) {
 }
 
 /* Router logits of a BF16 or Q8_0 router (the F32 router runs inside the
- * decode launches or through sf37k_f32_matmul below). */
+ * decode launches or through router_matmul below). */
 static int layer_router_typed(float *logits, const sf37_hip_moe_layer_weights *w, const float *x, uint32_t n_tok) {
     const uint64_t E = w->n_expert, D = w->in_dim;
     if (w->router_type == SF37_HIP_TYPE_Q8_0)
@@ -1706,7 +1717,7 @@ static int layer_router_typed(float *logits, const sf37_hip_moe_layer_weights *w
                          "router bf16 widen launch"))
             return 0;
     }
-    return f && LAUNCH(SF37_HIP_STAGE_ROUTER, sf37k_f32_matmul(logits, f, x, D, E, n_tok, (sf37_stream_t)g_stream),
+    return f && LAUNCH(SF37_HIP_STAGE_ROUTER, router_matmul(logits, f, x, D, E, n_tok, (sf37_stream_t)g_stream),
                        "moe_layer bf16 router launch");
 }
 
@@ -1942,7 +1953,7 @@ static int moe_layer_impl(sf37_hip_tensor *out, sf37_hip_tensor *selected, sf37_
     float *wts = weights ? (float *)weights->ptr : (float *)layer_buf(2, (uint64_t)n_tok * K * 4u);
     if (!sel || !wts) return 0;
     if (run_router && router_f32 &&
-        !LAUNCH(SF37_HIP_STAGE_ROUTER, sf37k_f32_matmul(lg_buf, (const float *)w->router->ptr, xl, D, E, n_tok, st),
+        !LAUNCH(SF37_HIP_STAGE_ROUTER, router_matmul(lg_buf, (const float *)w->router->ptr, xl, D, E, n_tok, st),
                 "moe_layer router launch"))
         return 0;
     if (!logits) logits = lg_buf;

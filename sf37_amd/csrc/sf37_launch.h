@@ -29,9 +29,13 @@ int sf37k_q3_f32_matvec(float *out, const uint8_t *w, const float *x, uint64_t i
 int sf37k_q2_f32_matvec(float *out, const uint8_t *w, const float *x, uint64_t in_dim,
                         uint64_t out_dim, sf37_stream_t s);
 
-/* fp32 dense GEMV/GEMM with binary64 accumulation (router logits). */
+/* fp32 dense GEMV/GEMM with binary64 accumulation (router logits).  Above
+ * 16 tokens the product may be split over K: part (at least
+ * sf37k_f32_matmul_part_bytes bytes) then holds the slices' binary64 partial
+ * sums; with part NULL or smaller the product runs unsplit. */
+uint64_t sf37k_f32_matmul_part_bytes(uint64_t in_dim, uint64_t out_dim, uint64_t n_tok);
 int sf37k_f32_matmul(float *out, const float *w, const float *x, uint64_t in_dim,
-                     uint64_t out_dim, uint64_t n_tok, sf37_stream_t s);
+                     uint64_t out_dim, uint64_t n_tok, double *part, uint64_t part_bytes, sf37_stream_t s);
 /* Router: sigmoid, +bias, top-k (score desc, index asc), renormalise. */
 int sf37k_router_select(int32_t *selected, float *weights, float *probs,
                         const float *logits, const float *bias, uint32_t n_experts,
