@@ -84,3 +84,22 @@ def test_device_exp_source_matches_libm_exhaustively(tmp_path):
     r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=600)
     assert r.returncode == 0, r.stdout + r.stderr
     assert "expf_mismatch 0 sigmoid_mismatch 0" in r.stdout
+
+
+def test_router_split_plan():
+    """The prefill router GEMM's K split (k_router.hip rl_plan): the smallest
+    power-of-two slice count up to 16 that gives about three workgroups per
+    CU (256 CUs without a device, as on MI355X), only where the slices keep
+    K in 64-wide chunks; the workspace is one binary64 partial per slice,
+    token and expert, and none where the product runs unsplit."""
+    import ctypes as C
+    from sf37_amd import hip
+    f = hip.lib().sf37k_f32_matmul_part_bytes
+    f.argtypes = [C.c_uint64, C.c_uint64, C.c_uint64]
+    f.restype = C.c_uint64
+    E = 288
+    for k, t, slices in [(4096, 512, 16), (4096, 1100, 8), (4096, 2048, 4), (4096, 4096, 2),
+                         (4096, 17, 16), (384, 512, 2), (4096, 40000, 1), (4096, 16, 1),
+                         (4000, 512, 1)]:
+        want = slices * t * E * 8 if slices > 1 else 0
+        assert f(k, E, t) == want, (k, t, slices, f(k, E, t))
