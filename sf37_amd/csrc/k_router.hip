@@ -225,6 +225,7 @@ __global__ void __launch_bounds__(256) router_select_kernel(int32_t *__restrict_
                                                             float *__restrict__ weights,
                                                             float *__restrict__ probs,
                                                             const float *__restrict__ logits,
+                                                            const double *__restrict__ part, uint32_t S,
                                                             const float *__restrict__ bias,
                                                             uint32_t n_experts, uint32_t topk,
                                                             float scale, uint32_t n_tok) {
@@ -233,11 +234,25 @@ __global__ void __launch_bounds__(256) router_select_kernel(int32_t *__restrict_
     __syncthreads();
     const uint32_t t = blockIdx.x * 4u + (threadIdx.x >> 6);
     if (t >= n_tok) return;
-    const float *lg = logits + (uint64_t)t * n_experts;
     int32_t *so[1] = {selected + (uint64_t)t * topk};
     float *wo[1] = {weights + (uint64_t)t * topk};
     float *po[1] = {probs ? probs + (uint64_t)t * n_experts : nullptr};
-    sf37_wave_topk<1>([lg](uint32_t, uint32_t e) { return lg[e]; }, bias, n_experts, topk, scale, tab, so, wo, po);
+    if (part) {
+        // logits left as S binary64 slices by the split router GEMM: added in
+        // slice order and rounded once, as rl_reduce_kernel does
+        const uint64_t n = (uint64_t)n_tok * n_experts;
+        const double *pt = part + (uint64_t)t * n_experts;
+        sf37_wave_topk<1>(
+            [pt, n, S](uint32_t, uint32_t e) {
+                double v = pt[e];
+                for (uint32_t k = 1; k < S; k++) v += pt[(uint64_t)k * n + e];
+                return (float)v;
+            },
+            bias, n_experts, topk, scale, tab, so, wo, po);
+    } else {
+        const float *lg = logits + (uint64_t)t * n_experts;
+        sf37_wave_topk<1>([lg](uint32_t, uint32_t e) { return lg[e]; }, bias, n_experts, topk, scale, tab, so, wo, po);
+    }
 }
 
 uint32_t router_cus() {
@@ -276,7 +291,8 @@ extern "C" uint64_t sf37k_f32_matmul_part_bytes(uint64_t in_dim, uint64_t out_di
 
 extern "C" int sf37k_f32_matmul(float *out, const float *w, const float *x, uint64_t in_dim,
                                 uint64_t out_dim, uint64_t n_tok, double *part, uint64_t part_bytes,
-                                sf37_stream_t s) {
+                                uint32_t *slices_left, sf37_stream_t s) {
+    if (slices_left) *slices_left = 1;
     if (out_dim == 0 || n_tok == 0) return 0;
     uint32_t te, S;
     if (n_tok <= 16) {
@@ -292,7 +308,9 @@ extern "C" int sf37k_f32_matmul(float *out, const float *w, const float *x, uint
         else
             hipLaunchKernelGGL(f64mm_router_lds_kernel<64>, grid, dim3(256), 0, (hipStream_t)s, out, part, w, x,
                                (uint32_t)in_dim, (uint32_t)out_dim, (uint32_t)n_tok);
-        if (S > 1u) {
+        if (S > 1u && slices_left) {
+            *slices_left = S;   // the caller's top-8 launch adds the slices
+        } else if (S > 1u) {
             const uint64_t n = n_tok * out_dim;
             hipLaunchKernelGGL(rl_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)s, out,
                                (const double *)part, S, n);
@@ -308,8 +326,15 @@ extern "C" int sf37k_f32_matmul(float *out, const float *w, const float *x, uint
 extern "C" int sf37k_router_select(int32_t *selected, float *weights, float *probs,
                                    const float *logits, const float *bias, uint32_t n_experts,
                                    uint32_t topk, float scale, uint32_t n_tok, sf37_stream_t s) {
+    return sf37k_router_select_part(selected, weights, probs, logits, NULL, 1, bias, n_experts, topk, scale, n_tok, s);
+}
+
+extern "C" int sf37k_router_select_part(int32_t *selected, float *weights, float *probs, const float *logits,
+                                        const double *part, uint32_t slices, const float *bias, uint32_t n_experts,
+                                        uint32_t topk, float scale, uint32_t n_tok, sf37_stream_t s) {
     if (n_tok == 0) return 0;
-    hipLaunchKernelGGL(router_select_kernel, dim3((n_tok + 3) / 4), dim3(256), 0, (hipStream_t)s,
-                       selected, weights, probs, logits, bias, n_experts, topk, scale, n_tok);
+    hipLaunchKernelGGL(router_select_kernel, dim3((n_tok + 3) / 4), dim3(256), 0, (hipStream_t)s, selected,
+                       weights, probs, logits, slices > 1u ? part : (const double *)NULL, slices, bias, n_experts,
+                       topk, scale, n_tok);
     return (int)hipGetLastError();
 }

@@ -227,11 +227,17 @@ static void *layer_buf(int i, uint64_t bytes);
  * over K into slices whose partial sums go to layer buffer 11 and are added
  * in slice order; if that buffer cannot be had it runs unsplit (same sums,
  * fewer workgroups). */
-static int router_matmul(float *out, const float *w, const float *x, uint64_t in_dim, uint64_t out_dim,
-                         uint64_t n_tok, sf37_stream_t s) {
+static int router_matmul_part(float *out, const float *w, const float *x, uint64_t in_dim, uint64_t out_dim,
+                              uint64_t n_tok, uint32_t *slices_left, double **part_out, sf37_stream_t s) {
     const uint64_t pb = sf37k_f32_matmul_part_bytes(in_dim, out_dim, n_tok);
     double *part = pb ? (double *)layer_buf(11, pb) : NULL;
-    return sf37k_f32_matmul(out, w, x, in_dim, out_dim, n_tok, part, part ? pb : 0, s);
+    if (part_out) *part_out = part;
+    return sf37k_f32_matmul(out, w, x, in_dim, out_dim, n_tok, part, part ? pb : 0, slices_left, s);
+}
+
+static int router_matmul(float *out, const float *w, const float *x, uint64_t in_dim, uint64_t out_dim,
+                         uint64_t n_tok, sf37_stream_t s) {
+    return router_matmul_part(out, w, x, in_dim, out_dim, n_tok, NULL, NULL, s);
 }
 
 /* Weight rows and activations are read with dword loads. */
@@ -1952,14 +1958,19 @@ static int moe_layer_impl(sf37_hip_tensor *out, sf37_hip_tensor *selected, sf37_
     int32_t *sel = selected ? (int32_t *)selected->ptr : (int32_t *)layer_buf(1, (uint64_t)n_tok * K * 4u);
     float *wts = weights ? (float *)weights->ptr : (float *)layer_buf(2, (uint64_t)n_tok * K * 4u);
     if (!sel || !wts) return 0;
+    /* logits computed here feed only the top-8: a K-split router leaves its
+     * slices for the top-8 launch to add (no launch of its own) */
+    uint32_t slices = 1;
+    double *rpart = NULL;
     if (run_router && router_f32 &&
-        !LAUNCH(SF37_HIP_STAGE_ROUTER, router_matmul(lg_buf, (const float *)w->router->ptr, xl, D, E, n_tok, st),
+        !LAUNCH(SF37_HIP_STAGE_ROUTER, router_matmul_part(lg_buf, (const float *)w->router->ptr, xl, D, E, n_tok,
+                                                          logits ? NULL : &slices, &rpart, st),
                 "moe_layer router launch"))
         return 0;
     if (!logits) logits = lg_buf;
     if (E > ROUTER_MAX_EXPERTS ||
-        !LAUNCH(SF37_HIP_STAGE_SELECT, sf37k_router_select(sel, wts, NULL, logits, (const float *)w->router_bias->ptr, E, K, w->scale,
-                                       n_tok, st),
+        !LAUNCH(SF37_HIP_STAGE_SELECT, sf37k_router_select_part(sel, wts, NULL, logits, rpart, slices,
+                                       (const float *)w->router_bias->ptr, E, K, w->scale, n_tok, st),
                    "moe_layer router_select launch"))
         return 0;
     /* shared expert into out: Q3GU/Q2D on the Q8_K path, or Q8_0 gate/up

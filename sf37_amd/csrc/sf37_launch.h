@@ -32,14 +32,22 @@ int sf37k_q2_f32_matvec(float *out, const uint8_t *w, const float *x, uint64_t i
 /* fp32 dense GEMV/GEMM with binary64 accumulation (router logits).  Above
  * 16 tokens the product may be split over K: part (at least
  * sf37k_f32_matmul_part_bytes bytes) then holds the slices' binary64 partial
- * sums; with part NULL or smaller the product runs unsplit. */
+ * sums; with part NULL or smaller the product runs unsplit.  With
+ * slices_left non-NULL a split product leaves its slices in part (count in
+ * *slices_left, out not written) for sf37k_router_select_part to add. */
 uint64_t sf37k_f32_matmul_part_bytes(uint64_t in_dim, uint64_t out_dim, uint64_t n_tok);
 int sf37k_f32_matmul(float *out, const float *w, const float *x, uint64_t in_dim,
-                     uint64_t out_dim, uint64_t n_tok, double *part, uint64_t part_bytes, sf37_stream_t s);
+                     uint64_t out_dim, uint64_t n_tok, double *part, uint64_t part_bytes,
+                     uint32_t *slices_left, sf37_stream_t s);
 /* Router: sigmoid, +bias, top-k (score desc, index asc), renormalise. */
 int sf37k_router_select(int32_t *selected, float *weights, float *probs,
                         const float *logits, const float *bias, uint32_t n_experts,
                         uint32_t topk, float scale, uint32_t n_tok, sf37_stream_t s);
+/* The same from slices > 1 binary64 slices in part ([slices][n_tok][n_experts],
+ * added in slice order), or from logits when slices is 1. */
+int sf37k_router_select_part(int32_t *selected, float *weights, float *probs, const float *logits,
+                             const double *part, uint32_t slices, const float *bias, uint32_t n_experts,
+                             uint32_t topk, float scale, uint32_t n_tok, sf37_stream_t s);
 
 /* Q8_0 activations (32-wide) and Q8_0 GEMV / pair / batch. */
 int sf37k_q8_0_quantize(int8_t *xq, float *xscale, const float *x, uint64_t in_dim,

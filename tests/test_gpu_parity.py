@@ -175,9 +175,9 @@ def test_qlow_small_shapes_fp32_and_q8k_paths(H, O):
 def test_f32_router_gemv_and_gemm(H, O, layer):
     """Router logits accumulate in binary64 like the CPU engine
     (sf37.c:1970-1976); the summation order differs, so <= 1 ulp.  1 and 3
-    tokens: the GEMV kernel; 40: the register fp64-MFMA kernel; 1100 and
-    2000: the LDS-staged one with 64- and 96-expert workgroups (partial
-    32-token tiles)."""
+    tokens: the GEMV kernel; 40, 1100 and 2000: the fp64-MFMA kernel split
+    over 16, 8 and 4 K slices with the slice-order sum (partial 32-token
+    tiles)."""
     wr = layer.router.read(np.float32)
     for n_tok in (1, 3, 40, 1100, 2000):
         x = np.random.default_rng(n_tok).standard_normal((n_tok, K)).astype(np.float32)
@@ -412,6 +412,27 @@ def test_layer_decode_configs_bit_exact(H, O, layer, config):
     assert np.array_equal(sel, wsel)
     assert_bitexact(w, ww, "routing weights")
     assert_bitexact(out, want, f"layer config {config}")
+
+
+def test_layer_router_slices_summed_in_top8(H, layer):
+    """Above 16 tokens the layer's own router leaves its K slices for the
+    top-8 launch to add; that launch must select, weight and combine exactly
+    as the layer does from the logits the slice-order reduce writes."""
+    for n_tok in (40, 512):
+        x = np.random.default_rng(7 + n_tok).standard_normal((n_tok, K)).astype(np.float32)
+        say(f"router slices in top-8: {n_tok} tokens")
+        lt = H.Tensor.alloc(n_tok * E * 4)
+        key = map_key()
+        H.check(H.lib().sf37_hip_register_device_range(key, layer.router.nbytes, 0,
+                                                       layer.router.nbytes, layer.router.h), "register")
+        H.check(H.lib().sf37_hip_matmul_f32_mapped(lt.h, key, layer.router.nbytes, 0, K, E,
+                                                   H.Tensor.from_array(x), n_tok), "matmul_f32_mapped")
+        logits = lt.read(np.float32).reshape(n_tok, E)
+        out0, sel0, w0 = layer_run(H, layer, x, None)
+        out1, sel1, w1 = layer_run(H, layer, x, logits)
+        assert np.array_equal(sel0, sel1), n_tok
+        assert_bitexact(w0, w1, f"routing weights, {n_tok} tokens")
+        assert_bitexact(out0, out1, f"layer, {n_tok} tokens")
 
 
 def test_layer_prefill_config2_sample(H, O, layer):
